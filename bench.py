@@ -1,0 +1,267 @@
+"""Benchmark of the MI355X quantized-weight matrix path (one GPU).
+
+A "step" is one pass of the hot path over one batch: one launch of the decode
+GEMV (or W8A8 linear) on weights already resident in HBM. The headline workload
+is BASELINE.json configs[1]: the group-wise int4 GEMV at the Qwen2.5-1.5B
+down-proj shape (M=1, K=8960, N=1536, fp16 x/y, fp16 group scales, g=32).
+
+Timing: W warm-up launches, then K launches captured in one HIP graph (so the
+GPU runs them back to back, free of host launch gaps) and replayed inside a
+pair of HIP events recorded on the launch stream; ms_per_step = region / K.
+The weights rotate over enough copies (>= 512 MiB in total) that each launch
+streams them from HBM rather than from the 256 MiB Infinity Cache. Bytes are
+algorithmic: every operand once (weights + scales + x + y).
+
+One JSON line on stdout; `--sweep` (default on) adds the other BASELINE configs
+under "sweep". The CPU baseline times the reference's own AVX2+OpenMP
+linear_q4g (oracle/_ref, built from the reference sources) — or the C
+restatement when that build is absent — on a bounded sample of the same
+workload, on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA
+ROTATE_BYTES = 512 << 20
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--no-sweep", action="store_true")
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--only", default="", help="comma list of sweep entries to run (debug)")
+    return p.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
+              "the path is single-GPU by design", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from nanoinfer_amd import _lib
+    from nanoinfer_amd import quant as nq
+
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20261201)
+
+    def rnd(shape, std, dtype=torch.float32):
+        return (torch.randn(shape, generator=gen, device=dev, dtype=torch.float32) * std).to(dtype)
+
+    def copies_for(nbytes):
+        return max(2, math.ceil(ROTATE_BYTES / max(nbytes, 1)))
+
+    def time_graph(launches, steps, warmup):
+        """launches: list of zero-arg callables (rotating weight copies).
+        Returns ms per launch over a graph of `steps` back-to-back launches."""
+        r = len(launches)
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            for i in range(warmup):
+                launches[i % r]()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(steps):
+                launches[i % r]()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            g.replay()                                   # untimed replay (first-replay setup)
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record(s)
+            g.replay()
+            e1.record(s)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    def stream_ptr():
+        return torch.cuda.current_stream().cuda_stream
+
+    P = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+
+    # ---------------- workloads ----------------------------------------------------------
+    def q4g_gemv(m, n, k, g=32):
+        x = rnd((m, k), 1.0, torch.float16)
+        w = rnd((n, k), 0.02)
+        t = nq.quantize_q4g(w, g, scale_dtype=torch.float16)
+        del w
+        wbytes = t.q.numel() + t.scale.numel() * 2
+        nb = wbytes + x.numel() * 2 + m * n * 2
+        qs = [t.q] + [t.q.clone() for _ in range(copies_for(wbytes) - 1)]
+        ss = [t.scale] + [t.scale.clone() for _ in range(len(qs) - 1)]
+        y = torch.empty((m, n), dtype=torch.float16, device=dev)
+
+        def mk(i):
+            return lambda: lib.nq_linear_q4g(P(x), 1, P(qs[i]), P(ss[i]), 1, g, None, P(y), 1, m, n, k, stream_ptr())
+        return [mk(i) for i in range(len(qs))], nb, 2 * m * n * k
+
+    def q8_gemv(m, n, k, xdt):
+        x = rnd((m, k), 1.0, xdt)
+        w = rnd((n, k), 0.02)
+        t = nq.quantize_q8(w)
+        del w
+        wbytes = t.q.numel() + t.scale.numel() * 4
+        esz = 2 if xdt == torch.float16 else 4
+        nb = wbytes + x.numel() * esz + m * n * esz
+        qs = [t.q] + [t.q.clone() for _ in range(copies_for(wbytes) - 1)]
+        ss = [t.scale] + [t.scale.clone() for _ in range(len(qs) - 1)]
+        y = torch.empty((m, n), dtype=xdt, device=dev)
+        dt = 1 if xdt == torch.float16 else 0
+
+        def mk(i):
+            return lambda: lib.nq_linear_q8(P(x), dt, P(qs[i]), P(ss[i]), None, P(y), dt, m, n, k, stream_ptr())
+        return [mk(i) for i in range(len(qs))], nb, 2 * m * n * k
+
+    def w8a8_linear(m, n, k, gemm_only=False):
+        x = rnd((m, k), 1.0, torch.float16)
+        w = rnd((n, k), 0.02)
+        t = nq.quantize_q8(w)
+        del w
+        wbytes = t.q.numel() + t.scale.numel() * 4
+        nb = wbytes + (m * k if gemm_only else 2 * m * k) + 2 * m * n
+        qs = [t.q] + [t.q.clone() for _ in range(copies_for(wbytes) - 1)]
+        ss = [t.scale] + [t.scale.clone() for _ in range(len(qs) - 1)]
+        y = torch.empty((m, n), dtype=torch.float16, device=dev)
+        if gemm_only:
+            xq, a_s = nq.act_quant(x)
+            wsb = lib.nq_gemm_w8a8_workspace_size(m, n, k)
+            ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+
+            def mk(i):
+                return lambda: lib.nq_gemm_w8a8(P(xq), P(a_s), P(qs[i]), P(ss[i]), None, P(y), 1, m, n, k,
+                                                P(ws), ws.numel(), 0, stream_ptr())
+        else:
+            wsb = lib.nq_linear_w8a8_workspace_size(m, n, k)
+            ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+
+            def mk(i):
+                return lambda: lib.nq_linear_w8a8(P(x), 1, P(qs[i]), P(ss[i]), None, P(y), 1, m, n, k,
+                                                  P(ws), ws.numel(), 0, stream_ptr())
+        return [mk(i) for i in range(len(qs))], nb, 2 * m * n * k
+
+    def entry(name, launches, nb, ops, bound):
+        ms = time_graph(launches, args.steps, args.warmup)
+        gbs = nb / (ms * 1e-3) / 1e9
+        tops = ops / (ms * 1e-3) / 1e12
+        e = {"name": name, "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "TOPS": round(tops, 2),
+             "bytes": nb, "ops": ops, "bound": bound,
+             "frac": round(gbs / HBM_PEAK_GBS if bound == "hbm" else tops / INT8_PEAK_TOPS, 4)}
+        return e
+
+    # ---------------- headline: configs[1] int4 GEMV ------------------------------------------
+    M, N, K, G = 1, 1536, 8960, 32
+    launches, nbytes, ops = q4g_gemv(M, N, K, G)
+    ms = time_graph(launches, args.steps, args.warmup)
+    del launches
+    torch.cuda.empty_cache()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+
+    sweep = []
+    if not args.no_sweep:
+        only = set(filter(None, args.only.split(",")))
+
+        def want(n):
+            return not only or n in only
+        if want("q8_gemv_cfg1"):
+            sweep.append(entry("q8_gemv_cfg1 M=1 K=896 N=4864 fp32", *q8_gemv(1, 4864, 896, torch.float32), "hbm"))
+        if want("lmhead_cfg5b"):
+            sweep.append(entry("q8_lmhead_cfg5b M=1 K=1536 N=151936 fp16", *q8_gemv(1, 151936, 1536, torch.float16), "hbm"))
+        torch.cuda.empty_cache()
+        if want("w8a8_cfg3"):
+            for m in (8, 16, 32, 64):
+                for nm, (n, k) in (("qo", (1536, 1536)), ("kv", (256, 1536)), ("gateup", (8960, 1536)),
+                                   ("down", (1536, 8960))):
+                    sweep.append(entry(f"w8a8_cfg3 {nm} M={m} K={k} N={n}", *w8a8_linear(m, n, k), "hbm"))
+                    torch.cuda.empty_cache()
+        if want("prefill_cfg5a"):
+            sweep.append(entry("w8a8_gemm_cfg5a M=2048 K=1536 N=8960 (pre-quantized x)",
+                               *w8a8_linear(2048, 8960, 1536, gemm_only=True), "mfma"))
+            sweep.append(entry("w8a8_linear_cfg5a M=2048 K=1536 N=8960 (incl. act quant)",
+                               *w8a8_linear(2048, 8960, 1536), "mfma"))
+        torch.cuda.empty_cache()
+
+    # ---------------- CPU baseline (rank 0, N=1) --------------------------------------------
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(M, N, K, G, nbytes, args.cpu_seconds)
+
+    out = {
+        "metric": "int8/int4 GEMV HBM GB/s (% peak); W8A8 GEMM int8 TOPS (% MFMA peak)",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 weights, fp16 x/y, fp32 accumulate",
+        "data": "synthetic (weights N(0,0.02) quantized on device, x N(0,1)); weights rotated over "
+                f">= {ROTATE_BYTES >> 20} MiB of copies",
+        "config": {"workload": "configs[1]: int4 group GEMV, Qwen2.5-1.5B down-proj",
+                   "M": M, "K": K, "N": N, "group": G, "scale_dtype": "fp16", "x_dtype": "fp16",
+                   "algorithmic_bytes": nbytes, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    if sweep:
+        out["sweep"] = sweep
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline(m, n, k, g, nbytes, seconds):
+    """Time the reference's CPU linear_q4g (quant.cpp:337-389) on the same shape."""
+    import numpy as np
+
+    import oracle
+    impl = oracle.reference()
+    kind = "reference"
+    if impl is None:
+        impl = oracle.oracle()
+        kind = "port"
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((m, k)).astype(np.float16).astype(np.float32)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    q, s = impl.quantize_q4g(w, g)
+    s = s.astype(np.float16).astype(np.float32)      # the fp16 storage variant's scales, widened
+    impl.linear_q4g(x, q, s, g)                      # warm
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        impl.linear_q4g(x, q, s, g)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": impl.max_threads(),
+            "kind": kind,
+            "sample": f"{len(times)} calls of linear_q4g M={m} K={k} N={n} g={g} (median {med * 1e3:.2f} ms), "
+                      f"~{seconds:.0f}s of CPU work, same algorithmic bytes; nproc={os.cpu_count()}"}
+
+
+if __name__ == "__main__":
+    main()

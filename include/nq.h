@@ -1,0 +1,132 @@
+/* nq.h — C ABI of libnq_hip.so, the MI355X (gfx950) quantized-weight matrix path.
+ *
+ * Every entry point takes device pointers, plain sizes and a HIP stream
+ * (hipStream_t passed as void*; NULL = the null stream), enqueues its kernels on
+ * that stream and returns without synchronizing. No entry point allocates
+ * device memory: scratch space, where a path needs it, is a caller-owned
+ * workspace whose size the matching *_workspace_size() call returns.
+ *
+ * Layouts follow the reference (cpp/src/quant.hpp:48-111):
+ *   weights        [n, k] row-major, k contiguous (n = out-features, k = in);
+ *   Q8 / W8A8      int8 codes [n*k] + fp32 per-row scale [n];
+ *   Q4G            packed nibbles [n*ceil(k/2)] (column 2i -> low nibble of byte
+ *                  i, stored as code+8) + one scale per (row, group)
+ *                  [n*ceil(k/group)], fp32 (reference) or fp16 (storage variant);
+ *   activations    x [m, k] row-major, fp32 or fp16; y [m, n] fp32 or fp16;
+ *   bias           fp32 [n] or NULL.
+ *
+ * Errors: a non-NQ_OK status leaves the stream untouched (validation happens
+ * before any launch) except NQ_HIP_ERROR, which reports a failed launch.
+ * nq_last_error() returns the calling thread's message for its last failure —
+ * the text the reference puts in its std::invalid_argument / runtime_error.
+ */
+#ifndef NQ_H
+#define NQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum nq_status {
+    NQ_OK = 0,
+    NQ_BAD_SHAPE = 1, /* dims negative / inconsistent / beyond the 32-bit index range */
+    NQ_BAD_ALIGN = 2, /* a pointer is not aligned to its element size */
+    NQ_HIP_ERROR = 3, /* a HIP runtime call or kernel launch failed */
+    NQ_BAD_ARG = 4,   /* null pointer, unknown enum, too-small workspace, bad id */
+} nq_status;
+
+typedef enum nq_dtype { NQ_F32 = 0, NQ_F16 = 1 } nq_dtype;
+
+/* Kernel selection for the W8A8 linears. AUTO: m <= 8 -> wave-per-row GEMV
+ * (v_dot4_i32_i8), m >= 9 -> int8 MFMA GEMM. The forced values exist for A/B
+ * tests, like the reference's CudaPolicy::force_tiled_w8a8
+ * (cuda_backend.hpp:43-89). GENERIC is the scalar bounds-checked kernel. */
+typedef enum nq_path { NQ_PATH_AUTO = 0, NQ_PATH_GEMV = 1, NQ_PATH_MFMA = 2, NQ_PATH_GENERIC = 3 } nq_path;
+
+/* Library identification and error text. */
+const char* nq_version(void);
+const char* nq_status_name(int status);
+const char* nq_last_error(void);
+
+/* ---- quantize / pack (device side) ------------------------------------------
+ * nq_quantize_q8 replaces the host quantize_q8 (quant.cpp:88-108) that
+ * make_cuda_w8a8 / make_cuda_q8_embed run before upload (cuda_quant.cu:345-388):
+ * scale[o] = max_j|w[o,j]| / 127 (fp32), q = round-half-even(w / scale)
+ * clamped to +-127, NaN -> 0, all-zero row -> scale 0. Bit-exact with the
+ * reference. w: fp32 [out, in]. */
+nq_status nq_quantize_q8(const float* w, int64_t out, int64_t in, int8_t* q, float* scale,
+                         void* stream);
+
+/* Replaces quantize_q4g (quant.cpp:295-321): per (row, group) scale = absmax/7
+ * computed in fp32, codes in [-7,7] from that fp32 scale, packed code+8 with the
+ * even column in the low nibble. scale_dtype NQ_F16 stores the fp32 scale rounded
+ * to fp16 (round-to-nearest-even); the codes are unchanged. q and scale are fully
+ * written (no pre-zeroing needed). */
+nq_status nq_quantize_q4g(const float* w, int64_t out, int64_t in, int64_t group, uint8_t* q,
+                          void* scale, nq_dtype scale_dtype, void* stream);
+
+/* Replaces activation_quant_kernel (cuda_quant.cu:38-58) / the act-quant loop of
+ * linear_w8a8 (quant.cpp:179-193): per-row a_scale = absmax/127 and int8 codes,
+ * computed on the fp32 value of x (fp16 x is widened exactly first). */
+nq_status nq_act_quant_i8(const void* x, nq_dtype x_dtype, int64_t m, int64_t k, int8_t* xq,
+                          float* a_scale, void* stream);
+
+/* ---- weight-only linears ------------------------------------------------------
+ * Replaces cuda_linear_q8 (cuda/cuda.hpp:53, cuda_quant.cu:300-322) and the CPU
+ * linear_q8 (quant.cpp:136-163): y[i,o] = (sum_j x[i,j]*q[o,j]) * w_scale[o] + b[o],
+ * fp32 accumulation. */
+nq_status nq_linear_q8(const void* x, nq_dtype x_dtype, const int8_t* q, const float* w_scale,
+                       const float* bias, void* y, nq_dtype y_dtype, int64_t m, int64_t n,
+                       int64_t k, void* stream);
+
+/* Replaces linear_q4g (quant.cpp:337-389; the reference has no GPU int4 kernel):
+ * y[i,o] = sum_blocks scale[o,blk] * (sum_{j in blk} x[i,j]*(nib-8)) + b[o]. */
+nq_status nq_linear_q4g(const void* x, nq_dtype x_dtype, const uint8_t* q, const void* scale,
+                        nq_dtype scale_dtype, int64_t group, const float* bias, void* y,
+                        nq_dtype y_dtype, int64_t m, int64_t n, int64_t k, void* stream);
+
+/* ---- W8A8 ------------------------------------------------------------------------
+ * Replaces cuda_linear_w8a8 (cuda/cuda.hpp:41, cuda_quant.cu:250-284) and the CPU
+ * linear_w8a8 (quant.cpp:165-210): dynamic per-row int8 activation quant, exact
+ * int32 accumulation, y = float(acc) * a_scale[i] * w_scale[o] + b[o].
+ * workspace: >= nq_linear_w8a8_workspace_size(m, n, k) bytes, 256-byte aligned;
+ * the reference allocated xq/a_scale per call (cuda_quant.cu:253-258). */
+size_t nq_linear_w8a8_workspace_size(int64_t m, int64_t n, int64_t k);
+nq_status nq_linear_w8a8(const void* x, nq_dtype x_dtype, const int8_t* wq, const float* w_scale,
+                         const float* bias, void* y, nq_dtype y_dtype, int64_t m, int64_t n,
+                         int64_t k, void* workspace, size_t workspace_bytes, int path,
+                         void* stream);
+
+/* The same linear on activations that are already quantized (xq, a_scale from
+ * nq_act_quant_i8) — the GEMM half of cuda_linear_w8a8 (cuda_quant.cu:260-283).
+ * workspace: >= nq_gemm_w8a8_workspace_size(m, n, k) bytes (split-K partials). */
+size_t nq_gemm_w8a8_workspace_size(int64_t m, int64_t n, int64_t k);
+nq_status nq_gemm_w8a8(const int8_t* xq, const float* a_scale, const int8_t* wq,
+                       const float* w_scale, const float* bias, void* y, nq_dtype y_dtype,
+                       int64_t m, int64_t n, int64_t k, void* workspace, size_t workspace_bytes,
+                       int path, void* stream);
+
+/* Debug/parity entry: the exact int32 accumulators acc[i,o] = sum_j xq[i,j]*wq[o,j]
+ * of the chosen path (the integer core of simd::dot_qq, simd.hpp:160-197, which
+ * the reference never exposes). Same workspace rule as nq_gemm_w8a8. */
+nq_status nq_w8a8_acc_i32(const int8_t* xq, const int8_t* wq, int32_t* acc, int64_t m, int64_t n,
+                          int64_t k, void* workspace, size_t workspace_bytes, int path,
+                          void* stream);
+
+/* ---- int8 embedding gather --------------------------------------------------------
+ * Replaces cuda_embedding_q8 (cuda/cuda.hpp:46, cuda_quant.cu:286-298) and
+ * embedding_q8 (quant.cpp:121-134): out[r,c] = codes[ids[r],c] * scale[ids[r]].
+ * ids is a HOST array, as in the reference; an id outside [0, vocab) returns
+ * NQ_BAD_ARG before anything is enqueued. */
+nq_status nq_embedding_q8(const int8_t* codes, const float* scale, int64_t vocab, int64_t hidden,
+                          const int64_t* ids, int64_t n, void* out, nq_dtype out_dtype,
+                          void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NQ_H */

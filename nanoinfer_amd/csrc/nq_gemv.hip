@@ -1,0 +1,507 @@
+// Decode GEMVs (m <= 8): weight-only int8, group-wise int4, and W8A8.
+//
+// Mapping (all three kernels): one workgroup owns R output rows and the whole
+// K extent of those rows. K is cut into 16-byte chunks (16 int8 codes, or 32
+// packed int4 codes); thread t of the workgroup owns chunk t of every one of
+// the R rows, so each lane issues R independent global_load_dwordx4 up front
+// (coalesced: the 64 lanes of a wave read 1 KiB contiguous per row) and reuses
+// the activation chunk it loads for all R rows. Per-lane partials are reduced
+// across the wave with DPP + two bpermutes, across waves through LDS in a fixed
+// order (deterministic), then scaled once per row at the store — the reference
+// "accumulate then scale" order (quant.cpp:155-161, cuda_quant.cu:217-235).
+//
+// Shapes outside the fast path (k not a multiple of the chunk, misaligned
+// pointers, k beyond the chunk budget of one workgroup) run a generic
+// bounds-checked wave-per-row kernel with the same arithmetic.
+#include <hip/hip_runtime.h>
+
+#include "nq_device.hpp"
+#include "nq_internal.hpp"
+
+namespace nq {
+namespace {
+
+constexpr int kMaxGemvWaves = 9;          // 576 lanes: int8 k <= 9216, int4 k <= 18432
+constexpr int kMaxGemvThreads = kMaxGemvWaves * kWave;
+
+// Rows per workgroup as a function of the activation-row count: more rows =
+// more reuse of each loaded activation chunk, fewer = more workgroups.
+template <int M>
+constexpr int rows_for() {
+    return M <= 2 ? 4 : 2;
+}
+
+// ---- chunk loaders ---------------------------------------------------------------
+__device__ __forceinline__ void load_x16(const float* p, float (&xf)[16]) {
+    const f4* v = reinterpret_cast<const f4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const f4 t = v[i];
+        xf[4 * i + 0] = t.x;
+        xf[4 * i + 1] = t.y;
+        xf[4 * i + 2] = t.z;
+        xf[4 * i + 3] = t.w;
+    }
+}
+__device__ __forceinline__ void load_x16(const _Float16* p, float (&xf)[16]) {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    const h8* v = reinterpret_cast<const h8*>(p);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const h8 t = v[i];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xf[8 * i + j] = static_cast<float>(t[j]);
+    }
+}
+
+// ---- weight-only int8 ------------------------------------------------------------
+template <int R, int M, typename XT, typename YT>
+__global__ __launch_bounds__(kMaxGemvThreads) void gemv_q8_kernel(
+    const XT* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ ws,
+    const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k) {
+    __shared__ float red[kMaxGemvWaves * R * M];
+    const int tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6;
+    const int chunks = k >> 4;
+    const bool act = tid < chunks;
+    const int row0 = blockIdx.x * R;
+
+    v4i wv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = min(row0 + r, n - 1);
+        wv[r] = act ? *reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * k + tid * 16)
+                    : v4i{0, 0, 0, 0};
+    }
+    float acc[R][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < M; ++i) acc[r][i] = 0.0f;
+
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        if (i < m && act) {
+            float xf[16];
+            load_x16(x + static_cast<size_t>(i) * k + tid * 16, xf);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const int wd = wv[r][d];
+                    acc[r][i] = __builtin_fmaf(xf[4 * d + 0], sbyte_f32<0>(wd), acc[r][i]);
+                    acc[r][i] = __builtin_fmaf(xf[4 * d + 1], sbyte_f32<1>(wd), acc[r][i]);
+                    acc[r][i] = __builtin_fmaf(xf[4 * d + 2], sbyte_f32<2>(wd), acc[r][i]);
+                    acc[r][i] = __builtin_fmaf(xf[4 * d + 3], sbyte_f32<3>(wd), acc[r][i]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            const float v = wave_sum_f32(acc[r][i]);
+            if ((tid & 63) == 0) red[(wave * R + r) * M + i] = v;
+        }
+    __syncthreads();
+    if (tid < R * M) {
+        const int r = tid / M, i = tid % M, row = row0 + r;
+        if (row < n && i < m) {
+            float s = 0.0f;
+            for (int wv_i = 0; wv_i < nw; ++wv_i) s += red[(wv_i * R + r) * M + i];
+            const float b = bias ? bias[row] : 0.0f;
+            y[static_cast<size_t>(i) * n + row] = from_f32<YT>(__builtin_fmaf(s, ws[row], b));
+        }
+    }
+}
+
+// ---- group-wise int4 ------------------------------------------------------------------
+template <typename ST>
+__device__ __forceinline__ float load_scale(const ST* p) { return to_f32(*p); }
+
+template <int R, int M, typename XT, typename YT, typename ST>
+__global__ __launch_bounds__(kMaxGemvThreads) void gemv_q4g_kernel(
+    const XT* __restrict__ x, const uint8_t* __restrict__ w, const ST* __restrict__ scale,
+    const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int group) {
+    __shared__ float red[kMaxGemvWaves * R * M];
+    const int tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6;
+    const int chunks = k >> 5;  // 32 codes per 16-byte chunk
+    const int rb = k >> 1, blocks = k / group;
+    const bool act = tid < chunks;
+    const int row0 = blockIdx.x * R;
+    const int blk = (tid * 32) / group;
+
+    v4i wv[R];
+    float sc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = min(row0 + r, n - 1);
+        wv[r] = act ? *reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * rb + tid * 16)
+                    : v4i{0, 0, 0, 0};
+        sc[r] = act ? load_scale(scale + static_cast<size_t>(row) * blocks + blk) : 0.0f;
+    }
+    float acc[R][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < M; ++i) acc[r][i] = 0.0f;
+
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        if (i < m && act) {
+            float xf[32];
+            const XT* xp = x + static_cast<size_t>(i) * k + tid * 32;
+            load_x16(xp, *reinterpret_cast<float(*)[16]>(&xf[0]));
+            load_x16(xp + 16, *reinterpret_cast<float(*)[16]>(&xf[16]));
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float p = 0.0f;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const unsigned wd = static_cast<unsigned>(wv[r][d]);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float c = static_cast<float>(static_cast<int>((wd >> (4 * e)) & 15u) - 8);
+                        p = __builtin_fmaf(xf[8 * d + e], c, p);
+                    }
+                }
+                acc[r][i] = __builtin_fmaf(p, sc[r], acc[r][i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            const float v = wave_sum_f32(acc[r][i]);
+            if ((tid & 63) == 0) red[(wave * R + r) * M + i] = v;
+        }
+    __syncthreads();
+    if (tid < R * M) {
+        const int r = tid / M, i = tid % M, row = row0 + r;
+        if (row < n && i < m) {
+            float s = 0.0f;
+            for (int wv_i = 0; wv_i < nw; ++wv_i) s += red[(wv_i * R + r) * M + i];
+            const float b = bias ? bias[row] : 0.0f;
+            y[static_cast<size_t>(i) * n + row] = from_f32<YT>(s + b);
+        }
+    }
+}
+
+// ---- W8A8 (int8 x int8 -> int32) ------------------------------------------------------
+// ACC_OUT: write the raw int32 accumulators instead of the scaled output.
+template <int R, int M, typename YT, bool ACC_OUT>
+__global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_kernel(
+    const int8_t* __restrict__ xq, const float* __restrict__ as, const int8_t* __restrict__ w,
+    const float* __restrict__ ws, const float* __restrict__ bias, YT* __restrict__ y,
+    int32_t* __restrict__ acc_out, int m, int n, int k) {
+    __shared__ int red[kMaxGemvWaves * R * M];
+    const int tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6;
+    const int chunks = k >> 4;
+    const bool act = tid < chunks;
+    const int row0 = blockIdx.x * R;
+
+    v4i wv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = min(row0 + r, n - 1);
+        wv[r] = act ? *reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * k + tid * 16)
+                    : v4i{0, 0, 0, 0};
+    }
+    int acc[R][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < M; ++i) acc[r][i] = 0;
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        if (i < m && act) {
+            const v4i xv = *reinterpret_cast<const v4i*>(xq + static_cast<size_t>(i) * k + tid * 16);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+#pragma unroll
+                for (int d = 0; d < 4; ++d) acc[r][i] = __builtin_amdgcn_sdot4(xv[d], wv[r][d], acc[r][i], false);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            const int v = wave_sum_i32(acc[r][i]);
+            if ((tid & 63) == 0) red[(wave * R + r) * M + i] = v;
+        }
+    __syncthreads();
+    if (tid < R * M) {
+        const int r = tid / M, i = tid % M, row = row0 + r;
+        if (row < n && i < m) {
+            int s = 0;
+            for (int wv_i = 0; wv_i < nw; ++wv_i) s += red[(wv_i * R + r) * M + i];
+            if constexpr (ACC_OUT) {
+                acc_out[static_cast<size_t>(i) * n + row] = s;
+            } else {
+                const float b = bias ? bias[row] : 0.0f;
+                y[static_cast<size_t>(i) * n + row] = from_f32<YT>(w8a8_epilogue(s, as[i], ws[row], b));
+            }
+        }
+    }
+}
+
+// ---- generic bounds-checked kernels (any k, any alignment) -----------------------------
+// One wave per output row; lanes stride K one element at a time; rows of x loop.
+template <typename XT, typename YT>
+__global__ void gemv_q8_generic_kernel(const XT* __restrict__ x, const int8_t* __restrict__ w,
+                                       const float* __restrict__ ws, const float* __restrict__ bias,
+                                       YT* __restrict__ y, int m, int n, int k) {
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= n) return;
+    const int8_t* wr = w + static_cast<size_t>(row) * k;
+    const float b = bias ? bias[row] : 0.0f;
+    for (int i = 0; i < m; ++i) {
+        const XT* xr = x + static_cast<size_t>(i) * k;
+        float p = 0.0f;
+        for (int j = lane; j < k; j += kWave) p = __builtin_fmaf(to_f32(xr[j]), static_cast<float>(wr[j]), p);
+        p = wave_sum_f32(p);
+        if (lane == 0) y[static_cast<size_t>(i) * n + row] = from_f32<YT>(__builtin_fmaf(p, ws[row], b));
+    }
+}
+
+template <typename XT, typename YT, typename ST>
+__global__ void gemv_q4g_generic_kernel(const XT* __restrict__ x, const uint8_t* __restrict__ w,
+                                        const ST* __restrict__ scale, const float* __restrict__ bias,
+                                        YT* __restrict__ y, int m, int n, int k, int group) {
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= n) return;
+    const int rb = (k + 1) / 2, blocks = (k + group - 1) / group;
+    const uint8_t* wr = w + static_cast<size_t>(row) * rb;
+    const ST* sr = scale + static_cast<size_t>(row) * blocks;
+    const float b = bias ? bias[row] : 0.0f;
+    for (int i = 0; i < m; ++i) {
+        const XT* xr = x + static_cast<size_t>(i) * k;
+        float acc = 0.0f;
+        // Lanes take whole blocks so each block's partial sum is scaled once.
+        for (int blk = lane; blk < blocks; blk += kWave) {
+            const int j0 = blk * group, j1 = min(j0 + group, k);
+            float p = 0.0f;
+            for (int j = j0; j < j1; ++j) {
+                const int nib = (j & 1) ? (wr[j >> 1] >> 4) : (wr[j >> 1] & 15);
+                p = __builtin_fmaf(to_f32(xr[j]), static_cast<float>(nib - 8), p);
+            }
+            acc = __builtin_fmaf(p, to_f32(sr[blk]), acc);
+        }
+        acc = wave_sum_f32(acc);
+        if (lane == 0) y[static_cast<size_t>(i) * n + row] = from_f32<YT>(acc + b);
+    }
+}
+
+template <typename YT, bool ACC_OUT>
+__global__ void gemv_w8a8_generic_kernel(const int8_t* __restrict__ xq, const float* __restrict__ as,
+                                         const int8_t* __restrict__ w, const float* __restrict__ ws,
+                                         const float* __restrict__ bias, YT* __restrict__ y,
+                                         int32_t* __restrict__ acc_out, int m, int n, int k) {
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= n) return;
+    const int8_t* wr = w + static_cast<size_t>(row) * k;
+    for (int i = 0; i < m; ++i) {
+        const int8_t* xr = xq + static_cast<size_t>(i) * k;
+        int p = 0;
+        for (int j = lane; j < k; j += kWave) p += static_cast<int>(xr[j]) * static_cast<int>(wr[j]);
+        p = wave_sum_i32(p);
+        if (lane == 0) {
+            if constexpr (ACC_OUT) {
+                acc_out[static_cast<size_t>(i) * n + row] = p;
+            } else {
+                const float b = bias ? bias[row] : 0.0f;
+                y[static_cast<size_t>(i) * n + row] = from_f32<YT>(w8a8_epilogue(p, as[i], ws[row], b));
+            }
+        }
+    }
+}
+
+// ---- host dispatch ----------------------------------------------------------------------
+inline int m_bucket(int64_t m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8; }
+
+template <int M, typename XT, typename YT>
+void launch_q8(const XT* x, const int8_t* w, const float* ws, const float* b, YT* y, int m, int n,
+               int k, hipStream_t s) {
+    constexpr int R = rows_for<M>();
+    const int chunks = k >> 4;
+    const int threads = ((chunks + kWave - 1) / kWave) * kWave;
+    gemv_q8_kernel<R, M, XT, YT><<<(n + R - 1) / R, threads, 0, s>>>(x, w, ws, b, y, m, n, k);
+}
+
+template <typename XT, typename YT>
+void dispatch_q8(const XT* x, const int8_t* w, const float* ws, const float* b, YT* y, int m, int n,
+                 int k, hipStream_t s) {
+    switch (m_bucket(m)) {
+        case 1: launch_q8<1>(x, w, ws, b, y, m, n, k, s); break;
+        case 2: launch_q8<2>(x, w, ws, b, y, m, n, k, s); break;
+        case 4: launch_q8<4>(x, w, ws, b, y, m, n, k, s); break;
+        default: launch_q8<8>(x, w, ws, b, y, m, n, k, s); break;
+    }
+}
+
+template <int M, typename XT, typename YT, typename ST>
+void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n,
+                int k, int g, hipStream_t s) {
+    constexpr int R = rows_for<M>();
+    const int chunks = k >> 5;
+    const int threads = ((chunks + kWave - 1) / kWave) * kWave;
+    gemv_q4g_kernel<R, M, XT, YT, ST><<<(n + R - 1) / R, threads, 0, s>>>(x, w, sc, b, y, m, n, k, g);
+}
+
+template <typename XT, typename YT, typename ST>
+void dispatch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n,
+                  int k, int g, hipStream_t s) {
+    switch (m_bucket(m)) {
+        case 1: launch_q4g<1>(x, w, sc, b, y, m, n, k, g, s); break;
+        case 2: launch_q4g<2>(x, w, sc, b, y, m, n, k, g, s); break;
+        case 4: launch_q4g<4>(x, w, sc, b, y, m, n, k, g, s); break;
+        default: launch_q4g<8>(x, w, sc, b, y, m, n, k, g, s); break;
+    }
+}
+
+nq_status check_linear(const void* x, const void* w, const void* y, int64_t m, int64_t n,
+                       int64_t k, const char* who) {
+    NQ_REQUIRE(m >= 0 && n >= 0 && k >= 0, NQ_BAD_SHAPE, "%s: negative shape", who);
+    NQ_REQUIRE(m <= kMaxIndex && n <= kMaxIndex && k <= kMaxIndex && m * k <= (int64_t(1) << 40) &&
+                   n * k <= (int64_t(1) << 40) && m * n <= (int64_t(1) << 40),
+               NQ_BAD_SHAPE, "%s: shape m=%lld n=%lld k=%lld exceeds the supported range", who,
+               (long long)m, (long long)n, (long long)k);
+    if (m == 0 || n == 0) return NQ_OK;
+    NQ_REQUIRE(y && (k == 0 || (x && w)), NQ_BAD_ARG, "%s: null pointer", who);
+    return NQ_OK;
+}
+
+}  // namespace
+
+// Exposed to the W8A8 entry points (nq_w8a8.hip).
+nq_status gemv_w8a8_launch(const int8_t* xq, const float* as, const int8_t* w, const float* ws,
+                           const float* bias, void* y, nq_dtype ydt, int32_t* acc_out, int64_t m,
+                           int64_t n, int64_t k, bool generic, hipStream_t s) {
+    const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
+    const bool fast = !generic && k % 16 == 0 && k / 16 <= kMaxGemvThreads && m <= 8 &&
+                      aligned(xq, 16) && aligned(w, 16);
+    if (!fast) {
+        const int wpb = 4;
+        const unsigned grid = static_cast<unsigned>((n + wpb - 1) / wpb);
+        if (acc_out)
+            gemv_w8a8_generic_kernel<float, true><<<grid, wpb * kWave, 0, s>>>(xq, as, w, ws, bias, nullptr, acc_out, mi, ni, ki);
+        else if (ydt == NQ_F32)
+            gemv_w8a8_generic_kernel<float, false><<<grid, wpb * kWave, 0, s>>>(xq, as, w, ws, bias, static_cast<float*>(y), nullptr, mi, ni, ki);
+        else
+            gemv_w8a8_generic_kernel<_Float16, false><<<grid, wpb * kWave, 0, s>>>(xq, as, w, ws, bias, static_cast<_Float16*>(y), nullptr, mi, ni, ki);
+        return launch_status("gemv_w8a8_generic_kernel");
+    }
+    const int threads = ((ki / 16 + kWave - 1) / kWave) * kWave;
+    auto go = [&](auto mtag) {
+        constexpr int M = decltype(mtag)::value;
+        constexpr int R = rows_for<M>();
+        const unsigned grid = static_cast<unsigned>((n + R - 1) / R);
+        if (acc_out)
+            gemv_w8a8_kernel<R, M, float, true><<<grid, threads, 0, s>>>(xq, as, w, ws, bias, nullptr, acc_out, mi, ni, ki);
+        else if (ydt == NQ_F32)
+            gemv_w8a8_kernel<R, M, float, false><<<grid, threads, 0, s>>>(xq, as, w, ws, bias, static_cast<float*>(y), nullptr, mi, ni, ki);
+        else
+            gemv_w8a8_kernel<R, M, _Float16, false><<<grid, threads, 0, s>>>(xq, as, w, ws, bias, static_cast<_Float16*>(y), nullptr, mi, ni, ki);
+    };
+    switch (m_bucket(m)) {
+        case 1: go(std::integral_constant<int, 1>{}); break;
+        case 2: go(std::integral_constant<int, 2>{}); break;
+        case 4: go(std::integral_constant<int, 4>{}); break;
+        default: go(std::integral_constant<int, 8>{}); break;
+    }
+    return launch_status("gemv_w8a8_kernel");
+}
+
+}  // namespace nq
+
+using namespace nq;
+
+extern "C" nq_status nq_linear_q8(const void* x, nq_dtype x_dtype, const int8_t* q,
+                                  const float* w_scale, const float* bias, void* y,
+                                  nq_dtype y_dtype, int64_t m, int64_t n, int64_t k,
+                                  void* stream) {
+    if (nq_status st = check_linear(x, q, y, m, n, k, "linear_q8")) return st;
+    NQ_REQUIRE(dtype_ok(x_dtype) && dtype_ok(y_dtype), NQ_BAD_ARG, "linear_q8: unknown dtype");
+    if (m == 0 || n == 0) return NQ_OK;
+    NQ_REQUIRE(w_scale, NQ_BAD_ARG, "linear_q8: null w_scale");
+    NQ_REQUIRE(aligned(x, dtype_size(x_dtype)) && aligned(y, dtype_size(y_dtype)) &&
+                   aligned(w_scale, 4) && aligned(bias, 4),
+               NQ_BAD_ALIGN, "linear_q8: misaligned pointer");
+    hipStream_t s = as_stream(stream);
+    const int ni = static_cast<int>(n), ki = static_cast<int>(k);
+    const bool fast = k % 16 == 0 && k > 0 && k / 16 <= kMaxGemvThreads && aligned(q, 16) && aligned(x, 16);
+    // x rows beyond 8 run in slices of 8 (each slice re-streams the weight).
+    for (int64_t r0 = 0; r0 < m; r0 += 8) {
+        const int mi = static_cast<int>(m - r0 < 8 ? m - r0 : 8);
+        const size_t xo = static_cast<size_t>(r0) * k, yo = static_cast<size_t>(r0) * n;
+        if (fast) {
+            if (x_dtype == NQ_F32 && y_dtype == NQ_F32)
+                dispatch_q8(static_cast<const float*>(x) + xo, q, w_scale, bias, static_cast<float*>(y) + yo, mi, ni, ki, s);
+            else if (x_dtype == NQ_F32)
+                dispatch_q8(static_cast<const float*>(x) + xo, q, w_scale, bias, static_cast<_Float16*>(y) + yo, mi, ni, ki, s);
+            else if (y_dtype == NQ_F32)
+                dispatch_q8(static_cast<const _Float16*>(x) + xo, q, w_scale, bias, static_cast<float*>(y) + yo, mi, ni, ki, s);
+            else
+                dispatch_q8(static_cast<const _Float16*>(x) + xo, q, w_scale, bias, static_cast<_Float16*>(y) + yo, mi, ni, ki, s);
+        } else {
+            const unsigned grid = static_cast<unsigned>((n + 3) / 4);
+            if (x_dtype == NQ_F32 && y_dtype == NQ_F32)
+                gemv_q8_generic_kernel<<<grid, 256, 0, s>>>(static_cast<const float*>(x) + xo, q, w_scale, bias, static_cast<float*>(y) + yo, mi, ni, ki);
+            else if (x_dtype == NQ_F32)
+                gemv_q8_generic_kernel<<<grid, 256, 0, s>>>(static_cast<const float*>(x) + xo, q, w_scale, bias, static_cast<_Float16*>(y) + yo, mi, ni, ki);
+            else if (y_dtype == NQ_F32)
+                gemv_q8_generic_kernel<<<grid, 256, 0, s>>>(static_cast<const _Float16*>(x) + xo, q, w_scale, bias, static_cast<float*>(y) + yo, mi, ni, ki);
+            else
+                gemv_q8_generic_kernel<<<grid, 256, 0, s>>>(static_cast<const _Float16*>(x) + xo, q, w_scale, bias, static_cast<_Float16*>(y) + yo, mi, ni, ki);
+        }
+        if (nq_status st = launch_status("gemv_q8_kernel")) return st;
+    }
+    return NQ_OK;
+}
+
+extern "C" nq_status nq_linear_q4g(const void* x, nq_dtype x_dtype, const uint8_t* q,
+                                   const void* scale, nq_dtype scale_dtype, int64_t group,
+                                   const float* bias, void* y, nq_dtype y_dtype, int64_t m,
+                                   int64_t n, int64_t k, void* stream) {
+    if (nq_status st = check_linear(x, q, y, m, n, k, "linear_q4g")) return st;
+    NQ_REQUIRE(group > 0 && group <= kMaxIndex, NQ_BAD_SHAPE, "linear_q4g: group must be positive");
+    NQ_REQUIRE(dtype_ok(x_dtype) && dtype_ok(y_dtype) && dtype_ok(scale_dtype), NQ_BAD_ARG,
+               "linear_q4g: unknown dtype");
+    if (m == 0 || n == 0) return NQ_OK;
+    NQ_REQUIRE(k == 0 || scale, NQ_BAD_ARG, "linear_q4g: null scale");
+    NQ_REQUIRE(aligned(x, dtype_size(x_dtype)) && aligned(y, dtype_size(y_dtype)) &&
+                   aligned(scale, dtype_size(scale_dtype)) && aligned(bias, 4),
+               NQ_BAD_ALIGN, "linear_q4g: misaligned pointer");
+    hipStream_t s = as_stream(stream);
+    const int ni = static_cast<int>(n), ki = static_cast<int>(k), gi = static_cast<int>(group);
+    const bool fast = k % 32 == 0 && k > 0 && group % 32 == 0 && k / 32 <= kMaxGemvThreads &&
+                      aligned(q, 16) && aligned(x, 16);
+    for (int64_t r0 = 0; r0 < m; r0 += 8) {
+        const int mi = static_cast<int>(m - r0 < 8 ? m - r0 : 8);
+        const size_t xo = static_cast<size_t>(r0) * k, yo = static_cast<size_t>(r0) * n;
+        auto run = [&](auto* xp, auto* yp, auto* sp) {
+            if (fast)
+                dispatch_q4g(xp + xo, q, sp, bias, yp + yo, mi, ni, ki, gi, s);
+            else
+                gemv_q4g_generic_kernel<<<static_cast<unsigned>((n + 3) / 4), 256, 0, s>>>(
+                    xp + xo, q, sp, bias, yp + yo, mi, ni, ki, gi);
+        };
+        auto with_scale = [&](auto* xp, auto* yp) {
+            if (scale_dtype == NQ_F32) run(xp, yp, static_cast<const float*>(scale));
+            else run(xp, yp, static_cast<const _Float16*>(scale));
+        };
+        auto with_y = [&](auto* xp) {
+            if (y_dtype == NQ_F32) with_scale(xp, static_cast<float*>(y));
+            else with_scale(xp, static_cast<_Float16*>(y));
+        };
+        if (x_dtype == NQ_F32) with_y(static_cast<const float*>(x));
+        else with_y(static_cast<const _Float16*>(x));
+        if (nq_status st = launch_status("gemv_q4g_kernel")) return st;
+    }
+    return NQ_OK;
+}

@@ -1,0 +1,175 @@
+// Quantize / pack kernels: per-row int8 (weights and dynamic activations) and
+// group-wise int4 nibble packing. All are bit-exact with the reference
+// quantizers (quant.cpp:88-108, :179-193, :295-321): the same fp32 absmax and
+// divide, round-half-even and clamp; max is order-free so the parallel absmax
+// equals the serial scan.
+#include <hip/hip_runtime.h>
+
+#include "nq_device.hpp"
+#include "nq_internal.hpp"
+
+namespace nq {
+namespace {
+
+constexpr int kRowThreads = 256;
+
+// One workgroup per row: absmax over the row (block reduction through LDS),
+// scale = absmax / 127, then each thread quantizes its strided elements.
+// Used for weights (quantize_q8) and activations (W8A8 act quant).
+template <typename XT>
+__global__ __launch_bounds__(kRowThreads) void quantize_rows_i8_kernel(
+    const XT* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ scale, int k) {
+    __shared__ float red[kRowThreads / kWave];
+    const int row = blockIdx.x;
+    const XT* xr = x + static_cast<size_t>(row) * k;
+    int8_t* qr = q + static_cast<size_t>(row) * k;
+    const int tid = threadIdx.x;
+
+    float am = 0.0f;
+    for (int j = tid; j < k; j += kRowThreads) am = absmax_step(am, to_f32(xr[j]));
+    am = wave_absmax(am);
+    if ((tid & (kWave - 1)) == 0) red[tid / kWave] = am;
+    __syncthreads();
+    float absmax = red[0];
+#pragma unroll
+    for (int w = 1; w < kRowThreads / kWave; ++w) absmax = absmax_step(absmax, red[w]);
+    const float s = absmax / 127.0f;
+    if (tid == 0) scale[row] = s;
+    for (int j = tid; j < k; j += kRowThreads)
+        qr[j] = static_cast<int8_t>(round_clamp(to_f32(xr[j]), s, 127.0f));
+}
+
+template <typename ST>
+__device__ __forceinline__ void store_scale(ST* p, float s);
+template <>
+__device__ __forceinline__ void store_scale<float>(float* p, float s) { *p = s; }
+template <>
+__device__ __forceinline__ void store_scale<_Float16>(_Float16* p, float s) {
+    *p = static_cast<_Float16>(s);
+}
+
+// Even group: one thread per (row, block). A block starts on an even column, so
+// the bytes it packs belong to it alone; a trailing odd column fills only the
+// low nibble (quant.cpp:71-75), exactly as the zero-initialised reference buffer.
+template <typename ST>
+__global__ void quantize_q4g_even_kernel(const float* __restrict__ w, uint8_t* __restrict__ q,
+                                         ST* __restrict__ scale, int out, int in, int group,
+                                         int blocks) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= static_cast<int64_t>(out) * blocks) return;
+    const int o = static_cast<int>(t / blocks), b = static_cast<int>(t % blocks);
+    const float* wr = w + static_cast<size_t>(o) * in;
+    uint8_t* row = q + static_cast<size_t>(o) * ((in + 1) / 2);
+    const int j0 = b * group, j1 = min(j0 + group, in);
+    float am = 0.0f;
+    for (int j = j0; j < j1; ++j) am = absmax_step(am, wr[j]);
+    const float s = am / 7.0f;
+    store_scale(scale + t, s);
+    for (int j = j0; j < j1; j += 2) {
+        const int lo = static_cast<int>(round_clamp(wr[j], s, 7.0f)) + 8;
+        const int hi = (j + 1 < j1) ? static_cast<int>(round_clamp(wr[j + 1], s, 7.0f)) + 8 : 0;
+        row[j / 2] = static_cast<uint8_t>(lo | (hi << 4));
+    }
+}
+
+// Odd group: one thread per packed byte; each of its two columns recomputes its
+// block's absmax (blocks can straddle bytes). The thread owning a block's first
+// column writes that block's scale.
+template <typename ST>
+__global__ void quantize_q4g_odd_kernel(const float* __restrict__ w, uint8_t* __restrict__ q,
+                                        ST* __restrict__ scale, int out, int in, int group,
+                                        int blocks) {
+    const int rb = (in + 1) / 2;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= static_cast<int64_t>(out) * rb) return;
+    const int o = static_cast<int>(t / rb), byte = static_cast<int>(t % rb);
+    const float* wr = w + static_cast<size_t>(o) * in;
+    int nib[2] = {0, 0};
+    for (int h = 0; h < 2; ++h) {
+        const int j = 2 * byte + h;
+        if (j >= in) break;
+        const int b = j / group, j0 = b * group, j1 = min(j0 + group, in);
+        float am = 0.0f;
+        for (int jj = j0; jj < j1; ++jj) am = absmax_step(am, wr[jj]);
+        const float s = am / 7.0f;
+        if (j == j0) store_scale(scale + static_cast<size_t>(o) * blocks + b, s);
+        nib[h] = static_cast<int>(round_clamp(wr[j], s, 7.0f)) + 8;
+    }
+    q[static_cast<size_t>(o) * rb + byte] = static_cast<uint8_t>(nib[0] | (nib[1] << 4));
+}
+
+nq_status check_rows(int64_t rows, int64_t cols, const char* who) {
+    NQ_REQUIRE(rows >= 0 && cols >= 0, NQ_BAD_SHAPE, "%s: negative shape [%lld, %lld]", who,
+               (long long)rows, (long long)cols);
+    NQ_REQUIRE(rows <= kMaxIndex && cols <= kMaxIndex && rows * cols <= (int64_t(1) << 40),
+               NQ_BAD_SHAPE, "%s: shape [%lld, %lld] exceeds the supported range", who,
+               (long long)rows, (long long)cols);
+    return NQ_OK;
+}
+
+}  // namespace
+}  // namespace nq
+
+using namespace nq;
+
+extern "C" nq_status nq_quantize_q8(const float* w, int64_t out, int64_t in, int8_t* q,
+                                    float* scale, void* stream) {
+    if (nq_status st = check_rows(out, in, "nq_quantize_q8")) return st;
+    if (out == 0) return NQ_OK;
+    NQ_REQUIRE(scale && (in == 0 || (w && q)), NQ_BAD_ARG, "nq_quantize_q8: null pointer");
+    NQ_REQUIRE(aligned(w, 4) && aligned(scale, 4), NQ_BAD_ALIGN, "nq_quantize_q8: misaligned fp32");
+    quantize_rows_i8_kernel<float><<<static_cast<unsigned>(out), kRowThreads, 0, as_stream(stream)>>>(
+        w, q, scale, static_cast<int>(in));
+    return launch_status("quantize_rows_i8_kernel");
+}
+
+extern "C" nq_status nq_act_quant_i8(const void* x, nq_dtype x_dtype, int64_t m, int64_t k,
+                                     int8_t* xq, float* a_scale, void* stream) {
+    if (nq_status st = check_rows(m, k, "nq_act_quant_i8")) return st;
+    NQ_REQUIRE(dtype_ok(x_dtype), NQ_BAD_ARG, "nq_act_quant_i8: unknown x dtype %d", int(x_dtype));
+    if (m == 0) return NQ_OK;
+    NQ_REQUIRE(a_scale && (k == 0 || (x && xq)), NQ_BAD_ARG, "nq_act_quant_i8: null pointer");
+    NQ_REQUIRE(aligned(x, dtype_size(x_dtype)) && aligned(a_scale, 4), NQ_BAD_ALIGN,
+               "nq_act_quant_i8: misaligned pointer");
+    const unsigned grid = static_cast<unsigned>(m);
+    if (x_dtype == NQ_F32)
+        quantize_rows_i8_kernel<float><<<grid, kRowThreads, 0, as_stream(stream)>>>(
+            static_cast<const float*>(x), xq, a_scale, static_cast<int>(k));
+    else
+        quantize_rows_i8_kernel<_Float16><<<grid, kRowThreads, 0, as_stream(stream)>>>(
+            static_cast<const _Float16*>(x), xq, a_scale, static_cast<int>(k));
+    return launch_status("quantize_rows_i8_kernel");
+}
+
+extern "C" nq_status nq_quantize_q4g(const float* w, int64_t out, int64_t in, int64_t group,
+                                     uint8_t* q, void* scale, nq_dtype scale_dtype,
+                                     void* stream) {
+    if (nq_status st = check_rows(out, in, "nq_quantize_q4g")) return st;
+    NQ_REQUIRE(group > 0, NQ_BAD_SHAPE, "quantize_q4g: group must be positive");
+    NQ_REQUIRE(group <= kMaxIndex, NQ_BAD_SHAPE, "quantize_q4g: group too large");
+    NQ_REQUIRE(dtype_ok(scale_dtype), NQ_BAD_ARG, "nq_quantize_q4g: unknown scale dtype");
+    if (out == 0 || in == 0) return NQ_OK;
+    NQ_REQUIRE(w && q && scale, NQ_BAD_ARG, "nq_quantize_q4g: null pointer");
+    NQ_REQUIRE(aligned(w, 4) && aligned(scale, dtype_size(scale_dtype)), NQ_BAD_ALIGN,
+               "nq_quantize_q4g: misaligned pointer");
+    const int o = static_cast<int>(out), k = static_cast<int>(in), g = static_cast<int>(group);
+    const int blocks = static_cast<int>((in + group - 1) / group);
+    const int threads = 256;
+    hipStream_t s = as_stream(stream);
+    if (g % 2 == 0) {
+        const int64_t total = out * blocks;
+        const unsigned grid = static_cast<unsigned>((total + threads - 1) / threads);
+        if (scale_dtype == NQ_F32)
+            quantize_q4g_even_kernel<float><<<grid, threads, 0, s>>>(w, q, static_cast<float*>(scale), o, k, g, blocks);
+        else
+            quantize_q4g_even_kernel<_Float16><<<grid, threads, 0, s>>>(w, q, static_cast<_Float16*>(scale), o, k, g, blocks);
+    } else {
+        const int64_t total = out * ((in + 1) / 2);
+        const unsigned grid = static_cast<unsigned>((total + threads - 1) / threads);
+        if (scale_dtype == NQ_F32)
+            quantize_q4g_odd_kernel<float><<<grid, threads, 0, s>>>(w, q, static_cast<float*>(scale), o, k, g, blocks);
+        else
+            quantize_q4g_odd_kernel<_Float16><<<grid, threads, 0, s>>>(w, q, static_cast<_Float16*>(scale), o, k, g, blocks);
+    }
+    return launch_status("quantize_q4g_kernel");
+}

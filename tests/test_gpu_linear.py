@@ -1,0 +1,202 @@
+"""GPU parity of the three linears against the oracle.
+
+Integer work is bit-exact (W8A8 int32 accumulators on every kernel path);
+floating-point outputs meet max|err| <= 1e-3 * RMS(y) (plus half an fp16 ulp
+for fp16 outputs); the W8A8 GEMV and MFMA paths give bit-identical outputs
+(cpp/tests/test_cuda.cpp:217-251's gemv==tiled claim)."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import assert_close_rms, host, to_dev
+from test_oracle import same_bits
+
+pytestmark = pytest.mark.gpu
+
+F32, F16 = torch.float32, torch.float16
+
+
+def data(m, n, k, seed, wsig=0.02, bias=False):
+    rng = np.random.default_rng(seed)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    w = rng.normal(0, wsig, (n, k)).astype(np.float32)
+    b = rng.normal(0, 1, n).astype(np.float32) if bias else None
+    return x, w, b
+
+
+# ---- weight-only int8 -----------------------------------------------------------------
+Q8_CASES = [
+    (1, 4864, 896, False, F32, F32),      # config 1
+    (1, 151936, 1536, False, F16, F16),   # config 5 LM head
+    (4, 8192, 896, False, F32, F32),      # test_cuda.cpp:437 batched decode
+    (2, 896, 896, True, F32, F32),        # :438 +bias
+    (8, 100, 90, False, F32, F32),        # :441 ragged k (generic kernel)
+    (3, 1536, 1536, True, F16, F32),
+    (16, 896, 896, True, F32, F16),       # m > 8: slices of 8 rows
+    (100, 896, 4864, False, F32, F32),    # :440 ragged m, wide k
+    (5, 64, 16384, False, F32, F32),      # k beyond one workgroup (generic)
+]
+
+
+@pytest.mark.parametrize("m,n,k,bias,xdt,ydt", Q8_CASES)
+def test_linear_q8(dev, nq, orc, m, n, k, bias, xdt, ydt):
+    x, w, b = data(m, n, k, m * 7 + n + k, bias=bias)
+    t = nq.quantize_q8(to_dev(w, dev))
+    xd = to_dev(x, dev, xdt)
+    y = nq.linear_q8(xd, t, None if b is None else to_dev(b, dev), out_dtype=ydt)
+    q, s = orc.quantize_q8(w)
+    ref = orc.linear_q8(host(xd.float()), q, s, b)
+    assert_close_rms(host(y.float()), ref, f"linear_q8 {m}x{n}x{k}", fp16_out=(ydt == F16))
+
+
+def test_linear_q8_golden(dev, nq, golden):
+    g = golden("q8_linear")
+    for i in range(6):
+        t = nq.QTensor(to_dev(g[f"c{i}_q"], dev), to_dev(g[f"c{i}_s"], dev), *g[f"c{i}_q"].shape)
+        b = to_dev(g[f"c{i}_b"], dev) if f"c{i}_b" in g.files else None
+        y = nq.linear_q8(to_dev(g[f"c{i}_x"], dev), t, b)
+        assert_close_rms(host(y), g[f"c{i}_y"], f"golden q8 c{i}")
+
+
+# ---- group-wise int4 -----------------------------------------------------------------------
+Q4_CASES = [
+    (1, 1536, 8960, 32, False, F16, F16, F16),   # config 2
+    (1, 1536, 8960, 32, False, F16, F16, F32),   # same kernel, fp32 output (bare bound)
+    (4, 896, 4864, 32, True, F32, F32, F32),
+    (8, 512, 2048, 64, False, F16, F32, F16),
+    (3, 40, 32, 8, True, F32, F32, F32),        # group < 32: generic kernel
+    (16, 64, 40, 8, False, F32, F32, F32),      # test_quant.cpp:265-280 shapes
+    (2, 33, 137, 5, True, F32, F32, F32),       # odd k, odd group
+    (9, 7, 40, 16, True, F32, F32, F32),
+]
+
+
+@pytest.mark.parametrize("m,n,k,g,bias,xdt,sdt,ydt", Q4_CASES)
+def test_linear_q4g(dev, nq, orc, m, n, k, g, bias, xdt, sdt, ydt):
+    x, w, b = data(m, n, k, m * 13 + n + k + g, bias=bias)
+    t = nq.quantize_q4g(to_dev(w, dev), g, scale_dtype=sdt)
+    xd = to_dev(x, dev, xdt)
+    y = nq.linear_q4g(xd, t, None if b is None else to_dev(b, dev), out_dtype=ydt)
+    q = host(t.q)
+    s = host(t.scale.float())                  # the scales the kernel used (fp16-rounded if fp16)
+    ref = orc.linear_q4g(host(xd.float()), q, s, g, b)
+    assert_close_rms(host(y.float()), ref, f"linear_q4g {m}x{n}x{k} g{g}", fp16_out=(ydt == F16))
+
+
+def test_linear_q4g_golden(dev, nq, golden):
+    gd = golden("q4g")
+    for i in range(6):
+        q, s, g = gd[f"lin{i}_q"], gd[f"lin{i}_s"], int(gd[f"lin{i}_g"])
+        k = gd[f"lin{i}_x"].shape[1]
+        t = nq.Q4GTensor(to_dev(q, dev), to_dev(s, dev), q.shape[0], k, g)
+        b = to_dev(gd[f"lin{i}_b"], dev) if f"lin{i}_b" in gd.files else None
+        y = nq.linear_q4g(to_dev(gd[f"lin{i}_x"], dev), t, b)
+        assert_close_rms(host(y), gd[f"lin{i}_y"], f"golden q4g lin{i}")
+
+
+def test_linear_q4_per_row(dev, nq, golden):
+    gd = golden("q4g")
+    for m in (3, 16):
+        q, s = gd[f"q4lin{m}_q"], gd[f"q4lin{m}_s"]
+        t = nq.Q4GTensor(to_dev(q, dev), to_dev(s, dev), q.shape[0], 40, 40)
+        y = nq.linear_q4(to_dev(gd[f"q4lin{m}_x"], dev), t, to_dev(gd[f"q4lin{m}_b"], dev))
+        assert_close_rms(host(y), gd[f"q4lin{m}_y"], f"golden q4 m={m}")
+
+
+# ---- W8A8 -----------------------------------------------------------------------------------
+W8A8_SHAPES = [(1536, 1536), (256, 1536), (8960, 1536), (1536, 8960)]  # q/o, k/v, gate/up, down
+
+
+@pytest.mark.parametrize("m", [1, 8, 16, 32, 64])
+@pytest.mark.parametrize("n,k", W8A8_SHAPES)
+def test_w8a8_acc_exact_all_paths(dev, nq, orc, m, n, k):
+    rng = np.random.default_rng(m + n + k)
+    xq = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    wq = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    xq[0, :] = 127
+    wq[0, :] = 127                              # largest positive int32 sum
+    ref = orc.w8a8_acc(xq, wq)
+    xd, wd = to_dev(xq, dev), to_dev(wq, dev)
+    for path in (nq._lib.NQ_PATH_GEMV, nq._lib.NQ_PATH_MFMA, nq._lib.NQ_PATH_AUTO):
+        acc = host(nq.w8a8_acc_i32(xd, wd, path))
+        assert np.array_equal(acc, ref), (m, n, k, path)
+
+
+def test_w8a8_acc_generic_and_ragged(dev, nq, orc):
+    rng = np.random.default_rng(3)
+    for m, n, k in [(3, 70, 90), (20, 33, 100), (130, 65, 48), (1, 1, 0)]:
+        xq = rng.integers(-127, 128, (m, k), dtype=np.int8)
+        wq = rng.integers(-127, 128, (n, k), dtype=np.int8)
+        ref = orc.w8a8_acc(xq, wq)
+        for path in (nq._lib.NQ_PATH_GENERIC, nq._lib.NQ_PATH_AUTO, nq._lib.NQ_PATH_MFMA):
+            assert np.array_equal(host(nq.w8a8_acc_i32(to_dev(xq, dev), to_dev(wq, dev), path)), ref), (m, n, k, path)
+
+
+@pytest.mark.parametrize("m", [1, 8, 16, 64])
+@pytest.mark.parametrize("n,k", W8A8_SHAPES)
+def test_linear_w8a8_sweep(dev, nq, orc, m, n, k):
+    x, w, _ = data(m, n, k, 100 + m + n + k)
+    t = nq.quantize_q8(to_dev(w, dev))
+    xd = to_dev(x, dev, F16)
+    xo = host(xd.float())
+    q, s = orc.quantize_q8(w)
+    ref = orc.linear_w8a8(xo, q, s)
+    y32 = nq.linear_w8a8(xd, t, out_dtype=F32)
+    assert_close_rms(host(y32), ref, f"w8a8 {m}x{n}x{k} fp32-out")
+    y16 = nq.linear_w8a8(xd, t, out_dtype=F16)
+    assert_close_rms(host(y16.float()), ref, f"w8a8 {m}x{n}x{k} fp16-out", fp16_out=True)
+    # the fp16 store is the only difference between the two outputs
+    assert same_bits(host(y16), host(y32).astype(np.float16))
+
+
+@pytest.mark.parametrize("m,n,k,bias", [(1, 896, 896, True), (8, 4864, 896, False), (16, 896, 4864, False),
+                                        (5, 1536, 1536, True)])
+def test_w8a8_gemv_equals_mfma_bitwise(dev, nq, m, n, k, bias):
+    x, w, b = data(m, n, k, m + n, wsig=0.5, bias=bias)       # test_cuda.cpp:217-251, :425-427
+    t = nq.quantize_q8(to_dev(w, dev))
+    bd = None if b is None else to_dev(b, dev)
+    xd = to_dev(x, dev)
+    yg = host(nq.linear_w8a8(xd, t, bd, path=nq._lib.NQ_PATH_GEMV))
+    ym = host(nq.linear_w8a8(xd, t, bd, path=nq._lib.NQ_PATH_MFMA))
+    assert same_bits(yg, ym)
+
+
+@pytest.mark.parametrize("m,n,k,bias", [(128, 896, 896, True), (128, 4864, 896, False), (100, 896, 4864, False),
+                                        (1, 896, 896, True), (16, 896, 4864, False)])
+def test_w8a8_reference_shapes(dev, nq, orc, m, n, k, bias):
+    rng = np.random.default_rng(1234 + m)                      # test_cuda.cpp:418-423, uniform(-1,1)
+    x = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    w = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, n).astype(np.float32) if bias else None
+    t = nq.quantize_q8(to_dev(w, dev))
+    y = host(nq.linear_w8a8(to_dev(x, dev), t, None if b is None else to_dev(b, dev)))
+    q, s = orc.quantize_q8(w)
+    ref = orc.linear_w8a8(x, q, s, b)
+    assert np.abs(y - ref).max() < 2e-3                        # the reference GPU tolerance
+    assert_close_rms(y, ref, "w8a8 ref shape")
+
+
+def test_w8a8_golden(dev, nq, golden):
+    g = golden("w8a8")
+    for i in range(6):
+        t = nq.QTensor(to_dev(g[f"c{i}_q"], dev), to_dev(g[f"c{i}_s"], dev), *g[f"c{i}_q"].shape)
+        b = to_dev(g[f"c{i}_b"], dev) if f"c{i}_b" in g.files else None
+        y = host(nq.linear_w8a8(to_dev(g[f"c{i}_x"], dev), t, b))
+        ref = g[f"c{i}_y"]
+        ok = ~np.isnan(ref)
+        assert_close_rms(y[ok], ref[ok], f"golden w8a8 c{i}")
+
+
+def test_w8a8_prefill_config5(dev, nq, orc):
+    """M=2048, K=1536, N=8960: the MFMA accumulators equal the independent
+    GEMV kernel's everywhere, and the oracle's on sampled rows."""
+    m, n, k = 2048, 8960, 1536
+    rng = np.random.default_rng(5)
+    xq = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    wq = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    xd, wd = to_dev(xq, dev), to_dev(wq, dev)
+    acc_m = nq.w8a8_acc_i32(xd, wd, nq._lib.NQ_PATH_MFMA)
+    acc_g = nq.w8a8_acc_i32(xd, wd, nq._lib.NQ_PATH_GEMV)
+    assert torch.equal(acc_m, acc_g)
+    rows = rng.choice(m, 24, replace=False)
+    assert np.array_equal(host(acc_m)[rows], orc.w8a8_acc(xq[rows], wq))
