@@ -22,8 +22,15 @@ template <typename T>
 __device__ __forceinline__ T from_f32(float v);
 template <>
 __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+// The fp16 store rounds the finished fp32 value (round-to-nearest-even): the
+// empty asm keeps the compiler from folding the producing fma/mul into a
+// mixed-precision v_fma_mix* that would round the exact result to fp16 once,
+// so an fp16 output is always the fp32 output rounded, bit for bit.
 template <>
-__device__ __forceinline__ _Float16 from_f32<_Float16>(float v) { return static_cast<_Float16>(v); }
+__device__ __forceinline__ _Float16 from_f32<_Float16>(float v) {
+    asm volatile("" : "+v"(v));
+    return static_cast<_Float16>(v);
+}
 
 // Quantizer rounding, bit-exact with the reference round_clamp (quant.cpp:31-38):
 // IEEE fp32 divide (hipcc keeps fp32 division correctly rounded), rint =

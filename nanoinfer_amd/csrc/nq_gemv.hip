@@ -383,7 +383,7 @@ nq_status gemv_w8a8_launch(const int8_t* xq, const float* as, const int8_t* w, c
                            const float* bias, void* y, nq_dtype ydt, int32_t* acc_out, int64_t m,
                            int64_t n, int64_t k, bool generic, hipStream_t s) {
     const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
-    const bool fast = !generic && k % 16 == 0 && k / 16 <= kMaxGemvThreads && m <= 8 &&
+    const bool fast = !generic && k > 0 && k % 16 == 0 && k / 16 <= kMaxGemvThreads && m <= 8 &&
                       aligned(xq, 16) && aligned(w, 16);
     if (!fast) {
         const int wpb = 4;
