@@ -45,6 +45,34 @@ __device__ __forceinline__ float round_clamp(float w, float scale, float qmax) {
     return r;
 }
 
+// The same rounding for a whole row that shares one scale, without a divide per
+// element in the common case. a = w * rcp(s) differs from the exact quotient
+// w / s by < 2^-21 relative (v_rcp_f32 is 1 ulp, the product adds half an ulp),
+// and for codes of one row |w / s| <= 127 * (1 + 2^-23), so with |a| < 128 the
+// error |a - w / s| is below 3e-5. When a is farther than 2e-4 from every
+// half-integer, the correctly rounded quotient lies in the same rounding
+// interval and rint(a) == rint(w / s); the rest (near-ties, NaN/Inf, |a| >= 128,
+// scales outside [2^-100, 2^100] where rcp could flush) take the exact divide of
+// round_clamp. The narrow band keeps that divergent slow path rare (~2.5% of
+// wave-wide element slots for uniformly spread fractions).
+struct RowQuantizer {
+    float s, inv;
+    bool fast;
+    __device__ __forceinline__ explicit RowQuantizer(float scale) : s(scale) {
+        fast = scale >= 0x1p-100f && scale <= 0x1p100f;
+        inv = fast ? __builtin_amdgcn_rcpf(scale) : 0.0f;
+    }
+    __device__ __forceinline__ float code(float w, float qmax) const {
+        if (fast) {
+            const float a = w * inv;
+            const float t = __builtin_rintf(a);
+            if (__builtin_fabsf(a - t) < 0.4998f && __builtin_fabsf(a) < 128.0f)
+                return __builtin_fminf(__builtin_fmaxf(t, -qmax), qmax);
+        }
+        return round_clamp(w, s, qmax);
+    }
+};
+
 // std::max(absmax, |v|) exactly as quant.cpp:100 evaluates it: a NaN |v| leaves
 // absmax unchanged.
 __device__ __forceinline__ float absmax_step(float absmax, float v) {
@@ -92,6 +120,38 @@ __device__ __forceinline__ float wave_absmax(float v) {
     v = absmax_step(v, __shfl_xor(v, 16));
     v = absmax_step(v, __shfl_xor(v, 32));
     return v;
+}
+
+// Sums NV per-lane values (NV a power of two <= 64) over the wave with NV - 1
+// exchanges plus log2(64 / NV) more: each exchange stage halves the values a
+// lane keeps (the half selected by its lane bit) and adds the partner's copy.
+// On return v[0] of lane l is the wave total of value index l / (64 / NV),
+// identical in the 64 / NV lanes of that group. Fixed order, deterministic.
+template <int CNT, int O, int NV, typename T>
+__device__ __forceinline__ void wave_reduce_stage(T (&v)[NV], int lane) {
+    if constexpr (O >= 1) {
+        if constexpr (CNT > 1) {
+            constexpr int half = CNT / 2;
+            const bool hi = (lane & O) != 0;
+#pragma unroll
+            for (int j = 0; j < half; ++j) {
+                const T keep = hi ? v[j + half] : v[j];
+                const T send = hi ? v[j] : v[j + half];
+                v[j] = keep + __shfl_xor(send, O);
+            }
+            wave_reduce_stage<half, O / 2>(v, lane);
+        } else {
+            v[0] += __shfl_xor(v[0], O);
+            wave_reduce_stage<1, O / 2>(v, lane);
+        }
+    }
+}
+
+template <int NV, typename T>
+__device__ __forceinline__ T wave_reduce_multi(T (&v)[NV], int lane) {
+    static_assert(NV >= 1 && NV <= 64 && (NV & (NV - 1)) == 0, "power of two");
+    wave_reduce_stage<NV, 32>(v, lane);
+    return v[0];
 }
 
 // Signed byte i of a dword as float.

@@ -15,6 +15,8 @@
 // bounds-checked wave-per-row kernel with the same arithmetic.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "nq_device.hpp"
 #include "nq_internal.hpp"
 
@@ -29,6 +31,35 @@ constexpr int kMaxGemvThreads = kMaxGemvWaves * kWave;
 template <int M>
 constexpr int rows_for() {
     return M <= 2 ? 4 : 2;
+}
+
+// W8A8 GEMV: every workgroup reads all M activation rows of its K range, so
+// R >= M rows per workgroup keeps those reads at or below the weight bytes.
+template <int M>
+constexpr int w8a8_rows_for() {
+    return M <= 4 ? 4 : M;
+}
+
+// Wave-reduces the R x M accumulators and leaves the wave totals in
+// red[wave][r * M + i] (one exchange network for all of them).
+template <int R, int M, typename T>
+__device__ __forceinline__ void reduce_to_lds(T (&acc)[R][M], T* red, int wave, int lane) {
+    constexpr int NV = R * M;
+    if constexpr (NV == 1) {
+        T v;
+        if constexpr (std::is_floating_point_v<T>) v = wave_sum_f32(acc[0][0]);
+        else v = wave_sum_i32(acc[0][0]);
+        if (lane == 0) red[wave] = v;
+    } else {
+        T v[NV];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int i = 0; i < M; ++i) v[r * M + i] = acc[r][i];
+        wave_reduce_multi<NV>(v, lane);
+        constexpr int G = 64 / NV;
+        if (lane % G == 0) red[wave * NV + lane / G] = v[0];
+    }
 }
 
 // ---- chunk loaders ---------------------------------------------------------------
@@ -69,7 +100,7 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q8_kernel(
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int row = min(row0 + r, n - 1);
-        wv[r] = act ? *reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * k + tid * 16)
+        wv[r] = act ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * k + tid * 16))
                     : v4i{0, 0, 0, 0};
     }
     float acc[R][M];
@@ -96,13 +127,7 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q8_kernel(
             }
         }
     }
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int i = 0; i < M; ++i) {
-            const float v = wave_sum_f32(acc[r][i]);
-            if ((tid & 63) == 0) red[(wave * R + r) * M + i] = v;
-        }
+    reduce_to_lds<R, M>(acc, red, wave, tid & 63);
     __syncthreads();
     if (tid < R * M) {
         const int r = tid / M, i = tid % M, row = row0 + r;
@@ -118,6 +143,41 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q8_kernel(
 // ---- group-wise int4 ------------------------------------------------------------------
 template <typename ST>
 __device__ __forceinline__ float load_scale(const ST* p) { return to_f32(*p); }
+
+// Exact int4 x fp16 dot over one 16-byte chunk (32 codes) with packed fp16 math.
+// Nibble e of dword d is column 8d+e. (w >> 4j) & 0x000F000F puts columns j and
+// j+4 into the low 4 bits of the two halves; OR 0x6400 makes each half the fp16
+// value 1024 + nibble (exact), and adding -1032 gives nibble - 8 exactly. Each
+// v_dot2_f32_f16 then multiplies two (code, x) pairs with exact products and
+// accumulates in fp32. xp[4d + j] holds the matching pair (x[8d+j], x[8d+j+4]).
+__device__ __forceinline__ float dot32_q4_f16(v4i wv, const h2 (&xp)[16]) {
+    const h2 off = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
+    float p = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const unsigned w = static_cast<unsigned>(wv[d]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const unsigned b = ((w >> (4 * j)) & 0x000F000Fu) | 0x64006400u;
+            const h2 h = __builtin_bit_cast(h2, b) + off;
+            p = __builtin_amdgcn_fdot2(h, xp[4 * d + j], p, false);
+        }
+    }
+    return p;
+}
+
+// The same chunk dot in fp32 for fp32 activations.
+__device__ __forceinline__ float dot32_q4_f32(v4i wv, const float (&xf)[32]) {
+    float p = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const unsigned wd = static_cast<unsigned>(wv[d]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            p = __builtin_fmaf(xf[8 * d + e], static_cast<float>(static_cast<int>((wd >> (4 * e)) & 15u) - 8), p);
+    }
+    return p;
+}
 
 template <int R, int M, typename XT, typename YT, typename ST>
 __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q4g_kernel(
@@ -136,7 +196,7 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q4g_kernel(
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int row = min(row0 + r, n - 1);
-        wv[r] = act ? *reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * rb + tid * 16)
+        wv[r] = act ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * rb + tid * 16))
                     : v4i{0, 0, 0, 0};
         sc[r] = act ? load_scale(scale + static_cast<size_t>(row) * blocks + blk) : 0.0f;
     }
@@ -149,33 +209,28 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q4g_kernel(
 #pragma unroll
     for (int i = 0; i < M; ++i) {
         if (i < m && act) {
-            float xf[32];
             const XT* xp = x + static_cast<size_t>(i) * k + tid * 32;
-            load_x16(xp, *reinterpret_cast<float(*)[16]>(&xf[0]));
-            load_x16(xp + 16, *reinterpret_cast<float(*)[16]>(&xf[16]));
+            if constexpr (sizeof(XT) == 2) {
+                typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+                const h8* xv = reinterpret_cast<const h8*>(xp);
+                const h8 q[4] = {xv[0], xv[1], xv[2], xv[3]};
+                h2 pairs[16];
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                float p = 0.0f;
+                for (int d = 0; d < 4; ++d)
 #pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    const unsigned wd = static_cast<unsigned>(wv[r][d]);
+                    for (int j = 0; j < 4; ++j) pairs[4 * d + j] = h2{q[d][j], q[d][j + 4]};
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float c = static_cast<float>(static_cast<int>((wd >> (4 * e)) & 15u) - 8);
-                        p = __builtin_fmaf(xf[8 * d + e], c, p);
-                    }
-                }
-                acc[r][i] = __builtin_fmaf(p, sc[r], acc[r][i]);
+                for (int r = 0; r < R; ++r) acc[r][i] = __builtin_fmaf(dot32_q4_f16(wv[r], pairs), sc[r], acc[r][i]);
+            } else {
+                float xf[32];
+                load_x16(xp, *reinterpret_cast<float(*)[16]>(&xf[0]));
+                load_x16(xp + 16, *reinterpret_cast<float(*)[16]>(&xf[16]));
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[r][i] = __builtin_fmaf(dot32_q4_f32(wv[r], xf), sc[r], acc[r][i]);
             }
         }
     }
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int i = 0; i < M; ++i) {
-            const float v = wave_sum_f32(acc[r][i]);
-            if ((tid & 63) == 0) red[(wave * R + r) * M + i] = v;
-        }
+    reduce_to_lds<R, M>(acc, red, wave, tid & 63);
     __syncthreads();
     if (tid < R * M) {
         const int r = tid / M, i = tid % M, row = row0 + r;
@@ -205,7 +260,7 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_kernel(
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int row = min(row0 + r, n - 1);
-        wv[r] = act ? *reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * k + tid * 16)
+        wv[r] = act ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * k + tid * 16))
                     : v4i{0, 0, 0, 0};
     }
     int acc[R][M];
@@ -224,13 +279,7 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_kernel(
             }
         }
     }
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int i = 0; i < M; ++i) {
-            const int v = wave_sum_i32(acc[r][i]);
-            if ((tid & 63) == 0) red[(wave * R + r) * M + i] = v;
-        }
+    reduce_to_lds<R, M>(acc, red, wave, tid & 63);
     __syncthreads();
     if (tid < R * M) {
         const int r = tid / M, i = tid % M, row = row0 + r;
@@ -243,6 +292,118 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_kernel(
                 const float b = bias ? bias[row] : 0.0f;
                 y[static_cast<size_t>(i) * n + row] = from_f32<YT>(w8a8_epilogue(s, as[i], ws[row], b));
             }
+        }
+    }
+}
+
+// ---- W8A8 decode with the activation quant fused in -----------------------------------
+// The workgroup already spans the whole K of its rows, so it holds every element
+// of the (at most 8) activation rows: it reduces each row's absmax across its
+// waves, derives a_scale = absmax / 127 exactly as the activation-quant kernel
+// does, quantizes its own 16-element chunk in registers and runs the same
+// v_dot4_i32_i8 core. Identical int32 accumulators and epilogue, one launch.
+template <typename XT>
+struct XChunk;
+template <>
+struct XChunk<float> {
+    f4 v[4];
+    __device__ __forceinline__ void load(const float* p) {
+        const f4* q = reinterpret_cast<const f4*>(p);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = q[i];
+    }
+    __device__ __forceinline__ float at(int e) const { return v[e >> 2][e & 3]; }
+};
+template <>
+struct XChunk<_Float16> {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    h8 v[2];
+    __device__ __forceinline__ void load(const _Float16* p) {
+        const h8* q = reinterpret_cast<const h8*>(p);
+        v[0] = q[0];
+        v[1] = q[1];
+    }
+    __device__ __forceinline__ float at(int e) const { return static_cast<float>(v[e >> 3][e & 7]); }
+};
+
+template <int R, int M, typename XT, typename YT>
+__global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_fused_kernel(
+    const XT* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ ws,
+    const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k) {
+    __shared__ float amax_red[kMaxGemvWaves * M];
+    __shared__ int red[kMaxGemvWaves * R * M];
+    const int tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6;
+    const int chunks = k >> 4;
+    const bool act = tid < chunks;
+    const int row0 = blockIdx.x * R;
+
+    v4i wv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = min(row0 + r, n - 1);
+        wv[r] = act ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * k + tid * 16))
+                    : v4i{0, 0, 0, 0};
+    }
+    XChunk<XT> xc[M];
+    float am[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        am[i] = 0.0f;
+        if (i < m && act) {
+            xc[i].load(x + static_cast<size_t>(i) * k + tid * 16);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) am[i] = absmax_step(am[i], xc[i].at(e));
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        const float a = wave_absmax(am[i]);
+        if ((tid & 63) == 0) amax_red[wave * M + i] = a;
+    }
+    __syncthreads();
+    float as[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        float a = 0.0f;
+        for (int v = 0; v < nw; ++v) a = absmax_step(a, amax_red[v * M + i]);
+        as[i] = a / 127.0f;
+    }
+
+    int acc[R][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < M; ++i) acc[r][i] = 0;
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        if (i < m && act) {
+            const RowQuantizer rq(as[i]);
+            int qd[4];
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                int packed = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int c = static_cast<int>(rq.code(xc[i].at(4 * d + e), 127.0f));
+                    packed |= (c & 0xFF) << (8 * e);
+                }
+                qd[d] = packed;
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int d = 0; d < 4; ++d) acc[r][i] = __builtin_amdgcn_sdot4(qd[d], wv[r][d], acc[r][i], false);
+        }
+    }
+    reduce_to_lds<R, M>(acc, red, wave, tid & 63);
+    __syncthreads();
+    if (tid < R * M) {
+        const int r = tid / M, i = tid % M, row = row0 + r;
+        if (row < n && i < m) {
+            int s = 0;
+            for (int v = 0; v < nw; ++v) s += red[(v * R + r) * M + i];
+            const float b = bias ? bias[row] : 0.0f;
+            y[static_cast<size_t>(i) * n + row] = from_f32<YT>(w8a8_epilogue(s, as[i], ws[row], b));
         }
     }
 }
@@ -347,7 +508,9 @@ void dispatch_q8(const XT* x, const int8_t* w, const float* ws, const float* b, 
 template <int M, typename XT, typename YT, typename ST>
 void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n,
                 int k, int g, hipStream_t s) {
-    constexpr int R = rows_for<M>();
+    // One row per workgroup at decode: the workgroup's 5..9 waves then split K,
+    // which spreads the unpack math over the most SIMDs (measured fastest).
+    constexpr int R = M <= 2 ? 1 : 2;
     const int chunks = k >> 5;
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
     gemv_q4g_kernel<R, M, XT, YT, ST><<<(n + R - 1) / R, threads, 0, s>>>(x, w, sc, b, y, m, n, k, g);
@@ -399,7 +562,7 @@ nq_status gemv_w8a8_launch(const int8_t* xq, const float* as, const int8_t* w, c
     const int threads = ((ki / 16 + kWave - 1) / kWave) * kWave;
     auto go = [&](auto mtag) {
         constexpr int M = decltype(mtag)::value;
-        constexpr int R = rows_for<M>();
+        constexpr int R = w8a8_rows_for<M>();
         const unsigned grid = static_cast<unsigned>((n + R - 1) / R);
         if (acc_out)
             gemv_w8a8_kernel<R, M, float, true><<<grid, threads, 0, s>>>(xq, as, w, ws, bias, nullptr, acc_out, mi, ni, ki);
@@ -415,6 +578,43 @@ nq_status gemv_w8a8_launch(const int8_t* xq, const float* as, const int8_t* w, c
         default: go(std::integral_constant<int, 8>{}); break;
     }
     return launch_status("gemv_w8a8_kernel");
+}
+
+// Fused act-quant + GEMV for m <= 2 (larger m re-quantizes too many activation
+// elements per workgroup to pay for the saved launch). Returns false (nothing launched) when the
+// shape is outside its fast path; the caller then quantizes and runs the GEMV.
+bool gemv_w8a8_fused_launch(const void* x, nq_dtype xdt, const int8_t* w, const float* ws,
+                            const float* bias, void* y, nq_dtype ydt, int64_t m, int64_t n,
+                            int64_t k, hipStream_t s, nq_status* st) {
+    if (!(m >= 1 && m <= 2 && k > 0 && k % 16 == 0 && k / 16 <= kMaxGemvThreads && aligned(w, 16) &&
+          aligned(x, 16)))
+        return false;
+    const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
+    const int threads = ((ki / 16 + kWave - 1) / kWave) * kWave;
+    auto go = [&](auto mtag, auto* xp, auto* yp) {
+        constexpr int M = decltype(mtag)::value;
+        constexpr int R = rows_for<M>();
+        using XT = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
+        using YT = std::remove_pointer_t<decltype(yp)>;
+        gemv_w8a8_fused_kernel<R, M, XT, YT><<<static_cast<unsigned>((n + R - 1) / R), threads, 0, s>>>(
+            xp, w, ws, bias, yp, mi, ni, ki);
+    };
+    auto with_m = [&](auto* xp, auto* yp) {
+        switch (m_bucket(m)) {
+            case 1: go(std::integral_constant<int, 1>{}, xp, yp); break;
+            case 2: go(std::integral_constant<int, 2>{}, xp, yp); break;
+            case 4: go(std::integral_constant<int, 4>{}, xp, yp); break;
+            default: go(std::integral_constant<int, 8>{}, xp, yp); break;
+        }
+    };
+    auto with_y = [&](auto* xp) {
+        if (ydt == NQ_F32) with_m(xp, static_cast<float*>(y));
+        else with_m(xp, static_cast<_Float16*>(y));
+    };
+    if (xdt == NQ_F32) with_y(static_cast<const float*>(x));
+    else with_y(static_cast<const _Float16*>(x));
+    *st = launch_status("gemv_w8a8_fused_kernel");
+    return true;
 }
 
 }  // namespace nq

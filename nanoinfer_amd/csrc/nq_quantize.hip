@@ -5,6 +5,9 @@
 // equals the serial scan.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <type_traits>
+
 #include "nq_device.hpp"
 #include "nq_internal.hpp"
 
@@ -35,8 +38,8 @@ __global__ __launch_bounds__(kRowThreads) void quantize_rows_i8_kernel(
     for (int w = 1; w < kRowThreads / kWave; ++w) absmax = absmax_step(absmax, red[w]);
     const float s = absmax / 127.0f;
     if (tid == 0) scale[row] = s;
-    for (int j = tid; j < k; j += kRowThreads)
-        qr[j] = static_cast<int8_t>(round_clamp(to_f32(xr[j]), s, 127.0f));
+    const RowQuantizer rq(s);
+    for (int j = tid; j < k; j += kRowThreads) qr[j] = static_cast<int8_t>(rq.code(to_f32(xr[j]), 127.0f));
 }
 
 template <typename ST>
@@ -65,9 +68,10 @@ __global__ void quantize_q4g_even_kernel(const float* __restrict__ w, uint8_t* _
     for (int j = j0; j < j1; ++j) am = absmax_step(am, wr[j]);
     const float s = am / 7.0f;
     store_scale(scale + t, s);
+    const RowQuantizer rq(s);
     for (int j = j0; j < j1; j += 2) {
-        const int lo = static_cast<int>(round_clamp(wr[j], s, 7.0f)) + 8;
-        const int hi = (j + 1 < j1) ? static_cast<int>(round_clamp(wr[j + 1], s, 7.0f)) + 8 : 0;
+        const int lo = static_cast<int>(rq.code(wr[j], 7.0f)) + 8;
+        const int hi = (j + 1 < j1) ? static_cast<int>(rq.code(wr[j + 1], 7.0f)) + 8 : 0;
         row[j / 2] = static_cast<uint8_t>(lo | (hi << 4));
     }
 }
@@ -98,6 +102,69 @@ __global__ void quantize_q4g_odd_kernel(const float* __restrict__ w, uint8_t* __
     q[static_cast<size_t>(o) * rb + byte] = static_cast<uint8_t>(nib[0] | (nib[1] << 4));
 }
 
+// ---- activation quant (vectorized) ------------------------------
+// One workgroup per row, 8 elements per 16-byte step held in registers between
+// the absmax pass and the quantize pass (x is read once).
+// Workgroups past the m rows clear `zero` (a 256-byte aligned scratch region of
+// the GEMM that follows) with 16-byte stores.
+template <typename XT, int CPT>
+__global__ __launch_bounds__(256) void act_quant_vec_kernel(const XT* __restrict__ x, int8_t* __restrict__ xq,
+                                                           float* __restrict__ a_scale, int m, int k,
+                                                           v4i* __restrict__ zero, int64_t zero_vecs) {
+    __shared__ float red[4];
+    const int tid = threadIdx.x;
+    if (static_cast<int>(blockIdx.x) >= m) {
+        for (int64_t i = static_cast<int64_t>(blockIdx.x - m) * 256 + tid; i < zero_vecs;
+             i += static_cast<int64_t>(gridDim.x - m) * 256)
+            zero[i] = v4i{0, 0, 0, 0};
+        return;
+    }
+    typedef XT v8 __attribute__((ext_vector_type(8)));
+    const int row = blockIdx.x, steps = k >> 3;
+    const v8* xr = reinterpret_cast<const v8*>(x + static_cast<size_t>(row) * k);
+    v8 v[CPT];
+    float am = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const int e = tid + c * 256;
+        if (e < steps) {
+            v[c] = xr[e];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) am = absmax_step(am, to_f32(v[c][j]));
+        }
+    }
+    am = wave_absmax(am);
+    if ((tid & 63) == 0) red[tid >> 6] = am;
+    __syncthreads();
+    float a = red[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) a = absmax_step(a, red[w]);
+    const float sc = a / 127.0f;
+    if (tid == 0) a_scale[row] = sc;
+    const RowQuantizer rq(sc);
+    typedef int v2i __attribute__((ext_vector_type(2)));
+    v2i* qr = reinterpret_cast<v2i*>(xq + static_cast<size_t>(row) * k);
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const int e = tid + c * 256;
+        if (e < steps) {
+            int lo = 0, hi = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                lo |= (static_cast<int>(rq.code(to_f32(v[c][j]), 127.0f)) & 0xFF) << (8 * j);
+                hi |= (static_cast<int>(rq.code(to_f32(v[c][j + 4]), 127.0f)) & 0xFF) << (8 * j);
+            }
+            qr[e] = v2i{lo, hi};
+        }
+    }
+}
+
+__global__ void zero_vec_kernel(v4i* __restrict__ p, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        p[i] = v4i{0, 0, 0, 0};
+}
+
 nq_status check_rows(int64_t rows, int64_t cols, const char* who) {
     NQ_REQUIRE(rows >= 0 && cols >= 0, NQ_BAD_SHAPE, "%s: negative shape [%lld, %lld]", who,
                (long long)rows, (long long)cols);
@@ -108,6 +175,45 @@ nq_status check_rows(int64_t rows, int64_t cols, const char* who) {
 }
 
 }  // namespace
+
+// Activation quant: the vectorized kernel when k fits it, else the scalar row kernel.
+nq_status act_quant(const void* x, nq_dtype xdt, int64_t m, int64_t k, int8_t* xq, float* as,
+                    void* zero, size_t zero_bytes, hipStream_t s) {
+    const bool vec = k > 0 && k % 8 == 0 && k <= 8 * 256 * 8 && aligned(x, 16) && aligned(xq, 8);
+    const int64_t zero_vecs = static_cast<int64_t>(zero_bytes / 16);
+    if (vec) {
+        const int64_t zero_blocks = std::min<int64_t>(256, (zero_vecs + 255) / 256);
+        const unsigned grid = static_cast<unsigned>(m + zero_blocks);
+        v4i* zp = static_cast<v4i*>(zero);
+        const int cpt = static_cast<int>((k / 8 + 255) / 256);
+        const int mi = static_cast<int>(m), ki = static_cast<int>(k);
+        auto go = [&](auto* xp) {
+            using XT = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
+            switch (cpt) {
+                case 1: act_quant_vec_kernel<XT, 1><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs); break;
+                case 2: act_quant_vec_kernel<XT, 2><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs); break;
+                case 3:
+                case 4: act_quant_vec_kernel<XT, 4><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs); break;
+                default: act_quant_vec_kernel<XT, 8><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs); break;
+            }
+        };
+        if (xdt == NQ_F32) go(static_cast<const float*>(x));
+        else go(static_cast<const _Float16*>(x));
+        return launch_status("act_quant_vec_kernel");
+    }
+    const unsigned grid = static_cast<unsigned>(m);
+    if (xdt == NQ_F32)
+        quantize_rows_i8_kernel<float><<<grid, kRowThreads, 0, s>>>(static_cast<const float*>(x), xq, as, static_cast<int>(k));
+    else
+        quantize_rows_i8_kernel<_Float16><<<grid, kRowThreads, 0, s>>>(static_cast<const _Float16*>(x), xq, as, static_cast<int>(k));
+    if (nq_status st = launch_status("quantize_rows_i8_kernel")) return st;
+    if (zero_vecs > 0) {
+        zero_vec_kernel<<<static_cast<unsigned>(std::min<int64_t>(1024, (zero_vecs + 255) / 256)), 256, 0, s>>>(
+            static_cast<v4i*>(zero), zero_vecs);
+        return launch_status("zero_vec_kernel");
+    }
+    return NQ_OK;
+}
 }  // namespace nq
 
 using namespace nq;
@@ -131,14 +237,7 @@ extern "C" nq_status nq_act_quant_i8(const void* x, nq_dtype x_dtype, int64_t m,
     NQ_REQUIRE(a_scale && (k == 0 || (x && xq)), NQ_BAD_ARG, "nq_act_quant_i8: null pointer");
     NQ_REQUIRE(aligned(x, dtype_size(x_dtype)) && aligned(a_scale, 4), NQ_BAD_ALIGN,
                "nq_act_quant_i8: misaligned pointer");
-    const unsigned grid = static_cast<unsigned>(m);
-    if (x_dtype == NQ_F32)
-        quantize_rows_i8_kernel<float><<<grid, kRowThreads, 0, as_stream(stream)>>>(
-            static_cast<const float*>(x), xq, a_scale, static_cast<int>(k));
-    else
-        quantize_rows_i8_kernel<_Float16><<<grid, kRowThreads, 0, as_stream(stream)>>>(
-            static_cast<const _Float16*>(x), xq, a_scale, static_cast<int>(k));
-    return launch_status("quantize_rows_i8_kernel");
+    return act_quant(x, x_dtype, m, k, xq, a_scale, nullptr, 0, as_stream(stream));
 }
 
 extern "C" nq_status nq_quantize_q4g(const float* w, int64_t out, int64_t in, int64_t group,

@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "nq_device.hpp"
 #include "nq_internal.hpp"
@@ -148,6 +149,103 @@ __global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t count) {
     if (i < count) p[i] = 0;
 }
 
+// ---- skinny W8A8 GEMM (3 <= m <= 64): batched decode ------------------------------------
+// A workgroup owns TN 16-column MFMA tiles of weight rows and all m activation
+// rows (TM 16-row tiles) over one K range; its waves take interleaved 64-byte K
+// steps of that range, with operands loaded straight from global memory in the
+// MFMA lane layout (weights streamed once, non-temporal; the small xq stays in
+// L2) and three steps in flight per wave. The per-wave int32 partial tiles are
+// added into one LDS tile with ds_add (exact, order-free). A single K range
+// applies the epilogue directly. With several K ranges (very long K only) each
+// range atomically adds its tile into a zeroed int32 accumulator and a separate
+// finalize launch applies the epilogue: on this multi-XCD part, finishing inside
+// the kernel would need agent-scope L2 writeback/invalidate fences, which cost
+// far more than the extra launch.
+template <int TM, int TN, Out OUT, typename YT>
+__global__ __launch_bounds__(1024) void gemm_w8a8_skinny_kernel(
+    const int8_t* __restrict__ xq, const float* __restrict__ as, const int8_t* __restrict__ wq,
+    const float* __restrict__ ws, const float* __restrict__ bias, YT* __restrict__ y,
+    int32_t* __restrict__ acc_out, int m, int n, int k, int k_split) {
+    constexpr int PD = 3;  // steps in flight per wave
+    __shared__ int tile[TM][TN][4][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nthr = blockDim.x;
+    const int nw = nthr >> 6;
+    const int n0 = blockIdx.x * (TN * 16);
+    const bool split = gridDim.y > 1;
+    const int kb = blockIdx.y * k_split, ke = min(k, kb + k_split);
+    const int fr = lane & 15, fk = (lane >> 4) * 16;
+    for (int q = tid; q < TM * TN * 256; q += nthr) (&tile[0][0][0][0])[q] = 0;
+
+    v4i acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+    auto load = [&](int k0, v4i (&a)[TM], v4i (&b)[TN]) {
+        const bool kin = k0 + fk < ke;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int row = i * 16 + fr;
+            a[i] = (kin && row < m) ? *reinterpret_cast<const v4i*>(xq + static_cast<size_t>(row) * k + k0 + fk)
+                                    : v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int col = n0 + j * 16 + fr;
+            b[j] = (kin && col < n)
+                       ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wq + static_cast<size_t>(col) * k + k0 + fk))
+                       : v4i{0, 0, 0, 0};
+        }
+    };
+    const int kstep = nw * kBK;
+    const int k0 = kb + wave * kBK;
+    v4i a[PD][TM], b[PD][TN];
+#pragma unroll
+    for (int p = 0; p < PD; ++p) load(k0 + p * kstep, a[p], b[p]);
+    for (int base = 0;; base += PD) {
+        bool done = false;
+#pragma unroll
+        for (int p = 0; p < PD; ++p) {
+            const int kc = k0 + (base + p) * kstep;
+            if (kc >= ke) {
+                done = true;
+                break;
+            }
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[p][i], b[p][j], acc[i][j], 0, 0, 0);
+            load(kc + PD * kstep, a[p], b[p]);
+        }
+        if (done) break;
+    }
+    __syncthreads();  // tile zeroed
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) atomicAdd(&tile[i][j][v][lane], acc[i][j][v]);
+    __syncthreads();
+    for (int q = tid; q < TM * TN * 256; q += nthr) {
+        const int l = q & 63, v = (q >> 6) & 3, j = (q >> 8) % TN, i = (q >> 8) / TN;
+        const int row = i * 16 + (l >> 4) * 4 + v, col = n0 + j * 16 + (l & 15);
+        if (row >= m || col >= n) continue;
+        const int sum = tile[i][j][v][l];
+        const size_t o = static_cast<size_t>(row) * n + col;
+        if (split) {
+            atomicAdd(acc_out + o, sum);
+        } else if constexpr (OUT == Out::ACC) {
+            acc_out[o] = sum;
+        } else {
+            const float bb = bias ? bias[col] : 0.0f;
+            y[o] = from_f32<YT>(w8a8_epilogue(sum, as[row], ws[col], bb));
+        }
+    }
+}
+
 template <typename YT>
 __global__ void w8a8_finalize_kernel(const int32_t* __restrict__ acc, const float* __restrict__ as,
                                      const float* __restrict__ ws, const float* __restrict__ bias,
@@ -159,76 +257,129 @@ __global__ void w8a8_finalize_kernel(const int32_t* __restrict__ acc, const floa
     y[i] = from_f32<YT>(w8a8_epilogue(acc[i], as[row], ws[col], b));
 }
 
-// ---- tile / split-K choice ------------------------------------------------------
-struct GemmPlan {
-    int cfg;      // 0: 128x128 (2x2 waves); 1: 16x64, 2: 32x64, 3: 64x64 (1x4 waves)
-    int bm, bn;
-    int splits;   // K ranges (1 = no split)
-    int k_split;  // bytes of K per range (multiple of kBK)
-};
-
+// ---- plans --------------------------------------------------------------------------
 constexpr int kTargetBlocks = 1024;  // ~4 workgroups per CU on 256 CUs
+constexpr int kSkinnyMaxM = 64;
 
-GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k) {
-    GemmPlan p{};
-    if (m > 64) {
-        p.cfg = 0;
-        p.bm = 128;
-        p.bn = 128;
-    } else {
-        p.cfg = m <= 16 ? 1 : (m <= 32 ? 2 : 3);
-        p.bm = m <= 16 ? 16 : (m <= 32 ? 32 : 64);
-        p.bn = 64;
-    }
-    const int64_t tiles = ((m + p.bm - 1) / p.bm) * ((n + p.bn - 1) / p.bn);
+// Large m: 128x128 tiles, K split (atomic int32 accumulation) only when the
+// tile count alone cannot fill the chip.
+struct BigPlan {
+    int splits, k_split;
+};
+BigPlan plan_big(int64_t m, int64_t n, int64_t k) {
+    const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
     const int64_t kslabs = (k + kBK - 1) / kBK;
     int64_t splits = 1;
-    if (tiles < kTargetBlocks) {
-        splits = (kTargetBlocks + tiles - 1) / tiles;
-        splits = std::min<int64_t>(splits, std::max<int64_t>(1, kslabs / 4));  // >= 256 B of K each
-    }
-    const int64_t slabs_per = (kslabs + splits - 1) / splits;
-    p.k_split = static_cast<int>(std::max<int64_t>(1, slabs_per) * kBK);
+    if (tiles < kTargetBlocks / 4) splits = std::min<int64_t>((kTargetBlocks / 4 + tiles - 1) / tiles, std::max<int64_t>(1, kslabs / 4));
+    const int64_t per = (kslabs + splits - 1) / splits;
+    BigPlan p;
+    p.k_split = static_cast<int>(std::max<int64_t>(1, per) * kBK);
     p.splits = static_cast<int>(std::max<int64_t>(1, (k + p.k_split - 1) / p.k_split));
+    return p;
+}
+
+// Skinny m: 32 columns per workgroup when that still gives >= 128 workgroups,
+// else 16; waves for about three K steps each (4..16). K is split across
+// workgroups only when one range would leave a wave more than 6 steps.
+struct SkinnyPlan {
+    int tm, tn, ntiles, splits, k_split, waves;
+    size_t acc_bytes;
+};
+SkinnyPlan plan_skinny(int64_t m, int64_t n, int64_t k) {
+    SkinnyPlan p{};
+    p.tm = static_cast<int>((m + 15) / 16);
+    p.tn = (n + 31) / 32 >= 128 ? 2 : 1;
+    p.ntiles = static_cast<int>((n + 16 * p.tn - 1) / (16 * p.tn));
+    const int64_t kslabs = (k + kBK - 1) / kBK;
+    const int64_t splits = std::max<int64_t>(1, (kslabs + 16 * 6 - 1) / (16 * 6));
+    const int64_t per = (kslabs + splits - 1) / splits;
+    p.k_split = static_cast<int>(per * kBK);
+    p.splits = static_cast<int>((k + p.k_split - 1) / p.k_split);
+    p.waves = static_cast<int>(std::min<int64_t>(16, std::max<int64_t>(4, (per + 2) / 3)));
+    if (p.splits > 1) p.acc_bytes = round_up(static_cast<size_t>(m * n) * 4, 256);
     return p;
 }
 
 size_t gemm_ws_bytes(int64_t m, int64_t n, int64_t k) {
     if (m <= 0 || n <= 0 || k <= 0) return 0;
-    const GemmPlan p = plan_gemm(m, n, k);
+    if (m <= kSkinnyMaxM) {
+        return plan_skinny(m, n, k).acc_bytes;
+    }
+    const BigPlan p = plan_big(m, n, k);
     return p.splits > 1 ? round_up(static_cast<size_t>(m * n) * 4, 256) : 0;
 }
 
-template <Out OUT, typename YT>
-void launch_cfg(const GemmPlan& p, dim3 grid, hipStream_t s, const int8_t* xq, const float* as,
-                const int8_t* wq, const float* ws, const float* bias, YT* y, int32_t* acc,
-                int m, int n, int k) {
-    switch (p.cfg) {
-        case 0: gemm_w8a8_mfma_kernel<128, 128, 2, 2, OUT, YT><<<grid, kGemmThreads, 0, s>>>(xq, as, wq, ws, bias, y, acc, m, n, k, p.k_split); break;
-        case 1: gemm_w8a8_mfma_kernel<16, 64, 1, 4, OUT, YT><<<grid, kGemmThreads, 0, s>>>(xq, as, wq, ws, bias, y, acc, m, n, k, p.k_split); break;
-        case 2: gemm_w8a8_mfma_kernel<32, 64, 1, 4, OUT, YT><<<grid, kGemmThreads, 0, s>>>(xq, as, wq, ws, bias, y, acc, m, n, k, p.k_split); break;
-        default: gemm_w8a8_mfma_kernel<64, 64, 1, 4, OUT, YT><<<grid, kGemmThreads, 0, s>>>(xq, as, wq, ws, bias, y, acc, m, n, k, p.k_split); break;
+// Skinny launch. zeroed: a split plan's accumulator was already cleared by
+// this call's activation-quant kernel; else it is cleared here.
+nq_status gemm_skinny(const int8_t* xq, const float* as, const int8_t* wq, const float* ws,
+                      const float* bias, void* y, nq_dtype ydt, int32_t* acc_out, int64_t m,
+                      int64_t n, int64_t k, void* workspace, size_t ws_bytes, bool zeroed,
+                      hipStream_t s) {
+    const SkinnyPlan p = plan_skinny(m, n, k);
+    int32_t* accum = acc_out;
+    if (p.splits > 1) {
+        if (!acc_out) {
+            NQ_REQUIRE(workspace && ws_bytes >= p.acc_bytes, NQ_BAD_ARG,
+                       "w8a8 gemm: workspace of %zu bytes required, %zu given", p.acc_bytes, ws_bytes);
+            NQ_REQUIRE(aligned(workspace, 256), NQ_BAD_ALIGN, "w8a8 gemm: workspace must be 256-byte aligned");
+            accum = static_cast<int32_t*>(workspace);
+        }
+        if (!zeroed || acc_out) {
+            fill_i32_kernel<<<static_cast<unsigned>((m * n + 255) / 256), 256, 0, s>>>(accum, m * n);
+            if (nq_status st = launch_status("fill_i32_kernel")) return st;
+        }
     }
+    const dim3 grid(static_cast<unsigned>(p.ntiles), static_cast<unsigned>(p.splits));
+    const int threads = p.waves * 64;
+    const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
+    auto go = [&](auto tmtag, auto tntag) {
+        constexpr int TM = decltype(tmtag)::value, TN = decltype(tntag)::value;
+        if (acc_out || p.splits > 1)
+            gemm_w8a8_skinny_kernel<TM, TN, Out::ACC, float><<<grid, threads, 0, s>>>(xq, as, wq, ws, bias, nullptr, accum, mi, ni, ki, p.k_split);
+        else if (ydt == NQ_F32)
+            gemm_w8a8_skinny_kernel<TM, TN, Out::Y, float><<<grid, threads, 0, s>>>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi, ni, ki, p.k_split);
+        else
+            gemm_w8a8_skinny_kernel<TM, TN, Out::Y, _Float16><<<grid, threads, 0, s>>>(xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr, mi, ni, ki, p.k_split);
+    };
+    auto with_tn = [&](auto tmtag) {
+        if (p.tn == 1) go(tmtag, std::integral_constant<int, 1>{});
+        else go(tmtag, std::integral_constant<int, 2>{});
+    };
+    switch (p.tm) {
+        case 1: with_tn(std::integral_constant<int, 1>{}); break;
+        case 2: with_tn(std::integral_constant<int, 2>{}); break;
+        case 3: with_tn(std::integral_constant<int, 3>{}); break;
+        default: with_tn(std::integral_constant<int, 4>{}); break;
+    }
+    if (nq_status st = launch_status("gemm_w8a8_skinny_kernel")) return st;
+    if (p.splits > 1 && !acc_out) {
+        const unsigned g = static_cast<unsigned>((m * n + 255) / 256);
+        if (ydt == NQ_F32)
+            w8a8_finalize_kernel<float><<<g, 256, 0, s>>>(accum, as, ws, bias, static_cast<float*>(y), mi, ni);
+        else
+            w8a8_finalize_kernel<_Float16><<<g, 256, 0, s>>>(accum, as, ws, bias, static_cast<_Float16*>(y), mi, ni);
+        return launch_status("w8a8_finalize_kernel");
+    }
+    return NQ_OK;
 }
 
-// MFMA path. acc_out != null: write raw int32 accumulators instead of y.
-nq_status gemm_mfma(const int8_t* xq, const float* as, const int8_t* wq, const float* ws,
-                    const float* bias, void* y, nq_dtype ydt, int32_t* acc_out, int64_t m,
-                    int64_t n, int64_t k, void* workspace, size_t ws_bytes, hipStream_t s) {
-    const GemmPlan p = plan_gemm(m, n, k);
+// Big-m launch (128x128 tiles).
+nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const float* ws,
+                   const float* bias, void* y, nq_dtype ydt, int32_t* acc_out, int64_t m, int64_t n,
+                   int64_t k, void* workspace, size_t ws_bytes, hipStream_t s) {
+    const BigPlan p = plan_big(m, n, k);
     const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
-    dim3 grid(static_cast<unsigned>((n + p.bn - 1) / p.bn), static_cast<unsigned>((m + p.bm - 1) / p.bm),
+    dim3 grid(static_cast<unsigned>((n + 127) / 128), static_cast<unsigned>((m + 127) / 128),
               static_cast<unsigned>(p.splits));
     if (p.splits == 1) {
         if (acc_out)
-            launch_cfg<Out::ACC, float>(p, grid, s, xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki);
+            gemm_w8a8_mfma_kernel<128, 128, 2, 2, Out::ACC, float><<<grid, kGemmThreads, 0, s>>>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, p.k_split);
         else if (ydt == NQ_F32)
-            launch_cfg<Out::Y, float>(p, grid, s, xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi, ni, ki);
+            gemm_w8a8_mfma_kernel<128, 128, 2, 2, Out::Y, float><<<grid, kGemmThreads, 0, s>>>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi, ni, ki, p.k_split);
         else
-            launch_cfg<Out::Y, _Float16>(p, grid, s, xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr, mi, ni, ki);
+            gemm_w8a8_mfma_kernel<128, 128, 2, 2, Out::Y, _Float16><<<grid, kGemmThreads, 0, s>>>(xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr, mi, ni, ki, p.k_split);
         return launch_status("gemm_w8a8_mfma_kernel");
     }
-    // Split-K: accumulate into the raw output (acc_out) or the workspace.
     const size_t need = round_up(static_cast<size_t>(m * n) * 4, 256);
     int32_t* acc = acc_out;
     if (!acc) {
@@ -239,7 +390,7 @@ nq_status gemm_mfma(const int8_t* xq, const float* as, const int8_t* wq, const f
     }
     const int64_t count = m * n;
     fill_i32_kernel<<<static_cast<unsigned>((count + 255) / 256), 256, 0, s>>>(acc, count);
-    launch_cfg<Out::ATOMIC, float>(p, grid, s, xq, as, wq, ws, bias, nullptr, acc, mi, ni, ki);
+    gemm_w8a8_mfma_kernel<128, 128, 2, 2, Out::ATOMIC, float><<<grid, kGemmThreads, 0, s>>>(xq, as, wq, ws, bias, nullptr, acc, mi, ni, ki, p.k_split);
     if (nq_status st = launch_status("gemm_w8a8_mfma_kernel(split)")) return st;
     if (!acc_out) {
         const unsigned g = static_cast<unsigned>((count + 255) / 256);
@@ -264,18 +415,27 @@ nq_status check_w8a8(int64_t m, int64_t n, int64_t k, int path, const char* who)
 }
 
 bool mfma_ok(const int8_t* xq, const int8_t* wq, int64_t k) {
-    return k % 16 == 0 && aligned(xq, 16) && aligned(wq, 16);
+    return k > 0 && k % 16 == 0 && aligned(xq, 16) && aligned(wq, 16);
+}
+
+// AUTO: the v_dot4 GEMV only at m <= 2 (its per-row dot work grows with m while
+// one 16x16x64 MFMA covers 16 activation rows), the MFMA kernels above.
+int resolve_path(int path, int64_t m) {
+    return path == NQ_PATH_AUTO ? (m <= 2 ? NQ_PATH_GEMV : NQ_PATH_MFMA) : path;
 }
 
 // Runs the chosen path on pre-quantized activations.
 nq_status run_gemm(const int8_t* xq, const float* as, const int8_t* wq, const float* ws,
                    const float* bias, void* y, nq_dtype ydt, int32_t* acc_out, int64_t m,
-                   int64_t n, int64_t k, void* workspace, size_t ws_bytes, int path, hipStream_t s) {
-    int p = path;
-    if (p == NQ_PATH_AUTO) p = m <= 8 ? NQ_PATH_GEMV : NQ_PATH_MFMA;
-    if (p == NQ_PATH_MFMA && (!mfma_ok(xq, wq, k) || k == 0)) p = NQ_PATH_GENERIC;
-    if (p == NQ_PATH_MFMA)
-        return gemm_mfma(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, workspace, ws_bytes, s);
+                   int64_t n, int64_t k, void* workspace, size_t ws_bytes, int path, bool zeroed,
+                   hipStream_t s) {
+    int p = resolve_path(path, m);
+    if (p == NQ_PATH_MFMA && !mfma_ok(xq, wq, k)) p = NQ_PATH_GENERIC;
+    if (p == NQ_PATH_MFMA) {
+        if (m <= kSkinnyMaxM)
+            return gemm_skinny(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, workspace, ws_bytes, zeroed, s);
+        return gemm_big(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, workspace, ws_bytes, s);
+    }
     if (p == NQ_PATH_GEMV && m > 8) {
         // The GEMV holds at most 8 activation rows; larger m runs in slices of 8.
         for (int64_t r0 = 0; r0 < m; r0 += 8) {
@@ -294,6 +454,15 @@ nq_status run_gemm(const int8_t* xq, const float* as, const int8_t* wq, const fl
 }  // namespace nq
 
 using namespace nq;
+
+namespace nq {
+nq_status act_quant(const void* x, nq_dtype xdt, int64_t m, int64_t k, int8_t* xq, float* as,
+                    void* zero, size_t zero_bytes, hipStream_t s);
+bool gemv_w8a8_fused_launch(const void* x, nq_dtype xdt, const int8_t* w, const float* ws,
+                            const float* bias, void* y, nq_dtype ydt, int64_t m, int64_t n,
+                            int64_t k, hipStream_t s, nq_status* st);
+
+}  // namespace nq
 
 extern "C" size_t nq_gemm_w8a8_workspace_size(int64_t m, int64_t n, int64_t k) {
     return gemm_ws_bytes(m, n, k);
@@ -318,7 +487,7 @@ extern "C" nq_status nq_gemm_w8a8(const int8_t* xq, const float* a_scale, const 
                    aligned(bias, 4),
                NQ_BAD_ALIGN, "gemm_w8a8: misaligned pointer");
     return run_gemm(xq, a_scale, wq, w_scale, bias, y, y_dtype, nullptr, m, n, k, workspace,
-                    workspace_bytes, path, as_stream(stream));
+                    workspace_bytes, path, false, as_stream(stream));
 }
 
 extern "C" nq_status nq_w8a8_acc_i32(const int8_t* xq, const int8_t* wq, int32_t* acc, int64_t m,
@@ -329,7 +498,7 @@ extern "C" nq_status nq_w8a8_acc_i32(const int8_t* xq, const int8_t* wq, int32_t
     NQ_REQUIRE(acc && (k == 0 || (xq && wq)), NQ_BAD_ARG, "w8a8_acc_i32: null pointer");
     NQ_REQUIRE(aligned(acc, 4), NQ_BAD_ALIGN, "w8a8_acc_i32: misaligned acc");
     return run_gemm(xq, nullptr, wq, nullptr, nullptr, nullptr, NQ_F32, acc, m, n, k, workspace,
-                    workspace_bytes, path, as_stream(stream));
+                    workspace_bytes, path, false, as_stream(stream));
 }
 
 extern "C" nq_status nq_linear_w8a8(const void* x, nq_dtype x_dtype, const int8_t* wq,
@@ -348,12 +517,29 @@ extern "C" nq_status nq_linear_w8a8(const void* x, nq_dtype x_dtype, const int8_
     NQ_REQUIRE(workspace && workspace_bytes >= need, NQ_BAD_ARG,
                "linear_w8a8: workspace of %zu bytes required, %zu given", need, workspace_bytes);
     NQ_REQUIRE(aligned(workspace, 256), NQ_BAD_ALIGN, "linear_w8a8: workspace must be 256-byte aligned");
+    hipStream_t s = as_stream(stream);
+    const int p = resolve_path(path, m);
+    if (p == NQ_PATH_GEMV) {
+        nq_status st = NQ_OK;
+        if (gemv_w8a8_fused_launch(x, x_dtype, wq, w_scale, bias, y, y_dtype, m, n, k, s, &st)) return st;
+    }
     char* base = static_cast<char*>(workspace);
     int8_t* xq = reinterpret_cast<int8_t*>(base);
     float* as = reinterpret_cast<float*>(base + round_up(static_cast<size_t>(m * k), 256));
     char* rest = reinterpret_cast<char*>(as) + round_up(static_cast<size_t>(m) * 4, 256);
     const size_t rest_bytes = workspace_bytes - static_cast<size_t>(rest - base);
-    if (nq_status st = nq_act_quant_i8(x, x_dtype, m, k, xq, as, stream)) return st;
-    return run_gemm(xq, as, wq, w_scale, bias, y, y_dtype, nullptr, m, n, k, rest, rest_bytes, path,
-                    as_stream(stream));
+    // A split skinny plan needs its accumulator cleared: the activation-quant
+    // launch does it with extra workgroups.
+    void* zero = nullptr;
+    size_t zero_bytes = 0;
+    if (p == NQ_PATH_MFMA && m <= kSkinnyMaxM && mfma_ok(xq, wq, k)) {
+        const SkinnyPlan sp = plan_skinny(m, n, k);
+        if (sp.splits > 1) {
+            zero = rest;
+            zero_bytes = sp.acc_bytes;
+        }
+    }
+    if (nq_status st = act_quant(x, x_dtype, m, k, xq, as, zero, zero_bytes, s)) return st;
+    return run_gemm(xq, as, wq, w_scale, bias, y, y_dtype, nullptr, m, n, k, rest, rest_bytes, p,
+                    zero_bytes > 0, s);
 }

@@ -200,3 +200,38 @@ def test_w8a8_prefill_config5(dev, nq, orc):
     assert torch.equal(acc_m, acc_g)
     rows = rng.choice(m, 24, replace=False)
     assert np.array_equal(host(acc_m)[rows], orc.w8a8_acc(xq[rows], wq))
+
+
+@pytest.mark.parametrize("m", [9, 24, 40, 57])
+@pytest.mark.parametrize("n,k", [(1536, 1536), (8960, 1536), (1536, 8960), (100, 272)])
+def test_w8a8_skinny_ragged_m(dev, nq, orc, m, n, k):
+    x, w, b = data(m, n, k, 7 * m + n + k, bias=True)
+    t = nq.quantize_q8(to_dev(w, dev))
+    y = host(nq.linear_w8a8(to_dev(x, dev), t, to_dev(b, dev)))
+    q, s = orc.quantize_q8(w)
+    assert_close_rms(y, orc.linear_w8a8(x, q, s, b), f"w8a8 skinny {m}x{n}x{k}")
+
+
+def test_w8a8_workspace_reuse_and_gemm_entry(dev, nq, orc):
+    """Split-K counters re-arm between calls sharing one workspace; the
+    pre-quantized entry (nq_gemm_w8a8) gives the same bits as the linear."""
+    import ctypes  # noqa: F401
+    from nanoinfer_amd import _lib
+    lib = _lib.load()
+    m, n, k = 32, 1536, 8960
+    rng = np.random.default_rng(77)
+    w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    t = nq.quantize_q8(to_dev(w, dev))
+    q, s = orc.quantize_q8(w)
+    ws = torch.empty(lib.nq_linear_w8a8_workspace_size(m, n, k), dtype=torch.uint8, device=dev)
+    ws.fill_(0xAB)                                     # garbage: the call must not depend on it
+    for it in range(3):
+        x = rng.normal(0, 1, (m, k)).astype(np.float32)
+        xd = to_dev(x, dev)
+        y = torch.empty((m, n), dtype=torch.float32, device=dev)
+        _lib.check(lib.nq_linear_w8a8(xd.data_ptr(), 0, t.q.data_ptr(), t.scale.data_ptr(), None, y.data_ptr(), 0,
+                                      m, n, k, ws.data_ptr(), ws.numel(), 0, torch.cuda.current_stream().cuda_stream))
+        assert_close_rms(host(y), orc.linear_w8a8(x, q, s), f"reuse {it}")
+        xq, a_s = nq.act_quant(xd)
+        y2 = nq.gemm_w8a8(xq, a_s, t, out_dtype=torch.float32)
+        assert same_bits(host(y2), host(y))

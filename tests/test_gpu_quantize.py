@@ -99,3 +99,22 @@ def test_embedding_q8(dev, nq, orc, golden):
     assert same_bits(h, orc.embedding_q8(q, s, ids).astype(np.float16))
     with pytest.raises(ValueError):
         nq.embedding_q8(t, [2048])
+
+
+def test_act_quant_ties_and_extremes(dev, nq, orc):
+    """Rows whose quotients hit exact half-integers (the fast reciprocal path must
+    hand them to the exact divide), tiny and huge scales, and non-finite values."""
+    rows = [
+        [127, 63.5, -63.5, 0.5, -0.5, 1.5, -2.5, 2.5, 126.5, -126.5, 3.5, 4.5] + [0] * 4,
+        [1e-38, 5e-39, -1e-39, 3e-40] + [0] * 12,                 # denormal-range scale
+        [3e38, -1e38, 1e30, 7] + [0] * 12,
+        [np.inf, 1, -2, 3] + [0] * 12,
+        [np.nan, np.nan, 1, -1] + [0] * 12,
+        list(np.linspace(-127, 127, 16)),
+    ]
+    x = np.array(rows, np.float32)
+    xq, s = nq.act_quant(to_dev(x, dev))
+    q_ref, s_ref = orc.act_quant(x)
+    assert same_bits(host(xq), q_ref) and same_bits(host(s), s_ref)
+    t = nq.quantize_q8(to_dev(x, dev))
+    assert same_bits(host(t.q), q_ref) and same_bits(host(t.scale), s_ref)
