@@ -37,111 +37,166 @@ constexpr int kGemmThreads = 256;
 
 enum class Out { Y, ACC, ATOMIC };
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, Out OUT, typename YT>
-__global__ __launch_bounds__(kGemmThreads) void gemm_w8a8_mfma_kernel(
+// ---- prefill W8A8 GEMM (m > 64) ---------------------------------------------------------
+// 128 x 128 output tile per workgroup, 4 waves of 64 x 64 (4 x 4 MFMA
+// 16x16x64 tiles). K advances in 64-byte slabs staged through a double-buffered
+// LDS (rows padded to 80 bytes: each 8-lane ds_read_b128 phase hits 32 distinct
+// banks). Global loads run three slabs ahead in a register ring, so about three
+// slabs of MFMA work cover the L2/MALL latency; one barrier per slab.
+// The MFMA computes D = W_tile * xq_tile^T (weights as the A operand), so a lane
+// ends with four consecutive output columns of one row: the epilogue issues
+// 8-byte fp16 stores (or 16-byte int32 / fp32 stores).
+// Workgroup ids are remapped so each XCD (ids are dealt round-robin over the 8
+// XCDs) covers a contiguous band of column tiles, walked row-tile fastest: the
+// XCD's band of the weight stays in its L2 while the row tiles stream past.
+constexpr int kPBM = 128, kPBN = 128, kPRow = kBK, kPRing = 3;
+
+// Byte offset of 16-byte chunk c of row r in a swizzled 64-byte-row LDS tile.
+__device__ __forceinline__ int swz(int r, int c) { return r * kPRow + ((c ^ ((r >> 1) & 3)) << 4); }
+
+template <Out OUT, typename YT>
+__global__ __launch_bounds__(256) void gemm_w8a8_prefill_kernel(
     const int8_t* __restrict__ xq, const float* __restrict__ as, const int8_t* __restrict__ wq,
     const float* __restrict__ ws, const float* __restrict__ bias, YT* __restrict__ y,
-    int32_t* __restrict__ acc_out, int m, int n, int k, int k_split) {
-    static_assert(WAVES_M * WAVES_N == 4, "4 waves per workgroup");
-    constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
-    constexpr int TM = WM / 16, TN = WN / 16;
-    static_assert(TM >= 1 && TN >= 1 && WM % 16 == 0 && WN % 16 == 0, "wave tile");
-    constexpr int A_CHUNKS = BM * kBK / 16, B_CHUNKS = BN * kBK / 16;
-    constexpr int A_PER = (A_CHUNKS + kGemmThreads - 1) / kGemmThreads;
-    constexpr int B_PER = (B_CHUNKS + kGemmThreads - 1) / kGemmThreads;
-
-    __shared__ __attribute__((aligned(16))) int8_t As[BM * kLdsRow];
-    __shared__ __attribute__((aligned(16))) int8_t Bs[BN * kLdsRow];
+    int32_t* __restrict__ acc_out, int m, int n, int k, int tiles_m, int tiles_n) {
+    __shared__ __attribute__((aligned(16))) int8_t sx[2][kPBM * kPRow];
+    __shared__ __attribute__((aligned(16))) int8_t sw[2][kPBN * kPRow];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const int kb = blockIdx.z * k_split;
-    const int ke = min(k, kb + k_split);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int total = tiles_m * tiles_n;
+    int lin = blockIdx.x;
+    if (total % 8 == 0) lin = (blockIdx.x % 8) * (total / 8) + blockIdx.x / 8;
+    const int mt = lin % tiles_m, nt = lin / tiles_m;
+    const int m0 = mt * kPBM, n0 = nt * kPBN;
 
-    v4i ra[A_PER], rb[B_PER];
-    auto load_slab = [&](int k0) {
+    // Each slab: 128 rows x 64 bytes per operand = 512 16-byte chunks, 2 per
+    // thread per operand; chunk c -> row c / 4, 16-byte column c % 4. The loads
+    // are raw buffer loads: the per-thread byte offset is fixed, the slab offset
+    // k0 rides in the scalar offset, and rows past m / n get an offset beyond the
+    // buffer's size so the hardware returns zeros (no per-load predicates or
+    // 64-bit address arithmetic in the loop).
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(xq), 0, m * k, 0x00020000);
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(wq), 0, n * k, 0x00020000);
+    int xoff[2], woff[2], soff[2];
 #pragma unroll
-        for (int i = 0; i < A_PER; ++i) {
-            const int c = tid + i * kGemmThreads;
-            const int row = c >> 2, kc = (c & 3) * 16;
-            const bool ok = (A_CHUNKS % kGemmThreads == 0 || c < A_CHUNKS) && m0 + row < m && k0 + kc < ke;
-            ra[i] = ok ? *reinterpret_cast<const v4i*>(xq + static_cast<size_t>(m0 + row) * k + k0 + kc)
-                       : v4i{0, 0, 0, 0};
-        }
-#pragma unroll
-        for (int i = 0; i < B_PER; ++i) {
-            const int c = tid + i * kGemmThreads;
-            const int row = c >> 2, kc = (c & 3) * 16;
-            const bool ok = (B_CHUNKS % kGemmThreads == 0 || c < B_CHUNKS) && n0 + row < n && k0 + kc < ke;
-            rb[i] = ok ? *reinterpret_cast<const v4i*>(wq + static_cast<size_t>(n0 + row) * k + k0 + kc)
-                       : v4i{0, 0, 0, 0};
-        }
-    };
-    auto store_slab = [&]() {
-#pragma unroll
-        for (int i = 0; i < A_PER; ++i) {
-            const int c = tid + i * kGemmThreads;
-            if (A_CHUNKS % kGemmThreads == 0 || c < A_CHUNKS)
-                *reinterpret_cast<v4i*>(As + (c >> 2) * kLdsRow + (c & 3) * 16) = ra[i];
-        }
-#pragma unroll
-        for (int i = 0; i < B_PER; ++i) {
-            const int c = tid + i * kGemmThreads;
-            if (B_CHUNKS % kGemmThreads == 0 || c < B_CHUNKS)
-                *reinterpret_cast<v4i*>(Bs + (c >> 2) * kLdsRow + (c & 3) * 16) = rb[i];
-        }
-    };
-
-    v4i acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
-
-    const int frag_row = lane & 15, frag_k = (lane >> 4) * 16;
-    if (kb < ke) load_slab(kb);
-    for (int k0 = kb; k0 < ke; k0 += kBK) {
-        store_slab();
-        __syncthreads();
-        if (k0 + kBK < ke) load_slab(k0 + kBK);
-        v4i fa[TM], fb[TN];
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-            fa[i] = *reinterpret_cast<const v4i*>(As + (wm * WM + i * 16 + frag_row) * kLdsRow + frag_k);
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-            fb[j] = *reinterpret_cast<const v4i*>(Bs + (wn * WN + j * 16 + frag_row) * kLdsRow + frag_k);
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
-        __syncthreads();
+    for (int i = 0; i < 2; ++i) {
+        const int c = tid + i * 256, r = c >> 2, kc = (c & 3) * 16;
+        xoff[i] = m0 + r < m ? (m0 + r) * k + kc : 0x7FFFFFF0;
+        woff[i] = n0 + r < n ? (n0 + r) * k + kc : 0x7FFFFFF0;
+        soff[i] = swz(r, c & 3);
     }
+    v4i rx[kPRing][2], rw[kPRing][2];
+    auto load = [&](int slot_k0, v4i (&dx)[2], v4i (&dw)[2]) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            dx[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff[i], slot_k0, 0));
+            dw[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wrs, woff[i], slot_k0, 0));
+        }
+    };
+    auto store = [&](int buf, const v4i (&dx)[2], const v4i (&dw)[2]) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            *reinterpret_cast<v4i*>(&sx[buf][soff[i]]) = dx[i];
+            *reinterpret_cast<v4i*>(&sw[buf][soff[i]]) = dw[i];
+        }
+    };
 
+    v4i acc[4][4];  // [n tile][m tile]
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int col = n0 + wn * WN + j * 16 + (lane & 15);
-            if (col >= n) continue;
-            const float wsc = (OUT == Out::Y) ? ws[col] : 0.0f;
-            const float b = (OUT == Out::Y && bias) ? bias[col] : 0.0f;
+        for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+    const int fr = lane & 15;
+    int fwo[4], fxo[4];
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int row = m0 + wm * WM + i * 16 + (lane >> 4) * 4 + v;
-                if (row >= m) continue;
-                const size_t o = static_cast<size_t>(row) * n + col;
-                if constexpr (OUT == Out::ATOMIC) {
-                    atomicAdd(acc_out + o, acc[i][j][v]);
-                } else if constexpr (OUT == Out::ACC) {
-                    acc_out[o] = acc[i][j][v];
+    for (int i = 0; i < 4; ++i) {
+        fwo[i] = swz(wn * 64 + i * 16 + fr, lane >> 4);
+        fxo[i] = swz(wm * 64 + i * 16 + fr, lane >> 4);
+    }
+    auto compute = [&](int buf) {
+        v4i fw[4], fx[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) fw[i] = *reinterpret_cast<const v4i*>(&sw[buf][fwo[i]]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) fx[j] = *reinterpret_cast<const v4i*>(&sx[buf][fxo[j]]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fw[i], fx[j], acc[i][j], 0, 0, 0);
+    };
+
+    const int nk = k / kBK;  // the prefill contract has k % kBK == 0
+    // Every step is unconditional so the compiler's in-order vmcnt bookkeeping
+    // sees the same three slabs in flight on every iteration (a conditional load
+    // makes it wait for all of them): slab indices past the end are clamped to
+    // the last slab, whose redundant copies are never multiplied.
+    auto slab = [&](int s_) { return (s_ < nk ? s_ : nk - 1) * kBK; };
+    load(0, rx[0], rw[0]);
+    store(0, rx[0], rw[0]);
+#pragma unroll
+    for (int p = 0; p < kPRing; ++p) load(slab(p + 1), rx[p], rw[p]);
+    __syncthreads();
+    // Slab kt is in LDS buffer kt & 1; slab kt + 1 sits in ring slot kt % 3.
+    auto step = [&](int kt, auto phase) {
+        constexpr int P = decltype(phase)::value;
+        compute(kt & 1);
+        store((kt + 1) & 1, rx[P], rw[P]);
+        load(slab(kt + 1 + kPRing), rx[P], rw[P]);
+        __syncthreads();
+    };
+    int kt = 0;
+    for (; kt + kPRing <= nk; kt += kPRing) {
+        step(kt, std::integral_constant<int, 0>{});
+        step(kt + 1, std::integral_constant<int, 1>{});
+        step(kt + 2, std::integral_constant<int, 2>{});
+    }
+    if (kt < nk) step(kt, std::integral_constant<int, 0>{});
+    if (kt + 1 < nk) step(kt + 1, std::integral_constant<int, 1>{});
+
+    // Lane l holds, for tile (i, j), output row m0 + wm*64 + j*16 + (l % 16) and
+    // columns n0 + wn*64 + i*16 + 4*(l / 16) + (0..3).
+    const int row_in = fr, col_in = (lane >> 4) * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = m0 + wm * 64 + j * 16 + row_in;
+        if (row >= m) continue;
+        const float a_s = OUT == Out::Y ? as[row] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int col = n0 + wn * 64 + i * 16 + col_in;
+            const size_t o = static_cast<size_t>(row) * n + col;
+            if (col + 3 < n && (n & 3) == 0) {
+                if constexpr (OUT == Out::ACC) {
+                    *reinterpret_cast<v4i*>(acc_out + o) = acc[i][j];
                 } else {
-                    y[o] = from_f32<YT>(w8a8_epilogue(acc[i][j][v], as[row], wsc, b));
+                    const f4 w4 = *reinterpret_cast<const f4*>(ws + col);
+                    const f4 b4 = bias ? *reinterpret_cast<const f4*>(bias + col) : f4{0, 0, 0, 0};
+                    if constexpr (sizeof(YT) == 4) {
+                        f4 r;
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) r[v] = w8a8_epilogue(acc[i][j][v], a_s, w4[v], b4[v]);
+                        *reinterpret_cast<f4*>(y + o) = r;
+                    } else {
+                        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+                        h4 r;
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) r[v] = from_f32<YT>(w8a8_epilogue(acc[i][j][v], a_s, w4[v], b4[v]));
+                        *reinterpret_cast<h4*>(y + o) = r;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    if (col + v >= n) break;
+                    if constexpr (OUT == Out::ACC) acc_out[o + v] = acc[i][j][v];
+                    else y[o + v] = from_f32<YT>(w8a8_epilogue(acc[i][j][v], a_s, ws[col + v], bias ? bias[col + v] : 0.0f));
                 }
             }
         }
+    }
 }
 
 __global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t count) {
@@ -261,23 +316,6 @@ __global__ void w8a8_finalize_kernel(const int32_t* __restrict__ acc, const floa
 constexpr int kTargetBlocks = 1024;  // ~4 workgroups per CU on 256 CUs
 constexpr int kSkinnyMaxM = 64;
 
-// Large m: 128x128 tiles, K split (atomic int32 accumulation) only when the
-// tile count alone cannot fill the chip.
-struct BigPlan {
-    int splits, k_split;
-};
-BigPlan plan_big(int64_t m, int64_t n, int64_t k) {
-    const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
-    const int64_t kslabs = (k + kBK - 1) / kBK;
-    int64_t splits = 1;
-    if (tiles < kTargetBlocks / 4) splits = std::min<int64_t>((kTargetBlocks / 4 + tiles - 1) / tiles, std::max<int64_t>(1, kslabs / 4));
-    const int64_t per = (kslabs + splits - 1) / splits;
-    BigPlan p;
-    p.k_split = static_cast<int>(std::max<int64_t>(1, per) * kBK);
-    p.splits = static_cast<int>(std::max<int64_t>(1, (k + p.k_split - 1) / p.k_split));
-    return p;
-}
-
 // Skinny m: 32 columns per workgroup when that still gives >= 128 workgroups,
 // else 16; waves for about three K steps each (4..16). K is split across
 // workgroups only when one range would leave a wave more than 6 steps.
@@ -305,8 +343,7 @@ size_t gemm_ws_bytes(int64_t m, int64_t n, int64_t k) {
     if (m <= kSkinnyMaxM) {
         return plan_skinny(m, n, k).acc_bytes;
     }
-    const BigPlan p = plan_big(m, n, k);
-    return p.splits > 1 ? round_up(static_cast<size_t>(m * n) * 4, 256) : 0;
+    return 0;
 }
 
 // Skinny launch. zeroed: a split plan's accumulator was already cleared by
@@ -363,43 +400,21 @@ nq_status gemm_skinny(const int8_t* xq, const float* as, const int8_t* wq, const
     return NQ_OK;
 }
 
-// Big-m launch (128x128 tiles).
+// Big-m launch.
 nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const float* ws,
                    const float* bias, void* y, nq_dtype ydt, int32_t* acc_out, int64_t m, int64_t n,
-                   int64_t k, void* workspace, size_t ws_bytes, hipStream_t s) {
-    const BigPlan p = plan_big(m, n, k);
+                   int64_t k, hipStream_t s) {
+    const int tm = static_cast<int>((m + kPBM - 1) / kPBM), tn = static_cast<int>((n + kPBN - 1) / kPBN);
+    const unsigned grid = static_cast<unsigned>(tm) * static_cast<unsigned>(tn);
+    const size_t lds = 0;
     const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
-    dim3 grid(static_cast<unsigned>((n + 127) / 128), static_cast<unsigned>((m + 127) / 128),
-              static_cast<unsigned>(p.splits));
-    if (p.splits == 1) {
-        if (acc_out)
-            gemm_w8a8_mfma_kernel<128, 128, 2, 2, Out::ACC, float><<<grid, kGemmThreads, 0, s>>>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, p.k_split);
-        else if (ydt == NQ_F32)
-            gemm_w8a8_mfma_kernel<128, 128, 2, 2, Out::Y, float><<<grid, kGemmThreads, 0, s>>>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi, ni, ki, p.k_split);
-        else
-            gemm_w8a8_mfma_kernel<128, 128, 2, 2, Out::Y, _Float16><<<grid, kGemmThreads, 0, s>>>(xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr, mi, ni, ki, p.k_split);
-        return launch_status("gemm_w8a8_mfma_kernel");
-    }
-    const size_t need = round_up(static_cast<size_t>(m * n) * 4, 256);
-    int32_t* acc = acc_out;
-    if (!acc) {
-        NQ_REQUIRE(workspace && ws_bytes >= need, NQ_BAD_ARG,
-                   "w8a8 gemm: workspace of %zu bytes required, %zu given", need, ws_bytes);
-        NQ_REQUIRE(aligned(workspace, 4), NQ_BAD_ALIGN, "w8a8 gemm: misaligned workspace");
-        acc = static_cast<int32_t*>(workspace);
-    }
-    const int64_t count = m * n;
-    fill_i32_kernel<<<static_cast<unsigned>((count + 255) / 256), 256, 0, s>>>(acc, count);
-    gemm_w8a8_mfma_kernel<128, 128, 2, 2, Out::ATOMIC, float><<<grid, kGemmThreads, 0, s>>>(xq, as, wq, ws, bias, nullptr, acc, mi, ni, ki, p.k_split);
-    if (nq_status st = launch_status("gemm_w8a8_mfma_kernel(split)")) return st;
-    if (!acc_out) {
-        const unsigned g = static_cast<unsigned>((count + 255) / 256);
-        if (ydt == NQ_F32)
-            w8a8_finalize_kernel<float><<<g, 256, 0, s>>>(acc, as, ws, bias, static_cast<float*>(y), mi, ni);
-        else
-            w8a8_finalize_kernel<_Float16><<<g, 256, 0, s>>>(acc, as, ws, bias, static_cast<_Float16*>(y), mi, ni);
-    }
-    return launch_status("w8a8_finalize_kernel");
+    if (acc_out)
+        gemm_w8a8_prefill_kernel<Out::ACC, float><<<grid, 256, lds, s>>>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, tm, tn);
+    else if (ydt == NQ_F32)
+        gemm_w8a8_prefill_kernel<Out::Y, float><<<grid, 256, lds, s>>>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi, ni, ki, tm, tn);
+    else
+        gemm_w8a8_prefill_kernel<Out::Y, _Float16><<<grid, 256, lds, s>>>(xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr, mi, ni, ki, tm, tn);
+    return launch_status("gemm_w8a8_prefill_kernel");
 }
 
 nq_status check_w8a8(int64_t m, int64_t n, int64_t k, int path, const char* who) {
@@ -420,6 +435,11 @@ bool mfma_ok(const int8_t* xq, const int8_t* wq, int64_t k) {
 
 // AUTO: the v_dot4 GEMV only at m <= 2 (its per-row dot work grows with m while
 // one 16x16x64 MFMA covers 16 activation rows), the MFMA kernels above.
+// The prefill kernel's contract: whole 64-byte K slabs and 32-bit buffer offsets.
+bool prefill_ok(int64_t m, int64_t n, int64_t k) {
+    return k % kBK == 0 && m * k < (int64_t(1) << 31) - 64 && n * k < (int64_t(1) << 31) - 64;
+}
+
 int resolve_path(int path, int64_t m) {
     return path == NQ_PATH_AUTO ? (m <= 2 ? NQ_PATH_GEMV : NQ_PATH_MFMA) : path;
 }
@@ -434,7 +454,18 @@ nq_status run_gemm(const int8_t* xq, const float* as, const int8_t* wq, const fl
     if (p == NQ_PATH_MFMA) {
         if (m <= kSkinnyMaxM)
             return gemm_skinny(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, workspace, ws_bytes, zeroed, s);
-        return gemm_big(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, workspace, ws_bytes, s);
+        if (prefill_ok(m, n, k)) return gemm_big(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, s);
+        // Shapes outside the prefill kernel's contract run the skinny kernel on
+        // 64-row blocks (each block re-streams the weight).
+        for (int64_t r0 = 0; r0 < m; r0 += kSkinnyMaxM) {
+            const int64_t mm = std::min<int64_t>(kSkinnyMaxM, m - r0);
+            char* yp = y ? static_cast<char*>(y) + static_cast<size_t>(r0 * n) * dtype_size(ydt) : nullptr;
+            if (nq_status st = gemm_skinny(xq + r0 * k, as ? as + r0 : nullptr, wq, ws, bias, yp, ydt,
+                                           acc_out ? acc_out + r0 * n : nullptr, mm, n, k, workspace, ws_bytes,
+                                           false, s))
+                return st;
+        }
+        return NQ_OK;
     }
     if (p == NQ_PATH_GEMV && m > 8) {
         // The GEMV holds at most 8 activation rows; larger m runs in slices of 8.
