@@ -18,6 +18,8 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libnq_hip.so")
+HOST_LIB = os.path.join(PKG, "libnq_host.so")
+HOST_TEST = os.path.join(ROOT, "tests", "cpp", "test_host.bin")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -42,18 +44,48 @@ def _compile(src: str) -> str:
     return obj
 
 
+def _run(cmd, what):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"{what} failed:\n{r.stderr}")
+
+
+def _host_artifacts():
+    """The C++ host layer, the nicpp pybind11 module and the C++ host test."""
+    import sysconfig
+
+    import pybind11
+
+    host_src = os.path.join(CSRC, "host")
+    rpath = "-Wl,-rpath,$ORIGIN"
+    cxx = [HIPCC, "-std=c++17", "-O2", "-fPIC", "-Wall", "-I", os.path.join(ROOT, "include")]
+    _run([*cxx, "-shared", "-o", HOST_LIB + ".tmp", os.path.join(host_src, "nq_host.cpp"),
+          "-L", PKG, "-lnq_hip", rpath], "libnq_host link")
+    os.replace(HOST_LIB + ".tmp", HOST_LIB)
+    ext = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
+    mod = os.path.join(PKG, "nicpp" + ext)
+    _run([*cxx, "-shared", "-fvisibility=hidden", "-I", pybind11.get_include(),
+          "-I", sysconfig.get_paths()["include"], "-o", mod + ".tmp", os.path.join(host_src, "nicpp.cpp"),
+          "-L", PKG, "-lnq_host", "-lnq_hip", rpath], "nicpp module")
+    os.replace(mod + ".tmp", mod)
+    _run([*cxx, "-o", HOST_TEST + ".tmp", os.path.join(ROOT, "tests", "cpp", "test_host.cpp"),
+          "-L", PKG, "-lnq_host", "-lnq_hip", "-Wl,-rpath," + PKG, "-Wl,-rpath,$ORIGIN/../../nanoinfer_amd"],
+         "C++ host test")
+    os.replace(HOST_TEST + ".tmp", HOST_TEST)
+    return [HOST_LIB, mod, HOST_TEST]
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stderr}")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], "libnq_hip link")
     os.replace(tmp, LIB)
+    extra = _host_artifacts()
     if verbose:
-        print("built", LIB)
+        for p in [LIB, *extra]:
+            print("built", p)
     return LIB
 
 

@@ -1,0 +1,133 @@
+// C++ host API of the MI355X quantized-weight path: the reference's nicore quant
+// interface (cpp/src/quant.hpp:32-141, cpp/src/backend.hpp:229-239) restated over
+// libnq_hip.so's C ABI, in namespace ni::hip (the reference's names, one level
+// down, so both can link into one program).
+//
+// Same names, argument meaning and error behaviour as the reference:
+//   quantize_q8 / quantize_q4g / quantize_q4      (quant.hpp:57, :97, :114)
+//   linear_q8 / linear_w8a8 / linear_q4g          (quant.hpp:64, :80, :116)
+//   embedding_q8                                  (quant.hpp:72)
+//   Weight, make_quantized, make_q8_embed         (quant.hpp:120-141)
+//   HipBackend::make_quant_weight / make_embed_weight (backend.hpp:234-239)
+// Shape and argument errors throw std::invalid_argument, device errors throw
+// std::runtime_error (quant.cpp:23-25, cuda_internal.cuh:24).
+//
+// Tensors live on the host (fp32, as the reference's Tensor) or on the GPU
+// (fp32 / fp16 / int8 / uint8 / int32 device buffers). Quantized weights are
+// always device-resident: unlike the reference CUDA backend, which uploads only
+// W8A8 and leaves Q8/Q4/Q4G on the host (cuda_quant.cu:390-395), every mode here
+// quantizes on the GPU and runs its linear there. Device ops are enqueued on the
+// calling thread's current stream and return without synchronizing; to_host()
+// synchronizes that stream.
+#pragma once
+
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace ni {
+namespace hip {
+
+enum class QuantMode { None, Q8, Q4, Q4G, W8A8 };       // quant.hpp:32
+enum class Format { F32, F16, BF16, Q8, Q4, Q4G, W8A8 };  // quant.hpp:41
+enum class DType { F32, F16, I8, U8, I32 };
+enum class Device { CPU, HIP };
+
+const char* format_name(Format f);     // quant.cpp:447-458
+QuantMode quant_mode(const std::string& name);  // nicpp.cpp:51-59
+size_t dtype_bytes(DType d);
+
+// The calling thread's stream for every device op (nullptr = the null stream).
+void set_stream(void* hip_stream);
+void* current_stream();
+
+// A row-major tensor: a host fp32 vector, or a device buffer of `dtype`.
+class Tensor {
+public:
+    Tensor() = default;
+    explicit Tensor(std::vector<int64_t> shape);                    // host fp32, zero-filled
+    Tensor(std::vector<int64_t> shape, DType dtype, Device device);  // device: uninitialised
+
+    const std::vector<int64_t>& shape() const { return shape_; }
+    int64_t ndim() const { return static_cast<int64_t>(shape_.size()); }
+    int64_t size(int64_t d) const { return shape_.at(static_cast<size_t>(d)); }
+    int64_t numel() const { return numel_; }
+    DType dtype() const { return dtype_; }
+    Device device() const { return device_; }
+    bool on_device() const { return device_ == Device::HIP; }
+
+    float* data() { return host_.data(); }               // host fp32 only
+    const float* data() const { return host_.data(); }
+    float& operator[](int64_t i) { return host_[static_cast<size_t>(i)]; }
+    float operator[](int64_t i) const { return host_[static_cast<size_t>(i)]; }
+
+    void* device_ptr() const { return dev_.get(); }     // device only
+    size_t nbytes() const { return static_cast<size_t>(numel_) * dtype_bytes(dtype_); }
+
+private:
+    std::vector<int64_t> shape_;
+    int64_t numel_ = 0;
+    DType dtype_ = DType::F32;
+    Device device_ = Device::CPU;
+    std::vector<float> host_;
+    std::shared_ptr<void> dev_;
+};
+
+Tensor to_device(const Tensor& host, DType dtype = DType::F32);  // fp32 host -> device (fp32 / fp16)
+Tensor to_host(const Tensor& dev);                               // device -> host fp32 (synchronizes)
+
+// An int8-quantized [out, in] weight on the device (quant.hpp:49-54).
+struct QTensor {
+    Tensor q;      // I8 [out, in]
+    Tensor scale;  // F32 [out]
+    int64_t out = 0, in = 0;
+};
+
+// Group-wise int4 [out, in] on the device (quant.hpp:105-111); scale is fp32
+// (the reference layout) or fp16 (storage variant), [out, ceil(in / group)].
+struct Q4GTensor {
+    Tensor q;      // U8 [out, ceil(in / 2)]
+    Tensor scale;  // F32 or F16 [out, ceil(in / group)]
+    int64_t out = 0, in = 0, group = 0;
+};
+
+QTensor quantize_q8(const Tensor& w);
+Q4GTensor quantize_q4g(const Tensor& w, int64_t group = 32, DType scale_dtype = DType::F32);
+Q4GTensor quantize_q4(const Tensor& w);  // group == in (quant.cpp:212-233)
+
+// x: device [m, in] (fp32 or fp16); returns device [m, out] of out_dtype
+// (default: x's dtype). bias: device fp32 [out] or nullptr.
+Tensor linear_q8(const Tensor& x, const QTensor& w, const Tensor* bias = nullptr);
+Tensor linear_w8a8(const Tensor& x, const QTensor& w, const Tensor* bias = nullptr);
+Tensor linear_q4g(const Tensor& x, const Q4GTensor& w, const Tensor* bias = nullptr);
+Tensor linear_q8(const Tensor& x, const QTensor& w, const Tensor* bias, DType out_dtype);
+Tensor linear_w8a8(const Tensor& x, const QTensor& w, const Tensor* bias, DType out_dtype);
+Tensor linear_q4g(const Tensor& x, const Q4GTensor& w, const Tensor* bias, DType out_dtype);
+Tensor embedding_q8(const QTensor& table, const std::vector<int64_t>& ids);
+
+// Polymorphic device weight (quant.hpp:120-133).
+class Weight {
+public:
+    virtual ~Weight() = default;
+    virtual Tensor linear(const Tensor& x, const Tensor* bias) const = 0;
+    virtual Tensor gather(const std::vector<int64_t>& ids) const;  // throws unless an embedding
+    virtual Format format() const = 0;
+    virtual int64_t bytes() const = 0;
+    virtual int64_t fp32_bytes() const = 0;
+};
+
+std::unique_ptr<Weight> make_quantized(const Tensor& w, QuantMode mode);  // nullptr for None
+std::unique_ptr<Weight> make_q8_embed(const Tensor& w);
+
+// The backend factory seam (backend.hpp:234-239): host fp32 weights in,
+// device-resident quantized weights out.
+class HipBackend {
+public:
+    std::unique_ptr<Weight> make_quant_weight(const Tensor& host, QuantMode mode) const;
+    std::unique_ptr<Weight> make_embed_weight(const Tensor& host) const;
+    const char* name() const { return "hip"; }
+};
+
+}  // namespace hip
+}  // namespace ni
