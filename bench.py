@@ -44,7 +44,22 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--only", default="", help="comma list of sweep entries to run (debug)")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="only run a device-to-device copy of MIB MiB (FETCH_SIZE/WRITE_SIZE calibration)")
     return p.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def measured_traffic(workload):
+    """HBM bytes per launch for `workload` from the committed rocprofv3 PMC
+    summary (FETCH_SIZE + WRITE_SIZE, calibrated against a copy kernel), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f).get(workload, {}).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
 
 
 def main():
@@ -54,8 +69,17 @@ def main():
               "the path is single-GPU by design", file=sys.stderr)
         sys.exit(2)
 
-    import numpy as np
     import torch
+
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        a = torch.ones(n // 4, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n}))
+        return
 
     from nanoinfer_amd import _lib
     from nanoinfer_amd import quant as nq
@@ -226,7 +250,7 @@ def main():
                    "M": M, "K": K, "N": N, "group": G, "scale_dtype": "fp16", "x_dtype": "fp16",
                    "algorithmic_bytes": nbytes, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic("q4g_gemv_cfg2")},
         "cpu_baseline": cpu,
     }
     if sweep:
