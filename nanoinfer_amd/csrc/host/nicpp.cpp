@@ -1,6 +1,6 @@
 // pybind11 module `nicpp` for the MI355X quant path: the reference's QuantMode /
 // quant_mode surface (cpp/bindings/nicpp.cpp:51-76) plus the device weight
-// factory (backend.hpp:234-239) with device "hip". Host arrays cross the
+// factory (backend.hpp:109-114) with device "hip". Host arrays cross the
 // boundary as numpy fp32; device work releases the GIL, as the reference's
 // forward does (nicpp.cpp:221-233). Errors: std::invalid_argument -> ValueError,
 // std::runtime_error -> RuntimeError (pybind11's standard translation).

@@ -1,5 +1,5 @@
 // C++ host API of the MI355X quantized-weight path: the reference's nicore quant
-// interface (cpp/src/quant.hpp:32-141, cpp/src/backend.hpp:229-239) restated over
+// interface (cpp/src/quant.hpp:32-141, cpp/src/backend.hpp:104-114) restated over
 // libnq_hip.so's C ABI, in namespace ni::hip (the reference's names, one level
 // down, so both can link into one program).
 //
@@ -8,7 +8,7 @@
 //   linear_q8 / linear_w8a8 / linear_q4g          (quant.hpp:64, :80, :116)
 //   embedding_q8                                  (quant.hpp:72)
 //   Weight, make_quantized, make_q8_embed         (quant.hpp:120-141)
-//   HipBackend::make_quant_weight / make_embed_weight (backend.hpp:234-239)
+//   HipBackend::make_quant_weight / make_embed_weight (backend.hpp:109-114)
 // Shape and argument errors throw std::invalid_argument, device errors throw
 // std::runtime_error (quant.cpp:23-25, cuda_internal.cuh:24).
 //
@@ -120,7 +120,7 @@ public:
 std::unique_ptr<Weight> make_quantized(const Tensor& w, QuantMode mode);  // nullptr for None
 std::unique_ptr<Weight> make_q8_embed(const Tensor& w);
 
-// The backend factory seam (backend.hpp:234-239): host fp32 weights in,
+// The backend factory seam (backend.hpp:109-114): host fp32 weights in,
 // device-resident quantized weights out.
 class HipBackend {
 public:

@@ -274,7 +274,7 @@ def dequantize_q8(w: QTensor) -> torch.Tensor:
     return embedding_q8(w, range(w.out))
 
 
-# ---- Weight / factory (quant.hpp:120-141, backend.hpp:234-239) -------------------------
+# ---- Weight / factory (quant.hpp:120-141, backend.hpp:109-114) -------------------------
 class Weight:
     """Polymorphic device weight (quant.hpp:120-133)."""
 
