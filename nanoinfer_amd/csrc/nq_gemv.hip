@@ -62,28 +62,35 @@ __device__ __forceinline__ void reduce_to_lds(T (&acc)[R][M], T* red, int wave, 
     }
 }
 
-// ---- chunk loaders ---------------------------------------------------------------
-__device__ __forceinline__ void load_x16(const float* p, float (&xf)[16]) {
-    const f4* v = reinterpret_cast<const f4*>(p);
+// ---- activation chunk loaders ------------------------------------------------------
+// One lane's 16-element activation chunk as raw vector registers. Every load in
+// the kernels below is unconditional (lanes past the last chunk re-read chunk 0,
+// activation rows past m re-read row m - 1, and their partial sums are dropped
+// by a select), so the compiler issues all weight, scale and activation loads of
+// a lane back to back and the lane waits for memory once.
+template <typename XT>
+struct XChunk;
+template <>
+struct XChunk<float> {
+    f4 v[4];
+    __device__ __forceinline__ void load(const float* p) {
+        const f4* q = reinterpret_cast<const f4*>(p);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const f4 t = v[i];
-        xf[4 * i + 0] = t.x;
-        xf[4 * i + 1] = t.y;
-        xf[4 * i + 2] = t.z;
-        xf[4 * i + 3] = t.w;
+        for (int i = 0; i < 4; ++i) v[i] = q[i];
     }
-}
-__device__ __forceinline__ void load_x16(const _Float16* p, float (&xf)[16]) {
+    __device__ __forceinline__ float at(int e) const { return v[e >> 2][e & 3]; }
+};
+template <>
+struct XChunk<_Float16> {
     typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-    const h8* v = reinterpret_cast<const h8*>(p);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const h8 t = v[i];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) xf[8 * i + j] = static_cast<float>(t[j]);
+    h8 v[2];
+    __device__ __forceinline__ void load(const _Float16* p) {
+        const h8* q = reinterpret_cast<const h8*>(p);
+        v[0] = q[0];
+        v[1] = q[1];
     }
-}
+    __device__ __forceinline__ float at(int e) const { return static_cast<float>(v[e >> 3][e & 7]); }
+};
 
 // ---- weight-only int8 ------------------------------------------------------------
 template <int R, int M, typename XT, typename YT>
@@ -96,35 +103,32 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q8_kernel(
     const bool act = tid < chunks;
     const int row0 = blockIdx.x * R;
 
+    const int c = act ? tid : 0;
     v4i wv[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int row = min(row0 + r, n - 1);
-        wv[r] = act ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * k + tid * 16))
-                    : v4i{0, 0, 0, 0};
+        wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * k + c * 16));
     }
+    XChunk<XT> xc[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) xc[i].load(x + static_cast<size_t>(min(i, m - 1)) * k + c * 16);
+
     float acc[R][M];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int i = 0; i < M; ++i) acc[r][i] = 0.0f;
-
-#pragma unroll
     for (int i = 0; i < M; ++i) {
-        if (i < m && act) {
-            float xf[16];
-            load_x16(x + static_cast<size_t>(i) * k + tid * 16, xf);
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
+        for (int r = 0; r < R; ++r) {
+            float p = 0.0f;
 #pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    const int wd = wv[r][d];
-                    acc[r][i] = __builtin_fmaf(xf[4 * d + 0], sbyte_f32<0>(wd), acc[r][i]);
-                    acc[r][i] = __builtin_fmaf(xf[4 * d + 1], sbyte_f32<1>(wd), acc[r][i]);
-                    acc[r][i] = __builtin_fmaf(xf[4 * d + 2], sbyte_f32<2>(wd), acc[r][i]);
-                    acc[r][i] = __builtin_fmaf(xf[4 * d + 3], sbyte_f32<3>(wd), acc[r][i]);
-                }
+            for (int d = 0; d < 4; ++d) {
+                const int wd = wv[r][d];
+                p = __builtin_fmaf(xc[i].at(4 * d + 0), sbyte_f32<0>(wd), p);
+                p = __builtin_fmaf(xc[i].at(4 * d + 1), sbyte_f32<1>(wd), p);
+                p = __builtin_fmaf(xc[i].at(4 * d + 2), sbyte_f32<2>(wd), p);
+                p = __builtin_fmaf(xc[i].at(4 * d + 3), sbyte_f32<3>(wd), p);
             }
+            acc[r][i] = act ? p : 0.0f;
         }
     }
     reduce_to_lds<R, M>(acc, red, wave, tid & 63);
@@ -141,9 +145,6 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q8_kernel(
 }
 
 // ---- group-wise int4 ------------------------------------------------------------------
-template <typename ST>
-__device__ __forceinline__ float load_scale(const ST* p) { return to_f32(*p); }
-
 // Exact int4 x fp16 dot over one 16-byte chunk (32 codes) with packed fp16 math.
 // Nibble e of dword d is column 8d+e. (w >> 4j) & 0x000F000F puts columns j and
 // j+4 into the low 4 bits of the two halves; OR 0x6400 makes each half the fp16
@@ -189,46 +190,62 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q4g_kernel(
     const int rb = k >> 1, blocks = k / group;
     const bool act = tid < chunks;
     const int row0 = blockIdx.x * R;
-    const int blk = (tid * 32) / group;
 
+    const int c = act ? tid : 0;
+    const int blk = group == 32 ? c : (c * 32) / group;
     v4i wv[R];
-    float sc[R];
+    ST sraw[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int row = min(row0 + r, n - 1);
-        wv[r] = act ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * rb + tid * 16))
-                    : v4i{0, 0, 0, 0};
-        sc[r] = act ? load_scale(scale + static_cast<size_t>(row) * blocks + blk) : 0.0f;
+        wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * rb + c * 16));
+        sraw[r] = scale[static_cast<size_t>(row) * blocks + blk];
     }
+    // Activation chunks of all M rows are loaded up front while they fit in 64
+    // VGPRs (fp16 m <= 4, fp32 m <= 2); larger batches load one row at a time.
+    constexpr bool kAllX = M * 32 * sizeof(XT) <= 256;
+    auto load_x = [&](int i, XChunk<XT>& lo, XChunk<XT>& hi) {
+        const XT* xp = x + static_cast<size_t>(min(i, m - 1)) * k + c * 32;
+        lo.load(xp);
+        hi.load(xp + 16);
+    };
+    XChunk<XT> xlo[kAllX ? M : 1], xhi[kAllX ? M : 1];
+    if constexpr (kAllX) {
+#pragma unroll
+        for (int i = 0; i < M; ++i) load_x(i, xlo[i], xhi[i]);
+    }
+
     float acc[R][M];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int i = 0; i < M; ++i) acc[r][i] = 0.0f;
-
-#pragma unroll
     for (int i = 0; i < M; ++i) {
-        if (i < m && act) {
-            const XT* xp = x + static_cast<size_t>(i) * k + tid * 32;
-            if constexpr (sizeof(XT) == 2) {
-                typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-                const h8* xv = reinterpret_cast<const h8*>(xp);
-                const h8 q[4] = {xv[0], xv[1], xv[2], xv[3]};
-                h2 pairs[16];
-#pragma unroll
-                for (int d = 0; d < 4; ++d)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) pairs[4 * d + j] = h2{q[d][j], q[d][j + 4]};
-#pragma unroll
-                for (int r = 0; r < R; ++r) acc[r][i] = __builtin_fmaf(dot32_q4_f16(wv[r], pairs), sc[r], acc[r][i]);
-            } else {
-                float xf[32];
-                load_x16(xp, *reinterpret_cast<float(*)[16]>(&xf[0]));
-                load_x16(xp + 16, *reinterpret_cast<float(*)[16]>(&xf[16]));
-#pragma unroll
-                for (int r = 0; r < R; ++r) acc[r][i] = __builtin_fmaf(dot32_q4_f32(wv[r], xf), sc[r], acc[r][i]);
-            }
+        XChunk<XT> lo, hi;
+        if constexpr (kAllX) {
+            lo = xlo[i];
+            hi = xhi[i];
+        } else {
+            load_x(i, lo, hi);
         }
+        if constexpr (sizeof(XT) == 2) {
+            const typename XChunk<XT>::h8 q[4] = {lo.v[0], lo.v[1], hi.v[0], hi.v[1]};
+            h2 pairs[16];
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) pairs[4 * d + j] = h2{q[d][j], q[d][j + 4]};
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r][i] = dot32_q4_f16(wv[r], pairs) * to_f32(sraw[r]);
+        } else {
+            float xf[32];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                xf[e] = lo.at(e);
+                xf[16 + e] = hi.at(e);
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r][i] = dot32_q4_f32(wv[r], xf) * to_f32(sraw[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r][i] = act ? acc[r][i] : 0.0f;
     }
     reduce_to_lds<R, M>(acc, red, wave, tid & 63);
     __syncthreads();
@@ -256,27 +273,25 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_kernel(
     const bool act = tid < chunks;
     const int row0 = blockIdx.x * R;
 
+    const int c = act ? tid : 0;
     v4i wv[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int row = min(row0 + r, n - 1);
-        wv[r] = act ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * k + tid * 16))
-                    : v4i{0, 0, 0, 0};
+        wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * k + c * 16));
     }
+    v4i xv[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) xv[i] = *reinterpret_cast<const v4i*>(xq + static_cast<size_t>(min(i, m - 1)) * k + c * 16);
     int acc[R][M];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int i = 0; i < M; ++i) acc[r][i] = 0;
-#pragma unroll
     for (int i = 0; i < M; ++i) {
-        if (i < m && act) {
-            const v4i xv = *reinterpret_cast<const v4i*>(xq + static_cast<size_t>(i) * k + tid * 16);
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
+        for (int r = 0; r < R; ++r) {
+            int p = 0;
 #pragma unroll
-                for (int d = 0; d < 4; ++d) acc[r][i] = __builtin_amdgcn_sdot4(xv[d], wv[r][d], acc[r][i], false);
-            }
+            for (int d = 0; d < 4; ++d) p = __builtin_amdgcn_sdot4(xv[i][d], wv[r][d], p, false);
+            acc[r][i] = act ? p : 0;
         }
     }
     reduce_to_lds<R, M>(acc, red, wave, tid & 63);
@@ -302,30 +317,6 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_kernel(
 // waves, derives a_scale = absmax / 127 exactly as the activation-quant kernel
 // does, quantizes its own 16-element chunk in registers and runs the same
 // v_dot4_i32_i8 core. Identical int32 accumulators and epilogue, one launch.
-template <typename XT>
-struct XChunk;
-template <>
-struct XChunk<float> {
-    f4 v[4];
-    __device__ __forceinline__ void load(const float* p) {
-        const f4* q = reinterpret_cast<const f4*>(p);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = q[i];
-    }
-    __device__ __forceinline__ float at(int e) const { return v[e >> 2][e & 3]; }
-};
-template <>
-struct XChunk<_Float16> {
-    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-    h8 v[2];
-    __device__ __forceinline__ void load(const _Float16* p) {
-        const h8* q = reinterpret_cast<const h8*>(p);
-        v[0] = q[0];
-        v[1] = q[1];
-    }
-    __device__ __forceinline__ float at(int e) const { return static_cast<float>(v[e >> 3][e & 7]); }
-};
-
 template <int R, int M, typename XT, typename YT>
 __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_fused_kernel(
     const XT* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ ws,
@@ -337,23 +328,23 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_fused_kernel(
     const bool act = tid < chunks;
     const int row0 = blockIdx.x * R;
 
+    const int c = act ? tid : 0;
     v4i wv[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int row = min(row0 + r, n - 1);
-        wv[r] = act ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * k + tid * 16))
-                    : v4i{0, 0, 0, 0};
+        wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * k + c * 16));
     }
     XChunk<XT> xc[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) xc[i].load(x + static_cast<size_t>(min(i, m - 1)) * k + c * 16);
     float am[M];
 #pragma unroll
     for (int i = 0; i < M; ++i) {
-        am[i] = 0.0f;
-        if (i < m && act) {
-            xc[i].load(x + static_cast<size_t>(i) * k + tid * 16);
+        float a = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) am[i] = absmax_step(am[i], xc[i].at(e));
-        }
+        for (int e = 0; e < 16; ++e) a = absmax_step(a, xc[i].at(e));
+        am[i] = act ? a : 0.0f;
     }
 #pragma unroll
     for (int i = 0; i < M; ++i) {
@@ -376,7 +367,7 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_fused_kernel(
         for (int i = 0; i < M; ++i) acc[r][i] = 0;
 #pragma unroll
     for (int i = 0; i < M; ++i) {
-        if (i < m && act) {
+        {
             const RowQuantizer rq(as[i]);
             int qd[4];
 #pragma unroll
@@ -384,8 +375,8 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_fused_kernel(
                 int packed = 0;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int c = static_cast<int>(rq.code(xc[i].at(4 * d + e), 127.0f));
-                    packed |= (c & 0xFF) << (8 * e);
+                    const int code = static_cast<int>(rq.code(xc[i].at(4 * d + e), 127.0f));
+                    packed |= (code & 0xFF) << (8 * e);
                 }
                 qd[d] = packed;
             }
@@ -393,6 +384,8 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_fused_kernel(
             for (int r = 0; r < R; ++r)
 #pragma unroll
                 for (int d = 0; d < 4; ++d) acc[r][i] = __builtin_amdgcn_sdot4(qd[d], wv[r][d], acc[r][i], false);
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r][i] = act ? acc[r][i] : 0;
         }
     }
     reduce_to_lds<R, M>(acc, red, wave, tid & 63);
