@@ -40,8 +40,8 @@ typedef enum nq_status {
 
 typedef enum nq_dtype { NQ_F32 = 0, NQ_F16 = 1 } nq_dtype;
 
-/* Kernel selection for the W8A8 linears. AUTO: m <= 8 -> wave-per-row GEMV
- * (v_dot4_i32_i8), m >= 9 -> int8 MFMA GEMM. The forced values exist for A/B
+/* Kernel selection for the W8A8 linears. AUTO: m <= 4 (m <= 8 when k >= 4096)
+ * -> workgroup-per-rows GEMV (v_dot4_i32_i8), larger m -> int8 MFMA GEMM. The forced values exist for A/B
  * tests, like the reference's CudaPolicy::force_tiled_w8a8
  * (cuda_backend.hpp:43-89). GENERIC is the scalar bounds-checked kernel. */
 typedef enum nq_path { NQ_PATH_AUTO = 0, NQ_PATH_GEMV = 1, NQ_PATH_MFMA = 2, NQ_PATH_GENERIC = 3 } nq_path;

@@ -107,15 +107,15 @@ __global__ void quantize_q4g_odd_kernel(const float* __restrict__ w, uint8_t* __
 // the absmax pass and the quantize pass (x is read once).
 // Workgroups past the m rows clear `zero` (a 256-byte aligned scratch region of
 // the GEMM that follows) with 16-byte stores.
-template <typename XT, int CPT>
-__global__ __launch_bounds__(256) void act_quant_vec_kernel(const XT* __restrict__ x, int8_t* __restrict__ xq,
+template <typename XT, int CPT, int NT>
+__global__ __launch_bounds__(NT) void act_quant_vec_kernel(const XT* __restrict__ x, int8_t* __restrict__ xq,
                                                            float* __restrict__ a_scale, int m, int k,
                                                            v4i* __restrict__ zero, int64_t zero_vecs) {
-    __shared__ float red[4];
+    __shared__ float red[NT / 64];
     const int tid = threadIdx.x;
     if (static_cast<int>(blockIdx.x) >= m) {
-        for (int64_t i = static_cast<int64_t>(blockIdx.x - m) * 256 + tid; i < zero_vecs;
-             i += static_cast<int64_t>(gridDim.x - m) * 256)
+        for (int64_t i = static_cast<int64_t>(blockIdx.x - m) * NT + tid; i < zero_vecs;
+             i += static_cast<int64_t>(gridDim.x - m) * NT)
             zero[i] = v4i{0, 0, 0, 0};
         return;
     }
@@ -124,21 +124,23 @@ __global__ __launch_bounds__(256) void act_quant_vec_kernel(const XT* __restrict
     const v8* xr = reinterpret_cast<const v8*>(x + static_cast<size_t>(row) * k);
     v8 v[CPT];
     float am = 0.0f;
+    // Loads are unconditional (indices past the row re-read its last vector and
+    // are left out of the absmax), so all CPT of them are in flight together.
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) v[c] = xr[min(tid + c * NT, steps - 1)];
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
-        const int e = tid + c * 256;
-        if (e < steps) {
-            v[c] = xr[e];
+        float a = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) am = absmax_step(am, to_f32(v[c][j]));
-        }
+        for (int j = 0; j < 8; ++j) a = absmax_step(a, to_f32(v[c][j]));
+        am = tid + c * NT < steps ? absmax_step(am, a) : am;
     }
     am = wave_absmax(am);
     if ((tid & 63) == 0) red[tid >> 6] = am;
     __syncthreads();
     float a = red[0];
 #pragma unroll
-    for (int w = 1; w < 4; ++w) a = absmax_step(a, red[w]);
+    for (int w = 1; w < NT / 64; ++w) a = absmax_step(a, red[w]);
     const float sc = a / 127.0f;
     if (tid == 0) a_scale[row] = sc;
     const RowQuantizer rq(sc);
@@ -146,7 +148,7 @@ __global__ __launch_bounds__(256) void act_quant_vec_kernel(const XT* __restrict
     v2i* qr = reinterpret_cast<v2i*>(xq + static_cast<size_t>(row) * k);
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
-        const int e = tid + c * 256;
+        const int e = tid + c * NT;
         if (e < steps) {
             int lo = 0, hi = 0;
 #pragma unroll
@@ -179,22 +181,28 @@ nq_status check_rows(int64_t rows, int64_t cols, const char* who) {
 // Activation quant: the vectorized kernel when k fits it, else the scalar row kernel.
 nq_status act_quant(const void* x, nq_dtype xdt, int64_t m, int64_t k, int8_t* xq, float* as,
                     void* zero, size_t zero_bytes, hipStream_t s) {
-    const bool vec = k > 0 && k % 8 == 0 && k <= 8 * 256 * 8 && aligned(x, 16) && aligned(xq, 8);
+    // One workgroup per row: 256 threads up to 2048 elements, else 1024 threads
+    // with up to 8 vectors of 8 elements each.
+    const bool vec = k > 0 && k % 8 == 0 && k <= 8 * 1024 * 8 && aligned(x, 16) && aligned(xq, 8);
     const int64_t zero_vecs = static_cast<int64_t>(zero_bytes / 16);
     if (vec) {
         const int64_t zero_blocks = std::min<int64_t>(256, (zero_vecs + 255) / 256);
         const unsigned grid = static_cast<unsigned>(m + zero_blocks);
         v4i* zp = static_cast<v4i*>(zero);
-        const int cpt = static_cast<int>((k / 8 + 255) / 256);
+        const int64_t steps = k / 8;
         const int mi = static_cast<int>(m), ki = static_cast<int>(k);
         auto go = [&](auto* xp) {
             using XT = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
-            switch (cpt) {
-                case 1: act_quant_vec_kernel<XT, 1><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs); break;
-                case 2: act_quant_vec_kernel<XT, 2><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs); break;
-                case 3:
-                case 4: act_quant_vec_kernel<XT, 4><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs); break;
-                default: act_quant_vec_kernel<XT, 8><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs); break;
+            if (steps <= 256) {
+                act_quant_vec_kernel<XT, 1, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs);
+                return;
+            }
+            switch ((steps + 1023) / 1024) {
+                case 1: act_quant_vec_kernel<XT, 1, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs); break;
+                case 2: act_quant_vec_kernel<XT, 2, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs); break;
+                case 3: act_quant_vec_kernel<XT, 3, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs); break;
+                case 4: act_quant_vec_kernel<XT, 4, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs); break;
+                default: act_quant_vec_kernel<XT, 8, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs); break;
             }
         };
         if (xdt == NQ_F32) go(static_cast<const float*>(x));

@@ -87,11 +87,16 @@ __global__ __launch_bounds__(256) void gemm_w8a8_prefill_kernel(
         soff[i] = swz(r, c & 3);
     }
     v4i rx[kPRing][2], rw[kPRing][2];
-    auto load = [&](int slot_k0, v4i (&dx)[2], v4i (&dw)[2]) {
+    const int nk = k / kBK;  // the prefill contract has k % kBK == 0
+    // Slab sl; slabs past the end (the ring's tail prefetch) read as zeros
+    // without touching memory.
+    auto load = [&](int sl, v4i (&dx)[2], v4i (&dw)[2]) {
+        const bool in = sl < nk;
+        const int k0 = (in ? sl : 0) * kBK;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            dx[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff[i], slot_k0, 0));
-            dw[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wrs, woff[i], slot_k0, 0));
+            dx[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xrs, in ? xoff[i] : 0x7FFFFFF0, k0, 0));
+            dw[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wrs, in ? woff[i] : 0x7FFFFFF0, k0, 0));
         }
     };
     auto store = [&](int buf, const v4i (&dx)[2], const v4i (&dw)[2]) {
@@ -128,23 +133,20 @@ __global__ __launch_bounds__(256) void gemm_w8a8_prefill_kernel(
                 acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fw[i], fx[j], acc[i][j], 0, 0, 0);
     };
 
-    const int nk = k / kBK;  // the prefill contract has k % kBK == 0
     // Every step is unconditional so the compiler's in-order vmcnt bookkeeping
     // sees the same three slabs in flight on every iteration (a conditional load
-    // makes it wait for all of them): slab indices past the end are clamped to
-    // the last slab, whose redundant copies are never multiplied.
-    auto slab = [&](int s_) { return (s_ < nk ? s_ : nk - 1) * kBK; };
+    // makes it wait for all of them).
     load(0, rx[0], rw[0]);
     store(0, rx[0], rw[0]);
 #pragma unroll
-    for (int p = 0; p < kPRing; ++p) load(slab(p + 1), rx[p], rw[p]);
+    for (int p = 0; p < kPRing; ++p) load(p + 1, rx[p], rw[p]);
     __syncthreads();
     // Slab kt is in LDS buffer kt & 1; slab kt + 1 sits in ring slot kt % 3.
     auto step = [&](int kt, auto phase) {
         constexpr int P = decltype(phase)::value;
         compute(kt & 1);
         store((kt + 1) & 1, rx[P], rw[P]);
-        load(slab(kt + 1 + kPRing), rx[P], rw[P]);
+        load(kt + 1 + kPRing, rx[P], rw[P]);
         __syncthreads();
     };
     int kt = 0;
@@ -237,45 +239,62 @@ __global__ __launch_bounds__(1024) void gemm_w8a8_skinny_kernel(
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
-    auto load = [&](int k0, v4i (&a)[TM], v4i (&b)[TN]) {
-        const bool kin = k0 + fk < ke;
+    // Raw buffer loads: rows past m / n, and K positions past this range, get an
+    // offset beyond the buffer so the hardware returns zeros. No load sits
+    // behind a branch, so the three steps of the ring really are in flight
+    // together (a predicated load makes the compiler wait for every
+    // outstanding load before each MFMA).
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(xq), 0, m * k, 0x00020000);
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(wq), 0, n * k, 0x00020000);
+    constexpr int kOob = 0x7FFFFFF0;
+    int xo[TM], wo[TN];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            const int row = i * 16 + fr;
-            a[i] = (kin && row < m) ? *reinterpret_cast<const v4i*>(xq + static_cast<size_t>(row) * k + k0 + fk)
-                                    : v4i{0, 0, 0, 0};
-        }
+    for (int i = 0; i < TM; ++i) xo[i] = i * 16 + fr < m ? (i * 16 + fr) * k + fk : kOob;
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int col = n0 + j * 16 + fr;
-            b[j] = (kin && col < n)
-                       ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wq + static_cast<size_t>(col) * k + k0 + fk))
-                       : v4i{0, 0, 0, 0};
-        }
+    for (int j = 0; j < TN; ++j) wo[j] = n0 + j * 16 + fr < n ? (n0 + j * 16 + fr) * k + fk : kOob;
+
+    // The range has S 64-byte steps; wave w takes steps w, w + nw, ... (its
+    // count: steps). Each workgroup starts at its own rotation of the range, so
+    // the hundreds of workgroups reading the same activation rows at once spread
+    // over different L2 lines instead of queueing on the same ones.
+    const int S = (ke - kb + kBK - 1) / kBK;
+    const int steps = wave < S ? (S - wave + nw - 1) / nw : 0;
+    const int rot = S > 0 ? static_cast<int>((blockIdx.x * 5u) % static_cast<unsigned>(S)) : 0;
+    auto load = [&](int t, v4i (&a)[TM], v4i (&b)[TN]) {
+        // Steps past the wave's last one (the ring's tail prefetch) read as
+        // zeros without touching memory.
+        const int st = wave + t * nw;
+        int sr = st + rot;
+        sr = sr >= S ? sr - S : sr;
+        const int kc = kb + sr * kBK;
+        const bool kin = st < S && kc + fk < ke;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+            a[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xrs, kin ? xo[i] + kc : kOob, 0, 0));
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            b[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wrs, kin ? wo[j] + kc : kOob, 0, 0));
     };
-    const int kstep = nw * kBK;
-    const int k0 = kb + wave * kBK;
     v4i a[PD][TM], b[PD][TN];
 #pragma unroll
-    for (int p = 0; p < PD; ++p) load(k0 + p * kstep, a[p], b[p]);
-    for (int base = 0;; base += PD) {
-        bool done = false;
+    for (int p = 0; p < PD; ++p) load(p, a[p], b[p]);
+    auto step = [&](int t, auto phase) {
+        constexpr int P = decltype(phase)::value;
 #pragma unroll
-        for (int p = 0; p < PD; ++p) {
-            const int kc = k0 + (base + p) * kstep;
-            if (kc >= ke) {
-                done = true;
-                break;
-            }
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[p][i], b[p][j], acc[i][j], 0, 0, 0);
-            load(kc + PD * kstep, a[p], b[p]);
-        }
-        if (done) break;
+            for (int j = 0; j < TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[P][i], b[P][j], acc[i][j], 0, 0, 0);
+        load(t + PD, a[P], b[P]);
+    };
+    int t = 0;
+    for (; t + PD <= steps; t += PD) {
+        step(t, std::integral_constant<int, 0>{});
+        step(t + 1, std::integral_constant<int, 1>{});
+        step(t + 2, std::integral_constant<int, 2>{});
     }
+    if (t < steps) step(t, std::integral_constant<int, 0>{});
+    if (t + 1 < steps) step(t + 1, std::integral_constant<int, 1>{});
     __syncthreads();  // tile zeroed
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -433,15 +452,23 @@ bool mfma_ok(const int8_t* xq, const int8_t* wq, int64_t k) {
     return k > 0 && k % 16 == 0 && aligned(xq, 16) && aligned(wq, 16);
 }
 
-// AUTO: the v_dot4 GEMV only at m <= 2 (its per-row dot work grows with m while
-// one 16x16x64 MFMA covers 16 activation rows), the MFMA kernels above.
 // The prefill kernel's contract: whole 64-byte K slabs and 32-bit buffer offsets.
 bool prefill_ok(int64_t m, int64_t n, int64_t k) {
     return k % kBK == 0 && m * k < (int64_t(1) << 31) - 64 && n * k < (int64_t(1) << 31) - 64;
 }
+// The skinny kernel's contract: 32-bit buffer offsets (k % 16 == 0 is mfma_ok's).
+bool skinny_ok(int64_t m, int64_t n, int64_t k) {
+    return std::min<int64_t>(m, kSkinnyMaxM) * k < (int64_t(1) << 31) - 64 && n * k < (int64_t(1) << 31) - 64;
+}
 
-int resolve_path(int path, int64_t m) {
-    return path == NQ_PATH_AUTO ? (m <= 2 ? NQ_PATH_GEMV : NQ_PATH_MFMA) : path;
+// AUTO: the v_dot4 GEMV up to m = 4, and up to m = 8 for long K (where the
+// skinny MFMA plan splits K and pays for atomics plus a finalize launch); the
+// GEMV's per-row dot work grows with m while one 16x16x64 MFMA covers 16
+// activation rows, so the MFMA kernels take larger m. Measured on the decode
+// shapes k = 1536 / 8960, n = 256 .. 8960.
+int resolve_path(int path, int64_t m, int64_t k) {
+    if (path != NQ_PATH_AUTO) return path;
+    return (m <= 4 || (m <= 8 && k >= 4096)) ? NQ_PATH_GEMV : NQ_PATH_MFMA;
 }
 
 // Runs the chosen path on pre-quantized activations.
@@ -449,8 +476,11 @@ nq_status run_gemm(const int8_t* xq, const float* as, const int8_t* wq, const fl
                    const float* bias, void* y, nq_dtype ydt, int32_t* acc_out, int64_t m,
                    int64_t n, int64_t k, void* workspace, size_t ws_bytes, int path, bool zeroed,
                    hipStream_t s) {
-    int p = resolve_path(path, m);
+    int p = resolve_path(path, m, k);
     if (p == NQ_PATH_MFMA && !mfma_ok(xq, wq, k)) p = NQ_PATH_GENERIC;
+    // Weights past 2^31 bytes exceed the MFMA kernels' 32-bit buffer offsets;
+    // the v_dot4 GEMV (64-bit addressing) takes them, in slices of 8 rows.
+    if (p == NQ_PATH_MFMA && !skinny_ok(m, n, k)) p = NQ_PATH_GEMV;
     if (p == NQ_PATH_MFMA) {
         if (m <= kSkinnyMaxM)
             return gemm_skinny(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, workspace, ws_bytes, zeroed, s);
@@ -549,7 +579,7 @@ extern "C" nq_status nq_linear_w8a8(const void* x, nq_dtype x_dtype, const int8_
                "linear_w8a8: workspace of %zu bytes required, %zu given", need, workspace_bytes);
     NQ_REQUIRE(aligned(workspace, 256), NQ_BAD_ALIGN, "linear_w8a8: workspace must be 256-byte aligned");
     hipStream_t s = as_stream(stream);
-    const int p = resolve_path(path, m);
+    const int p = resolve_path(path, m, k);
     if (p == NQ_PATH_GEMV) {
         nq_status st = NQ_OK;
         if (gemv_w8a8_fused_launch(x, x_dtype, wq, w_scale, bias, y, y_dtype, m, n, k, s, &st)) return st;
