@@ -225,6 +225,8 @@ def main():
                                *w8a8_linear(2048, 8960, 1536, gemm_only=True), "mfma"))
             sweep.append(entry("w8a8_linear_cfg5a M=2048 K=1536 N=8960 (incl. act quant)",
                                *w8a8_linear(2048, 8960, 1536), "mfma"))
+        if want("decoder_cfg4"):
+            sweep.append(decoder_layer_cfg4(rnd, time_graph, args, w8a8_linear, entry))
         torch.cuda.empty_cache()
 
     # ---------------- CPU baseline (rank 0, N=1) --------------------------------------------
@@ -256,6 +258,56 @@ def main():
     if sweep:
         out["sweep"] = sweep
     print(json.dumps(out), flush=True)
+
+
+def decoder_layer_cfg4(rnd, time_graph, args, w8a8_linear, entry):
+    """one Qwen2.5-1.5B decoder layer, M=512 prefill, all seven
+    projections W8A8 on libnq_hip.so, fp16 activations, rmsnorm / RoPE / causal
+    GQA attention / SwiGLU in torch. Layers with distinct weights are chained
+    (>= 512 MiB of weights) so each layer streams its own weights."""
+    import torch
+
+    from nanoinfer_amd import model as nm
+    from nanoinfer_amd import quant as nq
+    cfg = nm.qwen25_15b()
+    shapes = nm.proj_shapes(cfg)
+    layer_bytes = sum(o * i for o, i in shapes.values())
+    L = max(2, math.ceil(ROTATE_BYTES / layer_bytes))
+    w = {"embed_tokens.weight": torch.zeros(8, cfg.hidden), "norm.weight": torch.ones(cfg.hidden)}
+    for li in range(L):
+        p = f"layers.{li}."
+        for name, (o, i) in shapes.items():
+            w[p + name + ".weight"] = rnd((o, i), 0.02)
+        for b in ("q_proj", "k_proj", "v_proj"):
+            w[p + f"self_attn.{b}.bias"] = rnd((shapes[f"self_attn.{b}"][0],), 0.02)
+        w[p + "input_layernorm.weight"] = 1.0 + rnd((cfg.hidden,), 0.02)
+        w[p + "post_attention_layernorm.weight"] = 1.0 + rnd((cfg.hidden,), 0.02)
+    mdl = nm.Model(cfg, w, nq.QuantMode.W8A8, "cuda", act_dtype=torch.float16, quantize_embed=False, layers=L)
+    del w
+    m = 512
+    x0 = rnd((m, cfg.hidden), 1.0, torch.float16)
+
+    def run_layers():
+        x = x0
+        for li in range(L):
+            x = mdl.layer(x, li)
+        return x
+    steps = max(2, args.steps // L)
+    ms = time_graph([run_layers], steps, max(1, args.warmup // L)) / L
+    proj_ops = sum(2 * m * o * i for o, i in shapes.values())
+    e = {"name": f"decoder_layer_cfg4 M={m} Qwen2.5-1.5B, 7 W8A8 projections + attention (fp16)",
+         "us": round(ms * 1e3, 3), "TOPS": round(proj_ops / (ms * 1e-3) / 1e12, 2), "ops": proj_ops,
+         "bound": "mfma", "frac": round(proj_ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4), "layers_chained": L}
+    del mdl
+    torch.cuda.empty_cache()
+    projs = []
+    for name, (o, i) in shapes.items():
+        pe = entry(f"{name} M={m} K={i} N={o}", *w8a8_linear(m, o, i), "mfma")
+        projs.append(pe)
+        torch.cuda.empty_cache()
+    e["projections"] = projs
+    e["projections_us"] = round(sum(p["us"] for p in projs), 3)
+    return e
 
 
 def cpu_baseline(m, n, k, g, nbytes, seconds):

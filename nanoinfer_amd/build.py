@@ -27,9 +27,13 @@ SOURCES = ["nq_abi.cpp", "nq_quantize.hip", "nq_gemv.hip", "nq_w8a8.hip", "nq_em
 
 # -packed-fp32-ops: keep hipcc from forming v_pk_{add,mul,fma}_f32 (the host
 # pass prints that it does not know the feature; that is harmless).
+# -amdgpu-mfma-vgpr-form: MFMA accumulators in ordinary VGPRs; with AGPR
+# accumulators the register allocator shuffled the tiles with v_accvgpr moves
+# on every GEMM iteration.
 HIP_FLAGS = [
     "-std=c++17", "-O3", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I", os.path.join(ROOT, "include"),
 ]
 

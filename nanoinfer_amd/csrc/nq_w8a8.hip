@@ -33,134 +33,189 @@ namespace {
 
 constexpr int kBK = 64;         // K bytes per MFMA step / LDS slab
 constexpr int kLdsRow = kBK + 16;  // padded LDS row stride (bytes)
-constexpr int kGemmThreads = 256;
 
 enum class Out { Y, ACC, ATOMIC };
 
 // ---- prefill W8A8 GEMM (m > 64) ---------------------------------------------------------
-// 128 x 128 output tile per workgroup, 4 waves of 64 x 64 (4 x 4 MFMA
-// 16x16x64 tiles). K advances in 64-byte slabs staged through a double-buffered
-// LDS (rows padded to 80 bytes: each 8-lane ds_read_b128 phase hits 32 distinct
-// banks). Global loads run three slabs ahead in a register ring, so about three
-// slabs of MFMA work cover the L2/MALL latency; one barrier per slab.
+// A workgroup of WM x WN waves owns a (WM*64) x (WN*64) output tile; each wave
+// owns 64 x 64 (4 x 4 MFMA 16x16x64 fragments). K advances in 64-byte slabs
+// that the buffer unit writes straight into a D-deep LDS ring (buffer_load ...
+// lds: no VGPR staging, no ds_write); each lane picks the global chunk that
+// belongs at its LDS slot, which applies an XOR swizzle (16-byte chunk c of
+// row r lands in slot c ^ ((r >> 1) & 3); the MFMA fragment reads are then
+// bank-conflict free). One barrier per slab; the MFMAs of slab kt run while
+// slab kt + D - 1 is requested and the fragments of slab kt + 1 are read.
 // The MFMA computes D = W_tile * xq_tile^T (weights as the A operand), so a lane
-// ends with four consecutive output columns of one row: the epilogue issues
-// 8-byte fp16 stores (or 16-byte int32 / fp32 stores).
+// ends with four consecutive output columns of one row. fp16 outputs are staged
+// through LDS and written as whole 16-byte row chunks.
 // Workgroup ids are remapped so each XCD (ids are dealt round-robin over the 8
 // XCDs) covers a contiguous band of column tiles, walked row-tile fastest: the
 // XCD's band of the weight stays in its L2 while the row tiles stream past.
-constexpr int kPBM = 128, kPBN = 128, kPRow = kBK, kPRing = 3;
+// The LDS-DMA loads are issued from inline asm, so the compiler does not track
+// them: the kernel waits for them itself (s_waitcnt vmcnt) before each barrier
+// and before the epilogue.
+constexpr int kPRow = kBK;
 
 // Byte offset of 16-byte chunk c of row r in a swizzled 64-byte-row LDS tile.
 __device__ __forceinline__ int swz(int r, int c) { return r * kPRow + ((c ^ ((r >> 1) & 3)) << 4); }
 
-template <Out OUT, typename YT>
-__global__ __launch_bounds__(256) void gemm_w8a8_prefill_kernel(
+template <int WM, int WN, int D>
+struct PrefillShape {
+    static constexpr int kWaves = WM * WN, kBM = WM * 64, kBN = WN * 64;
+    static constexpr int kXB = kBM / 16, kWB = kBN / 16;   // 1 KB blocks (16 rows x 64 B) per slab
+    static constexpr int kQ = (kXB + kWB) / kWaves;        // LDS-DMA instructions per wave per slab
+    static constexpr int kSlab = (kBM + kBN) * kPRow;      // bytes per slab
+    static constexpr int kOutStride = kBN * 2 + 16;        // staged fp16 row stride (bytes)
+    static constexpr size_t kLds = std::max<size_t>(size_t(D) * kSlab, size_t(kBM) * kOutStride);
+    static_assert((kXB + kWB) % kWaves == 0, "whole LDS-DMA blocks per wave");
+};
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int WM, int WN, int D, Out OUT, typename YT>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_w8a8_prefill_kernel(
     const int8_t* __restrict__ xq, const float* __restrict__ as, const int8_t* __restrict__ wq,
     const float* __restrict__ ws, const float* __restrict__ bias, YT* __restrict__ y,
     int32_t* __restrict__ acc_out, int m, int n, int k, int tiles_m, int tiles_n) {
-    __shared__ __attribute__((aligned(16))) int8_t sx[2][kPBM * kPRow];
-    __shared__ __attribute__((aligned(16))) int8_t sw[2][kPBN * kPRow];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    using S = PrefillShape<WM, WN, D>;
+    constexpr int Q = S::kQ, XB = S::kXB, BM = S::kBM, BN = S::kBN;
+    extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
     const int total = tiles_m * tiles_n;
     int lin = blockIdx.x;
     if (total % 8 == 0) lin = (blockIdx.x % 8) * (total / 8) + blockIdx.x / 8;
     const int mt = lin % tiles_m, nt = lin / tiles_m;
-    const int m0 = mt * kPBM, n0 = nt * kPBN;
+    const int m0 = mt * BM, n0 = nt * BN;
 
-    // Each slab: 128 rows x 64 bytes per operand = 512 16-byte chunks, 2 per
-    // thread per operand; chunk c -> row c / 4, 16-byte column c % 4. The loads
-    // are raw buffer loads: the per-thread byte offset is fixed, the slab offset
-    // k0 rides in the scalar offset, and rows past m / n get an offset beyond the
-    // buffer's size so the hardware returns zeros (no per-load predicates or
-    // 64-bit address arithmetic in the loop).
+    // Raw buffers: rows past m / n and slabs past the end get an offset beyond
+    // the buffer, which reads zeros without touching memory.
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(xq), 0, m * k, 0x00020000);
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(wq), 0, n * k, 0x00020000);
-    int xoff[2], woff[2], soff[2];
+    constexpr int kOob = 0x7FFFFFF0;
+    // Wave w issues blocks w*Q .. w*Q+Q-1 of each slab: blocks [0, XB) are the
+    // activation tile, the rest the weight tile. Lane i of a block writes LDS
+    // bytes 16i..16i+15 of it (row i/4, slot i%4) and so loads the chunk that
+    // the swizzle puts in that slot.
+    int voff[Q];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = tid + i * 256, r = c >> 2, kc = (c & 3) * 16;
-        xoff[i] = m0 + r < m ? (m0 + r) * k + kc : 0x7FFFFFF0;
-        woff[i] = n0 + r < n ? (n0 + r) * k + kc : 0x7FFFFFF0;
-        soff[i] = swz(r, c & 3);
+    for (int q = 0; q < Q; ++q) {
+        const int blk = wave * Q + q;
+        const bool isx = blk < XB;
+        const int r = (isx ? blk : blk - XB) * 16 + (lane >> 2);
+        const int c = (lane & 3) ^ ((r >> 1) & 3);
+        const int grow = (isx ? m0 : n0) + r;
+        voff[q] = grow < (isx ? m : n) ? grow * k + c * 16 : kOob;
     }
-    v4i rx[kPRing][2], rw[kPRing][2];
     const int nk = k / kBK;  // the prefill contract has k % kBK == 0
-    // Slab sl; slabs past the end (the ring's tail prefetch) read as zeros
-    // without touching memory.
-    auto load = [&](int sl, v4i (&dx)[2], v4i (&dw)[2]) {
-        const bool in = sl < nk;
-        const int k0 = (in ? sl : 0) * kBK;
+    const unsigned lds_base = static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds));
+    auto issue = [&](int sl) {
+        const unsigned slot = static_cast<unsigned>(sl % D) * S::kSlab;
+        const int soff = sl < nk ? sl * kBK : kOob;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            dx[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xrs, in ? xoff[i] : 0x7FFFFFF0, k0, 0));
-            dw[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wrs, in ? woff[i] : 0x7FFFFFF0, k0, 0));
+        for (int q = 0; q < Q; ++q) {
+            const int blk = wave * Q + q;
+            const unsigned dst = lds_base + slot + blk * 1024;
+            if (blk < XB)
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                             ::"s"(dst), "v"(voff[q]), "s"(xrs), "s"(soff) : "memory");
+            else
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                             ::"s"(dst), "v"(voff[q]), "s"(wrs), "s"(soff) : "memory");
         }
     };
-    auto store = [&](int buf, const v4i (&dx)[2], const v4i (&dw)[2]) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            *reinterpret_cast<v4i*>(&sx[buf][soff[i]]) = dx[i];
-            *reinterpret_cast<v4i*>(&sw[buf][soff[i]]) = dw[i];
-        }
-    };
+    // Own LDS-DMA of the oldest in-flight slab landed (D - 2 younger slabs may fly).
+    auto wait_slab = [&]() { wait_vmcnt<Q * (D - 2)>(); };
 
-    v4i acc[4][4];  // [n tile][m tile]
+    v4i acc[4][4];  // [n fragment][m fragment]
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
-
-    const int fr = lane & 15;
-    int fwo[4], fxo[4];
+    const int fr = lane & 15, fc = lane >> 4;
+    int fxo[4], fwo[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        fwo[i] = swz(wn * 64 + i * 16 + fr, lane >> 4);
-        fxo[i] = swz(wm * 64 + i * 16 + fr, lane >> 4);
-    }
-    auto compute = [&](int buf) {
-        v4i fw[4], fx[4];
+    for (int j = 0; j < 4; ++j) fxo[j] = swz(wm * 64 + j * 16 + fr, fc);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) fw[i] = *reinterpret_cast<const v4i*>(&sw[buf][fwo[i]]);
+    for (int i = 0; i < 4; ++i) fwo[i] = BM * kPRow + swz(wn * 64 + i * 16 + fr, fc);
+    v4i fw[2][4], fx[2][4];
+    auto read = [&](int sl, v4i (&w)[4], v4i (&x)[4]) {
+        const int8_t* base = lds + (sl % D) * S::kSlab;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) fx[j] = *reinterpret_cast<const v4i*>(&sx[buf][fxo[j]]);
+        for (int i = 0; i < 4; ++i) w[i] = *reinterpret_cast<const v4i*>(base + fwo[i]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = *reinterpret_cast<const v4i*>(base + fxo[j]);
+    };
+    auto mma = [&](const v4i (&w)[4], const v4i (&x)[4]) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fw[i], fx[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[i], x[j], acc[i][j], 0, 0, 0);
     };
 
-    // Every step is unconditional so the compiler's in-order vmcnt bookkeeping
-    // sees the same three slabs in flight on every iteration (a conditional load
-    // makes it wait for all of them).
-    load(0, rx[0], rw[0]);
-    store(0, rx[0], rw[0]);
 #pragma unroll
-    for (int p = 0; p < kPRing; ++p) load(p + 1, rx[p], rw[p]);
-    __syncthreads();
-    // Slab kt is in LDS buffer kt & 1; slab kt + 1 sits in ring slot kt % 3.
-    auto step = [&](int kt, auto phase) {
-        constexpr int P = decltype(phase)::value;
-        compute(kt & 1);
-        store((kt + 1) & 1, rx[P], rw[P]);
-        load(kt + 1 + kPRing, rx[P], rw[P]);
-        __syncthreads();
+    for (int sl = 0; sl < D - 1; ++sl) issue(sl);
+    wait_slab();
+    __builtin_amdgcn_s_barrier();
+    read(0, fw[0], fx[0]);
+    // The slot refilled at iteration kt held slab kt - 1, whose fragments every
+    // wave read before the previous iteration's barrier.
+    auto iter = [&](int kt, auto par) {
+        constexpr int P = decltype(par)::value;
+        mma(fw[P], fx[P]);
+        issue(kt + D - 1);
+        wait_slab();
+        __builtin_amdgcn_s_barrier();
+        read(kt + 1, fw[P ^ 1], fx[P ^ 1]);
     };
     int kt = 0;
-    for (; kt + kPRing <= nk; kt += kPRing) {
-        step(kt, std::integral_constant<int, 0>{});
-        step(kt + 1, std::integral_constant<int, 1>{});
-        step(kt + 2, std::integral_constant<int, 2>{});
+    for (; kt + 2 <= nk; kt += 2) {
+        iter(kt, std::integral_constant<int, 0>{});
+        iter(kt + 1, std::integral_constant<int, 1>{});
     }
-    if (kt < nk) step(kt, std::integral_constant<int, 0>{});
-    if (kt + 1 < nk) step(kt + 1, std::integral_constant<int, 1>{});
+    if (kt < nk) iter(kt, std::integral_constant<int, 0>{});
+    wait_vmcnt<0>();  // the ring's tail requests (zero reads) have retired
 
-    // Lane l holds, for tile (i, j), output row m0 + wm*64 + j*16 + (l % 16) and
-    // columns n0 + wn*64 + i*16 + 4*(l / 16) + (0..3).
-    const int row_in = fr, col_in = (lane >> 4) * 4;
+    // Lane l holds, for fragment (i, j), output row m0 + wm*64 + j*16 + (l % 16)
+    // and columns n0 + wn*64 + i*16 + 4*(l / 16) + (0..3).
+    const int row_in = fr, col_in = fc * 4;
+    if constexpr (OUT == Out::Y && sizeof(YT) == 2) {
+        if ((n & 7) == 0) {
+            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+            __builtin_amdgcn_s_barrier();  // every wave is done reading the ring
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int rl = wm * 64 + j * 16 + row_in;
+                const float a_s = m0 + rl < m ? as[m0 + rl] : 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int cl = wn * 64 + i * 16 + col_in, col = n0 + cl;
+                    const bool cin = col < n;  // n % 8 == 0: a 4-column group is all in or all out
+                    const f4 w4 = cin ? *reinterpret_cast<const f4*>(ws + col) : f4{0, 0, 0, 0};
+                    const f4 b4 = cin && bias ? *reinterpret_cast<const f4*>(bias + col) : f4{0, 0, 0, 0};
+                    h4 r;
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) r[v] = from_f32<_Float16>(w8a8_epilogue(acc[i][j][v], a_s, w4[v], b4[v]));
+                    *reinterpret_cast<h4*>(lds + rl * S::kOutStride + cl * 2) = r;
+                }
+            }
+            __syncthreads();
+            constexpr int CPR = BN / 8;  // 16-byte chunks per tile row
+            for (int c = tid; c < BM * CPR; c += S::kWaves * 64) {
+                const int rl = c / CPR, cc = c % CPR;
+                const int row = m0 + rl, col = n0 + cc * 8;
+                if (row < m && col < n)
+                    *reinterpret_cast<v4i*>(y + static_cast<size_t>(row) * n + col) =
+                        *reinterpret_cast<const v4i*>(lds + rl * S::kOutStride + cc * 16);
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int row = m0 + wm * 64 + j * 16 + row_in;
@@ -419,21 +474,37 @@ nq_status gemm_skinny(const int8_t* xq, const float* as, const int8_t* wq, const
     return NQ_OK;
 }
 
-// Big-m launch.
+// Big-m launch: 256 x 128 tiles (8 waves, 3-slab ring) when they give at least
+// two tiles per CU, else 128 x 128 tiles (4 waves, 4-slab ring) for more
+// workgroups on mid-sized shapes.
+template <int WM, int WN, int D, Out OUT, typename YT>
+nq_status launch_prefill(const int8_t* xq, const float* as, const int8_t* wq, const float* ws, const float* bias,
+                         YT* y, int32_t* acc_out, int m, int n, int k, hipStream_t s) {
+    using S = PrefillShape<WM, WN, D>;
+    auto* fn = gemm_w8a8_prefill_kernel<WM, WN, D, OUT, YT>;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       static_cast<int>(S::kLds));
+    if (attr != hipSuccess) return fail(NQ_HIP_ERROR, "gemm_w8a8_prefill: LDS attribute: %s", hipGetErrorString(attr));
+    const int tm = (m + S::kBM - 1) / S::kBM, tn = (n + S::kBN - 1) / S::kBN;
+    fn<<<static_cast<unsigned>(tm * tn), S::kWaves * 64, S::kLds, s>>>(xq, as, wq, ws, bias, y, acc_out, m, n, k, tm, tn);
+    return launch_status("gemm_w8a8_prefill_kernel");
+}
+
 nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const float* ws,
                    const float* bias, void* y, nq_dtype ydt, int32_t* acc_out, int64_t m, int64_t n,
                    int64_t k, hipStream_t s) {
-    const int tm = static_cast<int>((m + kPBM - 1) / kPBM), tn = static_cast<int>((n + kPBN - 1) / kPBN);
-    const unsigned grid = static_cast<unsigned>(tm) * static_cast<unsigned>(tn);
-    const size_t lds = 0;
     const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
-    if (acc_out)
-        gemm_w8a8_prefill_kernel<Out::ACC, float><<<grid, 256, lds, s>>>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, tm, tn);
-    else if (ydt == NQ_F32)
-        gemm_w8a8_prefill_kernel<Out::Y, float><<<grid, 256, lds, s>>>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi, ni, ki, tm, tn);
-    else
-        gemm_w8a8_prefill_kernel<Out::Y, _Float16><<<grid, 256, lds, s>>>(xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr, mi, ni, ki, tm, tn);
-    return launch_status("gemm_w8a8_prefill_kernel");
+    const bool big = ((m + 255) / 256) * ((n + 127) / 128) >= 512;
+    auto go = [&](auto wmtag, auto dtag) {
+        constexpr int WM = decltype(wmtag)::value, D = decltype(dtag)::value;
+        if (acc_out) return launch_prefill<WM, 2, D, Out::ACC, float>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, s);
+        if (ydt == NQ_F32)
+            return launch_prefill<WM, 2, D, Out::Y, float>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi, ni, ki, s);
+        return launch_prefill<WM, 2, D, Out::Y, _Float16>(xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr, mi, ni, ki, s);
+    };
+    return big ? go(std::integral_constant<int, 4>{}, std::integral_constant<int, 3>{})
+               : go(std::integral_constant<int, 2>{}, std::integral_constant<int, 4>{});
 }
 
 nq_status check_w8a8(int64_t m, int64_t n, int64_t k, int path, const char* who) {
