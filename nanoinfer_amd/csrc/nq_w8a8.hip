@@ -34,7 +34,7 @@ namespace {
 constexpr int kBK = 64;         // K bytes per MFMA step / LDS slab
 constexpr int kLdsRow = kBK + 16;  // padded LDS row stride (bytes)
 
-enum class Out { Y, ACC, ATOMIC };
+enum class Out { Y, ACC, PARTIAL };
 
 // ---- prefill W8A8 GEMM (m > 64) ---------------------------------------------------------
 // A workgroup of WM x WN waves owns a (WM*64) x (WN*64) output tile; each wave
@@ -80,7 +80,7 @@ template <int WM, int WN, int D, Out OUT, typename YT>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_w8a8_prefill_kernel(
     const int8_t* __restrict__ xq, const float* __restrict__ as, const int8_t* __restrict__ wq,
     const float* __restrict__ ws, const float* __restrict__ bias, YT* __restrict__ y,
-    int32_t* __restrict__ acc_out, int m, int n, int k, int tiles_m, int tiles_n) {
+    int32_t* __restrict__ acc_out, int m, int n, int k, int tiles_m, int tiles_n, int k_slabs) {
     using S = PrefillShape<WM, WN, D>;
     constexpr int Q = S::kQ, XB = S::kXB, BM = S::kBM, BN = S::kBN;
     extern __shared__ __attribute__((aligned(16))) int8_t lds[];
@@ -112,11 +112,13 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_w8a8_prefill_kernel(
         const int grow = (isx ? m0 : n0) + r;
         voff[q] = grow < (isx ? m : n) ? grow * k + c * 16 : kOob;
     }
-    const int nk = k / kBK;  // the prefill contract has k % kBK == 0
+    // This workgroup's K range: slabs [s0, s1) (the whole K unless the launch
+    // splits K over gridDim.y; the prefill contract has k % kBK == 0).
+    const int s0 = blockIdx.y * k_slabs, s1 = min(k / kBK, s0 + k_slabs);
     const unsigned lds_base = static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds));
-    auto issue = [&](int sl) {
+    auto issue = [&](int sl) {  // sl counts from s0
         const unsigned slot = static_cast<unsigned>(sl % D) * S::kSlab;
-        const int soff = sl < nk ? sl * kBK : kOob;
+        const int soff = s0 + sl < s1 ? (s0 + sl) * kBK : kOob;
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
             const int blk = wave * Q + q;
@@ -173,6 +175,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_w8a8_prefill_kernel(
         __builtin_amdgcn_s_barrier();
         read(kt + 1, fw[P ^ 1], fx[P ^ 1]);
     };
+    const int nk = s1 - s0;
     int kt = 0;
     for (; kt + 2 <= nk; kt += 2) {
         iter(kt, std::integral_constant<int, 0>{});
@@ -184,6 +187,29 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_w8a8_prefill_kernel(
     // Lane l holds, for fragment (i, j), output row m0 + wm*64 + j*16 + (l % 16)
     // and columns n0 + wn*64 + i*16 + 4*(l / 16) + (0..3).
     const int row_in = fr, col_in = fc * 4;
+    if constexpr (OUT == Out::PARTIAL) {
+        // Split K: this range's int32 partial tile goes to plane blockIdx.y of
+        // the workspace; a reduction launch sums the planes in a fixed order.
+        int32_t* plane = acc_out + static_cast<size_t>(blockIdx.y) * m * n;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = m0 + wm * 64 + j * 16 + row_in;
+            if (row >= m) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int col = n0 + wn * 64 + i * 16 + col_in;
+                const size_t o = static_cast<size_t>(row) * n + col;
+                if (col + 3 < n && (n & 3) == 0) {
+                    *reinterpret_cast<v4i*>(plane + o) = acc[i][j];
+                } else {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        if (col + v < n) plane[o + v] = acc[i][j][v];
+                }
+            }
+        }
+        return;
+    }
     if constexpr (OUT == Out::Y && sizeof(YT) == 2) {
         if ((n & 7) == 0) {
             typedef _Float16 h4 __attribute__((ext_vector_type(4)));
@@ -386,6 +412,25 @@ __global__ void w8a8_finalize_kernel(const int32_t* __restrict__ acc, const floa
     y[i] = from_f32<YT>(w8a8_epilogue(acc[i], as[row], ws[col], b));
 }
 
+// Sums the split-K partial planes [splits][m][n] in plane order (int32: exact)
+// into the int32 accumulators (TO_ACC) or through the epilogue into y.
+template <typename YT, bool TO_ACC>
+__global__ void w8a8_reduce_kernel(const int32_t* __restrict__ parts, int splits, const float* __restrict__ as,
+                                   const float* __restrict__ ws, const float* __restrict__ bias,
+                                   YT* __restrict__ y, int32_t* __restrict__ acc, int m, int n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t mn = static_cast<int64_t>(m) * n;
+    if (i >= mn) return;
+    int sum = 0;
+    for (int sp = 0; sp < splits; ++sp) sum += parts[sp * mn + i];
+    if constexpr (TO_ACC) {
+        acc[i] = sum;
+    } else {
+        const int row = static_cast<int>(i / n), col = static_cast<int>(i % n);
+        y[i] = from_f32<YT>(w8a8_epilogue(sum, as[row], ws[col], bias ? bias[col] : 0.0f));
+    }
+}
+
 // ---- plans --------------------------------------------------------------------------
 constexpr int kTargetBlocks = 1024;  // ~4 workgroups per CU on 256 CUs
 constexpr int kSkinnyMaxM = 64;
@@ -412,13 +457,7 @@ SkinnyPlan plan_skinny(int64_t m, int64_t n, int64_t k) {
     return p;
 }
 
-size_t gemm_ws_bytes(int64_t m, int64_t n, int64_t k) {
-    if (m <= 0 || n <= 0 || k <= 0) return 0;
-    if (m <= kSkinnyMaxM) {
-        return plan_skinny(m, n, k).acc_bytes;
-    }
-    return 0;
-}
+size_t gemm_ws_bytes(int64_t m, int64_t n, int64_t k);
 
 // Skinny launch. zeroed: a split plan's accumulator was already cleared by
 // this call's activation-quant kernel; else it is cleared here.
@@ -474,12 +513,37 @@ nq_status gemm_skinny(const int8_t* xq, const float* as, const int8_t* wq, const
     return NQ_OK;
 }
 
-// Big-m launch: 256 x 128 tiles (8 waves, 3-slab ring) when they give at least
-// two tiles per CU, else 128 x 128 tiles (4 waves, 4-slab ring) for more
-// workgroups on mid-sized shapes.
+// Big-m plan: 256 x 128 tiles (8 waves, 3-slab ring) when they give at least
+// two tiles per CU, else 128 x 128 tiles (4 waves, 4-slab ring). A lone
+// workgroup pulls only ~30 GB/s from memory, so when there are fewer than 256
+// tiles K is split over workgroups (at least 8 slabs each) until there are
+// about 256: each range stores its int32 partial tile into its own workspace
+// plane and a reduction launch sums the planes and applies the epilogue
+// (device-scope atomics into one plane measured several times slower).
+struct PrefillPlan {
+    bool big;
+    int tiles, splits, k_slabs;
+    size_t acc_bytes;
+};
+PrefillPlan plan_prefill(int64_t m, int64_t n, int64_t k) {
+    PrefillPlan p{};
+    const int64_t big_tiles = ((m + 255) / 256) * ((n + 127) / 128);
+    p.big = big_tiles >= 512;
+    p.tiles = static_cast<int>(p.big ? big_tiles : ((m + 127) / 128) * ((n + 127) / 128));
+    const int nk = std::max(1, static_cast<int>(k / kBK));  // also sized for shapes outside the contract
+    int splits = 1;
+    if (p.tiles < 256) splits = std::max(1, std::min<int>(static_cast<int>((256 + p.tiles - 1) / p.tiles), nk / 8));
+    // at most 64 MiB of partial planes
+    splits = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(splits, (int64_t(64) << 20) / std::max<int64_t>(1, m * n * 4))));
+    p.k_slabs = (nk + splits - 1) / splits;
+    p.splits = (nk + p.k_slabs - 1) / p.k_slabs;
+    if (p.splits > 1) p.acc_bytes = round_up(static_cast<size_t>(p.splits) * static_cast<size_t>(m * n) * 4, 256);
+    return p;
+}
+
 template <int WM, int WN, int D, Out OUT, typename YT>
 nq_status launch_prefill(const int8_t* xq, const float* as, const int8_t* wq, const float* ws, const float* bias,
-                         YT* y, int32_t* acc_out, int m, int n, int k, hipStream_t s) {
+                         YT* y, int32_t* acc_out, int m, int n, int k, int splits, int k_slabs, hipStream_t s) {
     using S = PrefillShape<WM, WN, D>;
     auto* fn = gemm_w8a8_prefill_kernel<WM, WN, D, OUT, YT>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -487,24 +551,57 @@ nq_status launch_prefill(const int8_t* xq, const float* as, const int8_t* wq, co
                                                        static_cast<int>(S::kLds));
     if (attr != hipSuccess) return fail(NQ_HIP_ERROR, "gemm_w8a8_prefill: LDS attribute: %s", hipGetErrorString(attr));
     const int tm = (m + S::kBM - 1) / S::kBM, tn = (n + S::kBN - 1) / S::kBN;
-    fn<<<static_cast<unsigned>(tm * tn), S::kWaves * 64, S::kLds, s>>>(xq, as, wq, ws, bias, y, acc_out, m, n, k, tm, tn);
+    const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(splits));
+    fn<<<grid, S::kWaves * 64, S::kLds, s>>>(xq, as, wq, ws, bias, y, acc_out, m, n, k, tm, tn, k_slabs);
     return launch_status("gemm_w8a8_prefill_kernel");
 }
 
 nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const float* ws,
                    const float* bias, void* y, nq_dtype ydt, int32_t* acc_out, int64_t m, int64_t n,
-                   int64_t k, hipStream_t s) {
+                   int64_t k, void* workspace, size_t ws_bytes, hipStream_t s) {
     const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
-    const bool big = ((m + 255) / 256) * ((n + 127) / 128) >= 512;
-    auto go = [&](auto wmtag, auto dtag) {
+    const PrefillPlan p = plan_prefill(m, n, k);
+    int32_t* parts = nullptr;
+    if (p.splits > 1) {
+        NQ_REQUIRE(workspace && ws_bytes >= p.acc_bytes, NQ_BAD_ARG,
+                   "w8a8 gemm: workspace of %zu bytes required, %zu given", p.acc_bytes, ws_bytes);
+        NQ_REQUIRE(aligned(workspace, 256), NQ_BAD_ALIGN, "w8a8 gemm: workspace must be 256-byte aligned");
+        parts = static_cast<int32_t*>(workspace);
+    }
+    auto go = [&](auto wmtag, auto dtag) -> nq_status {
         constexpr int WM = decltype(wmtag)::value, D = decltype(dtag)::value;
-        if (acc_out) return launch_prefill<WM, 2, D, Out::ACC, float>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, s);
+        if (p.splits > 1)
+            return launch_prefill<WM, 2, D, Out::PARTIAL, float>(xq, as, wq, ws, bias, nullptr, parts, mi, ni, ki,
+                                                                p.splits, p.k_slabs, s);
+        if (acc_out)
+            return launch_prefill<WM, 2, D, Out::ACC, float>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, 1,
+                                                            p.k_slabs, s);
         if (ydt == NQ_F32)
-            return launch_prefill<WM, 2, D, Out::Y, float>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi, ni, ki, s);
-        return launch_prefill<WM, 2, D, Out::Y, _Float16>(xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr, mi, ni, ki, s);
+            return launch_prefill<WM, 2, D, Out::Y, float>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi,
+                                                          ni, ki, 1, p.k_slabs, s);
+        return launch_prefill<WM, 2, D, Out::Y, _Float16>(xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr,
+                                                         mi, ni, ki, 1, p.k_slabs, s);
     };
-    return big ? go(std::integral_constant<int, 4>{}, std::integral_constant<int, 3>{})
-               : go(std::integral_constant<int, 2>{}, std::integral_constant<int, 4>{});
+    const nq_status st = p.big ? go(std::integral_constant<int, 4>{}, std::integral_constant<int, 3>{})
+                               : go(std::integral_constant<int, 2>{}, std::integral_constant<int, 4>{});
+    if (st != NQ_OK || p.splits == 1) return st;
+    const unsigned g = static_cast<unsigned>((m * n + 255) / 256);
+    if (acc_out)
+        w8a8_reduce_kernel<float, true><<<g, 256, 0, s>>>(parts, p.splits, as, ws, bias, nullptr, acc_out, mi, ni);
+    else if (ydt == NQ_F32)
+        w8a8_reduce_kernel<float, false><<<g, 256, 0, s>>>(parts, p.splits, as, ws, bias, static_cast<float*>(y), nullptr, mi, ni);
+    else
+        w8a8_reduce_kernel<_Float16, false><<<g, 256, 0, s>>>(parts, p.splits, as, ws, bias, static_cast<_Float16*>(y), nullptr, mi, ni);
+    return launch_status("w8a8_reduce_kernel");
+}
+
+// Workspace of the MFMA GEMM for this shape: a split plan's int32
+// accumulator (skinny plans for m <= 64, the prefill plan above, and the
+// skinny 64-row blocks that shapes outside the prefill contract run).
+size_t gemm_ws_bytes(int64_t m, int64_t n, int64_t k) {
+    if (m <= 0 || n <= 0 || k <= 0) return 0;
+    if (m <= kSkinnyMaxM) return plan_skinny(m, n, k).acc_bytes;
+    return std::max(plan_prefill(m, n, k).acc_bytes, plan_skinny(kSkinnyMaxM, n, k).acc_bytes);
 }
 
 nq_status check_w8a8(int64_t m, int64_t n, int64_t k, int path, const char* who) {
@@ -555,7 +652,8 @@ nq_status run_gemm(const int8_t* xq, const float* as, const int8_t* wq, const fl
     if (p == NQ_PATH_MFMA) {
         if (m <= kSkinnyMaxM)
             return gemm_skinny(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, workspace, ws_bytes, zeroed, s);
-        if (prefill_ok(m, n, k)) return gemm_big(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, s);
+        if (prefill_ok(m, n, k))
+            return gemm_big(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, workspace, ws_bytes, s);
         // Shapes outside the prefill kernel's contract run the skinny kernel on
         // 64-row blocks (each block re-streams the weight).
         for (int64_t r0 = 0; r0 < m; r0 += kSkinnyMaxM) {
@@ -661,10 +759,11 @@ extern "C" nq_status nq_linear_w8a8(const void* x, nq_dtype x_dtype, const int8_
     char* rest = reinterpret_cast<char*>(as) + round_up(static_cast<size_t>(m) * 4, 256);
     const size_t rest_bytes = workspace_bytes - static_cast<size_t>(rest - base);
     // A split skinny plan needs its accumulator cleared: the activation-quant
-    // launch does it with extra workgroups.
+    // launch does it with extra workgroups. The conditions mirror run_gemm's
+    // choice of kernel.
     void* zero = nullptr;
     size_t zero_bytes = 0;
-    if (p == NQ_PATH_MFMA && m <= kSkinnyMaxM && mfma_ok(xq, wq, k)) {
+    if (p == NQ_PATH_MFMA && m <= kSkinnyMaxM && mfma_ok(xq, wq, k) && skinny_ok(m, n, k)) {
         const SkinnyPlan sp = plan_skinny(m, n, k);
         if (sp.splits > 1) {
             zero = rest;

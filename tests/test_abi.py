@@ -96,3 +96,17 @@ def test_check_maps_to_value_error():
         L.check(L.NQ_BAD_SHAPE)
     with pytest.raises(RuntimeError):
         L.check(L.NQ_HIP_ERROR)
+
+
+def test_workspace_sizes_all_shapes():
+    """Workspace queries are defined for every shape, including K shorter than
+    one MFMA slab (a division by zero once hid there) and m on either side of
+    the skinny / prefill boundary."""
+    from nanoinfer_amd import _lib
+    lib = _lib.load()
+    for m in (1, 3, 8, 64, 65, 130, 512, 2048):
+        for n in (1, 65, 256, 8960):
+            for k in (0, 1, 16, 48, 64, 1536, 8960):
+                g = lib.nq_gemm_w8a8_workspace_size(m, n, k)
+                lw = lib.nq_linear_w8a8_workspace_size(m, n, k)
+                assert g % 256 == 0 and lw >= g

@@ -235,3 +235,32 @@ def test_w8a8_workspace_reuse_and_gemm_entry(dev, nq, orc):
         xq, a_s = nq.act_quant(xd)
         y2 = nq.gemm_w8a8(xq, a_s, t, out_dtype=torch.float32)
         assert same_bits(host(y2), host(y))
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 256, 1536), (512, 1536, 1536), (512, 1536, 8960), (300, 1000, 960),
+                                   (2048, 8960, 1536)])
+def test_w8a8_prefill_plans_exact(dev, nq, orc, m, n, k):
+    """Every prefill plan (256x128 / 128x128 tiles, split K with atomic int32
+    partials) gives the GEMV path's accumulators bit for bit, and the linear's
+    fp16 output equals the GEMM entry's and the oracle's within tolerance."""
+    rng = np.random.default_rng(m + n + k)
+    xq = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    wq = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    xd, wd = to_dev(xq, dev), to_dev(wq, dev)
+    acc_m = nq.w8a8_acc_i32(xd, wd, nq._lib.NQ_PATH_MFMA)
+    acc_g = nq.w8a8_acc_i32(xd, wd, nq._lib.NQ_PATH_GEMV)
+    assert torch.equal(acc_m, acc_g)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    b = rng.normal(0, 0.1, n).astype(np.float32)
+    t = nq.quantize_q8(to_dev(w, dev))
+    xdv = to_dev(x, dev).half()
+    for _ in range(2):                                   # the split accumulator re-arms between calls
+        y = nq.linear_w8a8(xdv, t, to_dev(b, dev))
+        xq2, a_s = nq.act_quant(xdv)
+        y2 = nq.gemm_w8a8(xq2, a_s, t, to_dev(b, dev), out_dtype=torch.float16)
+        assert torch.equal(y, y2)
+    rows = rng.choice(m, 16, replace=False)
+    q, s = orc.quantize_q8(w)
+    ref = orc.linear_w8a8(host(xdv.float())[rows], q, s, b)
+    assert_close_rms(host(y.float())[rows], ref, f"w8a8 prefill {m}x{n}x{k}", fp16_out=True)
