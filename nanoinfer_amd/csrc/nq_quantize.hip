@@ -105,20 +105,11 @@ __global__ void quantize_q4g_odd_kernel(const float* __restrict__ w, uint8_t* __
 // ---- activation quant (vectorized) ------------------------------
 // One workgroup per row, 8 elements per 16-byte step held in registers between
 // the absmax pass and the quantize pass (x is read once).
-// Workgroups past the m rows clear `zero` (a 256-byte aligned scratch region of
-// the GEMM that follows) with 16-byte stores.
 template <typename XT, int CPT, int NT>
 __global__ __launch_bounds__(NT) void act_quant_vec_kernel(const XT* __restrict__ x, int8_t* __restrict__ xq,
-                                                           float* __restrict__ a_scale, int m, int k,
-                                                           v4i* __restrict__ zero, int64_t zero_vecs) {
+                                                           float* __restrict__ a_scale, int m, int k) {
     __shared__ float red[NT / 64];
     const int tid = threadIdx.x;
-    if (static_cast<int>(blockIdx.x) >= m) {
-        for (int64_t i = static_cast<int64_t>(blockIdx.x - m) * NT + tid; i < zero_vecs;
-             i += static_cast<int64_t>(gridDim.x - m) * NT)
-            zero[i] = v4i{0, 0, 0, 0};
-        return;
-    }
     typedef XT v8 __attribute__((ext_vector_type(8)));
     const int row = blockIdx.x, steps = k >> 3;
     const v8* xr = reinterpret_cast<const v8*>(x + static_cast<size_t>(row) * k);
@@ -161,12 +152,6 @@ __global__ __launch_bounds__(NT) void act_quant_vec_kernel(const XT* __restrict_
     }
 }
 
-__global__ void zero_vec_kernel(v4i* __restrict__ p, int64_t n) {
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
-        p[i] = v4i{0, 0, 0, 0};
-}
-
 nq_status check_rows(int64_t rows, int64_t cols, const char* who) {
     NQ_REQUIRE(rows >= 0 && cols >= 0, NQ_BAD_SHAPE, "%s: negative shape [%lld, %lld]", who,
                (long long)rows, (long long)cols);
@@ -180,29 +165,26 @@ nq_status check_rows(int64_t rows, int64_t cols, const char* who) {
 
 // Activation quant: the vectorized kernel when k fits it, else the scalar row kernel.
 nq_status act_quant(const void* x, nq_dtype xdt, int64_t m, int64_t k, int8_t* xq, float* as,
-                    void* zero, size_t zero_bytes, hipStream_t s) {
+                    hipStream_t s) {
     // One workgroup per row: 256 threads up to 2048 elements, else 1024 threads
     // with up to 8 vectors of 8 elements each.
     const bool vec = k > 0 && k % 8 == 0 && k <= 8 * 1024 * 8 && aligned(x, 16) && aligned(xq, 8);
-    const int64_t zero_vecs = static_cast<int64_t>(zero_bytes / 16);
     if (vec) {
-        const int64_t zero_blocks = std::min<int64_t>(256, (zero_vecs + 255) / 256);
-        const unsigned grid = static_cast<unsigned>(m + zero_blocks);
-        v4i* zp = static_cast<v4i*>(zero);
+        const unsigned grid = static_cast<unsigned>(m);
         const int64_t steps = k / 8;
         const int mi = static_cast<int>(m), ki = static_cast<int>(k);
         auto go = [&](auto* xp) {
             using XT = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
             if (steps <= 256) {
-                act_quant_vec_kernel<XT, 1, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs);
+                act_quant_vec_kernel<XT, 1, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki);
                 return;
             }
             switch ((steps + 1023) / 1024) {
-                case 1: act_quant_vec_kernel<XT, 1, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs); break;
-                case 2: act_quant_vec_kernel<XT, 2, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs); break;
-                case 3: act_quant_vec_kernel<XT, 3, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs); break;
-                case 4: act_quant_vec_kernel<XT, 4, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs); break;
-                default: act_quant_vec_kernel<XT, 8, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki, zp, zero_vecs); break;
+                case 1: act_quant_vec_kernel<XT, 1, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki); break;
+                case 2: act_quant_vec_kernel<XT, 2, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki); break;
+                case 3: act_quant_vec_kernel<XT, 3, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki); break;
+                case 4: act_quant_vec_kernel<XT, 4, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki); break;
+                default: act_quant_vec_kernel<XT, 8, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki); break;
             }
         };
         if (xdt == NQ_F32) go(static_cast<const float*>(x));
@@ -214,13 +196,7 @@ nq_status act_quant(const void* x, nq_dtype xdt, int64_t m, int64_t k, int8_t* x
         quantize_rows_i8_kernel<float><<<grid, kRowThreads, 0, s>>>(static_cast<const float*>(x), xq, as, static_cast<int>(k));
     else
         quantize_rows_i8_kernel<_Float16><<<grid, kRowThreads, 0, s>>>(static_cast<const _Float16*>(x), xq, as, static_cast<int>(k));
-    if (nq_status st = launch_status("quantize_rows_i8_kernel")) return st;
-    if (zero_vecs > 0) {
-        zero_vec_kernel<<<static_cast<unsigned>(std::min<int64_t>(1024, (zero_vecs + 255) / 256)), 256, 0, s>>>(
-            static_cast<v4i*>(zero), zero_vecs);
-        return launch_status("zero_vec_kernel");
-    }
-    return NQ_OK;
+    return launch_status("quantize_rows_i8_kernel");
 }
 }  // namespace nq
 
@@ -245,7 +221,7 @@ extern "C" nq_status nq_act_quant_i8(const void* x, nq_dtype x_dtype, int64_t m,
     NQ_REQUIRE(a_scale && (k == 0 || (x && xq)), NQ_BAD_ARG, "nq_act_quant_i8: null pointer");
     NQ_REQUIRE(aligned(x, dtype_size(x_dtype)) && aligned(a_scale, 4), NQ_BAD_ALIGN,
                "nq_act_quant_i8: misaligned pointer");
-    return act_quant(x, x_dtype, m, k, xq, a_scale, nullptr, 0, as_stream(stream));
+    return act_quant(x, x_dtype, m, k, xq, a_scale, as_stream(stream));
 }
 
 extern "C" nq_status nq_quantize_q4g(const float* w, int64_t out, int64_t in, int64_t group,

@@ -7,14 +7,13 @@
 // (l % 16) and of B column (l % 16) for K slice (l / 16); the 16x16 int32
 // result lands as rows 4*(l/16)+v, column l%16, v = 0..3.
 //
-// Tiles: a workgroup of 4 waves owns a BM x BN output tile; its A/B K-slabs
-// (64 bytes deep) are staged through LDS with a 16-byte row pad (80-byte row
-// stride) so the ds_read_b128 operand fetches of the 16 rows of an MFMA tile
-// spread over the banks. The next slab's global loads are issued before the
-// current slab's MFMAs. Skinny m (batched decode, 16..64 rows) uses split-K:
-// each K range adds its int32 partial tile into a zeroed workspace with
-// atomic adds (integer addition is exact and order-free, so the result is
-// bit-identical to a single pass), then a finalize pass applies the epilogue.
+// Two MFMA kernels: a skinny one for batched decode (m <= 64: operands loaded
+// straight into the MFMA lane layout, K steps interleaved over waves) and an
+// LDS-tiled prefill GEMM (m > 64). When a launch would have too few
+// workgroups, both split K: each K range writes its int32 partial tile to its
+// own workspace plane and a reduction launch sums the planes in a fixed order
+// (integer addition is exact, so the result is bit-identical to a single pass)
+// and applies the epilogue.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -282,10 +281,6 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_w8a8_prefill_kernel(
     }
 }
 
-__global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t count) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i < count) p[i] = 0;
-}
 
 // ---- skinny W8A8 GEMM (3 <= m <= 64): batched decode ------------------------------------
 // A workgroup owns TN 16-column MFMA tiles of weight rows and all m activation
@@ -295,10 +290,10 @@ __global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t count) {
 // L2) and three steps in flight per wave. The per-wave int32 partial tiles are
 // added into one LDS tile with ds_add (exact, order-free). A single K range
 // applies the epilogue directly. With several K ranges (very long K only) each
-// range atomically adds its tile into a zeroed int32 accumulator and a separate
-// finalize launch applies the epilogue: on this multi-XCD part, finishing inside
-// the kernel would need agent-scope L2 writeback/invalidate fences, which cost
-// far more than the extra launch.
+// range stores its tile into its own int32 workspace plane and a reduction
+// launch applies the epilogue: on this multi-XCD part, finishing inside the
+// kernel would need agent-scope L2 writeback/invalidate fences, and
+// device-scope atomics into one plane, both measured far slower.
 template <int TM, int TN, Out OUT, typename YT>
 __global__ __launch_bounds__(1024) void gemm_w8a8_skinny_kernel(
     const int8_t* __restrict__ xq, const float* __restrict__ as, const int8_t* __restrict__ wq,
@@ -391,7 +386,7 @@ __global__ __launch_bounds__(1024) void gemm_w8a8_skinny_kernel(
         const int sum = tile[i][j][v][l];
         const size_t o = static_cast<size_t>(row) * n + col;
         if (split) {
-            atomicAdd(acc_out + o, sum);
+            acc_out[static_cast<size_t>(blockIdx.y) * m * n + o] = sum;  // this range's plane
         } else if constexpr (OUT == Out::ACC) {
             acc_out[o] = sum;
         } else {
@@ -399,17 +394,6 @@ __global__ __launch_bounds__(1024) void gemm_w8a8_skinny_kernel(
             y[o] = from_f32<YT>(w8a8_epilogue(sum, as[row], ws[col], bb));
         }
     }
-}
-
-template <typename YT>
-__global__ void w8a8_finalize_kernel(const int32_t* __restrict__ acc, const float* __restrict__ as,
-                                     const float* __restrict__ ws, const float* __restrict__ bias,
-                                     YT* __restrict__ y, int m, int n) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= static_cast<int64_t>(m) * n) return;
-    const int row = static_cast<int>(i / n), col = static_cast<int>(i % n);
-    const float b = bias ? bias[col] : 0.0f;
-    y[i] = from_f32<YT>(w8a8_epilogue(acc[i], as[row], ws[col], b));
 }
 
 // Sums the split-K partial planes [splits][m][n] in plane order (int32: exact)
@@ -453,39 +437,47 @@ SkinnyPlan plan_skinny(int64_t m, int64_t n, int64_t k) {
     p.k_split = static_cast<int>(per * kBK);
     p.splits = static_cast<int>((k + p.k_split - 1) / p.k_split);
     p.waves = static_cast<int>(std::min<int64_t>(16, std::max<int64_t>(4, (per + 2) / 3)));
-    if (p.splits > 1) p.acc_bytes = round_up(static_cast<size_t>(m * n) * 4, 256);
+    if (p.splits > 1) p.acc_bytes = round_up(static_cast<size_t>(p.splits) * static_cast<size_t>(m * n) * 4, 256);
     return p;
 }
 
-size_t gemm_ws_bytes(int64_t m, int64_t n, int64_t k);
+// Sums split-K partial planes [splits][m][n] into acc_out, or through the
+// epilogue into y.
+nq_status reduce_partials(const int32_t* parts, int splits, const float* as, const float* ws, const float* bias,
+                          void* y, nq_dtype ydt, int32_t* acc_out, int m, int n, hipStream_t s) {
+    const unsigned g = static_cast<unsigned>((static_cast<int64_t>(m) * n + 255) / 256);
+    if (acc_out)
+        w8a8_reduce_kernel<float, true><<<g, 256, 0, s>>>(parts, splits, as, ws, bias, nullptr, acc_out, m, n);
+    else if (ydt == NQ_F32)
+        w8a8_reduce_kernel<float, false><<<g, 256, 0, s>>>(parts, splits, as, ws, bias, static_cast<float*>(y), nullptr, m, n);
+    else
+        w8a8_reduce_kernel<_Float16, false><<<g, 256, 0, s>>>(parts, splits, as, ws, bias, static_cast<_Float16*>(y), nullptr, m, n);
+    return launch_status("w8a8_reduce_kernel");
+}
 
-// Skinny launch. zeroed: a split plan's accumulator was already cleared by
-// this call's activation-quant kernel; else it is cleared here.
+// Skinny launch. A split plan stores one int32 partial plane per K range in
+// the workspace and a reduction launch sums them (into acc_out, or through the
+// epilogue into y).
 nq_status gemm_skinny(const int8_t* xq, const float* as, const int8_t* wq, const float* ws,
                       const float* bias, void* y, nq_dtype ydt, int32_t* acc_out, int64_t m,
-                      int64_t n, int64_t k, void* workspace, size_t ws_bytes, bool zeroed,
-                      hipStream_t s) {
+                      int64_t n, int64_t k, void* workspace, size_t ws_bytes, hipStream_t s) {
     const SkinnyPlan p = plan_skinny(m, n, k);
-    int32_t* accum = acc_out;
+    int32_t* parts = nullptr;
     if (p.splits > 1) {
-        if (!acc_out) {
-            NQ_REQUIRE(workspace && ws_bytes >= p.acc_bytes, NQ_BAD_ARG,
-                       "w8a8 gemm: workspace of %zu bytes required, %zu given", p.acc_bytes, ws_bytes);
-            NQ_REQUIRE(aligned(workspace, 256), NQ_BAD_ALIGN, "w8a8 gemm: workspace must be 256-byte aligned");
-            accum = static_cast<int32_t*>(workspace);
-        }
-        if (!zeroed || acc_out) {
-            fill_i32_kernel<<<static_cast<unsigned>((m * n + 255) / 256), 256, 0, s>>>(accum, m * n);
-            if (nq_status st = launch_status("fill_i32_kernel")) return st;
-        }
+        NQ_REQUIRE(workspace && ws_bytes >= p.acc_bytes, NQ_BAD_ARG,
+                   "w8a8 gemm: workspace of %zu bytes required, %zu given", p.acc_bytes, ws_bytes);
+        NQ_REQUIRE(aligned(workspace, 256), NQ_BAD_ALIGN, "w8a8 gemm: workspace must be 256-byte aligned");
+        parts = static_cast<int32_t*>(workspace);
     }
     const dim3 grid(static_cast<unsigned>(p.ntiles), static_cast<unsigned>(p.splits));
     const int threads = p.waves * 64;
     const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
     auto go = [&](auto tmtag, auto tntag) {
         constexpr int TM = decltype(tmtag)::value, TN = decltype(tntag)::value;
-        if (acc_out || p.splits > 1)
-            gemm_w8a8_skinny_kernel<TM, TN, Out::ACC, float><<<grid, threads, 0, s>>>(xq, as, wq, ws, bias, nullptr, accum, mi, ni, ki, p.k_split);
+        if (p.splits > 1)
+            gemm_w8a8_skinny_kernel<TM, TN, Out::ACC, float><<<grid, threads, 0, s>>>(xq, as, wq, ws, bias, nullptr, parts, mi, ni, ki, p.k_split);
+        else if (acc_out)
+            gemm_w8a8_skinny_kernel<TM, TN, Out::ACC, float><<<grid, threads, 0, s>>>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, p.k_split);
         else if (ydt == NQ_F32)
             gemm_w8a8_skinny_kernel<TM, TN, Out::Y, float><<<grid, threads, 0, s>>>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi, ni, ki, p.k_split);
         else
@@ -502,15 +494,8 @@ nq_status gemm_skinny(const int8_t* xq, const float* as, const int8_t* wq, const
         default: with_tn(std::integral_constant<int, 4>{}); break;
     }
     if (nq_status st = launch_status("gemm_w8a8_skinny_kernel")) return st;
-    if (p.splits > 1 && !acc_out) {
-        const unsigned g = static_cast<unsigned>((m * n + 255) / 256);
-        if (ydt == NQ_F32)
-            w8a8_finalize_kernel<float><<<g, 256, 0, s>>>(accum, as, ws, bias, static_cast<float*>(y), mi, ni);
-        else
-            w8a8_finalize_kernel<_Float16><<<g, 256, 0, s>>>(accum, as, ws, bias, static_cast<_Float16*>(y), mi, ni);
-        return launch_status("w8a8_finalize_kernel");
-    }
-    return NQ_OK;
+    if (p.splits == 1) return NQ_OK;
+    return reduce_partials(parts, p.splits, as, ws, bias, y, ydt, acc_out, mi, ni, s);
 }
 
 // Big-m plan: 256 x 128 tiles (8 waves, 3-slab ring) when they give at least
@@ -585,14 +570,7 @@ nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const fl
     const nq_status st = p.big ? go(std::integral_constant<int, 4>{}, std::integral_constant<int, 3>{})
                                : go(std::integral_constant<int, 2>{}, std::integral_constant<int, 4>{});
     if (st != NQ_OK || p.splits == 1) return st;
-    const unsigned g = static_cast<unsigned>((m * n + 255) / 256);
-    if (acc_out)
-        w8a8_reduce_kernel<float, true><<<g, 256, 0, s>>>(parts, p.splits, as, ws, bias, nullptr, acc_out, mi, ni);
-    else if (ydt == NQ_F32)
-        w8a8_reduce_kernel<float, false><<<g, 256, 0, s>>>(parts, p.splits, as, ws, bias, static_cast<float*>(y), nullptr, mi, ni);
-    else
-        w8a8_reduce_kernel<_Float16, false><<<g, 256, 0, s>>>(parts, p.splits, as, ws, bias, static_cast<_Float16*>(y), nullptr, mi, ni);
-    return launch_status("w8a8_reduce_kernel");
+    return reduce_partials(parts, p.splits, as, ws, bias, y, ydt, acc_out, mi, ni, s);
 }
 
 // Workspace of the MFMA GEMM for this shape: a split plan's int32
@@ -630,7 +608,7 @@ bool skinny_ok(int64_t m, int64_t n, int64_t k) {
 }
 
 // AUTO: the v_dot4 GEMV up to m = 4, and up to m = 8 for long K (where the
-// skinny MFMA plan splits K and pays for atomics plus a finalize launch); the
+// skinny MFMA plan splits K and pays for a reduction launch); the
 // GEMV's per-row dot work grows with m while one 16x16x64 MFMA covers 16
 // activation rows, so the MFMA kernels take larger m. Measured on the decode
 // shapes k = 1536 / 8960, n = 256 .. 8960.
@@ -642,8 +620,7 @@ int resolve_path(int path, int64_t m, int64_t k) {
 // Runs the chosen path on pre-quantized activations.
 nq_status run_gemm(const int8_t* xq, const float* as, const int8_t* wq, const float* ws,
                    const float* bias, void* y, nq_dtype ydt, int32_t* acc_out, int64_t m,
-                   int64_t n, int64_t k, void* workspace, size_t ws_bytes, int path, bool zeroed,
-                   hipStream_t s) {
+                   int64_t n, int64_t k, void* workspace, size_t ws_bytes, int path, hipStream_t s) {
     int p = resolve_path(path, m, k);
     if (p == NQ_PATH_MFMA && !mfma_ok(xq, wq, k)) p = NQ_PATH_GENERIC;
     // Weights past 2^31 bytes exceed the MFMA kernels' 32-bit buffer offsets;
@@ -651,7 +628,7 @@ nq_status run_gemm(const int8_t* xq, const float* as, const int8_t* wq, const fl
     if (p == NQ_PATH_MFMA && !skinny_ok(m, n, k)) p = NQ_PATH_GEMV;
     if (p == NQ_PATH_MFMA) {
         if (m <= kSkinnyMaxM)
-            return gemm_skinny(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, workspace, ws_bytes, zeroed, s);
+            return gemm_skinny(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, workspace, ws_bytes, s);
         if (prefill_ok(m, n, k))
             return gemm_big(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, workspace, ws_bytes, s);
         // Shapes outside the prefill kernel's contract run the skinny kernel on
@@ -660,8 +637,7 @@ nq_status run_gemm(const int8_t* xq, const float* as, const int8_t* wq, const fl
             const int64_t mm = std::min<int64_t>(kSkinnyMaxM, m - r0);
             char* yp = y ? static_cast<char*>(y) + static_cast<size_t>(r0 * n) * dtype_size(ydt) : nullptr;
             if (nq_status st = gemm_skinny(xq + r0 * k, as ? as + r0 : nullptr, wq, ws, bias, yp, ydt,
-                                           acc_out ? acc_out + r0 * n : nullptr, mm, n, k, workspace, ws_bytes,
-                                           false, s))
+                                           acc_out ? acc_out + r0 * n : nullptr, mm, n, k, workspace, ws_bytes, s))
                 return st;
         }
         return NQ_OK;
@@ -686,8 +662,7 @@ nq_status run_gemm(const int8_t* xq, const float* as, const int8_t* wq, const fl
 using namespace nq;
 
 namespace nq {
-nq_status act_quant(const void* x, nq_dtype xdt, int64_t m, int64_t k, int8_t* xq, float* as,
-                    void* zero, size_t zero_bytes, hipStream_t s);
+nq_status act_quant(const void* x, nq_dtype xdt, int64_t m, int64_t k, int8_t* xq, float* as, hipStream_t s);
 bool gemv_w8a8_fused_launch(const void* x, nq_dtype xdt, const int8_t* w, const float* ws,
                             const float* bias, void* y, nq_dtype ydt, int64_t m, int64_t n,
                             int64_t k, hipStream_t s, nq_status* st);
@@ -717,7 +692,7 @@ extern "C" nq_status nq_gemm_w8a8(const int8_t* xq, const float* a_scale, const 
                    aligned(bias, 4),
                NQ_BAD_ALIGN, "gemm_w8a8: misaligned pointer");
     return run_gemm(xq, a_scale, wq, w_scale, bias, y, y_dtype, nullptr, m, n, k, workspace,
-                    workspace_bytes, path, false, as_stream(stream));
+                    workspace_bytes, path, as_stream(stream));
 }
 
 extern "C" nq_status nq_w8a8_acc_i32(const int8_t* xq, const int8_t* wq, int32_t* acc, int64_t m,
@@ -728,7 +703,7 @@ extern "C" nq_status nq_w8a8_acc_i32(const int8_t* xq, const int8_t* wq, int32_t
     NQ_REQUIRE(acc && (k == 0 || (xq && wq)), NQ_BAD_ARG, "w8a8_acc_i32: null pointer");
     NQ_REQUIRE(aligned(acc, 4), NQ_BAD_ALIGN, "w8a8_acc_i32: misaligned acc");
     return run_gemm(xq, nullptr, wq, nullptr, nullptr, nullptr, NQ_F32, acc, m, n, k, workspace,
-                    workspace_bytes, path, false, as_stream(stream));
+                    workspace_bytes, path, as_stream(stream));
 }
 
 extern "C" nq_status nq_linear_w8a8(const void* x, nq_dtype x_dtype, const int8_t* wq,
@@ -758,19 +733,6 @@ extern "C" nq_status nq_linear_w8a8(const void* x, nq_dtype x_dtype, const int8_
     float* as = reinterpret_cast<float*>(base + round_up(static_cast<size_t>(m * k), 256));
     char* rest = reinterpret_cast<char*>(as) + round_up(static_cast<size_t>(m) * 4, 256);
     const size_t rest_bytes = workspace_bytes - static_cast<size_t>(rest - base);
-    // A split skinny plan needs its accumulator cleared: the activation-quant
-    // launch does it with extra workgroups. The conditions mirror run_gemm's
-    // choice of kernel.
-    void* zero = nullptr;
-    size_t zero_bytes = 0;
-    if (p == NQ_PATH_MFMA && m <= kSkinnyMaxM && mfma_ok(xq, wq, k) && skinny_ok(m, n, k)) {
-        const SkinnyPlan sp = plan_skinny(m, n, k);
-        if (sp.splits > 1) {
-            zero = rest;
-            zero_bytes = sp.acc_bytes;
-        }
-    }
-    if (nq_status st = act_quant(x, x_dtype, m, k, xq, as, zero, zero_bytes, s)) return st;
-    return run_gemm(xq, as, wq, w_scale, bias, y, y_dtype, nullptr, m, n, k, rest, rest_bytes, p,
-                    zero_bytes > 0, s);
+    if (nq_status st = act_quant(x, x_dtype, m, k, xq, as, s)) return st;
+    return run_gemm(xq, as, wq, w_scale, bias, y, y_dtype, nullptr, m, n, k, rest, rest_bytes, p, s);
 }
