@@ -93,9 +93,14 @@ def rope_tables(cfg: Config, device) -> tuple:
 
 
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
-    """ops.cpp:272-290: x * (1 / sqrt(mean(x^2) + eps)) * w, sum of squares in fp64."""
-    ms = (x.double() * x.double()).mean(-1, keepdim=True).float()
-    return (x.float() * torch.rsqrt(ms + eps) * w).to(x.dtype)
+    """ops.cpp:272-290: x * (1 / sqrt(mean(x^2) + eps)) * w. fp32 activations sum
+    the squares in fp64 as the reference does; fp16 activations in fp32."""
+    xf = x.float()
+    if x.dtype == torch.float32:
+        ms = (x.double() * x.double()).mean(-1, keepdim=True).float()
+    else:
+        ms = (xf * xf).mean(-1, keepdim=True)
+    return (xf * torch.rsqrt(ms + eps) * w).to(x.dtype)
 
 
 def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
@@ -108,7 +113,11 @@ def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
 
 def attention(q, k, v, n_rep: int) -> torch.Tensor:
     """ops.cpp:206-270: causal softmax(q k^T / sqrt(d)) v with the KV heads
-    repeated n_rep times (GQA); scores and softmax in fp32."""
+    repeated n_rep times (GQA); scores and softmax in fp32. fp16 activations use
+    torch's fused scaled-dot-product attention (fp32 softmax inside)."""
+    if q.dtype == torch.float16:
+        return torch.nn.functional.scaled_dot_product_attention(
+            q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0), is_causal=True, enable_gqa=n_rep > 1).squeeze(0)
     k = k.repeat_interleave(n_rep, 0)
     v = v.repeat_interleave(n_rep, 0)
     s = q.shape[1]
