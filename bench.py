@@ -262,8 +262,9 @@ def main():
 
 def decoder_layer_cfg4(rnd, time_graph, args, w8a8_linear, entry):
     """one Qwen2.5-1.5B decoder layer, M=512 prefill, all seven
-    projections W8A8 on libnq_hip.so, fp16 activations, rmsnorm / RoPE / causal
-    GQA attention / SwiGLU in torch. Layers with distinct weights are chained
+    projections W8A8 on libnq_hip.so (q|k|v and gate|up fused into two GEMMs,
+    activation quant fused into rmsnorm and silu*up), fp16 activations, RoPE and
+    causal GQA attention in torch. Layers with distinct weights are chained
     (>= 512 MiB of weights) so each layer streams its own weights."""
     import torch
 
@@ -300,9 +301,15 @@ def decoder_layer_cfg4(rnd, time_graph, args, w8a8_linear, entry):
          "bound": "mfma", "frac": round(proj_ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4), "layers_chained": L}
     del mdl
     torch.cuda.empty_cache()
+    # The layer runs q|k|v and gate|up as fused GEMMs on pre-quantized input
+    # (activation quant fused into rmsnorm / silu*up); these are timed as GEMMs.
+    fused = {"qkv_proj": (shapes["self_attn.q_proj"][0] + 2 * shapes["self_attn.k_proj"][0], cfg.hidden),
+             "o_proj": shapes["self_attn.o_proj"],
+             "gate_up_proj": (2 * cfg.intermediate, cfg.hidden),
+             "down_proj": shapes["mlp.down_proj"]}
     projs = []
-    for name, (o, i) in shapes.items():
-        pe = entry(f"{name} M={m} K={i} N={o}", *w8a8_linear(m, o, i), "mfma")
+    for name, (o, i) in fused.items():
+        pe = entry(f"{name} M={m} K={i} N={o} (GEMM on pre-quantized x)", *w8a8_linear(m, o, i, gemm_only=True), "mfma")
         projs.append(pe)
         torch.cuda.empty_cache()
     e["projections"] = projs

@@ -74,6 +74,19 @@ nq_status nq_quantize_q4g(const float* w, int64_t out, int64_t in, int64_t group
 nq_status nq_act_quant_i8(const void* x, nq_dtype x_dtype, int64_t m, int64_t k, int8_t* xq,
                           float* a_scale, void* stream);
 
+/* ---- activation quant fused into its producer ------------------------------------
+ * The act-quant of linear_w8a8 (quant.cpp:179-193) applied to the output of the
+ * op that produces the activation, without writing that output: the W8A8 GEMM
+ * (nq_gemm_w8a8) then consumes xq / a_scale. No reference counterpart as one
+ * call: the reference runs rmsnorm (ops.cpp:272-290) or silu + mul
+ * (ops.cpp:86-100) and then linear_w8a8 on the materialised tensor
+ * (model.cpp:176-190). rmsnorm: y = x * (1/sqrt(mean(x^2) + eps)) * w, w fp32 [k];
+ * silu_mul: y = gate / (1 + exp(-gate)) * up, gate and up rows at stride ld. */
+nq_status nq_rmsnorm_quant_i8(const void* x, nq_dtype x_dtype, const float* w, float eps, int64_t m,
+                              int64_t k, int8_t* xq, float* a_scale, void* stream);
+nq_status nq_silu_mul_quant_i8(const void* gate, const void* up, nq_dtype dtype, int64_t m, int64_t k,
+                               int64_t ld, int8_t* xq, float* a_scale, void* stream);
+
 /* ---- weight-only linears ------------------------------------------------------
  * Replaces cuda_linear_q8 (cuda/cuda.hpp:53, cuda_quant.cu:300-322) and the CPU
  * linear_q8 (quant.cpp:136-163): y[i,o] = (sum_j x[i,j]*q[o,j]) * w_scale[o] + b[o],

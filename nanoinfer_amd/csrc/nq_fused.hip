@@ -1,0 +1,271 @@
+// Activation quantization fused into its producers: rmsnorm -> int8 and
+// silu(gate) * up -> int8. Each workgroup owns one row, keeps the produced fp32
+// values in registers, reduces their absmax across the workgroup and writes the
+// int8 codes and the row scale exactly as the activation quant of linear_w8a8
+// does (quant.cpp:179-193: a_scale = absmax / 127, round half to even, clamp),
+// so the W8A8 GEMM can consume them directly (nq_gemm_w8a8). The producer math
+// follows the reference ops: rmsnorm ops.cpp:272-290 (x * (1 / sqrt(mean(x^2) +
+// eps)) * w; the sum of squares is fp32 here, fp64 in the reference), silu
+// ops.cpp:86-93 (v / (1 + exp(-v))) and mul ops.cpp:95-100.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <type_traits>
+
+#include "nq_device.hpp"
+#include "nq_internal.hpp"
+
+namespace nq {
+namespace {
+
+// Workgroup-wide reduction of one float through LDS (wave reduction first).
+template <int NT, bool MAX>
+__device__ __forceinline__ float block_reduce(float v, float* red) {
+    v = MAX ? wave_absmax(v) : wave_sum_f32(v);
+    const int tid = threadIdx.x;
+    __syncthreads();  // red may still be read from a previous reduction
+    if ((tid & 63) == 0) red[tid >> 6] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; ++w) r = MAX ? absmax_step(r, red[w]) : r + red[w];
+    return r;
+}
+
+// Quantizes the CPT x 8 fp32 values a thread holds (vector e = tid + c*NT of
+// the row) with the row's absmax, and stores them as 8-byte code vectors.
+template <int CPT, int NT>
+__device__ __forceinline__ void quantize_store(const float (&v)[CPT][8], int steps, float am, float* red,
+                                               int8_t* qr, float* a_scale_row) {
+    const float absmax = block_reduce<NT, true>(am, red);
+    const float sc = absmax / 127.0f;
+    if (threadIdx.x == 0) *a_scale_row = sc;
+    const RowQuantizer rq(sc);
+    typedef int v2i __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const int e = threadIdx.x + c * NT;
+        if (e < steps) {
+            int lo = 0, hi = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                lo |= (static_cast<int>(rq.code(v[c][j], 127.0f)) & 0xFF) << (8 * j);
+                hi |= (static_cast<int>(rq.code(v[c][j + 4], 127.0f)) & 0xFF) << (8 * j);
+            }
+            reinterpret_cast<v2i*>(qr)[e] = v2i{lo, hi};
+        }
+    }
+}
+
+template <typename XT>
+struct Vec8;
+template <>
+struct Vec8<float> {
+    f4 a, b;
+    __device__ __forceinline__ void load(const float* p) {
+        a = reinterpret_cast<const f4*>(p)[0];
+        b = reinterpret_cast<const f4*>(p)[1];
+    }
+    __device__ __forceinline__ float at(int j) const { return j < 4 ? a[j] : b[j - 4]; }
+};
+template <>
+struct Vec8<_Float16> {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    h8 a;
+    __device__ __forceinline__ void load(const _Float16* p) { a = *reinterpret_cast<const h8*>(p); }
+    __device__ __forceinline__ float at(int j) const { return static_cast<float>(a[j]); }
+};
+
+// rmsnorm + quant: x row [k] (k % 8 == 0, 16-byte aligned rows), w fp32 [k].
+template <typename XT, int CPT, int NT>
+__global__ __launch_bounds__(NT) void rmsnorm_quant_kernel(const XT* __restrict__ x, const float* __restrict__ w,
+                                                           float eps, int k, int8_t* __restrict__ xq,
+                                                           float* __restrict__ a_scale) {
+    __shared__ float red[NT / 64];
+    const int row = blockIdx.x, tid = threadIdx.x, steps = k >> 3;
+    const XT* xr = x + static_cast<size_t>(row) * k;
+    Vec8<XT> xv[CPT];
+    f4 wv[CPT][2];
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const int e = min(tid + c * NT, steps - 1);  // unconditional: all loads in flight together
+        xv[c].load(xr + 8 * e);
+        wv[c][0] = reinterpret_cast<const f4*>(w + 8 * e)[0];
+        wv[c][1] = reinterpret_cast<const f4*>(w + 8 * e)[1];
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        float p = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) p = __builtin_fmaf(xv[c].at(j), xv[c].at(j), p);
+        ss += tid + c * NT < steps ? p : 0.0f;
+    }
+    ss = block_reduce<NT, false>(ss, red);
+    const float scale = 1.0f / __builtin_sqrtf(ss / static_cast<float>(k) + eps);
+    float v[CPT][8];
+    float am = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        float a = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            v[c][j] = xv[c].at(j) * scale * (j < 4 ? wv[c][0][j] : wv[c][1][j - 4]);
+            a = absmax_step(a, v[c][j]);
+        }
+        am = tid + c * NT < steps ? absmax_step(am, a) : am;
+    }
+    quantize_store<CPT, NT>(v, steps, am, red, xq + static_cast<size_t>(row) * k, a_scale + row);
+}
+
+// silu(gate) * up + quant: gate / up rows [k] at row stride ld elements.
+template <typename XT, int CPT, int NT>
+__global__ __launch_bounds__(NT) void silu_mul_quant_kernel(const XT* __restrict__ gate, const XT* __restrict__ up,
+                                                            int64_t ld, int k, int8_t* __restrict__ xq,
+                                                            float* __restrict__ a_scale) {
+    __shared__ float red[NT / 64];
+    const int row = blockIdx.x, tid = threadIdx.x, steps = k >> 3;
+    const XT* gr = gate + static_cast<size_t>(row) * ld;
+    const XT* ur = up + static_cast<size_t>(row) * ld;
+    Vec8<XT> gv[CPT], uv[CPT];
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const int e = min(tid + c * NT, steps - 1);
+        gv[c].load(gr + 8 * e);
+        uv[c].load(ur + 8 * e);
+    }
+    float v[CPT][8];
+    float am = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        float a = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float g = gv[c].at(j);
+            v[c][j] = g / (1.0f + expf(-g)) * uv[c].at(j);
+            a = absmax_step(a, v[c][j]);
+        }
+        am = tid + c * NT < steps ? absmax_step(am, a) : am;
+    }
+    quantize_store<CPT, NT>(v, steps, am, red, xq + static_cast<size_t>(row) * k, a_scale + row);
+}
+
+// Rows too long or not vector-aligned for the kernels above: one workgroup per
+// row, strided scalar loops; the produced values are recomputed in the quantize
+// pass instead of being held in registers.
+template <typename XT, bool RMS>
+__global__ __launch_bounds__(256) void fused_quant_generic_kernel(const XT* __restrict__ a, const XT* __restrict__ b,
+                                                                  const float* __restrict__ w, float eps, int64_t ld,
+                                                                  int k, int8_t* __restrict__ xq,
+                                                                  float* __restrict__ a_scale) {
+    __shared__ float red[4];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const XT* ar = a + static_cast<size_t>(row) * ld;
+    const XT* br = RMS ? nullptr : b + static_cast<size_t>(row) * ld;
+    float scale = 1.0f;
+    if constexpr (RMS) {
+        float ss = 0.0f;
+        for (int j = tid; j < k; j += 256) ss = __builtin_fmaf(to_f32(ar[j]), to_f32(ar[j]), ss);
+        ss = block_reduce<256, false>(ss, red);
+        scale = 1.0f / __builtin_sqrtf(ss / static_cast<float>(k) + eps);
+    }
+    auto value = [&](int j) {
+        if constexpr (RMS) {
+            return to_f32(ar[j]) * scale * w[j];
+        } else {
+            const float g = to_f32(ar[j]);
+            return g / (1.0f + expf(-g)) * to_f32(br[j]);
+        }
+    };
+    float am = 0.0f;
+    for (int j = tid; j < k; j += 256) am = absmax_step(am, value(j));
+    const float absmax = block_reduce<256, true>(am, red);
+    const float sc = absmax / 127.0f;
+    if (tid == 0) a_scale[row] = sc;
+    const RowQuantizer rq(sc);
+    int8_t* qr = xq + static_cast<size_t>(row) * k;
+    for (int j = tid; j < k; j += 256) qr[j] = static_cast<int8_t>(rq.code(value(j), 127.0f));
+}
+
+// Launch shape: 256 threads up to 2048 elements per row, else 1024 threads with
+// up to 4 vectors of 8 elements each (k <= 32768).
+template <typename Fn>
+void by_shape(int64_t k, Fn&& fn) {
+    const int64_t steps = k / 8;
+    if (steps <= 256) return fn(std::integral_constant<int, 1>{}, std::integral_constant<int, 256>{});
+    switch ((steps + 1023) / 1024) {
+        case 1: return fn(std::integral_constant<int, 1>{}, std::integral_constant<int, 1024>{});
+        case 2: return fn(std::integral_constant<int, 2>{}, std::integral_constant<int, 1024>{});
+        case 3: return fn(std::integral_constant<int, 3>{}, std::integral_constant<int, 1024>{});
+        default: return fn(std::integral_constant<int, 4>{}, std::integral_constant<int, 1024>{});
+    }
+}
+
+nq_status check_fused(int64_t m, int64_t k, const void* xq, const float* a_scale, nq_dtype dt, const char* who) {
+    NQ_REQUIRE(m >= 0 && k >= 0 && m <= kMaxIndex && k <= kMaxIndex, NQ_BAD_SHAPE, "%s: bad shape m=%lld k=%lld",
+               who, (long long)m, (long long)k);
+    NQ_REQUIRE(dtype_ok(dt), NQ_BAD_ARG, "%s: unknown dtype %d", who, int(dt));
+    NQ_REQUIRE(m == 0 || (a_scale && (k == 0 || xq)), NQ_BAD_ARG, "%s: null pointer", who);
+    NQ_REQUIRE(aligned(a_scale, 4), NQ_BAD_ALIGN, "%s: misaligned a_scale", who);
+    return NQ_OK;
+}
+
+}  // namespace
+}  // namespace nq
+
+using namespace nq;
+
+extern "C" nq_status nq_rmsnorm_quant_i8(const void* x, nq_dtype x_dtype, const float* w, float eps, int64_t m,
+                                         int64_t k, int8_t* xq, float* a_scale, void* stream) {
+    if (nq_status st = check_fused(m, k, xq, a_scale, x_dtype, "rmsnorm_quant_i8")) return st;
+    if (m == 0) return NQ_OK;
+    NQ_REQUIRE(k > 0, NQ_BAD_SHAPE, "rmsnorm_quant_i8: k must be positive");
+    NQ_REQUIRE(x && w, NQ_BAD_ARG, "rmsnorm_quant_i8: null pointer");
+    NQ_REQUIRE(aligned(x, dtype_size(x_dtype)) && aligned(w, 4), NQ_BAD_ALIGN, "rmsnorm_quant_i8: misaligned pointer");
+    hipStream_t s = as_stream(stream);
+    const unsigned grid = static_cast<unsigned>(m);
+    const int ki = static_cast<int>(k);
+    const bool vec = k % 8 == 0 && k <= 32768 && aligned(x, 16) && aligned(w, 16) && aligned(xq, 8);
+    auto go = [&](auto* xp) {
+        using XT = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
+        if (vec)
+            by_shape(k, [&](auto cpt, auto nt) {
+                rmsnorm_quant_kernel<XT, decltype(cpt)::value, decltype(nt)::value>
+                    <<<grid, decltype(nt)::value, 0, s>>>(xp, w, eps, ki, xq, a_scale);
+            });
+        else
+            fused_quant_generic_kernel<XT, true><<<grid, 256, 0, s>>>(xp, nullptr, w, eps, k, ki, xq, a_scale);
+    };
+    if (x_dtype == NQ_F32) go(static_cast<const float*>(x));
+    else go(static_cast<const _Float16*>(x));
+    return launch_status("rmsnorm_quant_i8");
+}
+
+extern "C" nq_status nq_silu_mul_quant_i8(const void* gate, const void* up, nq_dtype dtype, int64_t m, int64_t k,
+                                          int64_t ld, int8_t* xq, float* a_scale, void* stream) {
+    if (nq_status st = check_fused(m, k, xq, a_scale, dtype, "silu_mul_quant_i8")) return st;
+    if (m == 0) return NQ_OK;
+    NQ_REQUIRE(k > 0 && ld >= k, NQ_BAD_SHAPE, "silu_mul_quant_i8: need 0 < k <= ld");
+    NQ_REQUIRE(gate && up, NQ_BAD_ARG, "silu_mul_quant_i8: null pointer");
+    const size_t es = dtype_size(dtype);
+    NQ_REQUIRE(aligned(gate, es) && aligned(up, es), NQ_BAD_ALIGN, "silu_mul_quant_i8: misaligned pointer");
+    hipStream_t s = as_stream(stream);
+    const unsigned grid = static_cast<unsigned>(m);
+    const int ki = static_cast<int>(k);
+    const bool vec = k % 8 == 0 && k <= 32768 && (ld * es) % 16 == 0 && aligned(gate, 16) && aligned(up, 16) &&
+                     aligned(xq, 8);
+    auto go = [&](auto* gp, auto* upp) {
+        using XT = std::remove_const_t<std::remove_pointer_t<decltype(gp)>>;
+        if (vec)
+            by_shape(k, [&](auto cpt, auto nt) {
+                silu_mul_quant_kernel<XT, decltype(cpt)::value, decltype(nt)::value>
+                    <<<grid, decltype(nt)::value, 0, s>>>(gp, upp, ld, ki, xq, a_scale);
+            });
+        else
+            fused_quant_generic_kernel<XT, false><<<grid, 256, 0, s>>>(gp, upp, nullptr, 0.0f, ld, ki, xq, a_scale);
+    };
+    if (dtype == NQ_F32) go(static_cast<const float*>(gate), static_cast<const float*>(up));
+    else go(static_cast<const _Float16*>(gate), static_cast<const _Float16*>(up));
+    return launch_status("silu_mul_quant_i8");
+}

@@ -142,16 +142,31 @@ class Model:
         self.n_layers = cfg.layers if layers is None else layers
         dev = lambda t: t.to(self.device, torch.float32).contiguous()
         self.proj, self.bias, self.norm = {}, {}, {}
+        # W8A8 fuses the projections that share an input: q|k|v and gate|up are
+        # concatenated along the output rows (per-row quantization, so the codes
+        # and scales equal the separate projections'), their activation quant is
+        # fused into rmsnorm, and the down projection's into silu * up.
+        self.fused = self.mode == quant.QuantMode.W8A8
         for li in range(self.n_layers):
             L = f"layers.{li}."
-            for p in PROJ:
-                wt = dev(weights[L + p + ".weight"])
+            groups = {p: (p,) for p in PROJ}
+            if self.fused:
+                groups = {"self_attn.qkv_proj": ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj"),
+                          "self_attn.o_proj": ("self_attn.o_proj",),
+                          "mlp.gate_up_proj": ("mlp.gate_proj", "mlp.up_proj"),
+                          "mlp.down_proj": ("mlp.down_proj",)}
+            for name, parts in groups.items():
+                wt = torch.cat([dev(weights[L + p + ".weight"]) for p in parts], 0)
                 q = quant.make_quantized(wt, self.mode)
-                self.proj[L + p] = q if q is not None else wt
-            for p in ("q_proj", "k_proj", "v_proj"):
-                key = L + f"self_attn.{p}.bias"
-                if cfg.qkv_bias:
-                    self.bias[L + f"self_attn.{p}"] = dev(weights[key])
+                self.proj[L + name] = q if q is not None else wt
+                del wt
+            if cfg.qkv_bias:
+                bs = {p: dev(weights[L + f"self_attn.{p}.bias"]) for p in ("q_proj", "k_proj", "v_proj")}
+                if self.fused:
+                    self.bias[L + "self_attn.qkv_proj"] = torch.cat([bs["q_proj"], bs["k_proj"], bs["v_proj"]])
+                else:
+                    for p, b in bs.items():
+                        self.bias[L + f"self_attn.{p}"] = b
             for nme in ("input_layernorm", "post_attention_layernorm"):
                 self.norm[L + nme] = dev(weights[L + nme + ".weight"])
         self.final_norm = dev(weights["norm.weight"])
@@ -185,17 +200,35 @@ class Model:
             return torch.nn.functional.linear(x.float(), self.head)
         return quant.linear_q8(x, self.head.t, None, out_dtype=torch.float32)
 
+    def gemm(self, xq_as, name: str) -> torch.Tensor:
+        """W8A8 projection of activations quantized by a fused producer."""
+        xq, a_s = xq_as
+        return quant.gemm_w8a8(xq, a_s, self.proj[name].t, self.bias.get(name), out_dtype=self.act_dtype)
+
     def layer(self, x: torch.Tensor, li: int) -> torch.Tensor:
         """One pre-norm decoder layer (model.cpp:166-190)."""
         cfg, L = self.cfg, f"layers.{li}."
         s = x.shape[0]
-        h = rmsnorm(x, self.norm[L + "input_layernorm"], cfg.eps)
-        q = self.project(h, L + "self_attn.q_proj").view(s, cfg.heads, cfg.head_dim).transpose(0, 1)
-        k = self.project(h, L + "self_attn.k_proj").view(s, cfg.kv_heads, cfg.head_dim).transpose(0, 1)
-        v = self.project(h, L + "self_attn.v_proj").view(s, cfg.kv_heads, cfg.head_dim).transpose(0, 1)
+        hq, hkv = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+        if self.fused:
+            qkv = self.gemm(quant.rmsnorm_quant(x, self.norm[L + "input_layernorm"], cfg.eps), L + "self_attn.qkv_proj")
+            q, k, v = qkv.split([hq, hkv, hkv], 1)
+        else:
+            h = rmsnorm(x, self.norm[L + "input_layernorm"], cfg.eps)
+            q = self.project(h, L + "self_attn.q_proj")
+            k = self.project(h, L + "self_attn.k_proj")
+            v = self.project(h, L + "self_attn.v_proj")
+        q = q.reshape(s, cfg.heads, cfg.head_dim).transpose(0, 1)
+        k = k.reshape(s, cfg.kv_heads, cfg.head_dim).transpose(0, 1)
+        v = v.reshape(s, cfg.kv_heads, cfg.head_dim).transpose(0, 1)
         q, k = apply_rope(q, self.cos, self.sin), apply_rope(k, self.cos, self.sin)
-        a = attention(q, k, v, cfg.n_rep).transpose(0, 1).reshape(s, cfg.heads * cfg.head_dim).contiguous()
+        a = attention(q, k, v, cfg.n_rep).transpose(0, 1).reshape(s, hq).contiguous()
         x = x + self.project(a, L + "self_attn.o_proj")
+        if self.fused:
+            gu = self.gemm(quant.rmsnorm_quant(x, self.norm[L + "post_attention_layernorm"], cfg.eps),
+                           L + "mlp.gate_up_proj")
+            i = cfg.intermediate
+            return x + self.gemm(quant.silu_mul_quant(gu[:, :i], gu[:, i:]), L + "mlp.down_proj")
         hm = rmsnorm(x, self.norm[L + "post_attention_layernorm"], cfg.eps)
         gate = torch.nn.functional.silu(self.project(hm, L + "mlp.gate_proj").float())
         up = self.project(hm, L + "mlp.up_proj").float()

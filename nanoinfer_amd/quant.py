@@ -170,6 +170,41 @@ def act_quant(x: torch.Tensor):
     return xq, s
 
 
+def rmsnorm_quant(x: torch.Tensor, w: torch.Tensor, eps: float):
+    """rmsnorm (ops.cpp:272-290) with the act quant of linear_w8a8 fused in:
+    (xq int8, a_scale fp32) of x * (1/sqrt(mean(x^2) + eps)) * w."""
+    x = _dev(x, "x")
+    if x.dim() != 2:
+        raise ValueError("rmsnorm_quant expects 2-D x")
+    m, k = x.shape
+    w = _dev(w, "w").to(torch.float32)
+    if w.numel() != k:
+        raise ValueError("rmsnorm_quant: weight must match the last dimension")
+    xq = torch.empty((m, k), dtype=torch.int8, device=x.device)
+    s = torch.empty(m, dtype=torch.float32, device=x.device)
+    check(_lib.load().nq_rmsnorm_quant_i8(_ptr(x), _dtype_code(x, "x"), _ptr(w), float(eps), m, k, _ptr(xq), _ptr(s),
+                                          _stream()))
+    return xq, s
+
+
+def silu_mul_quant(gate: torch.Tensor, up: torch.Tensor):
+    """silu(gate) * up (ops.cpp:86-100) with the act quant fused in. gate and up
+    are [m, k] views with unit column stride and one common row stride (e.g. the
+    two halves of a fused gate|up projection output)."""
+    if not (isinstance(gate, torch.Tensor) and gate.is_cuda and isinstance(up, torch.Tensor) and up.is_cuda):
+        raise ValueError("gate and up must be device tensors")
+    if gate.shape != up.shape or gate.dim() != 2 or gate.dtype != up.dtype:
+        raise ValueError("silu_mul_quant: gate and up must be 2-D tensors of one shape and dtype")
+    if gate.stride(1) != 1 or up.stride(1) != 1 or gate.stride(0) != up.stride(0):
+        raise ValueError("silu_mul_quant: unit column stride and a common row stride required")
+    m, k = gate.shape
+    xq = torch.empty((m, k), dtype=torch.int8, device=gate.device)
+    s = torch.empty(m, dtype=torch.float32, device=gate.device)
+    check(_lib.load().nq_silu_mul_quant_i8(_ptr(gate), _ptr(up), _dtype_code(gate, "gate"), m, k, gate.stride(0),
+                                           _ptr(xq), _ptr(s), _stream()))
+    return xq, s
+
+
 def _x2d(x, w_in, who):
     x = _dev(x, "x")
     if x.dim() != 2:
