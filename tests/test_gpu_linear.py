@@ -238,7 +238,7 @@ def test_w8a8_workspace_reuse_and_gemm_entry(dev, nq, orc):
 
 
 @pytest.mark.parametrize("m,n,k", [(512, 256, 1536), (512, 1536, 1536), (512, 1536, 8960), (300, 1000, 960),
-                                   (2048, 8960, 1536)])
+                                   (2048, 8960, 1536), (200, 1003, 192), (77, 517, 1024), (129, 36, 2048)])
 def test_w8a8_prefill_plans_exact(dev, nq, orc, m, n, k):
     """Every prefill plan (256x128 / 128x128 tiles, split K with atomic int32
     partials) gives the GEMV path's accumulators bit for bit, and the linear's
@@ -264,3 +264,5 @@ def test_w8a8_prefill_plans_exact(dev, nq, orc, m, n, k):
     q, s = orc.quantize_q8(w)
     ref = orc.linear_w8a8(host(xdv.float())[rows], q, s, b)
     assert_close_rms(host(y.float())[rows], ref, f"w8a8 prefill {m}x{n}x{k}", fp16_out=True)
+    y32 = nq.linear_w8a8(xdv, t, to_dev(b, dev), out_dtype=torch.float32)   # fp32 epilogue path
+    assert_close_rms(host(y32)[rows], ref, f"w8a8 prefill fp32-out {m}x{n}x{k}")
