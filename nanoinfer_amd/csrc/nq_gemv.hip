@@ -21,6 +21,12 @@
 #include "nq_internal.hpp"
 
 namespace nq {
+bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m, int64_t n, int64_t k,
+                int64_t group);
+template <bool Q4, typename XT, typename YT, typename ST>
+nq_status wq_gemm(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int64_t m, int64_t n,
+                  int64_t k, int64_t group, hipStream_t s);
+
 namespace {
 
 constexpr int kMaxGemvWaves = 9;          // 576 lanes: int8 k <= 9216, int4 k <= 18432
@@ -646,8 +652,19 @@ extern "C" nq_status nq_linear_q8(const void* x, nq_dtype x_dtype, const int8_t*
                NQ_BAD_ALIGN, "linear_q8: misaligned pointer");
     hipStream_t s = as_stream(stream);
     const int ni = static_cast<int>(n), ki = static_cast<int>(k);
+    // More than 8 activation rows: the fp16 MFMA GEMM (one weight pass per 64 rows).
+    if (m > 8 && wq_gemm_ok(false, x, dtype_size(x_dtype), q, m, n, k, 32)) {
+        const uint8_t* w = reinterpret_cast<const uint8_t*>(q);
+        if (x_dtype == NQ_F32 && y_dtype == NQ_F32)
+            return wq_gemm<false>(static_cast<const float*>(x), w, w_scale, bias, static_cast<float*>(y), m, n, k, 32, s);
+        if (x_dtype == NQ_F32)
+            return wq_gemm<false>(static_cast<const float*>(x), w, w_scale, bias, static_cast<_Float16*>(y), m, n, k, 32, s);
+        if (y_dtype == NQ_F32)
+            return wq_gemm<false>(static_cast<const _Float16*>(x), w, w_scale, bias, static_cast<float*>(y), m, n, k, 32, s);
+        return wq_gemm<false>(static_cast<const _Float16*>(x), w, w_scale, bias, static_cast<_Float16*>(y), m, n, k, 32, s);
+    }
     const bool fast = k % 16 == 0 && k > 0 && k / 16 <= kMaxGemvThreads && aligned(q, 16) && aligned(x, 16);
-    // x rows beyond 8 run in slices of 8 (each slice re-streams the weight).
+    // Otherwise x rows beyond 8 run in slices of 8 (each slice re-streams the weight).
     for (int64_t r0 = 0; r0 < m; r0 += 8) {
         const int mi = static_cast<int>(m - r0 < 8 ? m - r0 : 8);
         const size_t xo = static_cast<size_t>(r0) * k, yo = static_cast<size_t>(r0) * n;
@@ -691,6 +708,20 @@ extern "C" nq_status nq_linear_q4g(const void* x, nq_dtype x_dtype, const uint8_
                NQ_BAD_ALIGN, "linear_q4g: misaligned pointer");
     hipStream_t s = as_stream(stream);
     const int ni = static_cast<int>(n), ki = static_cast<int>(k), gi = static_cast<int>(group);
+    // More than 8 activation rows: the fp16 MFMA GEMM (one weight pass per 64 rows).
+    if (m > 8 && wq_gemm_ok(true, x, dtype_size(x_dtype), q, m, n, k, group)) {
+        auto go = [&](auto* xp, auto* yp) {
+            if (scale_dtype == NQ_F32)
+                return wq_gemm<true>(xp, q, static_cast<const float*>(scale), bias, yp, m, n, k, group, s);
+            return wq_gemm<true>(xp, q, static_cast<const _Float16*>(scale), bias, yp, m, n, k, group, s);
+        };
+        auto with_y = [&](auto* xp) {
+            if (y_dtype == NQ_F32) return go(xp, static_cast<float*>(y));
+            return go(xp, static_cast<_Float16*>(y));
+        };
+        if (x_dtype == NQ_F32) return with_y(static_cast<const float*>(x));
+        return with_y(static_cast<const _Float16*>(x));
+    }
     const bool fast = k % 32 == 0 && k > 0 && group % 32 == 0 && k / 32 <= kMaxGemvThreads &&
                       aligned(q, 16) && aligned(x, 16);
     for (int64_t r0 = 0; r0 < m; r0 += 8) {

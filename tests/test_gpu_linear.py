@@ -83,6 +83,36 @@ def test_linear_q4g(dev, nq, orc, m, n, k, g, bias, xdt, sdt, ydt):
     assert_close_rms(host(y.float()), ref, f"linear_q4g {m}x{n}x{k} g{g}", fp16_out=(ydt == F16))
 
 
+WQ_GEMM_CASES = [  # m > 8: the fp16 MFMA GEMM (one weight pass per 64 rows)
+    ("q8", 9, 896, 896, 0, True, F16, F16, F16),
+    ("q8", 64, 4864, 896, 0, False, F32, F32, F32),    # fp32 x: hi/lo split
+    ("q8", 300, 1536, 1536, 0, True, F16, F32, F16),   # several 64-row blocks
+    ("q8", 33, 8960, 1536, 0, False, F16, F32, F16),   # 32 rows per workgroup
+    ("q4g", 16, 1536, 8960, 32, False, F16, F16, F16),
+    ("q4g", 40, 8960, 1536, 32, True, F32, F32, F32),
+    ("q4g", 64, 896, 4864, 64, False, F16, F32, F16),  # group 64
+    ("q4g", 130, 512, 2048, 128, True, F16, F16, F32),
+]
+
+
+@pytest.mark.parametrize("mode,m,n,k,g,bias,xdt,sdt,ydt", WQ_GEMM_CASES)
+def test_weight_only_gemm_batched(dev, nq, orc, mode, m, n, k, g, bias, xdt, sdt, ydt):
+    x, w, b = data(m, n, k, m * 31 + n + k + g, bias=bias)
+    xd = to_dev(x, dev, xdt)
+    bd = None if b is None else to_dev(b, dev)
+    xo = host(xd.float())
+    if mode == "q8":
+        t = nq.quantize_q8(to_dev(w, dev))
+        y = nq.linear_q8(xd, t, bd, out_dtype=ydt)
+        q, s = orc.quantize_q8(w)
+        ref = orc.linear_q8(xo, q, s, b)
+    else:
+        t = nq.quantize_q4g(to_dev(w, dev), g, scale_dtype=sdt)
+        y = nq.linear_q4g(xd, t, bd, out_dtype=ydt)
+        ref = orc.linear_q4g(xo, host(t.q), host(t.scale.float()), g, b)
+    assert_close_rms(host(y.float()), ref, f"{mode} gemm {m}x{n}x{k}", fp16_out=(ydt == F16))
+
+
 def test_linear_q4g_golden(dev, nq, golden):
     gd = golden("q4g")
     for i in range(6):
