@@ -652,8 +652,9 @@ extern "C" nq_status nq_linear_q8(const void* x, nq_dtype x_dtype, const int8_t*
                NQ_BAD_ALIGN, "linear_q8: misaligned pointer");
     hipStream_t s = as_stream(stream);
     const int ni = static_cast<int>(n), ki = static_cast<int>(k);
-    // More than 8 activation rows: the fp16 MFMA GEMM (one weight pass per 64 rows).
-    if (m > 8 && wq_gemm_ok(false, x, dtype_size(x_dtype), q, m, n, k, 32)) {
+    // Batched activations: the fp16 MFMA GEMM when the shape rule in wq_gemm_ok
+    // picks it, else GEMV slices of 8 rows.
+    if (wq_gemm_ok(false, x, dtype_size(x_dtype), q, m, n, k, 32)) {
         const uint8_t* w = reinterpret_cast<const uint8_t*>(q);
         if (x_dtype == NQ_F32 && y_dtype == NQ_F32)
             return wq_gemm<false>(static_cast<const float*>(x), w, w_scale, bias, static_cast<float*>(y), m, n, k, 32, s);
@@ -708,8 +709,9 @@ extern "C" nq_status nq_linear_q4g(const void* x, nq_dtype x_dtype, const uint8_
                NQ_BAD_ALIGN, "linear_q4g: misaligned pointer");
     hipStream_t s = as_stream(stream);
     const int ni = static_cast<int>(n), ki = static_cast<int>(k), gi = static_cast<int>(group);
-    // More than 8 activation rows: the fp16 MFMA GEMM (one weight pass per 64 rows).
-    if (m > 8 && wq_gemm_ok(true, x, dtype_size(x_dtype), q, m, n, k, group)) {
+    // Batched activations: the fp16 MFMA GEMM when the shape rule in wq_gemm_ok
+    // picks it, else GEMV slices of 8 rows.
+    if (wq_gemm_ok(true, x, dtype_size(x_dtype), q, m, n, k, group)) {
         auto go = [&](auto* xp, auto* yp) {
             if (scale_dtype == NQ_F32)
                 return wq_gemm<true>(xp, q, static_cast<const float*>(scale), bias, yp, m, n, k, group, s);

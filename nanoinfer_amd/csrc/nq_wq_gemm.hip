@@ -31,7 +31,11 @@ namespace nq {
 namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-constexpr int kWqWaves = 8, kWqRing = 4, kOob = 0x7FFFFFF0;
+constexpr int kWqRing = 4, kOob = 0x7FFFFFF0;
+// Waves per workgroup: 16 for one 16-row tile of x (more loads in flight per
+// CU), 8 for larger tiles (their prefetch ring needs up to 256 VGPRs).
+template <int TM>
+constexpr int wq_waves() { return TM == 1 ? 16 : 8; }
 
 // Activation fragment of one chunk: 8 values of one row, as fp16 pairs (c, c+4).
 template <typename XT>
@@ -122,21 +126,28 @@ struct WFrag<false> {  // 8 int8 codes = two dwords, byte t of dword d = column 
 };
 
 template <bool Q4, int TM, int TN, typename XT, typename YT, typename ST>
-__global__ __launch_bounds__(kWqWaves * 64) void gemm_wq_kernel(
+__global__ __launch_bounds__(wq_waves<TM>() * 64) void gemm_wq_kernel(
     const XT* __restrict__ x, const uint8_t* __restrict__ wq, const ST* __restrict__ scale,
     const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int group) {
+    constexpr int kWqWaves = wq_waves<TM>();
     __shared__ f4 part[kWqWaves][TM][TN][64];
+    // group / 32 is a power of two (checked on the host): chunk c uses group c >> gsh.
+    const int gsh = Q4 ? __builtin_ctz(static_cast<unsigned>(group >> 5)) : 0;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, q = lane >> 4;
     const int n0 = blockIdx.x * (16 * TN);
+    // gridDim.y blocks of 64 activation rows
+    x += static_cast<size_t>(blockIdx.y) * 64 * k;
+    y += static_cast<size_t>(blockIdx.y) * 64 * n;
+    m = min(64, m - static_cast<int>(blockIdx.y) * 64);
     const int chunks = k >> 5;
     const int rowb = Q4 ? (k >> 1) : k;  // weight bytes per row
     const int groups = Q4 ? k / group : 1;
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<XT*>(x), 0, m * k * static_cast<int>(sizeof(XT)), 0x00020000);
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(wq), 0, n * rowb, 0x00020000);
 
-    int xo[TM], wo[TN];
-    const ST* srow[TN];
+    const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<ST*>(scale), 0, n * groups * static_cast<int>(sizeof(ST)), 0x00020000);
+    int xo[TM], wo[TN], so[TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         const int row = i * 16 + r;
@@ -146,7 +157,7 @@ __global__ __launch_bounds__(kWqWaves * 64) void gemm_wq_kernel(
     for (int j = 0; j < TN; ++j) {
         const int row = n0 + j * 16 + r;
         wo[j] = row < n ? row * rowb + (Q4 ? 4 * q : 8 * q) : kOob;
-        srow[j] = Q4 ? scale + static_cast<size_t>(row < n ? row : 0) * groups : scale;
+        so[j] = row < n ? row * groups * static_cast<int>(sizeof(ST)) : kOob;
     }
 
     // Wave w takes chunks w, w + W, ...; steps = its count.
@@ -166,9 +177,11 @@ __global__ __launch_bounds__(kWqWaves * 64) void gemm_wq_kernel(
         for (int j = 0; j < TN; ++j) {
             st.wf[j].load(wrs, in && wo[j] != kOob ? wo[j] + c * (Q4 ? 16 : 32) : kOob);
             if constexpr (Q4) {
-                const int cc = min(c, chunks - 1);  // unconditional load, dropped past the end
-                const float sv = to_f32(srow[j][group == 32 ? cc : (cc * 32) / group]);
-                st.s[j] = in ? sv : 0.0f;
+                const int o = in && so[j] != kOob ? so[j] + (c >> gsh) * static_cast<int>(sizeof(ST)) : kOob;
+                if constexpr (sizeof(ST) == 4)
+                    st.s[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(srs, o, 0, 0));
+                else
+                    st.s[j] = static_cast<float>(__builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(srs, o, 0, 0)));
             }
         }
     };
@@ -239,17 +252,21 @@ template <bool Q4, typename XT, typename YT, typename ST>
 nq_status launch_wq(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n, int k,
                     int g, hipStream_t s) {
     // 16 weight rows per workgroup, 32 for tall weights at m <= 32 (the LDS
-    // tile of per-wave partials stays within 32 KB).
+    // tile of per-wave partials stays within 32 KB); 64-row blocks of x over
+    // gridDim.y.
+    const unsigned mblocks = static_cast<unsigned>((m + 63) / 64);
     auto go = [&](auto tmtag, auto tntag) {
         constexpr int TM = decltype(tmtag)::value, TN = decltype(tntag)::value;
-        gemm_wq_kernel<Q4, TM, TN, XT, YT, ST>
-            <<<static_cast<unsigned>((n + 16 * TN - 1) / (16 * TN)), kWqWaves * 64, 0, s>>>(x, w, sc, b, y, m, n, k, g);
+        const dim3 grid(static_cast<unsigned>((n + 16 * TN - 1) / (16 * TN)), mblocks);
+        gemm_wq_kernel<Q4, TM, TN, XT, YT, ST><<<grid, wq_waves<TM>() * 64, 0, s>>>(x, w, sc, b, y, m, n, k, g);
     };
     auto with_tn = [&](auto tmtag) {
-        if (n > 4096 && decltype(tmtag)::value <= 2) go(tmtag, std::integral_constant<int, 2>{});
-        else go(tmtag, std::integral_constant<int, 1>{});
+        if constexpr (decltype(tmtag)::value <= 2) {
+            if (n > 4096) return go(tmtag, std::integral_constant<int, 2>{});
+        }
+        go(tmtag, std::integral_constant<int, 1>{});
     };
-    switch ((m + 15) / 16) {
+    switch (m > 64 ? 4 : (m + 15) / 16) {
         case 1: with_tn(std::integral_constant<int, 1>{}); break;
         case 2: with_tn(std::integral_constant<int, 2>{}); break;
         case 3: with_tn(std::integral_constant<int, 3>{}); break;
@@ -260,28 +277,28 @@ nq_status launch_wq(const XT* x, const uint8_t* w, const ST* sc, const float* b,
 
 }  // namespace
 
-// The contract of the MFMA path (the caller falls back to the GEMV otherwise):
-// whole 32-column chunks, groups of whole chunks, 16-byte aligned operands and
+// Whether the MFMA path takes this call (the caller runs GEMV slices otherwise):
+// whole 32-column chunks, groups of a power-of-two number of chunks, 16-byte aligned operands and
 // 32-bit buffer offsets.
 bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m, int64_t n, int64_t k,
                 int64_t group) {
     const int64_t rowb = q4 ? k / 2 : k;
-    return k > 0 && k % 32 == 0 && (!q4 || group % 32 == 0) && aligned(x, 16) && aligned(w, 16) &&
-           std::min<int64_t>(m, 64) * k * static_cast<int64_t>(x_elem) < (int64_t(1) << 31) - 64 &&
+    // Shape rule (measured): the GEMM runs one workgroup per 16 (or 32) weight
+    // rows, each reading all of x, so below 4096 rows it fills under 256 CUs; a
+    // GEMV slice of 8 rows plus a remainder slice is then faster up to m = 15.
+    if (m <= 8 || (m < 16 && n < 4096)) return false;
+    return k > 0 && k % 32 == 0 && (!q4 || (group % 32 == 0 && ((group / 32) & (group / 32 - 1)) == 0)) && aligned(x, 16) && aligned(w, 16) &&
+           m <= (int64_t(65535) * 64) && std::min<int64_t>(m, 64) * k * static_cast<int64_t>(x_elem) < (int64_t(1) << 31) - 64 &&
            n * rowb < (int64_t(1) << 31) - 64;
 }
 
-// m rows of x in blocks of at most 64 (each block streams the weight once).
+// All m rows in one launch: 64-row blocks of x over gridDim.y (each block
+// streams the weight once).
 template <bool Q4, typename XT, typename YT, typename ST>
 nq_status wq_gemm(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int64_t m, int64_t n,
                   int64_t k, int64_t group, hipStream_t s) {
-    for (int64_t r0 = 0; r0 < m; r0 += 64) {
-        const int mi = static_cast<int>(std::min<int64_t>(64, m - r0));
-        if (nq_status st = launch_wq<Q4>(x + r0 * k, w, sc, b, y + r0 * n, mi, static_cast<int>(n),
-                                         static_cast<int>(k), static_cast<int>(group), s))
-            return st;
-    }
-    return NQ_OK;
+    return launch_wq<Q4>(x, w, sc, b, y, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
+                         static_cast<int>(group), s);
 }
 
 #define NQ_WQ_INST(Q4, XT, YT, ST)                                                                          \

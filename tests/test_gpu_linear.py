@@ -83,8 +83,10 @@ def test_linear_q4g(dev, nq, orc, m, n, k, g, bias, xdt, sdt, ydt):
     assert_close_rms(host(y.float()), ref, f"linear_q4g {m}x{n}x{k} g{g}", fp16_out=(ydt == F16))
 
 
-WQ_GEMM_CASES = [  # m > 8: the fp16 MFMA GEMM (one weight pass per 64 rows)
-    ("q8", 9, 896, 896, 0, True, F16, F16, F16),
+WQ_GEMM_CASES = [  # m > 8: the fp16 MFMA GEMM (m >= 16 or n >= 4096) or GEMV slices
+    ("q8", 9, 896, 896, 0, True, F16, F16, F16),       # GEMV slices 8 + 1
+    ("q8", 9, 4608, 896, 0, True, F16, F16, F16),      # GEMM, tall weight
+    ("q4g", 12, 4104, 512, 32, False, F32, F16, F32),  # GEMM, ragged last tile
     ("q8", 64, 4864, 896, 0, False, F32, F32, F32),    # fp32 x: hi/lo split
     ("q8", 300, 1536, 1536, 0, True, F16, F32, F16),   # several 64-row blocks
     ("q8", 33, 8960, 1536, 0, False, F16, F32, F16),   # 32 rows per workgroup
@@ -92,6 +94,7 @@ WQ_GEMM_CASES = [  # m > 8: the fp16 MFMA GEMM (one weight pass per 64 rows)
     ("q4g", 40, 8960, 1536, 32, True, F32, F32, F32),
     ("q4g", 64, 896, 4864, 64, False, F16, F32, F16),  # group 64
     ("q4g", 130, 512, 2048, 128, True, F16, F16, F32),
+    ("q4g", 20, 256, 1536, 96, False, F16, F32, F16),  # group 96 (3 chunks): GEMV slices
 ]
 
 
