@@ -282,6 +282,204 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_w8a8_prefill_kernel(
 }
 
 
+// ---- wide-tile W8A8 GEMM: one 256 x (32*FN) tile per CU -----------------------------------
+// For shapes whose 256 x 256..320 tiles number at most one per CU (e.g. m = 2048,
+// n = 8960: 8 x 32 tiles of 256 x 288), a single round of tiles beats two
+// rounds of 256 x 128 tiles: every output tile costs one pass over its A rows
+// and B rows, and a second round would leave most CUs idle. 8 waves as 4 (m)
+// x 2 (n), each 64 x 16*FN outputs (4 x FN fragments, 4*FN int32 accumulator
+// registers). K advances in 64-byte slabs through a 4-deep LDS ring filled by
+// LDS-DMA as in the prefill kernel; the slab kt + 3 request goes out right
+// after the barrier that frees its slot, so three slabs are in flight while
+// slab kt is multiplied. All fragment reads of a slab are issued before its
+// first MFMA (a scheduling barrier keeps the compiler from sinking them next
+// to their uses, which left LDS latency exposed). The 256 x BN block of
+// DMA requests does not split evenly over 8 waves; the spare requests read
+// zeros into a 1 KB sink so every wave counts the same number per slab.
+// fp16 results go through LDS in two 128-row halves and leave as 16-byte row
+// chunks with non-temporal stores (a one-round grid writes its whole output
+// at the end, which no later work overlaps).
+template <int FN>
+struct WideShape {
+    static constexpr int kWM = 4, kWN = 2, kWaves = 8, kD = 4;
+    static constexpr int kBM = kWM * 64, kBN = kWN * FN * 16;
+    static constexpr int kXB = kBM / 16, kNB = kXB + kBN / 16, kQ = (kNB + kWaves - 1) / kWaves;
+    static constexpr int kSlab = (kBM + kBN) * kPRow;
+    static constexpr int kSink = kD * kSlab;  // 1 KB
+    static constexpr size_t kLds = std::max<size_t>(size_t(kSink) + 1024, size_t(kBM / 2) * kBN * 2);
+};
+
+template <int FN, Out OUT, typename YT>
+__global__ __launch_bounds__(512) void gemm_w8a8_wide_kernel(
+    const int8_t* __restrict__ xq, const float* __restrict__ as, const int8_t* __restrict__ wq,
+    const float* __restrict__ ws, const float* __restrict__ bias, YT* __restrict__ y,
+    int32_t* __restrict__ acc_out, int m, int n, int k, int tiles_m, int tiles_n) {
+    using S = WideShape<FN>;
+    constexpr int NW = S::kWaves, Q = S::kQ, XB = S::kXB, NB = S::kNB, BM = S::kBM, BN = S::kBN, D = S::kD;
+    extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / S::kWN, wn = wave % S::kWN;
+    // Workgroup ids are dealt round-robin over the 8 XCDs: XCD x takes a
+    // contiguous range of tiles (row tile fastest), so its tiles share A row
+    // blocks and B column blocks in its L2.
+    const int total = tiles_m * tiles_n;
+    const int per = (total + 7) / 8, xcd = blockIdx.x % 8, idx = blockIdx.x / 8;
+    const int full = total - 8 * (per - 1);  // XCDs [0, full) own `per` tiles, the rest per - 1
+    const int lin = xcd < full ? xcd * per + idx : full * per + (xcd - full) * (per - 1) + idx;
+    const int m0 = (lin % tiles_m) * BM, n0 = (lin / tiles_m) * BN;
+
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(xq), 0, m * k, 0x00020000);
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(wq), 0, n * k, 0x00020000);
+    constexpr int kOob = 0x7FFFFFF0;
+    // Request q of wave w moves 1 KB block b = q * 8 + w of the slab: blocks
+    // [0, XB) are 16 activation rows each, [XB, NB) 16 weight rows, the rest
+    // spares. Lane i writes LDS bytes 16i..16i+15 of the block (row i/4,
+    // slot i%4) and loads the chunk the swizzle puts there.
+    int voff[Q], loff[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const int b = q * NW + wave;
+        const bool real = b < NB, isx = b < XB;
+        const int r = (isx ? b : b - XB) * 16 + (lane >> 2);
+        const int c = (lane & 3) ^ ((r >> 1) & 3);
+        const int grow = (isx ? m0 : n0) + r;
+        voff[q] = real && grow < (isx ? m : n) ? grow * k + c * 16 : kOob;
+        loff[q] = real ? (isx ? b * 1024 : BM * kPRow + (b - XB) * 1024) : S::kSink;
+    }
+    const int nk = k / kBK;
+    const unsigned lds_base = static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds));
+    auto issue = [&](int sl) {
+        const unsigned slot = static_cast<unsigned>(sl % D) * S::kSlab;
+        const int soff = sl < nk ? sl * kBK : kOob;
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const int b = q * NW + wave;  // wave-uniform
+            const unsigned dst = lds_base + (b < NB ? slot : 0u) + static_cast<unsigned>(loff[q]);
+            if (b < XB)
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                             ::"s"(dst), "v"(voff[q]), "s"(xrs), "s"(soff) : "memory");
+            else
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                             ::"s"(dst), "v"(voff[q]), "s"(wrs), "s"(soff) : "memory");
+        }
+    };
+
+    v4i acc[FN][4];  // [n fragment][m fragment]
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+    const int fr = lane & 15, fc = lane >> 4;
+    int fxo[4], fwo[FN];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) fxo[j] = swz(wm * 64 + j * 16 + fr, fc);
+#pragma unroll
+    for (int i = 0; i < FN; ++i) fwo[i] = BM * kPRow + swz(wn * FN * 16 + i * 16 + fr, fc);
+
+#pragma unroll
+    for (int sl = 0; sl < D - 1; ++sl) issue(sl);
+    for (int kt = 0; kt < nk; ++kt) {
+        wait_vmcnt<Q * (D - 2)>();  // own requests of slab kt landed
+        __builtin_amdgcn_s_barrier();  // everyone's landed; slot of slab kt - 1 is free
+        issue(kt + D - 1);
+        const int8_t* base = lds + (kt % D) * S::kSlab;
+        v4i fx[4], fw[FN];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) fx[j] = *reinterpret_cast<const v4i*>(base + fxo[j]);
+#pragma unroll
+        for (int i = 0; i < FN; ++i) fw[i] = *reinterpret_cast<const v4i*>(base + fwo[i]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fw[i], fx[j], acc[i][j], 0, 0, 0);
+        // this slab's fragment reads are done before the next barrier frees its slot
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    wait_vmcnt<0>();  // the ring's tail requests (zero reads) have retired
+
+    // Lane l holds, for fragment (i, j), output row m0 + wm*64 + j*16 + (l % 16)
+    // and columns n0 + wn*16*FN + i*16 + 4*(l / 16) + (0..3).
+    const int row_in = fr, col_in = fc * 4;
+    if constexpr (OUT == Out::Y && sizeof(YT) == 2) {
+        if ((n & 7) == 0) {
+            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+            constexpr int CPR = BN / 8;  // 16-byte chunks per tile row
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                __syncthreads();  // the ring (first half) or the staging rows (second) are free
+                if (wm / 2 == half) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int rl = (wm % 2) * 64 + j * 16 + row_in;  // row within the half
+                        const int row = m0 + half * 128 + rl;
+                        const float a_s = row < m ? as[row] : 0.0f;
+#pragma unroll
+                        for (int i = 0; i < FN; ++i) {
+                            const int cl = wn * FN * 16 + i * 16 + col_in, col = n0 + cl;
+                            const bool cin = col < n;  // n % 8 == 0: a 4-column group is all in or all out
+                            const f4 w4 = cin ? *reinterpret_cast<const f4*>(ws + col) : f4{0, 0, 0, 0};
+                            const f4 b4 = cin && bias ? *reinterpret_cast<const f4*>(bias + col) : f4{0, 0, 0, 0};
+                            h4 r;
+#pragma unroll
+                            for (int v = 0; v < 4; ++v) r[v] = from_f32<_Float16>(w8a8_epilogue(acc[i][j][v], a_s, w4[v], b4[v]));
+                            *reinterpret_cast<h4*>(lds + (rl * BN + cl) * 2) = r;
+                        }
+                    }
+                }
+                __syncthreads();
+                for (int c = tid; c < 128 * CPR; c += NW * 64) {
+                    const int rl = c / CPR, cc = c % CPR;
+                    const int row = m0 + half * 128 + rl, col = n0 + cc * 8;
+                    if (row < m && col < n)
+                        __builtin_nontemporal_store(*reinterpret_cast<const v4i*>(lds + (rl * BN + cc * 8) * 2),
+                                                    reinterpret_cast<v4i*>(y + static_cast<size_t>(row) * n + col));
+                }
+            }
+            return;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = m0 + wm * 64 + j * 16 + row_in;
+        if (row >= m) continue;
+        const float a_s = OUT == Out::Y ? as[row] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < FN; ++i) {
+            const int col = n0 + wn * FN * 16 + i * 16 + col_in;
+            const size_t o = static_cast<size_t>(row) * n + col;
+            if (col + 3 < n && (n & 3) == 0) {
+                if constexpr (OUT == Out::ACC) {
+                    *reinterpret_cast<v4i*>(acc_out + o) = acc[i][j];
+                } else {
+                    const f4 w4 = *reinterpret_cast<const f4*>(ws + col);
+                    const f4 b4 = bias ? *reinterpret_cast<const f4*>(bias + col) : f4{0, 0, 0, 0};
+                    if constexpr (sizeof(YT) == 4) {
+                        f4 r;
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) r[v] = w8a8_epilogue(acc[i][j][v], a_s, w4[v], b4[v]);
+                        *reinterpret_cast<f4*>(y + o) = r;
+                    } else {
+                        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+                        h4 r;
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) r[v] = from_f32<YT>(w8a8_epilogue(acc[i][j][v], a_s, w4[v], b4[v]));
+                        *reinterpret_cast<h4*>(y + o) = r;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    if (col + v >= n) break;
+                    if constexpr (OUT == Out::ACC) acc_out[o + v] = acc[i][j][v];
+                    else y[o + v] = from_f32<YT>(w8a8_epilogue(acc[i][j][v], a_s, ws[col + v], bias ? bias[col + v] : 0.0f));
+                }
+            }
+        }
+    }
+}
+
 // ---- skinny W8A8 GEMM (3 <= m <= 64): batched decode ------------------------------------
 // A workgroup owns TN 16-column MFMA tiles of weight rows and all m activation
 // rows (TM 16-row tiles) over one K range; its waves take interleaved 64-byte K
@@ -498,20 +696,36 @@ nq_status gemm_skinny(const int8_t* xq, const float* as, const int8_t* wq, const
     return reduce_partials(parts, p.splits, as, ws, bias, y, ydt, acc_out, mi, ni, s);
 }
 
-// Big-m plan: 256 x 128 tiles (8 waves, 3-slab ring) when they give at least
-// two tiles per CU, else 128 x 128 tiles (4 waves, 4-slab ring). A lone
-// workgroup pulls only ~30 GB/s from memory, so when there are fewer than 256
-// tiles K is split over workgroups (at least 8 slabs each) until there are
-// about 256: each range stores its int32 partial tile into its own workspace
-// plane and a reduction launch sums the planes and applies the epilogue
-// (device-scope atomics into one plane measured several times slower).
+// Big-m plan. When 256 x (32*fn) tiles, fn = 8..10, number between 192 and 256
+// (one per CU, one round) the wide-tile kernel runs. Otherwise 256 x 128 tiles
+// (8 waves, 3-slab ring) when they give at least two tiles per CU, else
+// 128 x 128 tiles (4 waves, 4-slab ring). A lone workgroup pulls only ~30 GB/s
+// from memory, so when there are fewer than 256 tiles K is split over
+// workgroups (at least 8 slabs each) until there are about 256: each range
+// stores its int32 partial tile into its own workspace plane and a reduction
+// launch sums the planes and applies the epilogue (device-scope atomics into
+// one plane measured several times slower).
 struct PrefillPlan {
     bool big;
+    int wide_fn;  // 0: not wide
     int tiles, splits, k_slabs;
     size_t acc_bytes;
 };
 PrefillPlan plan_prefill(int64_t m, int64_t n, int64_t k) {
     PrefillPlan p{};
+    for (int fn = 8; fn <= 10; ++fn) {
+        const int64_t t = ((m + 255) / 256) * ((n + 32 * fn - 1) / (32 * fn));
+        if (t <= 256) {
+            if (t >= 192) {
+                p.wide_fn = fn;
+                p.tiles = static_cast<int>(t);
+                p.splits = 1;
+                p.k_slabs = std::max(1, static_cast<int>(k / kBK));
+                return p;
+            }
+            break;
+        }
+    }
     const int64_t big_tiles = ((m + 255) / 256) * ((n + 127) / 128);
     p.big = big_tiles >= 512;
     p.tiles = static_cast<int>(p.big ? big_tiles : ((m + 127) / 128) * ((n + 127) / 128));
@@ -541,11 +755,38 @@ nq_status launch_prefill(const int8_t* xq, const float* as, const int8_t* wq, co
     return launch_status("gemm_w8a8_prefill_kernel");
 }
 
+template <int FN, Out OUT, typename YT>
+nq_status launch_wide(const int8_t* xq, const float* as, const int8_t* wq, const float* ws, const float* bias,
+                      YT* y, int32_t* acc_out, int m, int n, int k, hipStream_t s) {
+    using S = WideShape<FN>;
+    auto* fn = gemm_w8a8_wide_kernel<FN, OUT, YT>;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       static_cast<int>(S::kLds));
+    if (attr != hipSuccess) return fail(NQ_HIP_ERROR, "gemm_w8a8_wide: LDS attribute: %s", hipGetErrorString(attr));
+    const int tm = (m + S::kBM - 1) / S::kBM, tn = (n + S::kBN - 1) / S::kBN;
+    fn<<<tm * tn, S::kWaves * 64, S::kLds, s>>>(xq, as, wq, ws, bias, y, acc_out, m, n, k, tm, tn);
+    return launch_status("gemm_w8a8_wide_kernel");
+}
+
 nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const float* ws,
                    const float* bias, void* y, nq_dtype ydt, int32_t* acc_out, int64_t m, int64_t n,
                    int64_t k, void* workspace, size_t ws_bytes, hipStream_t s) {
     const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
     const PrefillPlan p = plan_prefill(m, n, k);
+    if (p.wide_fn) {
+        auto wide = [&](auto fntag) -> nq_status {
+            constexpr int FN = decltype(fntag)::value;
+            if (acc_out) return launch_wide<FN, Out::ACC, float>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, s);
+            if (ydt == NQ_F32)
+                return launch_wide<FN, Out::Y, float>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi, ni, ki, s);
+            return launch_wide<FN, Out::Y, _Float16>(xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr, mi, ni,
+                                                     ki, s);
+        };
+        if (p.wide_fn == 8) return wide(std::integral_constant<int, 8>{});
+        if (p.wide_fn == 9) return wide(std::integral_constant<int, 9>{});
+        return wide(std::integral_constant<int, 10>{});
+    }
     int32_t* parts = nullptr;
     if (p.splits > 1) {
         NQ_REQUIRE(workspace && ws_bytes >= p.acc_bytes, NQ_BAD_ARG,

@@ -271,10 +271,13 @@ def test_w8a8_workspace_reuse_and_gemm_entry(dev, nq, orc):
 
 
 @pytest.mark.parametrize("m,n,k", [(512, 256, 1536), (512, 1536, 1536), (512, 1536, 8960), (300, 1000, 960),
-                                   (2048, 8960, 1536), (200, 1003, 192), (77, 517, 1024), (129, 36, 2048)])
+                                   (2048, 8960, 1536), (200, 1003, 192), (77, 517, 1024), (129, 36, 2048),
+                                   # wide-tile plans: 256 x 256 / 288 / 320 tiles, ragged m and n, n % 8 != 0
+                                   (1800, 6000, 192), (1900, 7996, 128), (2048, 10000, 64), (1700, 8191, 64),
+                                   (1537, 9000, 64)])
 def test_w8a8_prefill_plans_exact(dev, nq, orc, m, n, k):
-    """Every prefill plan (256x128 / 128x128 tiles, split K with atomic int32
-    partials) gives the GEMV path's accumulators bit for bit, and the linear's
+    """Every prefill plan (wide 256 x 256..320 tiles, 256x128 / 128x128 tiles,
+    split K with int32 partial planes) gives the GEMV path's accumulators bit for bit, and the linear's
     fp16 output equals the GEMM entry's and the oracle's within tolerance."""
     rng = np.random.default_rng(m + n + k)
     xq = rng.integers(-127, 128, (m, k), dtype=np.int8)
