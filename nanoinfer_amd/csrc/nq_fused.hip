@@ -19,6 +19,15 @@
 namespace nq {
 namespace {
 
+// silu(g) = g / (1 + exp(-g)) from the hardware exp2 and reciprocal (about 1 ulp
+// each): the vector kernels are VALU-bound, and the libm-accurate expf plus an
+// IEEE divide cost ~25 instructions per element. Limits match the formula:
+// g -> -inf gives -0 (NaN at -inf, as -inf / inf), +inf gives +inf, NaN stays NaN.
+__device__ __forceinline__ float silu_f32(float g) {
+    const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+    return g * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
 // Workgroup-wide reduction of one float through LDS (wave reduction first).
 template <int NT, bool MAX>
 __device__ __forceinline__ float block_reduce(float v, float* red) {
@@ -94,6 +103,7 @@ __global__ __launch_bounds__(NT) void rmsnorm_quant_kernel(const XT* __restrict_
         wv[c][0] = reinterpret_cast<const f4*>(w + 8 * e)[0];
         wv[c][1] = reinterpret_cast<const f4*>(w + 8 * e)[1];
     }
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before the math (the scheduler interleaved them)
     float ss = 0.0f;
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
@@ -135,6 +145,7 @@ __global__ __launch_bounds__(NT) void silu_mul_quant_kernel(const XT* __restrict
         gv[c].load(gr + 8 * e);
         uv[c].load(ur + 8 * e);
     }
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before the math (the scheduler interleaved them)
     float v[CPT][8];
     float am = 0.0f;
 #pragma unroll
@@ -143,7 +154,7 @@ __global__ __launch_bounds__(NT) void silu_mul_quant_kernel(const XT* __restrict
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const float g = gv[c].at(j);
-            v[c][j] = g / (1.0f + expf(-g)) * uv[c].at(j);
+            v[c][j] = silu_f32(g) * uv[c].at(j);
             a = absmax_step(a, v[c][j]);
         }
         am = tid + c * NT < steps ? absmax_step(am, a) : am;
@@ -175,7 +186,7 @@ __global__ __launch_bounds__(256) void fused_quant_generic_kernel(const XT* __re
             return to_f32(ar[j]) * scale * w[j];
         } else {
             const float g = to_f32(ar[j]);
-            return g / (1.0f + expf(-g)) * to_f32(br[j]);
+            return silu_f32(g) * to_f32(br[j]);
         }
     };
     float am = 0.0f;
@@ -192,11 +203,24 @@ __global__ __launch_bounds__(256) void fused_quant_generic_kernel(const XT* __re
 // up to 4 vectors of 8 elements each (k <= 32768).
 template <typename Fn>
 void by_shape(int64_t k, Fn&& fn) {
+    // 256 threads per row up to 2048 vectors (k <= 16384): several vectors per
+    // thread keep more loads in flight and let 4-6 rows share a CU, where a
+    // 1024-thread row with one vector per thread ran at a third of the rate.
     const int64_t steps = k / 8;
-    if (steps <= 256) return fn(std::integral_constant<int, 1>{}, std::integral_constant<int, 256>{});
+    using I = std::integral_constant<int, 256>;
+    switch ((steps + 255) / 256) {
+        case 0:
+        case 1: return fn(std::integral_constant<int, 1>{}, I{});
+        case 2: return fn(std::integral_constant<int, 2>{}, I{});
+        case 3: return fn(std::integral_constant<int, 3>{}, I{});
+        case 4: return fn(std::integral_constant<int, 4>{}, I{});
+        case 5: return fn(std::integral_constant<int, 5>{}, I{});
+        case 6: return fn(std::integral_constant<int, 6>{}, I{});
+        case 7: return fn(std::integral_constant<int, 7>{}, I{});
+        case 8: return fn(std::integral_constant<int, 8>{}, I{});
+        default: break;
+    }
     switch ((steps + 1023) / 1024) {
-        case 1: return fn(std::integral_constant<int, 1>{}, std::integral_constant<int, 1024>{});
-        case 2: return fn(std::integral_constant<int, 2>{}, std::integral_constant<int, 1024>{});
         case 3: return fn(std::integral_constant<int, 3>{}, std::integral_constant<int, 1024>{});
         default: return fn(std::integral_constant<int, 4>{}, std::integral_constant<int, 1024>{});
     }

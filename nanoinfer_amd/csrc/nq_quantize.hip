@@ -119,6 +119,7 @@ __global__ __launch_bounds__(NT) void act_quant_vec_kernel(const XT* __restrict_
     // are left out of the absmax), so all CPT of them are in flight together.
 #pragma unroll
     for (int c = 0; c < CPT; ++c) v[c] = xr[min(tid + c * NT, steps - 1)];
+    __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the absmax math
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
         float a = 0.0f;
@@ -166,8 +167,9 @@ nq_status check_rows(int64_t rows, int64_t cols, const char* who) {
 // Activation quant: the vectorized kernel when k fits it, else the scalar row kernel.
 nq_status act_quant(const void* x, nq_dtype xdt, int64_t m, int64_t k, int8_t* xq, float* as,
                     hipStream_t s) {
-    // One workgroup per row: 256 threads up to 2048 elements, else 1024 threads
-    // with up to 8 vectors of 8 elements each.
+    // One workgroup per row: 256 threads with up to 8 vectors of 8 elements
+    // each (k <= 16384; several vectors per thread keep more loads in flight
+    // and let several rows share a CU), else 1024 threads with up to 8.
     const bool vec = k > 0 && k % 8 == 0 && k <= 8 * 1024 * 8 && aligned(x, 16) && aligned(xq, 8);
     if (vec) {
         const unsigned grid = static_cast<unsigned>(m);
@@ -175,13 +177,19 @@ nq_status act_quant(const void* x, nq_dtype xdt, int64_t m, int64_t k, int8_t* x
         const int mi = static_cast<int>(m), ki = static_cast<int>(k);
         auto go = [&](auto* xp) {
             using XT = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
-            if (steps <= 256) {
-                act_quant_vec_kernel<XT, 1, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki);
-                return;
+            switch ((steps + 255) / 256) {
+                case 0:
+                case 1: act_quant_vec_kernel<XT, 1, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki); return;
+                case 2: act_quant_vec_kernel<XT, 2, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki); return;
+                case 3: act_quant_vec_kernel<XT, 3, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki); return;
+                case 4: act_quant_vec_kernel<XT, 4, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki); return;
+                case 5: act_quant_vec_kernel<XT, 5, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki); return;
+                case 6: act_quant_vec_kernel<XT, 6, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki); return;
+                case 7: act_quant_vec_kernel<XT, 7, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki); return;
+                case 8: act_quant_vec_kernel<XT, 8, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki); return;
+                default: break;
             }
             switch ((steps + 1023) / 1024) {
-                case 1: act_quant_vec_kernel<XT, 1, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki); break;
-                case 2: act_quant_vec_kernel<XT, 2, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki); break;
                 case 3: act_quant_vec_kernel<XT, 3, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki); break;
                 case 4: act_quant_vec_kernel<XT, 4, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki); break;
                 default: act_quant_vec_kernel<XT, 8, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki); break;
