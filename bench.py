@@ -159,6 +159,28 @@ def main():
             return lambda: lib.nq_linear_q8(P(x), dt, P(qs[i]), P(ss[i]), None, P(y), dt, m, n, k, stream_ptr())
         return [mk(i) for i in range(len(qs))], nb, 2 * m * n * k
 
+    def q8_lmhead_argmax(m, n, k, xdt):
+        """LM head with the greedy argmax fused in: no logits are written, so
+        the algorithmic bytes are weights + scales + x + the int64 ids."""
+        x = rnd((m, k), 1.0, xdt)
+        w = rnd((n, k), 0.02)
+        t = nq.quantize_q8(w)
+        del w
+        wbytes = t.q.numel() + t.scale.numel() * 4
+        esz = 2 if xdt == torch.float16 else 4
+        nb = wbytes + x.numel() * esz + m * 8
+        qs = [t.q] + [t.q.clone() for _ in range(copies_for(wbytes) - 1)]
+        ss = [t.scale] + [t.scale.clone() for _ in range(len(qs) - 1)]
+        ids = torch.empty(m, dtype=torch.int64, device=dev)
+        wsb = lib.nq_lm_head_argmax_q8_workspace_size(m, n, k)
+        ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+        dt = 1 if xdt == torch.float16 else 0
+
+        def mk(i):
+            return lambda: lib.nq_lm_head_argmax_q8(P(x), dt, P(qs[i]), P(ss[i]), None, P(ids), m, n, k, P(ws),
+                                                    ws.numel(), stream_ptr())
+        return [mk(i) for i in range(len(qs))], nb, 2 * m * n * k
+
     def w8a8_linear(m, n, k, gemm_only=False):
         x = rnd((m, k), 1.0, torch.float16)
         w = rnd((n, k), 0.02)
@@ -213,6 +235,9 @@ def main():
             sweep.append(entry("q8_gemv_cfg1 M=1 K=896 N=4864 fp32", *q8_gemv(1, 4864, 896, torch.float32), "hbm"))
         if want("lmhead_cfg5b"):
             sweep.append(entry("q8_lmhead_cfg5b M=1 K=1536 N=151936 fp16", *q8_gemv(1, 151936, 1536, torch.float16), "hbm"))
+            torch.cuda.empty_cache()
+            sweep.append(entry("q8_lmhead_argmax_cfg5b M=1 K=1536 N=151936 fp16 (greedy id, no logits)",
+                               *q8_lmhead_argmax(1, 151936, 1536, torch.float16), "hbm"))
         torch.cuda.empty_cache()
         if want("w8a8_cfg3"):
             for m in (8, 16, 32, 64):

@@ -95,6 +95,24 @@ nq_status nq_linear_q8(const void* x, nq_dtype x_dtype, const int8_t* q, const f
                        const float* bias, void* y, nq_dtype y_dtype, int64_t m, int64_t n,
                        int64_t k, void* stream);
 
+/* LM head with the greedy pick fused in: ids[i] = argmax_o y[i,o] of the
+ * nq_linear_q8 fp32 logits, with the reference's tie and NaN rules (argmax,
+ * sampling.cpp:14-20: first index of the maximum under a strict >, and 0 when
+ * logit 0 is NaN). Replaces the decode step's cuda_linear_q8 on the int8 embed /
+ * lm_head weight followed by the host argmax (cuda_quant.cu:357-379 ->
+ * sampling.cpp:95) without writing the vocabulary-sized logits: every GEMV
+ * workgroup reduces its rows to one (value, index) partial. The logits are
+ * the q8 GEMV's fp32 values, bit for bit nq_linear_q8's output for m <= 8 (same
+ * kernel and row grouping); larger m runs the GEMV in slices of 8 rows (as
+ * nq_linear_q8 does where its MFMA GEMM does not apply). Shapes outside the GEMV's fast path (k %
+ * 16 != 0, k > 16384, misaligned operands) compute the logits into the
+ * workspace first. ids: int64 [m], 8-byte aligned. workspace: >=
+ * nq_lm_head_argmax_q8_workspace_size(m, n, k) bytes, 256-byte aligned. */
+size_t nq_lm_head_argmax_q8_workspace_size(int64_t m, int64_t n, int64_t k);
+nq_status nq_lm_head_argmax_q8(const void* x, nq_dtype x_dtype, const int8_t* q, const float* w_scale,
+                               const float* bias, int64_t* ids, int64_t m, int64_t n, int64_t k,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
 /* Replaces linear_q4g (quant.cpp:337-389; the reference has no GPU int4 kernel):
  * y[i,o] = sum_blocks scale[o,blk] * (sum_{j in blk} x[i,j]*(nib-8)) + b[o]. */
 nq_status nq_linear_q4g(const void* x, nq_dtype x_dtype, const uint8_t* q, const void* scale,

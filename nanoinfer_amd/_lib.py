@@ -32,6 +32,8 @@ SIGNATURES = {
     "nq_silu_mul_quant_i8": (_D, [_P, _P, _D, _I, _I, _I, _P, _P, _P]),
     "nq_linear_q8": (_D, [_P, _D, _P, _P, _P, _P, _D, _I, _I, _I, _P]),
     "nq_linear_q4g": (_D, [_P, _D, _P, _P, _D, _I, _P, _P, _D, _I, _I, _I, _P]),
+    "nq_lm_head_argmax_q8_workspace_size": (_Z, [_I, _I, _I]),
+    "nq_lm_head_argmax_q8": (_D, [_P, _D, _P, _P, _P, _P, _I, _I, _I, _P, _Z, _P]),
     "nq_linear_w8a8_workspace_size": (_Z, [_I, _I, _I]),
     "nq_linear_w8a8": (_D, [_P, _D, _P, _P, _P, _P, _D, _I, _I, _I, _P, _Z, ctypes.c_int, _P]),
     "nq_gemm_w8a8_workspace_size": (_Z, [_I, _I, _I]),

@@ -98,11 +98,28 @@ struct XChunk<_Float16> {
     __device__ __forceinline__ float at(int e) const { return static_cast<float>(v[e >> 3][e & 7]); }
 };
 
+// Greedy-argmax partial of a run of logits: the best (value, index) by
+// "greater value, then smaller index" over the non-NaN values, i.e. the
+// reference's left-to-right scan with a strict > (sampling.cpp:14-20); i ==
+// INT_MAX when the run holds no non-NaN value. i == -1 flags that logit 0 is
+// NaN, which makes that scan return 0 whatever follows.
+struct ArgPart {
+    float v;
+    int i;
+};
+constexpr int kArgNone = 0x7FFFFFFF;
+__device__ __forceinline__ bool arg_better(float v, int i, float bv, int bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
 // ---- weight-only int8 ------------------------------------------------------------
-template <int R, int M, typename XT, typename YT>
+// AM: instead of storing y, reduce this workgroup's R logits of each activation
+// row to an ArgPart (part[i * gridDim.x + blockIdx.x]); the logits are the same
+// fp32 values the plain kernel would store, so argmax(fused) == argmax(y).
+template <int R, int M, typename XT, typename YT, bool AM = false>
 __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q8_kernel(
     const XT* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ ws,
-    const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k) {
+    const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, ArgPart* __restrict__ part) {
     __shared__ float red[kMaxGemvWaves * R * M];
     const int tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6;
     const int chunks = k >> 4;
@@ -139,6 +156,36 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q8_kernel(
     }
     reduce_to_lds<R, M>(acc, red, wave, tid & 63);
     __syncthreads();
+    if constexpr (AM) {
+        __shared__ float logit[R * M];
+        if (tid < R * M) {
+            const int r = tid / M, i = tid % M, row = row0 + r;
+            if (row < n && i < m) {
+                float s = 0.0f;
+                for (int wv_i = 0; wv_i < nw; ++wv_i) s += red[(wv_i * R + r) * M + i];
+                const float b = bias ? bias[row] : 0.0f;
+                logit[r * M + i] = __builtin_fmaf(s, ws[row], b);
+            }
+        }
+        __syncthreads();
+        if (tid < M && tid < m) {
+            float bv = -__builtin_inff();
+            int bi = kArgNone;
+            for (int r = 0; r < R && row0 + r < n; ++r) {
+                const float v = logit[r * M + tid];
+                if (row0 + r == 0 && v != v) {
+                    bi = -1;
+                    break;
+                }
+                if (arg_better(v, row0 + r, bv, bi)) {
+                    bv = v;
+                    bi = row0 + r;
+                }
+            }
+            part[static_cast<size_t>(tid) * gridDim.x + blockIdx.x] = ArgPart{bv, bi};
+        }
+        return;
+    }
     if (tid < R * M) {
         const int r = tid / M, i = tid % M, row = row0 + r;
         if (row < n && i < m) {
@@ -492,23 +539,113 @@ __global__ void gemv_w8a8_generic_kernel(const int8_t* __restrict__ xq, const fl
     }
 }
 
+// ---- greedy argmax over logits ---------------------------------------------------------
+// Wave then workgroup reduction of (value, index) pairs by arg_better; the
+// order is a total one on distinct indices, so the result does not depend on
+// the reduction tree.
+template <int NT>
+__device__ __forceinline__ void arg_reduce_block(float& bv, int& bi, float* sv, int* si) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        if (arg_better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    const int tid = threadIdx.x;
+    if ((tid & 63) == 0) {
+        sv[tid >> 6] = bv;
+        si[tid >> 6] = bi;
+    }
+    __syncthreads();
+    bv = sv[0];
+    bi = si[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; ++w)
+        if (arg_better(sv[w], si[w], bv, bi)) {
+            bv = sv[w];
+            bi = si[w];
+        }
+}
+
+// Partials of fp32 logits [m, n]: workgroup (j, i) scans elements
+// [j * seg, (j + 1) * seg) of row i.
+__global__ __launch_bounds__(256) void argmax_logits_kernel(const float* __restrict__ logits, int n, int seg,
+                                                            ArgPart* __restrict__ part) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int i = blockIdx.y, j = blockIdx.x, tid = threadIdx.x;
+    const float* row = logits + static_cast<size_t>(i) * n;
+    const int beg = j * seg, end = min(n, beg + seg);
+    float bv = -__builtin_inff();
+    int bi = kArgNone;
+    for (int e = beg + tid; e < end; e += 256) {
+        const float v = row[e];
+        if (arg_better(v, e, bv, bi)) {
+            bv = v;
+            bi = e;
+        }
+    }
+    arg_reduce_block<256>(bv, bi, sv, si);
+    if (tid == 0) {
+        if (j == 0 && row[0] != row[0]) bi = -1;
+        part[static_cast<size_t>(i) * gridDim.x + j] = ArgPart{bv, bi};
+    }
+}
+
+// Final pass: row i's nparts partials -> ids[i] (0 when logit 0 is NaN). Each
+// thread issues 8 independent loads before comparing (a load-compare chain
+// waited one memory latency per partial: 18992 partials took ~20 us).
+__global__ __launch_bounds__(1024) void argmax_final_kernel(const ArgPart* __restrict__ part, int nparts,
+                                                            int64_t* __restrict__ ids) {
+    constexpr int U = 8;
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const int i = blockIdx.x, tid = threadIdx.x;
+    const ArgPart* p = part + static_cast<size_t>(i) * nparts;
+    float bv = -__builtin_inff();
+    int bi = kArgNone;
+    for (int base = tid; base < nparts; base += 1024 * U) {
+        ArgPart q[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = base + u * 1024;
+            q[u] = p[min(j, nparts - 1)];
+            if (j >= nparts) q[u].i = kArgNone;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (q[u].i >= 0 && arg_better(q[u].v, q[u].i, bv, bi)) {
+                bv = q[u].v;
+                bi = q[u].i;
+            }
+    }
+    arg_reduce_block<1024>(bv, bi, sv, si);
+    if (tid == 0) ids[i] = (p[0].i == -1 || bi == kArgNone) ? 0 : bi;
+}
+
 // ---- host dispatch ----------------------------------------------------------------------
 inline int m_bucket(int64_t m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8; }
 
-template <int M, typename XT, typename YT>
+// Rows per workgroup of the q8 GEMV. Very tall weights (an LM head) have
+// workgroups to spare: 8 rows per workgroup halves the activation re-reads
+// (measured 38.5 -> 36 us at n = 151936, k = 1536; 4 rows stay best at n = 4864).
+template <int M>
+int q8_rows(int n) { return (M <= 2 && n >= 32768) ? 8 : rows_for<M>(); }
+
+template <int M, bool AM = false, typename XT, typename YT>
 void launch_q8(const XT* x, const int8_t* w, const float* ws, const float* b, YT* y, int m, int n,
-               int k, hipStream_t s) {
+               int k, hipStream_t s, ArgPart* part = nullptr) {
     const int chunks = k >> 4;
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
     constexpr int R = rows_for<M>();
-    // Very tall weights (an LM head) have workgroups to spare: 8 rows per
-    // workgroup halves the activation re-reads (measured 38.5 -> 36 us at
-    // n = 151936, k = 1536; 4 rows stay best at n = 4864).
-    if (M <= 2 && n >= 32768) {
-        gemv_q8_kernel<8, M, XT, YT><<<(n + 7) / 8, threads, 0, s>>>(x, w, ws, b, y, m, n, k);
+    if (q8_rows<M>(n) == 8 && R != 8) {
+        gemv_q8_kernel<8, M, XT, YT, AM><<<(n + 7) / 8, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part);
         return;
     }
-    gemv_q8_kernel<R, M, XT, YT><<<(n + R - 1) / R, threads, 0, s>>>(x, w, ws, b, y, m, n, k);
+    gemv_q8_kernel<R, M, XT, YT, AM><<<(n + R - 1) / R, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part);
 }
 
 template <typename XT, typename YT>
@@ -747,6 +884,83 @@ extern "C" nq_status nq_linear_q4g(const void* x, nq_dtype x_dtype, const uint8_
         if (x_dtype == NQ_F32) with_y(static_cast<const float*>(x));
         else with_y(static_cast<const _Float16*>(x));
         if (nq_status st = launch_status("gemv_q4g_kernel")) return st;
+    }
+    return NQ_OK;
+}
+
+// ---- LM head with fused greedy argmax ----------------------------------------------------
+namespace nq {
+namespace {
+constexpr int kArgSeg = 4096;  // logits per partial on the unfused path
+// Fused path: the q8 GEMV's fast kernel (k % 16 == 0, k / 16 within one
+// workgroup, 16-byte aligned operands) writes one partial per workgroup.
+bool lm_head_fused_ok(const void* x, const int8_t* q, int64_t k) {
+    return k > 0 && k % 16 == 0 && k / 16 <= kMaxGemvThreads && aligned(q, 16) && aligned(x, 16);
+}
+size_t lm_head_ws(int64_t m, int64_t n, int64_t k, bool fused) {
+    // one partial per workgroup of at least 2 rows (rows_for), per activation row of a slice
+    if (fused) return round_up(static_cast<size_t>(std::min<int64_t>(m, 8)) * ((n + 1) / 2) * sizeof(ArgPart), 256);
+    return round_up(static_cast<size_t>(m) * n * 4, 256) +
+           round_up(static_cast<size_t>(m) * ((n + kArgSeg - 1) / kArgSeg) * sizeof(ArgPart), 256);
+}
+}  // namespace
+}  // namespace nq
+
+extern "C" size_t nq_lm_head_argmax_q8_workspace_size(int64_t m, int64_t n, int64_t k) {
+    if (m <= 0 || n <= 0 || k < 0) return 0;
+    return std::max(lm_head_ws(m, n, k, true), lm_head_ws(m, n, k, false));
+}
+
+extern "C" nq_status nq_lm_head_argmax_q8(const void* x, nq_dtype x_dtype, const int8_t* q, const float* w_scale,
+                                          const float* bias, int64_t* ids, int64_t m, int64_t n, int64_t k,
+                                          void* workspace, size_t workspace_bytes, void* stream) {
+    NQ_REQUIRE(m >= 0 && n >= 0 && k >= 0 && m <= kMaxIndex && n < kArgNone && k <= kMaxIndex, NQ_BAD_SHAPE,
+               "lm_head_argmax_q8: bad shape m=%lld n=%lld k=%lld", (long long)m, (long long)n, (long long)k);
+    NQ_REQUIRE(dtype_ok(x_dtype), NQ_BAD_ARG, "lm_head_argmax_q8: unknown dtype");
+    if (m == 0) return NQ_OK;
+    NQ_REQUIRE(n > 0, NQ_BAD_SHAPE, "lm_head_argmax_q8: empty vocabulary");
+    NQ_REQUIRE(ids && w_scale && (k == 0 || (x && q)), NQ_BAD_ARG, "lm_head_argmax_q8: null pointer");
+    NQ_REQUIRE(aligned(ids, 8) && aligned(w_scale, 4) && aligned(bias, 4) && aligned(x, dtype_size(x_dtype)),
+               NQ_BAD_ALIGN, "lm_head_argmax_q8: misaligned pointer");
+    const bool fused = lm_head_fused_ok(x, q, k);
+    const size_t need = lm_head_ws(m, n, k, fused);
+    NQ_REQUIRE(workspace && workspace_bytes >= need, NQ_BAD_ARG,
+               "lm_head_argmax_q8: workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    NQ_REQUIRE(aligned(workspace, 256), NQ_BAD_ALIGN, "lm_head_argmax_q8: workspace must be 256-byte aligned");
+    hipStream_t s = as_stream(stream);
+    const int ni = static_cast<int>(n), ki = static_cast<int>(k);
+    if (!fused) {
+        // Logits through nq_linear_q8 (fp32), then a two-pass argmax over them.
+        float* logits = static_cast<float*>(workspace);
+        ArgPart* part = reinterpret_cast<ArgPart*>(static_cast<char*>(workspace) + round_up(static_cast<size_t>(m) * n * 4, 256));
+        if (nq_status st = nq_linear_q8(x, x_dtype, q, w_scale, bias, logits, NQ_F32, m, n, k, stream)) return st;
+        const int nseg = (ni + kArgSeg - 1) / kArgSeg;
+        argmax_logits_kernel<<<dim3(static_cast<unsigned>(nseg), static_cast<unsigned>(m)), 256, 0, s>>>(logits, ni, kArgSeg, part);
+        argmax_final_kernel<<<static_cast<unsigned>(m), 1024, 0, s>>>(part, nseg, ids);
+        return launch_status("lm_head_argmax_q8");
+    }
+    ArgPart* part = static_cast<ArgPart*>(workspace);
+    // Activation rows in slices of 8 (the GEMV's batch), each with the kernel
+    // and row grouping nq_linear_q8 uses for that slice, so the fused logits
+    // equal nq_linear_q8's fp32 output bit for bit.
+    for (int64_t r0 = 0; r0 < m; r0 += 8) {
+        const int mi = static_cast<int>(std::min<int64_t>(8, m - r0));
+        int nwg = 0;
+        auto go = [&](auto* xp) {
+            using XT = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
+            const XT* xs = xp + static_cast<size_t>(r0) * k;
+            float* none = nullptr;
+            switch (m_bucket(mi)) {
+                case 1: nwg = (ni + q8_rows<1>(ni) - 1) / q8_rows<1>(ni); launch_q8<1, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part); break;
+                case 2: nwg = (ni + q8_rows<2>(ni) - 1) / q8_rows<2>(ni); launch_q8<2, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part); break;
+                case 4: nwg = (ni + q8_rows<4>(ni) - 1) / q8_rows<4>(ni); launch_q8<4, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part); break;
+                default: nwg = (ni + q8_rows<8>(ni) - 1) / q8_rows<8>(ni); launch_q8<8, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part); break;
+            }
+        };
+        if (x_dtype == NQ_F32) go(static_cast<const float*>(x));
+        else go(static_cast<const _Float16*>(x));
+        argmax_final_kernel<<<static_cast<unsigned>(mi), 1024, 0, s>>>(part, nwg, ids + r0);
+        if (nq_status st = launch_status("lm_head_argmax_q8")) return st;
     }
     return NQ_OK;
 }

@@ -234,13 +234,24 @@ class Model:
         up = self.project(hm, L + "mlp.up_proj").float()
         return x + self.project((gate * up).to(self.act_dtype).contiguous(), L + "mlp.down_proj")
 
-    def forward(self, ids) -> torch.Tensor:
-        """Logits [len(ids), vocab] (fp32, on the device) for positions 0..len-1."""
+    def hidden(self, ids) -> torch.Tensor:
+        """Final-norm hidden states [len(ids), hidden] for positions 0..len-1."""
         x = self.embed_tokens(ids)
         for li in range(self.n_layers):
             x = self.layer(x, li)
-        x = rmsnorm(x, self.final_norm, self.cfg.eps)
-        return self.lm_head(x.contiguous())
+        return rmsnorm(x, self.final_norm, self.cfg.eps).contiguous()
+
+    def forward(self, ids) -> torch.Tensor:
+        """Logits [len(ids), vocab] (fp32, on the device) for positions 0..len-1."""
+        return self.lm_head(self.hidden(ids))
+
+    def next_token(self, ids) -> int:
+        """Greedy pick for the last position (sampling.cpp:95). With the int8
+        head the argmax is fused into the LM-head GEMV (no logits written)."""
+        h = self.hidden(ids)[-1:]
+        if isinstance(self.head, torch.Tensor):
+            return int(torch.argmax(self.lm_head(h)[0]).item())
+        return int(quant.lm_head_argmax(h, self.head.t)[0].item())
 
     @torch.no_grad()
     def generate(self, prompt, max_new: int) -> list:
@@ -248,7 +259,7 @@ class Model:
         ids = list(prompt)
         out = []
         for _ in range(max_new):
-            nxt = int(torch.argmax(self.forward(ids)[-1]).item())
+            nxt = self.next_token(ids)
             out.append(nxt)
             ids.append(nxt)
         return out

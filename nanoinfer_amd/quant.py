@@ -240,6 +240,22 @@ def linear_q4g(x: torch.Tensor, w: Q4GTensor, bias=None, out_dtype=None) -> torc
 linear_q4 = linear_q4g  # quant.cpp:247-293: Q4 is Q4G with group == in
 
 
+def lm_head_argmax(x: torch.Tensor, w: QTensor, bias=None) -> torch.Tensor:
+    """Greedy next-token ids (int64 [m]) = argmax of linear_q8(x, w, bias) in
+    fp32, with the reference's first-index / NaN rules (sampling.cpp:14-20),
+    without materialising the logits (cuda_quant.cu:357-379 -> sampling.cpp:95)."""
+    w.check()
+    x = _x2d(x, w.in_, "lm_head_argmax")
+    b = _bias(bias, w.out)
+    m = x.shape[0]
+    ids = torch.empty(m, dtype=torch.int64, device=x.device)
+    lib = _lib.load()
+    ws = _workspace(lib.nq_lm_head_argmax_q8_workspace_size(m, w.out, w.in_), x.device)
+    check(lib.nq_lm_head_argmax_q8(_ptr(x), _dtype_code(x, "x"), _ptr(w.q), _ptr(w.scale), _ptr(b), _ptr(ids),
+                                   m, w.out, w.in_, _ptr(ws), ws.numel(), _stream()))
+    return ids
+
+
 def _workspace(nbytes: int, device) -> torch.Tensor:
     # 256-byte aligned by the caching allocator; at least one element.
     return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)

@@ -49,6 +49,87 @@ def test_linear_q8(dev, nq, orc, m, n, k, bias, xdt, ydt):
     assert_close_rms(host(y.float()), ref, f"linear_q8 {m}x{n}x{k}", fp16_out=(ydt == F16))
 
 
+def ref_argmax(v):
+    """sampling.cpp:14-20: scan left to right with a strict >; logit 0 NaN -> 0."""
+    v = np.asarray(v, np.float32)
+    if np.isnan(v[0]):
+        return 0
+    u = np.where(np.isnan(v), -np.inf, v)
+    return int(np.argmax(u))          # numpy: first index of the maximum
+
+
+def gemv_logits(nq, xd, t, b):
+    """fp32 logits of the q8 GEMV, in slices of 8 rows (the GEMV's batch)."""
+    return torch.cat([nq.linear_q8(xd[r:r + 8], t, b, out_dtype=F32) for r in range(0, xd.shape[0], 8)])
+
+
+@pytest.mark.parametrize("m,n,k,bias,xdt", [
+    (1, 151936, 1536, False, F16),    # config 5 LM head (8 rows per workgroup)
+    (1, 4864, 896, True, F32),
+    (2, 151936, 1536, True, F32),
+    (3, 8192, 896, False, F16),       # 2 rows per workgroup
+    (8, 1000, 512, True, F32),
+    (11, 5000, 256, False, F16),      # two slices of 8
+    (3, 700, 90, True, F32),          # ragged k: logits in the workspace, then argmax
+])
+def test_lm_head_argmax(dev, nq, orc, m, n, k, bias, xdt):
+    x, w, b = data(m, n, k, m * 13 + n + k, bias=bias)
+    t = nq.quantize_q8(to_dev(w, dev))
+    xd = to_dev(x, dev, xdt)
+    bd = None if b is None else to_dev(b, dev)
+    ids = nq.lm_head_argmax(xd, t, bd)
+    logits = host(gemv_logits(nq, xd, t, bd))
+    assert ids.dtype == torch.int64 and ids.shape == (m,)
+    assert host(ids).tolist() == [ref_argmax(r) for r in logits]
+    # against the oracle's CPU logits where the top-2 margin dwarfs the 1e-3 RMS tolerance
+    q, s = orc.quantize_q8(w)
+    ref = orc.linear_q8(host(xd.float()), q, s, b)
+    for i in range(m):
+        top = np.sort(ref[i])[-2:]
+        if top[1] - top[0] > 4e-3 * np.sqrt(np.mean(ref[i] ** 2)):
+            assert int(host(ids)[i]) == int(np.argmax(ref[i])), i
+
+
+def test_lm_head_argmax_ties_nan_inf(dev, nq):
+    """Ties go to the first index (within and across workgroups); a NaN logit 0
+    gives 0; other NaN logits are skipped; all -inf gives 0. Each case is also
+    checked against the scan over the GEMV's own logits."""
+    n, k = 40000, 256                                   # 8 rows per workgroup at m = 1
+    rng = np.random.default_rng(3)
+    w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    x = rng.normal(0, 1, (1, k)).astype(np.float32)
+    top = np.sign(x[0]) * 0.05                          # the largest dot product by far
+    for r in (9, 10, 30001):                            # 9 and 10 share a workgroup, 30001 does not
+        w[r] = top
+    t = nq.quantize_q8(to_dev(w, dev))
+    xd = to_dev(x, dev)
+
+    def run(xv, b, expect):
+        bd = None if b is None else to_dev(b, dev)
+        got = int(nq.lm_head_argmax(xv, t, bd)[0])
+        assert got == ref_argmax(host(gemv_logits(nq, xv, t, bd))[0])
+        assert got == expect
+        return got
+
+    lg = host(gemv_logits(nq, xd, t, None))[0]
+    assert lg[9] == lg[10] == lg[30001]                 # identical rows give identical logits
+    run(xd, None, 9)
+    b = np.zeros(n, np.float32)
+    b[9] = np.nan                                       # skipped: 10 is next among the equals
+    run(xd, b, 10)
+    b[10] = np.nan
+    run(xd, b, 30001)                                   # the tie across workgroups
+    b[0] = np.nan                                       # logit 0 NaN -> 0
+    run(xd, b, 0)
+    run(xd, np.full(n, -np.inf, np.float32), 0)         # all -inf -> 0
+    xn = xd.clone()
+    xn[0, 5] = float("nan")                             # every logit NaN -> 0
+    run(xn, None, 0)
+    b = np.zeros(n, np.float32)
+    b[n - 1] = 1e30                                     # the last row, in the last workgroup
+    run(xd, b, n - 1)
+
+
 def test_linear_q8_golden(dev, nq, golden):
     g = golden("q8_linear")
     for i in range(6):
