@@ -36,6 +36,7 @@ typedef enum nq_status {
     NQ_BAD_ALIGN = 2, /* a pointer is not aligned to its element size */
     NQ_HIP_ERROR = 3, /* a HIP runtime call or kernel launch failed */
     NQ_BAD_ARG = 4,   /* null pointer, unknown enum, too-small workspace, bad id */
+    NQ_IO_ERROR = 5,  /* a weight file cannot be read or is malformed (load_bin's errors) */
 } nq_status;
 
 typedef enum nq_dtype { NQ_F32 = 0, NQ_F16 = 1 } nq_dtype;
@@ -94,6 +95,22 @@ nq_status nq_silu_mul_quant_i8(const void* gate, const void* up, nq_dtype dtype,
 nq_status nq_linear_q8(const void* x, nq_dtype x_dtype, const int8_t* q, const float* w_scale,
                        const float* bias, void* y, nq_dtype y_dtype, int64_t m, int64_t n,
                        int64_t k, void* stream);
+
+/* ---- weight files: quantize on load -------------------------------------------
+ * NIT0 / NIT1 files (serialize.hpp:1-23; load_bin serialize.cpp:11-72): the same
+ * header checks as load_bin (bad magic, unknown dtype, negative ndim or dim,
+ * short payload, trailing bytes -> NQ_IO_ERROR; at most 8 dims). The payload is
+ * uploaded in row chunks of at most 64 MiB (a bf16 payload at 2 bytes per
+ * element and inflated on the device by bits << 16, exact as in load_bin) and
+ * quantized there by nq_quantize_q8 / nq_quantize_q4g, so the codes and scales
+ * equal quantize_q8 / quantize_q4g of load_bin's fp32 tensor bit for bit. The
+ * calls return after the stream has drained (they allocate and free pinned
+ * host and device staging). */
+nq_status nq_nit_info(const char* path, int32_t* dtype, int32_t* ndim, int64_t* shape, int32_t max_dims);
+nq_status nq_nit_load_f32(const char* path, float* dst, int64_t numel, void* stream);
+nq_status nq_nit_load_q8(const char* path, int8_t* q, float* scale, int64_t out, int64_t in, void* stream);
+nq_status nq_nit_load_q4g(const char* path, uint8_t* q, void* scale, nq_dtype scale_dtype, int64_t group,
+                          int64_t out, int64_t in, void* stream);
 
 /* LM head with the greedy pick fused in: ids[i] = argmax_o y[i,o] of the
  * nq_linear_q8 fp32 logits, with the reference's tie and NaN rules (argmax,

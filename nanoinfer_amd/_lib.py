@@ -11,7 +11,7 @@ import os
 PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG, "libnq_hip.so")
 
-NQ_OK, NQ_BAD_SHAPE, NQ_BAD_ALIGN, NQ_HIP_ERROR, NQ_BAD_ARG = 0, 1, 2, 3, 4
+NQ_OK, NQ_BAD_SHAPE, NQ_BAD_ALIGN, NQ_HIP_ERROR, NQ_BAD_ARG, NQ_IO_ERROR = 0, 1, 2, 3, 4, 5
 NQ_F32, NQ_F16 = 0, 1
 NQ_PATH_AUTO, NQ_PATH_GEMV, NQ_PATH_MFMA, NQ_PATH_GENERIC = 0, 1, 2, 3
 
@@ -40,6 +40,10 @@ SIGNATURES = {
     "nq_gemm_w8a8": (_D, [_P, _P, _P, _P, _P, _P, _D, _I, _I, _I, _P, _Z, ctypes.c_int, _P]),
     "nq_w8a8_acc_i32": (_D, [_P, _P, _P, _I, _I, _I, _P, _Z, ctypes.c_int, _P]),
     "nq_embedding_q8": (_D, [_P, _P, _I, _I, _P, _I, _P, _D, _P]),
+    "nq_nit_info": (_D, [ctypes.c_char_p, _P, _P, _P, ctypes.c_int32]),
+    "nq_nit_load_f32": (_D, [ctypes.c_char_p, _P, _I, _P]),
+    "nq_nit_load_q8": (_D, [ctypes.c_char_p, _P, _P, _I, _I, _P]),
+    "nq_nit_load_q4g": (_D, [ctypes.c_char_p, _P, _P, _D, _I, _I, _I, _P]),
 }
 
 

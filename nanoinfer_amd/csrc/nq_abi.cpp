@@ -37,6 +37,7 @@ const char* nq_status_name(int status) {
         case NQ_BAD_ALIGN: return "NQ_BAD_ALIGN";
         case NQ_HIP_ERROR: return "NQ_HIP_ERROR";
         case NQ_BAD_ARG: return "NQ_BAD_ARG";
+        case NQ_IO_ERROR: return "NQ_IO_ERROR";
     }
     return "NQ_UNKNOWN";
 }

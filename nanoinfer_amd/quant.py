@@ -11,6 +11,7 @@ the library is not built.
 from __future__ import annotations
 
 import enum
+import os
 from dataclasses import dataclass
 
 import torch
@@ -238,6 +239,58 @@ def linear_q4g(x: torch.Tensor, w: Q4GTensor, bias=None, out_dtype=None) -> torc
 
 
 linear_q4 = linear_q4g  # quant.cpp:247-293: Q4 is Q4G with group == in
+
+
+def nit_info(path: str):
+    """(dtype, shape) of a NIT0 / NIT1 weight file (serialize.hpp:1-23); dtype 0
+    fp32, 1 bf16. Raises NqError (NQ_IO_ERROR) for load_bin's malformed cases."""
+    import ctypes
+    dt, nd = ctypes.c_int32(0), ctypes.c_int32(0)
+    shape = (ctypes.c_int64 * 8)()
+    check(_lib.load().nq_nit_info(os.fsencode(path), ctypes.addressof(dt), ctypes.addressof(nd),
+                                  ctypes.addressof(shape), 8))
+    return dt.value, tuple(shape[i] for i in range(nd.value))
+
+
+def load_nit(path: str, device="cuda") -> torch.Tensor:
+    """load_bin (serialize.cpp:11-72) onto the device as fp32 (bf16 payloads
+    inflated exactly, bits << 16)."""
+    _, shape = nit_info(path)
+    t = torch.empty(shape, dtype=torch.float32, device=device)
+    with torch.cuda.device(t.device):
+        check(_lib.load().nq_nit_load_f32(os.fsencode(path), _ptr(t), t.numel(), _stream()))
+    return t
+
+
+def _nit_2d(path, who):
+    _, shape = nit_info(path)
+    if len(shape) != 2:
+        raise ValueError(f"{who}: {path} holds a {len(shape)}-d tensor, expected [out, in]")
+    return shape
+
+
+def load_nit_q8(path: str, device="cuda") -> QTensor:
+    """quantize_q8(load_bin(path)) with the payload streamed to the device and
+    quantized there (bit-exact codes and scales)."""
+    out, k = _nit_2d(path, "load_nit_q8")
+    q = torch.empty((out, k), dtype=torch.int8, device=device)
+    s = torch.empty(out, dtype=torch.float32, device=device)
+    with torch.cuda.device(q.device):
+        check(_lib.load().nq_nit_load_q8(os.fsencode(path), _ptr(q), _ptr(s), out, k, _stream()))
+    return QTensor(q, s, out, k)
+
+
+def load_nit_q4g(path: str, group: int = 32, scale_dtype=torch.float32, device="cuda") -> Q4GTensor:
+    """quantize_q4g(load_bin(path), group) on the device (bit-exact codes)."""
+    out, k = _nit_2d(path, "load_nit_q4g")
+    if group <= 0:
+        raise ValueError("load_nit_q4g: group must be positive")
+    q = torch.empty((out, (k + 1) // 2), dtype=torch.uint8, device=device)
+    s = torch.empty((out, (k + group - 1) // group), dtype=scale_dtype, device=device)
+    with torch.cuda.device(q.device):
+        check(_lib.load().nq_nit_load_q4g(os.fsencode(path), _ptr(q), _ptr(s), _dtype_code(s, "scale"), group,
+                                          out, k, _stream()))
+    return Q4GTensor(q, s, out, k, group)
 
 
 def lm_head_argmax(x: torch.Tensor, w: QTensor, bias=None) -> torch.Tensor:
