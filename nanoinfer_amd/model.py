@@ -16,6 +16,7 @@ Weights are named as the reference's exporter names them
 from __future__ import annotations
 
 import math
+import os
 from dataclasses import dataclass
 
 import torch
@@ -126,6 +127,17 @@ def attention(q, k, v, n_rep: int) -> torch.Tensor:
     scores.masked_fill_(mask, float("-inf"))
     p = torch.softmax(scores, -1)
     return torch.matmul(p, v.float()).to(q.dtype)
+
+
+def load_weights_dir(path: str, device="cuda") -> dict:
+    """Every NIT0 / NIT1 ``<name>.bin`` in ``path`` as a device fp32 tensor keyed
+    by ``<name>`` (model.cpp:50-57: the file stem keeps the dotted name, e.g.
+    "layers.0.self_attn.q_proj.weight"). bf16 payloads are uploaded at 2 bytes
+    per element and inflated on the device; Model then quantizes on the device."""
+    names = sorted(f for f in os.listdir(path) if f.endswith(".bin"))
+    if not names:
+        raise RuntimeError(f"load_weights_dir: no .bin weights in {path}")
+    return {f[:-4]: quant.load_nit(os.path.join(path, f), device) for f in names}
 
 
 class Model:

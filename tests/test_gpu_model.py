@@ -42,3 +42,23 @@ def test_model_uses_quant_weights(dev):
     m = model.Model(cfg, model.random_weights(cfg, 0), quant.QuantMode.W8A8, dev, layers=1)
     assert m.proj["layers.0.mlp.down_proj"].format() == quant.Format.W8A8
     assert m.embed.format() == quant.Format.Q8
+
+
+@pytest.mark.parametrize("payload", [0, 1])
+def test_model_from_nit_dir(dev, tmp_path, payload):
+    """The model loaded from a directory of NIT files (fp32 / bf16 payloads,
+    quantized on the device) generates the same tokens as the in-memory build
+    of the same (bf16-exact) weights."""
+    from nanoinfer_amd import model, quant
+    from nit_util import bf16_exact, write_nit1
+    cfg = tiny()
+    w = {k: torch.from_numpy(bf16_exact(v.numpy())) for k, v in model.random_weights(cfg, 3).items()}
+    for name, t in w.items():
+        write_nit1(str(tmp_path / f"{name}.bin"), t.numpy(), payload)
+    loaded = model.load_weights_dir(str(tmp_path), dev)
+    assert set(loaded) == set(w)
+    for name, t in w.items():
+        assert torch.equal(loaded[name].cpu(), t), name
+    a = model.Model(cfg, loaded, quant.QuantMode.W8A8, dev)
+    b = model.Model(cfg, w, quant.QuantMode.W8A8, dev)
+    assert a.generate(PROMPT, 6) == b.generate(PROMPT, 6)
