@@ -202,14 +202,17 @@ __global__ __launch_bounds__(256) void fused_quant_generic_kernel(const XT* __re
 // Launch shape: 256 threads up to 2048 elements per row, else 1024 threads with
 // up to 4 vectors of 8 elements each (k <= 32768).
 template <typename Fn>
-void by_shape(int64_t k, Fn&& fn) {
-    // 256 threads per row up to 2048 vectors (k <= 16384): several vectors per
-    // thread keep more loads in flight and let 4-6 rows share a CU, where a
-    // 1024-thread row with one vector per thread ran at a third of the rate.
+void by_shape(int64_t m, int64_t k, Fn&& fn) {
+    // With m >= 256 rows, 256 threads per row up to 2048 vectors (k <= 16384):
+    // several vectors per thread keep more loads in flight and let 4-6 rows
+    // share a CU, where a 1024-thread row with one vector per thread ran at
+    // two thirds of the rate. Fewer rows cannot fill the GPU that way and take
+    // 1024 threads per row (shorter per-row latency).
     const int64_t steps = k / 8;
     using I = std::integral_constant<int, 256>;
-    switch ((steps + 255) / 256) {
-        case 0:
+    const int64_t per = m >= 256 ? (steps + 255) / 256 : (steps <= 256 ? 1 : 0);
+    switch (per) {
+        case 0: break;
         case 1: return fn(std::integral_constant<int, 1>{}, I{});
         case 2: return fn(std::integral_constant<int, 2>{}, I{});
         case 3: return fn(std::integral_constant<int, 3>{}, I{});
@@ -221,6 +224,8 @@ void by_shape(int64_t k, Fn&& fn) {
         default: break;
     }
     switch ((steps + 1023) / 1024) {
+        case 1: return fn(std::integral_constant<int, 1>{}, std::integral_constant<int, 1024>{});
+        case 2: return fn(std::integral_constant<int, 2>{}, std::integral_constant<int, 1024>{});
         case 3: return fn(std::integral_constant<int, 3>{}, std::integral_constant<int, 1024>{});
         default: return fn(std::integral_constant<int, 4>{}, std::integral_constant<int, 1024>{});
     }
@@ -254,7 +259,7 @@ extern "C" nq_status nq_rmsnorm_quant_i8(const void* x, nq_dtype x_dtype, const 
     auto go = [&](auto* xp) {
         using XT = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
         if (vec)
-            by_shape(k, [&](auto cpt, auto nt) {
+            by_shape(m, k, [&](auto cpt, auto nt) {
                 rmsnorm_quant_kernel<XT, decltype(cpt)::value, decltype(nt)::value>
                     <<<grid, decltype(nt)::value, 0, s>>>(xp, w, eps, ki, xq, a_scale);
             });
@@ -282,7 +287,7 @@ extern "C" nq_status nq_silu_mul_quant_i8(const void* gate, const void* up, nq_d
     auto go = [&](auto* gp, auto* upp) {
         using XT = std::remove_const_t<std::remove_pointer_t<decltype(gp)>>;
         if (vec)
-            by_shape(k, [&](auto cpt, auto nt) {
+            by_shape(m, k, [&](auto cpt, auto nt) {
                 silu_mul_quant_kernel<XT, decltype(cpt)::value, decltype(nt)::value>
                     <<<grid, decltype(nt)::value, 0, s>>>(gp, upp, ld, ki, xq, a_scale);
             });

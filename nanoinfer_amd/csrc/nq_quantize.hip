@@ -167,9 +167,9 @@ nq_status check_rows(int64_t rows, int64_t cols, const char* who) {
 // Activation quant: the vectorized kernel when k fits it, else the scalar row kernel.
 nq_status act_quant(const void* x, nq_dtype xdt, int64_t m, int64_t k, int8_t* xq, float* as,
                     hipStream_t s) {
-    // One workgroup per row: 256 threads with up to 8 vectors of 8 elements
-    // each (k <= 16384; several vectors per thread keep more loads in flight
-    // and let several rows share a CU), else 1024 threads with up to 8.
+    // One workgroup per row: for m >= 256, 256 threads with up to 8 vectors of
+    // 8 elements each (k <= 16384; several vectors per thread keep more loads
+    // in flight and let several rows share a CU), else 1024 threads with up to 8.
     const bool vec = k > 0 && k % 8 == 0 && k <= 8 * 1024 * 8 && aligned(x, 16) && aligned(xq, 8);
     if (vec) {
         const unsigned grid = static_cast<unsigned>(m);
@@ -177,8 +177,13 @@ nq_status act_quant(const void* x, nq_dtype xdt, int64_t m, int64_t k, int8_t* x
         const int mi = static_cast<int>(m), ki = static_cast<int>(k);
         auto go = [&](auto* xp) {
             using XT = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
-            switch ((steps + 255) / 256) {
-                case 0:
+            // Few rows (m < 256) cannot fill the GPU with 256-thread rows: their
+            // per-row latency rules, so they take 1024 threads (the k = 8960 act
+            // quant at m = 16: 256 threads 8.0 us, 1024 threads 6.0 us; at m = 2048
+            // the opposite, 31 vs 41 us).
+            const int64_t per = m >= 256 ? (steps + 255) / 256 : (steps <= 256 ? 1 : 0);
+            switch (per) {
+                case 0: break;
                 case 1: act_quant_vec_kernel<XT, 1, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki); return;
                 case 2: act_quant_vec_kernel<XT, 2, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki); return;
                 case 3: act_quant_vec_kernel<XT, 3, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki); return;
@@ -190,6 +195,8 @@ nq_status act_quant(const void* x, nq_dtype xdt, int64_t m, int64_t k, int8_t* x
                 default: break;
             }
             switch ((steps + 1023) / 1024) {
+                case 1: act_quant_vec_kernel<XT, 1, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki); break;
+                case 2: act_quant_vec_kernel<XT, 2, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki); break;
                 case 3: act_quant_vec_kernel<XT, 3, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki); break;
                 case 4: act_quant_vec_kernel<XT, 4, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki); break;
                 default: act_quant_vec_kernel<XT, 8, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki); break;
