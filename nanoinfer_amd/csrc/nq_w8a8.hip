@@ -282,26 +282,26 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_w8a8_prefill_kernel(
 }
 
 
-// ---- wide-tile W8A8 GEMM: one 256 x (32*FN) tile per CU -----------------------------------
-// For shapes whose 256 x 256..320 tiles number at most one per CU (e.g. m = 2048,
-// n = 8960: 8 x 32 tiles of 256 x 288), a single round of tiles beats two
-// rounds of 256 x 128 tiles: every output tile costs one pass over its A rows
-// and B rows, and a second round would leave most CUs idle. 8 waves as 4 (m)
-// x 2 (n), each 64 x 16*FN outputs (4 x FN fragments, 4*FN int32 accumulator
-// registers). K advances in 64-byte slabs through a 4-deep LDS ring filled by
+// ---- wide-tile W8A8 GEMM: one (64*WM) x (32*FN) tile per CU ------------------------------
+// For shapes whose 256 x 256..320 (or 128 x 256..320) tiles number at most one
+// per CU (m = 2048, n = 8960: 8 x 32 tiles of 256 x 288; m = 512, n = 17920:
+// 4 x 63 tiles of 128 x 288), a single round of tiles beats two rounds of
+// smaller tiles: every output tile costs one pass over its A rows and B rows,
+// and a second round would leave most CUs idle. WM x 2 waves (WM = 4 or 2), each
+// 64 x 16*FN outputs (4 x FN fragments, 4*FN int32 accumulator registers). K advances in 64-byte slabs through a 4-deep LDS ring filled by
 // LDS-DMA as in the prefill kernel; the slab kt + 3 request goes out right
 // after the barrier that frees its slot, so three slabs are in flight while
 // slab kt is multiplied. All fragment reads of a slab are issued before its
 // first MFMA (a scheduling barrier keeps the compiler from sinking them next
 // to their uses, which left LDS latency exposed). The 256 x BN block of
-// DMA requests does not split evenly over 8 waves; the spare requests read
+// DMA requests does not split evenly over the waves; the spare requests read
 // zeros into a 1 KB sink so every wave counts the same number per slab.
-// fp16 results go through LDS in two 128-row halves and leave as 16-byte row
-// chunks with non-temporal stores (a one-round grid writes its whole output
-// at the end, which no later work overlaps).
-template <int FN>
+// fp16 results go through LDS in two halves of the tile's rows and leave as
+// 16-byte row chunks with non-temporal stores (a one-round grid writes its
+// whole output at the end, which no later work overlaps).
+template <int WM, int FN>
 struct WideShape {
-    static constexpr int kWM = 4, kWN = 2, kWaves = 8, kD = 4;
+    static constexpr int kWM = WM, kWN = 2, kWaves = WM * 2, kD = 4;
     static constexpr int kBM = kWM * 64, kBN = kWN * FN * 16;
     static constexpr int kXB = kBM / 16, kNB = kXB + kBN / 16, kQ = (kNB + kWaves - 1) / kWaves;
     static constexpr int kSlab = (kBM + kBN) * kPRow;
@@ -309,12 +309,12 @@ struct WideShape {
     static constexpr size_t kLds = std::max<size_t>(size_t(kSink) + 1024, size_t(kBM / 2) * kBN * 2);
 };
 
-template <int FN, Out OUT, typename YT>
-__global__ __launch_bounds__(512) void gemm_w8a8_wide_kernel(
+template <int WM, int FN, Out OUT, typename YT>
+__global__ __launch_bounds__(WM * 2 * 64) void gemm_w8a8_wide_kernel(
     const int8_t* __restrict__ xq, const float* __restrict__ as, const int8_t* __restrict__ wq,
     const float* __restrict__ ws, const float* __restrict__ bias, YT* __restrict__ y,
     int32_t* __restrict__ acc_out, int m, int n, int k, int tiles_m, int tiles_n) {
-    using S = WideShape<FN>;
+    using S = WideShape<WM, FN>;
     constexpr int NW = S::kWaves, Q = S::kQ, XB = S::kXB, NB = S::kNB, BM = S::kBM, BN = S::kBN, D = S::kD;
     extern __shared__ __attribute__((aligned(16))) int8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -406,14 +406,15 @@ __global__ __launch_bounds__(512) void gemm_w8a8_wide_kernel(
         if ((n & 7) == 0) {
             typedef _Float16 h4 __attribute__((ext_vector_type(4)));
             constexpr int CPR = BN / 8;  // 16-byte chunks per tile row
+            constexpr int HW = WM / 2, HR = BM / 2;  // wave rows and tile rows per half
 #pragma unroll
             for (int half = 0; half < 2; ++half) {
                 __syncthreads();  // the ring (first half) or the staging rows (second) are free
-                if (wm / 2 == half) {
+                if (wm / HW == half) {
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const int rl = (wm % 2) * 64 + j * 16 + row_in;  // row within the half
-                        const int row = m0 + half * 128 + rl;
+                        const int rl = (wm % HW) * 64 + j * 16 + row_in;  // row within the half
+                        const int row = m0 + half * HR + rl;
                         const float a_s = row < m ? as[row] : 0.0f;
 #pragma unroll
                         for (int i = 0; i < FN; ++i) {
@@ -429,9 +430,9 @@ __global__ __launch_bounds__(512) void gemm_w8a8_wide_kernel(
                     }
                 }
                 __syncthreads();
-                for (int c = tid; c < 128 * CPR; c += NW * 64) {
+                for (int c = tid; c < HR * CPR; c += NW * 64) {
                     const int rl = c / CPR, cc = c % CPR;
-                    const int row = m0 + half * 128 + rl, col = n0 + cc * 8;
+                    const int row = m0 + half * HR + rl, col = n0 + cc * 8;
                     if (row < m && col < n)
                         __builtin_nontemporal_store(*reinterpret_cast<const v4i*>(lds + (rl * BN + cc * 8) * 2),
                                                     reinterpret_cast<v4i*>(y + static_cast<size_t>(row) * n + col));
@@ -696,8 +697,9 @@ nq_status gemm_skinny(const int8_t* xq, const float* as, const int8_t* wq, const
     return reduce_partials(parts, p.splits, as, ws, bias, y, ydt, acc_out, mi, ni, s);
 }
 
-// Big-m plan. When 256 x (32*fn) tiles, fn = 8..10, number between 192 and 256
-// (one per CU, one round) the wide-tile kernel runs. Otherwise 256 x 128 tiles
+// Big-m plan. When 256 x (32*fn) tiles, fn = 8..10, or else 128 x (32*fn)
+// tiles number between 192 and 256 (one per CU, one round), the wide-tile
+// kernel runs (smallest fn that fits, 256-row tiles first). Otherwise 256 x 128 tiles
 // (8 waves, 3-slab ring) when they give at least two tiles per CU, else
 // 128 x 128 tiles (4 waves, 4-slab ring). A lone workgroup pulls only ~30 GB/s
 // from memory, so when there are fewer than 256 tiles K is split over
@@ -708,22 +710,26 @@ nq_status gemm_skinny(const int8_t* xq, const float* as, const int8_t* wq, const
 struct PrefillPlan {
     bool big;
     int wide_fn;  // 0: not wide
+    int wide_wm;  // wide tile rows / 64
     int tiles, splits, k_slabs;
     size_t acc_bytes;
 };
 PrefillPlan plan_prefill(int64_t m, int64_t n, int64_t k) {
     PrefillPlan p{};
-    for (int fn = 8; fn <= 10; ++fn) {
-        const int64_t t = ((m + 255) / 256) * ((n + 32 * fn - 1) / (32 * fn));
-        if (t <= 256) {
-            if (t >= 192) {
-                p.wide_fn = fn;
-                p.tiles = static_cast<int>(t);
-                p.splits = 1;
-                p.k_slabs = std::max(1, static_cast<int>(k / kBK));
-                return p;
+    for (int wm = 4; wm >= 2; wm -= 2) {
+        for (int fn = 8; fn <= 10; ++fn) {
+            const int64_t t = ((m + 64 * wm - 1) / (64 * wm)) * ((n + 32 * fn - 1) / (32 * fn));
+            if (t <= 256) {
+                if (t >= 192) {
+                    p.wide_fn = fn;
+                    p.wide_wm = wm;
+                    p.tiles = static_cast<int>(t);
+                    p.splits = 1;
+                    p.k_slabs = std::max(1, static_cast<int>(k / kBK));
+                    return p;
+                }
+                break;
             }
-            break;
         }
     }
     const int64_t big_tiles = ((m + 255) / 256) * ((n + 127) / 128);
@@ -755,11 +761,11 @@ nq_status launch_prefill(const int8_t* xq, const float* as, const int8_t* wq, co
     return launch_status("gemm_w8a8_prefill_kernel");
 }
 
-template <int FN, Out OUT, typename YT>
+template <int WM, int FN, Out OUT, typename YT>
 nq_status launch_wide(const int8_t* xq, const float* as, const int8_t* wq, const float* ws, const float* bias,
                       YT* y, int32_t* acc_out, int m, int n, int k, hipStream_t s) {
-    using S = WideShape<FN>;
-    auto* fn = gemm_w8a8_wide_kernel<FN, OUT, YT>;
+    using S = WideShape<WM, FN>;
+    auto* fn = gemm_w8a8_wide_kernel<WM, FN, OUT, YT>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                                        static_cast<int>(S::kLds));
@@ -775,17 +781,22 @@ nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const fl
     const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
     const PrefillPlan p = plan_prefill(m, n, k);
     if (p.wide_fn) {
-        auto wide = [&](auto fntag) -> nq_status {
-            constexpr int FN = decltype(fntag)::value;
-            if (acc_out) return launch_wide<FN, Out::ACC, float>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, s);
+        auto wide = [&](auto wmtag, auto fntag) -> nq_status {
+            constexpr int WM = decltype(wmtag)::value, FN = decltype(fntag)::value;
+            if (acc_out)
+                return launch_wide<WM, FN, Out::ACC, float>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, s);
             if (ydt == NQ_F32)
-                return launch_wide<FN, Out::Y, float>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi, ni, ki, s);
-            return launch_wide<FN, Out::Y, _Float16>(xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr, mi, ni,
-                                                     ki, s);
+                return launch_wide<WM, FN, Out::Y, float>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi,
+                                                          ni, ki, s);
+            return launch_wide<WM, FN, Out::Y, _Float16>(xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr,
+                                                         mi, ni, ki, s);
         };
-        if (p.wide_fn == 8) return wide(std::integral_constant<int, 8>{});
-        if (p.wide_fn == 9) return wide(std::integral_constant<int, 9>{});
-        return wide(std::integral_constant<int, 10>{});
+        auto by_fn = [&](auto wmtag) -> nq_status {
+            if (p.wide_fn == 8) return wide(wmtag, std::integral_constant<int, 8>{});
+            if (p.wide_fn == 9) return wide(wmtag, std::integral_constant<int, 9>{});
+            return wide(wmtag, std::integral_constant<int, 10>{});
+        };
+        return p.wide_wm == 4 ? by_fn(std::integral_constant<int, 4>{}) : by_fn(std::integral_constant<int, 2>{});
     }
     int32_t* parts = nullptr;
     if (p.splits > 1) {
