@@ -497,9 +497,16 @@ template <int TM, int TN, Out OUT, typename YT>
 __global__ __launch_bounds__(1024) void gemm_w8a8_skinny_kernel(
     const int8_t* __restrict__ xq, const float* __restrict__ as, const int8_t* __restrict__ wq,
     const float* __restrict__ ws, const float* __restrict__ bias, YT* __restrict__ y,
-    int32_t* __restrict__ acc_out, int m, int n, int k, int k_split) {
+    int32_t* __restrict__ acc_out, int m_total, int n, int k, int k_split) {
     constexpr int PD = 3;  // steps in flight per wave
     __shared__ int tile[TM][TN][4][64];
+    // gridDim.z blocks of 64 activation rows (m > 64 in one launch); split
+    // planes keep the full [m_total, n] layout.
+    const size_t row_base = static_cast<size_t>(blockIdx.z) * 64;
+    const int m = min(64, m_total - static_cast<int>(row_base));
+    xq += row_base * k;
+    if (as) as += row_base;
+    const size_t out_base = row_base * n;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nthr = blockDim.x;
     const int nw = nthr >> 6;
     const int n0 = blockIdx.x * (TN * 16);
@@ -583,9 +590,9 @@ __global__ __launch_bounds__(1024) void gemm_w8a8_skinny_kernel(
         const int row = i * 16 + (l >> 4) * 4 + v, col = n0 + j * 16 + (l & 15);
         if (row >= m || col >= n) continue;
         const int sum = tile[i][j][v][l];
-        const size_t o = static_cast<size_t>(row) * n + col;
+        const size_t o = out_base + static_cast<size_t>(row) * n + col;
         if (split) {
-            acc_out[static_cast<size_t>(blockIdx.y) * m * n + o] = sum;  // this range's plane
+            acc_out[static_cast<size_t>(blockIdx.y) * m_total * n + o] = sum;  // this range's plane
         } else if constexpr (OUT == Out::ACC) {
             acc_out[o] = sum;
         } else {
@@ -627,7 +634,7 @@ struct SkinnyPlan {
 };
 SkinnyPlan plan_skinny(int64_t m, int64_t n, int64_t k) {
     SkinnyPlan p{};
-    p.tm = static_cast<int>((m + 15) / 16);
+    p.tm = static_cast<int>((std::min<int64_t>(m, kSkinnyMaxM) + 15) / 16);
     p.tn = (n + 31) / 32 >= 128 ? 2 : 1;
     p.ntiles = static_cast<int>((n + 16 * p.tn - 1) / (16 * p.tn));
     const int64_t kslabs = (k + kBK - 1) / kBK;
@@ -668,7 +675,8 @@ nq_status gemm_skinny(const int8_t* xq, const float* as, const int8_t* wq, const
         NQ_REQUIRE(aligned(workspace, 256), NQ_BAD_ALIGN, "w8a8 gemm: workspace must be 256-byte aligned");
         parts = static_cast<int32_t*>(workspace);
     }
-    const dim3 grid(static_cast<unsigned>(p.ntiles), static_cast<unsigned>(p.splits));
+    const dim3 grid(static_cast<unsigned>(p.ntiles), static_cast<unsigned>(p.splits),
+                    static_cast<unsigned>((m + kSkinnyMaxM - 1) / kSkinnyMaxM));
     const int threads = p.waves * 64;
     const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
     auto go = [&](auto tmtag, auto tntag) {
@@ -828,10 +836,17 @@ nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const fl
 // Workspace of the MFMA GEMM for this shape: a split plan's int32
 // accumulator (skinny plans for m <= 64, the prefill plan above, and the
 // skinny 64-row blocks that shapes outside the prefill contract run).
+// One skinny launch covers all m rows (64-row blocks over gridDim.z) when its
+// split planes stay within 64 MiB.
+bool skinny_one_launch(int64_t m, int64_t n, int64_t k) {
+    return (m + kSkinnyMaxM - 1) / kSkinnyMaxM <= 65535 && plan_skinny(m, n, k).acc_bytes <= (size_t(64) << 20);
+}
+
 size_t gemm_ws_bytes(int64_t m, int64_t n, int64_t k) {
     if (m <= 0 || n <= 0 || k <= 0) return 0;
     if (m <= kSkinnyMaxM) return plan_skinny(m, n, k).acc_bytes;
-    return std::max(plan_prefill(m, n, k).acc_bytes, plan_skinny(kSkinnyMaxM, n, k).acc_bytes);
+    const size_t sk = skinny_one_launch(m, n, k) ? plan_skinny(m, n, k).acc_bytes : plan_skinny(kSkinnyMaxM, n, k).acc_bytes;
+    return std::max(plan_prefill(m, n, k).acc_bytes, sk);
 }
 
 nq_status check_w8a8(int64_t m, int64_t n, int64_t k, int path, const char* who) {
@@ -881,10 +896,16 @@ nq_status run_gemm(const int8_t* xq, const float* as, const int8_t* wq, const fl
     if (p == NQ_PATH_MFMA) {
         if (m <= kSkinnyMaxM)
             return gemm_skinny(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, workspace, ws_bytes, s);
+        // (The skinny kernel over 64-row blocks in one launch was measured on the
+        // m = 512 decoder shapes too: qkv 12.9 -> 20.7 us, down 29.6 -> 78 us
+        // against the split prefill plan, so it only takes what the prefill
+        // kernel cannot.)
         if (prefill_ok(m, n, k))
             return gemm_big(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, workspace, ws_bytes, s);
-        // Shapes outside the prefill kernel's contract run the skinny kernel on
-        // 64-row blocks (each block re-streams the weight).
+        if (skinny_one_launch(m, n, k))
+            return gemm_skinny(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, workspace, ws_bytes, s);
+        // Otherwise the skinny kernel on 64-row blocks, one launch each (each
+        // block re-streams the weight).
         for (int64_t r0 = 0; r0 < m; r0 += kSkinnyMaxM) {
             const int64_t mm = std::min<int64_t>(kSkinnyMaxM, m - r0);
             char* yp = y ? static_cast<char*>(y) + static_cast<size_t>(r0 * n) * dtype_size(ydt) : nullptr;

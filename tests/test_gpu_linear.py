@@ -357,7 +357,10 @@ def test_w8a8_workspace_reuse_and_gemm_entry(dev, nq, orc):
                                    (1800, 6000, 192), (1900, 7996, 128), (2048, 10000, 64), (1700, 8191, 64),
                                    (1537, 9000, 64),
                                    # 128-row wide tiles (m = 512 class), ragged m and n, n odd
-                                   (512, 17920, 192), (400, 15000, 64), (450, 16001, 64)])
+                                   (512, 17920, 192), (400, 15000, 64), (450, 16001, 64),
+                                   # k % 64 != 0: the skinny kernel over 64-row blocks in one launch,
+                                   # with split K and its partial planes for the long k
+                                   (200, 1000, 528), (130, 512, 6160)])
 def test_w8a8_prefill_plans_exact(dev, nq, orc, m, n, k):
     """Every prefill plan (wide 256 x 256..320 tiles, 256x128 / 128x128 tiles,
     split K with int32 partial planes) gives the GEMV path's accumulators bit for bit, and the linear's
