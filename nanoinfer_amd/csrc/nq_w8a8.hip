@@ -709,14 +709,15 @@ nq_status gemm_skinny(const int8_t* xq, const float* as, const int8_t* wq, const
 // tiles number between 192 and 256 (one per CU, one round), the wide-tile
 // kernel runs (smallest fn that fits, 256-row tiles first). Otherwise 256 x 128 tiles
 // (8 waves, 3-slab ring) when they give at least two tiles per CU, else
-// 128 x 128 tiles (4 waves, 4-slab ring). A lone workgroup pulls only ~30 GB/s
-// from memory, so when there are fewer than 256 tiles K is split over
-// workgroups (at least 8 slabs each) until there are about 256: each range
-// stores its int32 partial tile into its own workspace plane and a reduction
-// launch sums the planes and applies the epilogue (device-scope atomics into
-// one plane measured several times slower).
+// 128 x 128 tiles (4 waves, 4-slab ring; 64 x 128 with 2 waves for short K and
+// few tiles). With fewer than 256 tiles a long K is split over workgroups in
+// ranges of at least 32 slabs: each range stores its int32 partial tile into
+// its own workspace plane and a reduction launch sums the planes and applies
+// the epilogue (device-scope atomics into one plane measured several times
+// slower).
 struct PrefillPlan {
     bool big;
+    bool narrow;  // 64 x 128 tiles
     int wide_fn;  // 0: not wide
     int wide_wm;  // wide tile rows / 64
     int tiles, splits, k_slabs;
@@ -745,7 +746,18 @@ PrefillPlan plan_prefill(int64_t m, int64_t n, int64_t k) {
     p.tiles = static_cast<int>(p.big ? big_tiles : ((m + 127) / 128) * ((n + 127) / 128));
     const int nk = std::max(1, static_cast<int>(k / kBK));  // also sized for shapes outside the contract
     int splits = 1;
-    if (p.tiles < 256) splits = std::max(1, std::min<int>(static_cast<int>((256 + p.tiles - 1) / p.tiles), nk / 8));
+    // Fewer than 256 tiles: K splits into ranges of at least 32 slabs (the
+    // partial planes and the reduction launch cost more than a short K loop
+    // saves: m = 512, n = 1536, k = 1536 ran 13.0 us unsplit vs 15.4 in three
+    // ranges; k = 8960 ran best in four ranges, 25.3 us vs 29.5 in six). Short-K
+    // shapes left with fewer than 128 tiles use 64 x 128 tiles instead.
+    if (p.tiles < 256) {
+        splits = std::max(1, nk / 32);
+        if (splits == 1 && p.tiles < 128) {
+            p.narrow = true;
+            p.tiles = static_cast<int>(((m + 63) / 64) * ((n + 127) / 128));
+        }
+    }
     // at most 64 MiB of partial planes
     splits = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(splits, (int64_t(64) << 20) / std::max<int64_t>(1, m * n * 4))));
     p.k_slabs = (nk + splits - 1) / splits;
@@ -813,22 +825,23 @@ nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const fl
         NQ_REQUIRE(aligned(workspace, 256), NQ_BAD_ALIGN, "w8a8 gemm: workspace must be 256-byte aligned");
         parts = static_cast<int32_t*>(workspace);
     }
-    auto go = [&](auto wmtag, auto dtag) -> nq_status {
-        constexpr int WM = decltype(wmtag)::value, D = decltype(dtag)::value;
+    auto go = [&](auto wmtag, auto wntag, auto dtag) -> nq_status {
+        constexpr int WM = decltype(wmtag)::value, WN = decltype(wntag)::value, D = decltype(dtag)::value;
         if (p.splits > 1)
-            return launch_prefill<WM, 2, D, Out::PARTIAL, float>(xq, as, wq, ws, bias, nullptr, parts, mi, ni, ki,
-                                                                p.splits, p.k_slabs, s);
+            return launch_prefill<WM, WN, D, Out::PARTIAL, float>(xq, as, wq, ws, bias, nullptr, parts, mi, ni, ki,
+                                                                 p.splits, p.k_slabs, s);
         if (acc_out)
-            return launch_prefill<WM, 2, D, Out::ACC, float>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, 1,
-                                                            p.k_slabs, s);
+            return launch_prefill<WM, WN, D, Out::ACC, float>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, 1,
+                                                             p.k_slabs, s);
         if (ydt == NQ_F32)
-            return launch_prefill<WM, 2, D, Out::Y, float>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi,
-                                                          ni, ki, 1, p.k_slabs, s);
-        return launch_prefill<WM, 2, D, Out::Y, _Float16>(xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr,
-                                                         mi, ni, ki, 1, p.k_slabs, s);
+            return launch_prefill<WM, WN, D, Out::Y, float>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi,
+                                                           ni, ki, 1, p.k_slabs, s);
+        return launch_prefill<WM, WN, D, Out::Y, _Float16>(xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr,
+                                                          mi, ni, ki, 1, p.k_slabs, s);
     };
-    const nq_status st = p.big ? go(std::integral_constant<int, 4>{}, std::integral_constant<int, 3>{})
-                               : go(std::integral_constant<int, 2>{}, std::integral_constant<int, 4>{});
+    const nq_status st = p.big      ? go(std::integral_constant<int, 4>{}, std::integral_constant<int, 2>{}, std::integral_constant<int, 3>{})
+                         : p.narrow ? go(std::integral_constant<int, 1>{}, std::integral_constant<int, 2>{}, std::integral_constant<int, 4>{})
+                                    : go(std::integral_constant<int, 2>{}, std::integral_constant<int, 2>{}, std::integral_constant<int, 4>{});
     if (st != NQ_OK || p.splits == 1) return st;
     return reduce_partials(parts, p.splits, as, ws, bias, y, ydt, acc_out, mi, ni, s);
 }
