@@ -96,6 +96,15 @@ nq_status nq_linear_q8(const void* x, nq_dtype x_dtype, const int8_t* q, const f
                        const float* bias, void* y, nq_dtype y_dtype, int64_t m, int64_t n,
                        int64_t k, void* stream);
 
+/* ---- decoder-caller support (outside the quantized matrix path) ----------------
+ * RoPE of the q and k heads of a fused q|k|v output (ops.cpp:120-166: half-split
+ * tables, x*cos + rotate_half(x)*sin in fp32) written head-major q [heads, s, d],
+ * k [kv, s, d], with v copied to [kv, s, d]: the layout the attention takes.
+ * qkv [s, ld] (ld >= (heads + 2 kv) d), cos/sin fp32 [>= s, d]. */
+nq_status nq_rope_qkv(const void* qkv, nq_dtype dtype, int64_t s, int64_t ld, int64_t heads, int64_t kv_heads,
+                      int64_t head_dim, const float* cos, const float* sin, void* q, void* k, void* v,
+                      void* stream);
+
 /* ---- weight files: quantize on load -------------------------------------------
  * NIT0 / NIT1 files (serialize.hpp:1-23; load_bin serialize.cpp:11-72): the same
  * header checks as load_bin (bad magic, unknown dtype, negative ndim or dim,

@@ -40,6 +40,7 @@ SIGNATURES = {
     "nq_gemm_w8a8": (_D, [_P, _P, _P, _P, _P, _P, _D, _I, _I, _I, _P, _Z, ctypes.c_int, _P]),
     "nq_w8a8_acc_i32": (_D, [_P, _P, _P, _I, _I, _I, _P, _Z, ctypes.c_int, _P]),
     "nq_embedding_q8": (_D, [_P, _P, _I, _I, _P, _I, _P, _D, _P]),
+    "nq_rope_qkv": (_D, [_P, _D, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
     "nq_nit_info": (_D, [ctypes.c_char_p, _P, _P, _P, ctypes.c_int32]),
     "nq_nit_load_f32": (_D, [ctypes.c_char_p, _P, _I, _P]),
     "nq_nit_load_q8": (_D, [ctypes.c_char_p, _P, _P, _I, _I, _P]),

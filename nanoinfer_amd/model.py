@@ -112,6 +112,22 @@ def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
     return x * cos[:s].to(x.dtype) + rot * sin[:s].to(x.dtype)
 
 
+def rope_qkv(qkv: torch.Tensor, heads: int, kv_heads: int, head_dim: int, cos: torch.Tensor, sin: torch.Tensor):
+    """One launch for the fused q|k|v output [s, (heads + 2 kv) d]: RoPE on q and
+    k (ops.cpp:145-166) and all three written head-major [h, s, d]."""
+    from ._lib import check, load
+    s = qkv.shape[0]
+    if qkv.stride(1) != 1 or cos.dtype != torch.float32 or cos.shape[0] < s:
+        raise ValueError("rope_qkv: unit column stride, fp32 tables of >= s rows required")
+    q = torch.empty((heads, s, head_dim), dtype=qkv.dtype, device=qkv.device)
+    k = torch.empty((kv_heads, s, head_dim), dtype=qkv.dtype, device=qkv.device)
+    v = torch.empty_like(k)
+    dt = quant._dtype_code(qkv, "qkv")
+    check(load().nq_rope_qkv(qkv.data_ptr(), dt, s, qkv.stride(0), heads, kv_heads, head_dim, cos.data_ptr(),
+                             sin.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), quant._stream()))
+    return q, k, v
+
+
 def attention(q, k, v, n_rep: int) -> torch.Tensor:
     """ops.cpp:206-270: causal softmax(q k^T / sqrt(d)) v with the KV heads
     repeated n_rep times (GQA); scores and softmax in fp32. fp16 activations use
@@ -224,16 +240,13 @@ class Model:
         hq, hkv = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
         if self.fused:
             qkv = self.gemm(quant.rmsnorm_quant(x, self.norm[L + "input_layernorm"], cfg.eps), L + "self_attn.qkv_proj")
-            q, k, v = qkv.split([hq, hkv, hkv], 1)
+            q, k, v = rope_qkv(qkv, cfg.heads, cfg.kv_heads, cfg.head_dim, self.cos, self.sin)
         else:
             h = rmsnorm(x, self.norm[L + "input_layernorm"], cfg.eps)
-            q = self.project(h, L + "self_attn.q_proj")
-            k = self.project(h, L + "self_attn.k_proj")
-            v = self.project(h, L + "self_attn.v_proj")
-        q = q.reshape(s, cfg.heads, cfg.head_dim).transpose(0, 1)
-        k = k.reshape(s, cfg.kv_heads, cfg.head_dim).transpose(0, 1)
-        v = v.reshape(s, cfg.kv_heads, cfg.head_dim).transpose(0, 1)
-        q, k = apply_rope(q, self.cos, self.sin), apply_rope(k, self.cos, self.sin)
+            q = self.project(h, L + "self_attn.q_proj").reshape(s, cfg.heads, cfg.head_dim).transpose(0, 1)
+            k = self.project(h, L + "self_attn.k_proj").reshape(s, cfg.kv_heads, cfg.head_dim).transpose(0, 1)
+            v = self.project(h, L + "self_attn.v_proj").reshape(s, cfg.kv_heads, cfg.head_dim).transpose(0, 1)
+            q, k = apply_rope(q, self.cos, self.sin), apply_rope(k, self.cos, self.sin)
         a = attention(q, k, v, cfg.n_rep).transpose(0, 1).reshape(s, hq).contiguous()
         x = x + self.project(a, L + "self_attn.o_proj")
         if self.fused:

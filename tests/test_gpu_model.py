@@ -62,3 +62,23 @@ def test_model_from_nit_dir(dev, tmp_path, payload):
     a = model.Model(cfg, loaded, quant.QuantMode.W8A8, dev)
     b = model.Model(cfg, w, quant.QuantMode.W8A8, dev)
     assert a.generate(PROMPT, 6) == b.generate(PROMPT, 6)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+def test_rope_qkv_matches_torch(dev, dt):
+    """nq_rope_qkv equals the tensor-op RoPE (apply_rope) on the split heads."""
+    from nanoinfer_amd import model
+    cfg = model.Config(hidden=256, heads=12, kv_heads=2, head_dim=128, intermediate=512, layers=1, vocab=64,
+                       max_pos=96)
+    cos, sin = model.rope_tables(cfg, dev)
+    s, hq, hkv = 77, 12 * 128, 2 * 128
+    g = torch.Generator(device=dev).manual_seed(4)
+    qkv = torch.randn((s, hq + 2 * hkv + 8), generator=g, device=dev).to(dt)[:, : hq + 2 * hkv]   # ld > width
+    q, k, v = model.rope_qkv(qkv, 12, 2, 128, cos, sin)
+    rq, rk, rv = qkv.float().split([hq, hkv, hkv], 1)
+    rq = model.apply_rope(rq.reshape(s, 12, 128).transpose(0, 1), cos, sin)
+    rk = model.apply_rope(rk.reshape(s, 2, 128).transpose(0, 1), cos, sin)
+    rv = rv.reshape(s, 2, 128).transpose(0, 1)
+    tol = 1e-5 if dt == torch.float32 else 2e-3
+    assert torch.allclose(q.float(), rq, atol=tol, rtol=tol) and torch.allclose(k.float(), rk, atol=tol, rtol=tol)
+    assert torch.equal(v.float(), rv)
