@@ -314,10 +314,7 @@ def decoder_layer_cfg4(rnd, time_graph, args, w8a8_linear, entry):
     x0 = rnd((m, cfg.hidden), 1.0, torch.float16)
 
     def run_layers():
-        x = x0
-        for li in range(L):
-            x = mdl.layer(x, li)
-        return x
+        return mdl.run_layers(x0)
     steps = max(2, args.steps // L)
     ms = time_graph([run_layers], steps, max(1, args.warmup // L)) / L
     proj_ops = sum(2 * m * o * i for o, i in shapes.values())

@@ -85,6 +85,12 @@ nq_status nq_act_quant_i8(const void* x, nq_dtype x_dtype, int64_t m, int64_t k,
  * silu_mul: y = gate / (1 + exp(-gate)) * up, gate and up rows at stride ld. */
 nq_status nq_rmsnorm_quant_i8(const void* x, nq_dtype x_dtype, const float* w, float eps, int64_t m,
                               int64_t k, int8_t* xq, float* a_scale, void* stream);
+/* The residual add before a norm fused in as well: h = x + r (stored to h as the
+ * tensor add would, fp32 sum rounded once to the dtype; h may be x), then the
+ * rmsnorm + act quant of nq_rmsnorm_quant_i8 on h (model.cpp:175-186: x += attn
+ * / mlp output, then the next pre-norm). */
+nq_status nq_add_rmsnorm_quant_i8(const void* x, const void* r, nq_dtype dtype, const float* w, float eps,
+                                  int64_t m, int64_t k, void* h, int8_t* xq, float* a_scale, void* stream);
 nq_status nq_silu_mul_quant_i8(const void* gate, const void* up, nq_dtype dtype, int64_t m, int64_t k,
                                int64_t ld, int8_t* xq, float* a_scale, void* stream);
 

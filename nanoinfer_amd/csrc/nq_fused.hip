@@ -77,6 +77,15 @@ struct Vec8<float> {
         b = reinterpret_cast<const f4*>(p)[1];
     }
     __device__ __forceinline__ float at(int j) const { return j < 4 ? a[j] : b[j - 4]; }
+    // this = u + v, element-wise in fp32 (the sum a tensor add would store)
+    __device__ __forceinline__ void set_sum(const Vec8& u, const Vec8& v) {
+        a = u.a + v.a;
+        b = u.b + v.b;
+    }
+    __device__ __forceinline__ void store(float* p) const {
+        reinterpret_cast<f4*>(p)[0] = a;
+        reinterpret_cast<f4*>(p)[1] = b;
+    }
 };
 template <>
 struct Vec8<_Float16> {
@@ -84,13 +93,22 @@ struct Vec8<_Float16> {
     h8 a;
     __device__ __forceinline__ void load(const _Float16* p) { a = *reinterpret_cast<const h8*>(p); }
     __device__ __forceinline__ float at(int j) const { return static_cast<float>(a[j]); }
+    // fp32 sum rounded once to fp16, as an fp16 tensor add stores it
+    __device__ __forceinline__ void set_sum(const Vec8& u, const Vec8& v) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a[j] = from_f32<_Float16>(u.at(j) + v.at(j));
+    }
+    __device__ __forceinline__ void store(_Float16* p) const { *reinterpret_cast<h8*>(p) = a; }
 };
 
 // rmsnorm + quant: x row [k] (k % 8 == 0, 16-byte aligned rows), w fp32 [k].
-template <typename XT, int CPT, int NT>
+// ADD: the row is first h = x + r (the residual add that precedes the norm),
+// stored to h as a tensor add would, and the norm runs on h.
+template <typename XT, int CPT, int NT, bool ADD = false>
 __global__ __launch_bounds__(NT) void rmsnorm_quant_kernel(const XT* __restrict__ x, const float* __restrict__ w,
                                                            float eps, int k, int8_t* __restrict__ xq,
-                                                           float* __restrict__ a_scale) {
+                                                           float* __restrict__ a_scale, const XT* __restrict__ r = nullptr,
+                                                           XT* h = nullptr) {
     __shared__ float red[NT / 64];
     const int row = blockIdx.x, tid = threadIdx.x, steps = k >> 3;
     const XT* xr = x + static_cast<size_t>(row) * k;
@@ -102,6 +120,18 @@ __global__ __launch_bounds__(NT) void rmsnorm_quant_kernel(const XT* __restrict_
         xv[c].load(xr + 8 * e);
         wv[c][0] = reinterpret_cast<const f4*>(w + 8 * e)[0];
         wv[c][1] = reinterpret_cast<const f4*>(w + 8 * e)[1];
+    }
+    if constexpr (ADD) {
+        const XT* rr = r + static_cast<size_t>(row) * k;
+        Vec8<XT> rv[CPT];
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) rv[c].load(rr + 8 * min(tid + c * NT, steps - 1));
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            xv[c].set_sum(xv[c], rv[c]);
+            // h may alias x: every element is read above before this thread writes it
+            if (tid + c * NT < steps) xv[c].store(h + static_cast<size_t>(row) * k + 8 * (tid + c * NT));
+        }
     }
     __builtin_amdgcn_sched_barrier(0);  // every load issued before the math (the scheduler interleaved them)
     float ss = 0.0f;
@@ -269,6 +299,50 @@ extern "C" nq_status nq_rmsnorm_quant_i8(const void* x, nq_dtype x_dtype, const 
     if (x_dtype == NQ_F32) go(static_cast<const float*>(x));
     else go(static_cast<const _Float16*>(x));
     return launch_status("rmsnorm_quant_i8");
+}
+
+__global__ void add_rows_kernel(const float* x, const float* r, float* h, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) h[i] = x[i] + r[i];
+}
+__global__ void add_rows_kernel(const _Float16* x, const _Float16* r, _Float16* h, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) h[i] = from_f32<_Float16>(static_cast<float>(x[i]) + static_cast<float>(r[i]));
+}
+
+extern "C" nq_status nq_add_rmsnorm_quant_i8(const void* x, const void* r, nq_dtype dtype, const float* w, float eps,
+                                             int64_t m, int64_t k, void* h, int8_t* xq, float* a_scale,
+                                             void* stream) {
+    if (nq_status st = check_fused(m, k, xq, a_scale, dtype, "add_rmsnorm_quant_i8")) return st;
+    if (m == 0) return NQ_OK;
+    NQ_REQUIRE(k > 0, NQ_BAD_SHAPE, "add_rmsnorm_quant_i8: k must be positive");
+    NQ_REQUIRE(x && r && h && w, NQ_BAD_ARG, "add_rmsnorm_quant_i8: null pointer");
+    const size_t es = dtype_size(dtype);
+    NQ_REQUIRE(aligned(x, es) && aligned(r, es) && aligned(h, es) && aligned(w, 4), NQ_BAD_ALIGN,
+               "add_rmsnorm_quant_i8: misaligned pointer");
+    hipStream_t s = as_stream(stream);
+    const unsigned grid = static_cast<unsigned>(m);
+    const int ki = static_cast<int>(k);
+    const bool vec = k % 8 == 0 && k <= 32768 && aligned(x, 16) && aligned(r, 16) && aligned(h, 16) &&
+                     aligned(w, 16) && aligned(xq, 8);
+    auto go = [&](auto* xp, auto* rp, auto* hp) {
+        using XT = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
+        if (vec) {
+            by_shape(m, k, [&](auto cpt, auto nt) {
+                rmsnorm_quant_kernel<XT, decltype(cpt)::value, decltype(nt)::value, true>
+                    <<<grid, decltype(nt)::value, 0, s>>>(xp, w, eps, ki, xq, a_scale, rp, hp);
+            });
+        } else {
+            const int64_t n = m * k;
+            add_rows_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(xp, rp, hp, n);
+            fused_quant_generic_kernel<XT, true><<<grid, 256, 0, s>>>(hp, nullptr, w, eps, k, ki, xq, a_scale);
+        }
+    };
+    if (dtype == NQ_F32)
+        go(static_cast<const float*>(x), static_cast<const float*>(r), static_cast<float*>(h));
+    else
+        go(static_cast<const _Float16*>(x), static_cast<const _Float16*>(r), static_cast<_Float16*>(h));
+    return launch_status("add_rmsnorm_quant_i8");
 }
 
 extern "C" nq_status nq_silu_mul_quant_i8(const void* gate, const void* up, nq_dtype dtype, int64_t m, int64_t k,

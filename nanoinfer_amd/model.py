@@ -233,13 +233,19 @@ class Model:
         xq, a_s = xq_as
         return quant.gemm_w8a8(xq, a_s, self.proj[name].t, self.bias.get(name), out_dtype=self.act_dtype)
 
-    def layer(self, x: torch.Tensor, li: int) -> torch.Tensor:
-        """One pre-norm decoder layer (model.cpp:166-190)."""
+    def layer(self, x: torch.Tensor, li: int, pending=None):
+        """One pre-norm decoder layer (model.cpp:166-190). In W8A8 mode the MLP
+        output is returned unadded, as (x, y): the residual add joins the next
+        norm (add_rmsnorm_quant); settle() adds a pending y. Other modes return x."""
         cfg, L = self.cfg, f"layers.{li}."
         s = x.shape[0]
         hq, hkv = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
         if self.fused:
-            qkv = self.gemm(quant.rmsnorm_quant(x, self.norm[L + "input_layernorm"], cfg.eps), L + "self_attn.qkv_proj")
+            if pending is None:
+                xq = quant.rmsnorm_quant(x, self.norm[L + "input_layernorm"], cfg.eps)
+            else:
+                x, *xq = quant.add_rmsnorm_quant(x, pending, self.norm[L + "input_layernorm"], cfg.eps)
+            qkv = self.gemm(tuple(xq), L + "self_attn.qkv_proj")
             q, k, v = rope_qkv(qkv, cfg.heads, cfg.kv_heads, cfg.head_dim, self.cos, self.sin)
         else:
             h = rmsnorm(x, self.norm[L + "input_layernorm"], cfg.eps)
@@ -248,22 +254,32 @@ class Model:
             v = self.project(h, L + "self_attn.v_proj").reshape(s, cfg.kv_heads, cfg.head_dim).transpose(0, 1)
             q, k = apply_rope(q, self.cos, self.sin), apply_rope(k, self.cos, self.sin)
         a = attention(q, k, v, cfg.n_rep).transpose(0, 1).reshape(s, hq).contiguous()
-        x = x + self.project(a, L + "self_attn.o_proj")
         if self.fused:
-            gu = self.gemm(quant.rmsnorm_quant(x, self.norm[L + "post_attention_layernorm"], cfg.eps),
-                           L + "mlp.gate_up_proj")
+            x, *xq = quant.add_rmsnorm_quant(x, self.project(a, L + "self_attn.o_proj"),
+                                             self.norm[L + "post_attention_layernorm"], cfg.eps)
+            gu = self.gemm(tuple(xq), L + "mlp.gate_up_proj")
             i = cfg.intermediate
-            return x + self.gemm(quant.silu_mul_quant(gu[:, :i], gu[:, i:]), L + "mlp.down_proj")
+            return x, self.gemm(quant.silu_mul_quant(gu[:, :i], gu[:, i:]), L + "mlp.down_proj")
+        x = x + self.project(a, L + "self_attn.o_proj")
         hm = rmsnorm(x, self.norm[L + "post_attention_layernorm"], cfg.eps)
         gate = torch.nn.functional.silu(self.project(hm, L + "mlp.gate_proj").float())
         up = self.project(hm, L + "mlp.up_proj").float()
         return x + self.project((gate * up).to(self.act_dtype).contiguous(), L + "mlp.down_proj")
 
+    @staticmethod
+    def settle(out) -> torch.Tensor:
+        """The residual stream after layer(): x, or x + the pending MLP output."""
+        return out[0] + out[1] if isinstance(out, tuple) else out
+
+    def run_layers(self, x: torch.Tensor) -> torch.Tensor:
+        out = x
+        for li in range(self.n_layers):
+            out = self.layer(out[0], li, out[1]) if isinstance(out, tuple) else self.layer(out, li)
+        return self.settle(out)
+
     def hidden(self, ids) -> torch.Tensor:
         """Final-norm hidden states [len(ids), hidden] for positions 0..len-1."""
-        x = self.embed_tokens(ids)
-        for li in range(self.n_layers):
-            x = self.layer(x, li)
+        x = self.run_layers(self.embed_tokens(ids))
         return rmsnorm(x, self.final_norm, self.cfg.eps).contiguous()
 
     def forward(self, ids) -> torch.Tensor:

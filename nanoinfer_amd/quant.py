@@ -188,6 +188,24 @@ def rmsnorm_quant(x: torch.Tensor, w: torch.Tensor, eps: float):
     return xq, s
 
 
+def add_rmsnorm_quant(x: torch.Tensor, r: torch.Tensor, w: torch.Tensor, eps: float, inplace: bool = False):
+    """h = x + r (the residual add, model.cpp:175-186) and rmsnorm_quant(h) in one
+    launch: returns (h, xq, a_scale); with inplace=True h is written into x."""
+    x, r = _dev(x, "x"), _dev(r, "r")
+    if x.dim() != 2 or r.shape != x.shape or r.dtype != x.dtype or not x.is_contiguous() or not r.is_contiguous():
+        raise ValueError("add_rmsnorm_quant: x and r must be contiguous 2-D tensors of one shape and dtype")
+    m, k = x.shape
+    w = _dev(w, "w").to(torch.float32)
+    if w.numel() != k:
+        raise ValueError("add_rmsnorm_quant: weight must match the last dimension")
+    h = x if inplace else torch.empty_like(x)
+    xq = torch.empty((m, k), dtype=torch.int8, device=x.device)
+    s = torch.empty(m, dtype=torch.float32, device=x.device)
+    check(_lib.load().nq_add_rmsnorm_quant_i8(_ptr(x), _ptr(r), _dtype_code(x, "x"), _ptr(w), float(eps), m, k,
+                                              _ptr(h), _ptr(xq), _ptr(s), _stream()))
+    return h, xq, s
+
+
 def silu_mul_quant(gate: torch.Tensor, up: torch.Tensor):
     """silu(gate) * up (ops.cpp:86-100) with the act quant fused in. gate and up
     are [m, k] views with unit column stride and one common row stride (e.g. the

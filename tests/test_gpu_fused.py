@@ -59,3 +59,23 @@ def test_fused_errors(dev, nq):
         nq.rmsnorm_quant(x, torch.ones(8, device=dev), 1e-6)
     with pytest.raises(ValueError):
         nq.silu_mul_quant(x[:, :8], x[:, :4])
+
+
+@pytest.mark.parametrize("m,k,dt,inplace", [(1, 1536, torch.float16, False), (512, 1536, torch.float16, True),
+                                            (7, 1536, torch.float32, True), (5, 100, torch.float32, False),
+                                            (300, 8960, torch.float16, False)])
+def test_add_rmsnorm_quant(dev, nq, m, k, dt, inplace):
+    """h equals the tensor add x + r bit for bit; codes and scales follow the
+    fused rmsnorm quant of h (and equal nq.rmsnorm_quant(h) exactly)."""
+    rng = np.random.default_rng(m + k)
+    x = to_dev(rng.normal(0, 1, (m, k)).astype(np.float32), dev).to(dt)
+    r = to_dev(rng.normal(0, 1, (m, k)).astype(np.float32), dev).to(dt)
+    w = to_dev((1 + 0.1 * rng.normal(0, 1, k)).astype(np.float32), dev)
+    h_ref = x + r
+    x_in = x.clone()
+    h, xq, s = nq.add_rmsnorm_quant(x_in, r, w, 1e-6, inplace=inplace)
+    assert torch.equal(h, h_ref)
+    if inplace:
+        assert h.data_ptr() == x_in.data_ptr()
+    xq2, s2 = nq.rmsnorm_quant(h_ref, w, 1e-6)
+    assert torch.equal(xq, xq2) and torch.equal(s, s2)
