@@ -83,6 +83,13 @@ nq_status nq_act_quant_i8(const void* x, nq_dtype x_dtype, int64_t m, int64_t k,
  * (ops.cpp:86-100) and then linear_w8a8 on the materialised tensor
  * (model.cpp:176-190). rmsnorm: y = x * (1/sqrt(mean(x^2) + eps)) * w, w fp32 [k];
  * silu_mul: y = gate / (1 + exp(-gate)) * up, gate and up rows at stride ld. */
+/* The act quant of a head-major attention output x [heads, s, head_dim]: row p
+ * of the result is row p of the [s, heads * head_dim] matrix its transpose
+ * gives (the o_proj input, model.cpp:175-178), without materialising it. Same
+ * codes and scales as nq_act_quant_i8 on that matrix. head_dim % 8 == 0,
+ * heads * head_dim <= 16384, x 16-byte aligned. */
+nq_status nq_act_quant_i8_heads(const void* x, nq_dtype x_dtype, int64_t heads, int64_t s, int64_t head_dim,
+                                int8_t* xq, float* a_scale, void* stream);
 nq_status nq_rmsnorm_quant_i8(const void* x, nq_dtype x_dtype, const float* w, float eps, int64_t m,
                               int64_t k, int8_t* xq, float* a_scale, void* stream);
 /* The residual add before a norm fused in as well: h = x + r (stored to h as the

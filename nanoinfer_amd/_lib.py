@@ -28,6 +28,7 @@ SIGNATURES = {
     "nq_quantize_q8": (_D, [_P, _I, _I, _P, _P, _P]),
     "nq_quantize_q4g": (_D, [_P, _I, _I, _I, _P, _P, _D, _P]),
     "nq_act_quant_i8": (_D, [_P, _D, _I, _I, _P, _P, _P]),
+    "nq_act_quant_i8_heads": (_D, [_P, _D, _I, _I, _I, _P, _P, _P]),
     "nq_rmsnorm_quant_i8": (_D, [_P, _D, _P, ctypes.c_float, _I, _I, _P, _P, _P]),
     "nq_add_rmsnorm_quant_i8": (_D, [_P, _P, _D, _P, ctypes.c_float, _I, _I, _P, _P, _P, _P]),
     "nq_silu_mul_quant_i8": (_D, [_P, _P, _D, _I, _I, _I, _P, _P, _P]),

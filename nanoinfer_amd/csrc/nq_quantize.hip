@@ -105,20 +105,29 @@ __global__ void quantize_q4g_odd_kernel(const float* __restrict__ w, uint8_t* __
 // ---- activation quant (vectorized) ------------------------------
 // One workgroup per row, 8 elements per 16-byte step held in registers between
 // the absmax pass and the quantize pass (x is read once).
-template <typename XT, int CPT, int NT>
+// HEADS: x is head-major [k / hd, m, hd] (an attention output) and row `row`
+// is the concatenation of its heads' row-`row` segments, i.e. the rows of the
+// [m, k] matrix its transpose would produce (hd = 8 * epr elements per head).
+template <typename XT, int CPT, int NT, bool HEADS = false>
 __global__ __launch_bounds__(NT) void act_quant_vec_kernel(const XT* __restrict__ x, int8_t* __restrict__ xq,
-                                                           float* __restrict__ a_scale, int m, int k) {
+                                                           float* __restrict__ a_scale, int m, int k, int epr = 0) {
     __shared__ float red[NT / 64];
     const int tid = threadIdx.x;
     typedef XT v8 __attribute__((ext_vector_type(8)));
     const int row = blockIdx.x, steps = k >> 3;
-    const v8* xr = reinterpret_cast<const v8*>(x + static_cast<size_t>(row) * k);
+    const v8* xr = reinterpret_cast<const v8*>(x + static_cast<size_t>(row) * (HEADS ? 8 * epr : k));
     v8 v[CPT];
     float am = 0.0f;
     // Loads are unconditional (indices past the row re-read its last vector and
     // are left out of the absmax), so all CPT of them are in flight together.
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) v[c] = xr[min(tid + c * NT, steps - 1)];
+    for (int c = 0; c < CPT; ++c) {
+        const int e = min(tid + c * NT, steps - 1);
+        if constexpr (HEADS)
+            v[c] = xr[static_cast<size_t>(e / epr) * m * epr + e % epr];
+        else
+            v[c] = xr[e];
+    }
     __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the absmax math
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
@@ -226,6 +235,38 @@ extern "C" nq_status nq_quantize_q8(const float* w, int64_t out, int64_t in, int
     quantize_rows_i8_kernel<float><<<static_cast<unsigned>(out), kRowThreads, 0, as_stream(stream)>>>(
         w, q, scale, static_cast<int>(in));
     return launch_status("quantize_rows_i8_kernel");
+}
+
+extern "C" nq_status nq_act_quant_i8_heads(const void* x, nq_dtype x_dtype, int64_t heads, int64_t s,
+                                           int64_t head_dim, int8_t* xq, float* a_scale, void* stream) {
+    NQ_REQUIRE(heads >= 0 && s >= 0 && head_dim >= 0 && s <= kMaxIndex, NQ_BAD_SHAPE,
+               "nq_act_quant_i8_heads: negative shape");
+    NQ_REQUIRE(dtype_ok(x_dtype), NQ_BAD_ARG, "nq_act_quant_i8_heads: unknown x dtype %d", int(x_dtype));
+    const int64_t k = heads * head_dim;
+    NQ_REQUIRE(head_dim % 8 == 0 && k <= 16384 && (heads * s * head_dim) <= (int64_t(1) << 40), NQ_BAD_SHAPE,
+               "nq_act_quant_i8_heads: needs head_dim %% 8 == 0 and heads * head_dim <= 16384");
+    if (s == 0) return NQ_OK;
+    NQ_REQUIRE(a_scale && (k == 0 || (x && xq)), NQ_BAD_ARG, "nq_act_quant_i8_heads: null pointer");
+    NQ_REQUIRE(aligned(x, 16) && aligned(xq, 8) && aligned(a_scale, 4), NQ_BAD_ALIGN,
+               "nq_act_quant_i8_heads: x must be 16-byte aligned, xq 8-byte aligned");
+    if (k == 0) return act_quant(x, x_dtype, s, 0, xq, a_scale, as_stream(stream));
+    hipStream_t st = as_stream(stream);
+    const unsigned grid = static_cast<unsigned>(s);
+    const int mi = static_cast<int>(s), ki = static_cast<int>(k), epr = static_cast<int>(head_dim / 8);
+    const int64_t steps = k / 8;
+    auto go = [&](auto* xp) {
+        using XT = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
+        switch ((steps + 255) / 256) {
+            case 1: act_quant_vec_kernel<XT, 1, 256, true><<<grid, 256, 0, st>>>(xp, xq, a_scale, mi, ki, epr); break;
+            case 2: act_quant_vec_kernel<XT, 2, 256, true><<<grid, 256, 0, st>>>(xp, xq, a_scale, mi, ki, epr); break;
+            case 3: act_quant_vec_kernel<XT, 3, 256, true><<<grid, 256, 0, st>>>(xp, xq, a_scale, mi, ki, epr); break;
+            case 4: act_quant_vec_kernel<XT, 4, 256, true><<<grid, 256, 0, st>>>(xp, xq, a_scale, mi, ki, epr); break;
+            default: act_quant_vec_kernel<XT, 8, 256, true><<<grid, 256, 0, st>>>(xp, xq, a_scale, mi, ki, epr); break;
+        }
+    };
+    if (x_dtype == NQ_F32) go(static_cast<const float*>(x));
+    else go(static_cast<const _Float16*>(x));
+    return launch_status("act_quant_i8_heads");
 }
 
 extern "C" nq_status nq_act_quant_i8(const void* x, nq_dtype x_dtype, int64_t m, int64_t k,

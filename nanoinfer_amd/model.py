@@ -253,13 +253,14 @@ class Model:
             k = self.project(h, L + "self_attn.k_proj").reshape(s, cfg.kv_heads, cfg.head_dim).transpose(0, 1)
             v = self.project(h, L + "self_attn.v_proj").reshape(s, cfg.kv_heads, cfg.head_dim).transpose(0, 1)
             q, k = apply_rope(q, self.cos, self.sin), apply_rope(k, self.cos, self.sin)
-        a = attention(q, k, v, cfg.n_rep).transpose(0, 1).reshape(s, hq).contiguous()
+        a = attention(q, k, v, cfg.n_rep)
         if self.fused:
-            x, *xq = quant.add_rmsnorm_quant(x, self.project(a, L + "self_attn.o_proj"),
-                                             self.norm[L + "post_attention_layernorm"], cfg.eps)
+            o = self.gemm(quant.act_quant_heads(a.contiguous()), L + "self_attn.o_proj")
+            x, *xq = quant.add_rmsnorm_quant(x, o, self.norm[L + "post_attention_layernorm"], cfg.eps)
             gu = self.gemm(tuple(xq), L + "mlp.gate_up_proj")
             i = cfg.intermediate
             return x, self.gemm(quant.silu_mul_quant(gu[:, :i], gu[:, i:]), L + "mlp.down_proj")
+        a = a.transpose(0, 1).reshape(s, hq).contiguous()
         x = x + self.project(a, L + "self_attn.o_proj")
         hm = rmsnorm(x, self.norm[L + "post_attention_layernorm"], cfg.eps)
         gate = torch.nn.functional.silu(self.project(hm, L + "mlp.gate_proj").float())

@@ -171,6 +171,19 @@ def act_quant(x: torch.Tensor):
     return xq, s
 
 
+def act_quant_heads(a: torch.Tensor):
+    """act_quant of a head-major [heads, s, d] tensor's transpose [s, heads*d]
+    (an attention output feeding o_proj) without the transpose copy."""
+    a = _dev(a, "a")
+    if a.dim() != 3 or not a.is_contiguous():
+        raise ValueError("act_quant_heads expects a contiguous [heads, s, d] tensor")
+    h, s, d = a.shape
+    xq = torch.empty((s, h * d), dtype=torch.int8, device=a.device)
+    sc = torch.empty(s, dtype=torch.float32, device=a.device)
+    check(_lib.load().nq_act_quant_i8_heads(_ptr(a), _dtype_code(a, "a"), h, s, d, _ptr(xq), _ptr(sc), _stream()))
+    return xq, sc
+
+
 def rmsnorm_quant(x: torch.Tensor, w: torch.Tensor, eps: float):
     """rmsnorm (ops.cpp:272-290) with the act quant of linear_w8a8 fused in:
     (xq int8, a_scale fp32) of x * (1/sqrt(mean(x^2) + eps)) * w."""

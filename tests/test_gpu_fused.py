@@ -79,3 +79,15 @@ def test_add_rmsnorm_quant(dev, nq, m, k, dt, inplace):
         assert h.data_ptr() == x_in.data_ptr()
     xq2, s2 = nq.rmsnorm_quant(h_ref, w, 1e-6)
     assert torch.equal(xq, xq2) and torch.equal(s, s2)
+
+
+@pytest.mark.parametrize("h,s,d,dt", [(12, 512, 128, torch.float16), (2, 7, 64, torch.float32), (12, 1, 128, torch.float16),
+                                      (3, 300, 24, torch.float16)])
+def test_act_quant_heads(dev, nq, h, s, d, dt):
+    """Codes and scales of the head-major variant equal nq.act_quant of the
+    transposed matrix bit for bit."""
+    g = torch.Generator(device=dev).manual_seed(h * s + d)
+    a = torch.randn((h, s, d), generator=g, device=dev).to(dt)
+    xq, sc = nq.act_quant_heads(a)
+    xq2, sc2 = nq.act_quant(a.transpose(0, 1).reshape(s, h * d).contiguous())
+    assert torch.equal(xq, xq2) and torch.equal(sc, sc2)
