@@ -41,7 +41,7 @@ typedef enum nq_status {
 
 typedef enum nq_dtype { NQ_F32 = 0, NQ_F16 = 1 } nq_dtype;
 
-/* Kernel selection for the W8A8 linears. AUTO: m <= 4 (m <= 8 when k >= 4096)
+/* Kernel selection for the W8A8 linears. AUTO: m <= 4 (m <= 8 when k >= 4096 or n >= 8192)
  * -> workgroup-per-rows GEMV (v_dot4_i32_i8), larger m -> int8 MFMA GEMM. The forced values exist for A/B
  * tests, like the reference's CudaPolicy::force_tiled_w8a8
  * (cuda_backend.hpp:43-89). GENERIC is the scalar bounds-checked kernel. */

@@ -888,20 +888,21 @@ bool skinny_ok(int64_t m, int64_t n, int64_t k) {
 }
 
 // AUTO: the v_dot4 GEMV up to m = 4, and up to m = 8 for long K (where the
-// skinny MFMA plan splits K and pays for a reduction launch); the
+// skinny MFMA plan splits K and pays for a reduction launch) or tall weights
+// (n >= 8192: m = 8, n = 8960, k = 1536 GEMV 10.25 us vs MFMA 10.83); the
 // GEMV's per-row dot work grows with m while one 16x16x64 MFMA covers 16
 // activation rows, so the MFMA kernels take larger m. Measured on the decode
 // shapes k = 1536 / 8960, n = 256 .. 8960.
-int resolve_path(int path, int64_t m, int64_t k) {
+int resolve_path(int path, int64_t m, int64_t n, int64_t k) {
     if (path != NQ_PATH_AUTO) return path;
-    return (m <= 4 || (m <= 8 && k >= 4096)) ? NQ_PATH_GEMV : NQ_PATH_MFMA;
+    return (m <= 4 || (m <= 8 && (k >= 4096 || n >= 8192))) ? NQ_PATH_GEMV : NQ_PATH_MFMA;
 }
 
 // Runs the chosen path on pre-quantized activations.
 nq_status run_gemm(const int8_t* xq, const float* as, const int8_t* wq, const float* ws,
                    const float* bias, void* y, nq_dtype ydt, int32_t* acc_out, int64_t m,
                    int64_t n, int64_t k, void* workspace, size_t ws_bytes, int path, hipStream_t s) {
-    int p = resolve_path(path, m, k);
+    int p = resolve_path(path, m, n, k);
     if (p == NQ_PATH_MFMA && !mfma_ok(xq, wq, k)) p = NQ_PATH_GENERIC;
     // Weights past 2^31 bytes exceed the MFMA kernels' 32-bit buffer offsets;
     // the v_dot4 GEMV (64-bit addressing) takes them, in slices of 8 rows.
@@ -1009,7 +1010,7 @@ extern "C" nq_status nq_linear_w8a8(const void* x, nq_dtype x_dtype, const int8_
                "linear_w8a8: workspace of %zu bytes required, %zu given", need, workspace_bytes);
     NQ_REQUIRE(aligned(workspace, 256), NQ_BAD_ALIGN, "linear_w8a8: workspace must be 256-byte aligned");
     hipStream_t s = as_stream(stream);
-    const int p = resolve_path(path, m, k);
+    const int p = resolve_path(path, m, n, k);
     if (p == NQ_PATH_GEMV) {
         nq_status st = NQ_OK;
         if (gemv_w8a8_fused_launch(x, x_dtype, wq, w_scale, bias, y, y_dtype, m, n, k, s, &st)) return st;
