@@ -31,7 +31,7 @@ void hip_check(hipError_t e, const char* what) {
 void nq_check(nq_status st) {
     if (st == NQ_OK) return;
     const std::string msg = std::string(nq_status_name(st)) + ": " + nq_last_error();
-    if (st == NQ_HIP_ERROR) throw std::runtime_error(msg);
+    if (st == NQ_HIP_ERROR || st == NQ_IO_ERROR) throw std::runtime_error(msg);
     throw std::invalid_argument(msg);
 }
 
@@ -353,6 +353,66 @@ std::unique_ptr<Weight> make_quantized(const Tensor& w, QuantMode mode) {
 }
 
 std::unique_ptr<Weight> make_q8_embed(const Tensor& w) { return std::make_unique<HipEmbedQ8Weight>(quantize_q8(w)); }
+
+Tensor load_bin(const std::string& path) {
+    int32_t dt = 0, nd = 0;
+    int64_t shape[8] = {};
+    nq_check(nq_nit_info(path.c_str(), &dt, &nd, shape, 8));
+    Tensor t(std::vector<int64_t>(shape, shape + nd), DType::F32, Device::HIP);
+    nq_check(nq_nit_load_f32(path.c_str(), static_cast<float*>(t.device_ptr()), t.numel(), g_stream));
+    return t;
+}
+
+std::unique_ptr<Weight> load_quantized(const std::string& path, QuantMode mode) {
+    int32_t dt = 0, nd = 0;
+    int64_t shape[8] = {};
+    nq_check(nq_nit_info(path.c_str(), &dt, &nd, shape, 8));
+    require(nd == 2, "load_quantized expects a 2-D [out, in] weight file");
+    const int64_t out = shape[0], in = shape[1];
+    if (mode == QuantMode::None) return nullptr;
+    if (mode == QuantMode::Q8 || mode == QuantMode::W8A8) {
+        QTensor t;
+        t.out = out;
+        t.in = in;
+        t.q = Tensor({out, in}, DType::I8, Device::HIP);
+        t.scale = Tensor({out}, DType::F32, Device::HIP);
+        nq_check(nq_nit_load_q8(path.c_str(), static_cast<int8_t*>(t.q.device_ptr()),
+                                static_cast<float*>(t.scale.device_ptr()), out, in, g_stream));
+        if (mode == QuantMode::Q8) return std::make_unique<HipQ8Weight>(std::move(t));
+        return std::make_unique<HipW8A8Weight>(std::move(t));
+    }
+    const int64_t group = mode == QuantMode::Q4 ? std::max<int64_t>(1, in) : 32;
+    Q4GTensor t;
+    t.out = out;
+    t.in = in;
+    t.group = group;
+    t.q = Tensor({out, (in + 1) / 2}, DType::U8, Device::HIP);
+    t.scale = Tensor({out, (in + group - 1) / group}, DType::F32, Device::HIP);
+    nq_check(nq_nit_load_q4g(path.c_str(), static_cast<uint8_t*>(t.q.device_ptr()), t.scale.device_ptr(), NQ_F32,
+                             group, out, in, g_stream));
+    return std::make_unique<HipQ4GWeight>(std::move(t), mode == QuantMode::Q4 ? Format::Q4 : Format::Q4G);
+}
+
+std::vector<int64_t> lm_head_argmax(const Tensor& x, const QTensor& head, const Tensor* bias) {
+    check_device_2d(x, "lm_head_argmax expects a device [m, in] activation");
+    require(x.size(1) == head.in, "lm_head_argmax: x cols must match weight in-features");
+    const int64_t m = x.size(0);
+    Tensor ids64({2 * m}, DType::I32, Device::HIP);  // int64 ids, held as pairs of int32
+    const size_t wsb = nq_lm_head_argmax_q8_workspace_size(m, head.out, head.in);
+    Tensor ws({static_cast<int64_t>((wsb + 3) / 4 + 64)}, DType::I32, Device::HIP);
+    nq_check(nq_lm_head_argmax_q8(x.device_ptr(), x.dtype() == DType::F16 ? NQ_F16 : NQ_F32,
+                                  static_cast<const int8_t*>(head.q.device_ptr()),
+                                  static_cast<const float*>(head.scale.device_ptr()),
+                                  bias ? static_cast<const float*>(bias->device_ptr()) : nullptr,
+                                  static_cast<int64_t*>(ids64.device_ptr()), m, head.out, head.in,
+                                  ws.device_ptr(), ws.nbytes(), g_stream));
+    std::vector<int64_t> out(static_cast<size_t>(m));
+    hip_check(hipMemcpyAsync(out.data(), ids64.device_ptr(), out.size() * sizeof(int64_t), hipMemcpyDeviceToHost,
+                             static_cast<hipStream_t>(g_stream)),
+              "hipMemcpyAsync");
+    hip_check(hipStreamSynchronize(static_cast<hipStream_t>(g_stream)), "hipStreamSynchronize");
+    return out;
+}
 
 std::unique_ptr<Weight> HipBackend::make_quant_weight(const Tensor& host, QuantMode mode) const {
     return make_quantized(host, mode);

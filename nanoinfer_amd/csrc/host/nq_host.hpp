@@ -9,6 +9,7 @@
 //   embedding_q8                                  (quant.hpp:72)
 //   Weight, make_quantized, make_q8_embed         (quant.hpp:120-141)
 //   HipBackend::make_quant_weight / make_embed_weight (backend.hpp:109-114)
+//   load_bin (serialize.hpp:32), argmax of the LM head (sampling.cpp:14-20)
 // Shape and argument errors throw std::invalid_argument, device errors throw
 // std::runtime_error (quant.cpp:23-25, cuda_internal.cuh:24).
 //
@@ -119,6 +120,18 @@ public:
 
 std::unique_ptr<Weight> make_quantized(const Tensor& w, QuantMode mode);  // nullptr for None
 std::unique_ptr<Weight> make_q8_embed(const Tensor& w);
+
+// Weight files (serialize.hpp:1-35): load_bin's NIT0/NIT1 tensor onto the device
+// as fp32, and a quantized weight read and quantized on the device (the file's
+// payload never exists as an fp32 host tensor). File errors throw
+// std::runtime_error, as load_bin does.
+Tensor load_bin(const std::string& path);
+std::unique_ptr<Weight> load_quantized(const std::string& path, QuantMode mode);  // nullptr for None
+
+// Greedy next-token ids for each row of x: the argmax of linear_q8(x, head, bias)
+// with the reference's first-index / NaN rules (sampling.cpp:14-20), computed
+// without writing the logits. Synchronizes the stream.
+std::vector<int64_t> lm_head_argmax(const Tensor& x, const QTensor& head, const Tensor* bias = nullptr);
 
 // The backend factory seam (backend.hpp:109-114): host fp32 weights in,
 // device-resident quantized weights out.

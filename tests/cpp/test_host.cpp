@@ -167,6 +167,42 @@ int main() {
         try { quant_mode("int3"); } catch (const std::invalid_argument&) { threw = true; }
         CHECK(threw && quant_mode("w8a8") == QuantMode::W8A8);
     }
+    // weight files (serialize.cpp:11-72, test_io.cpp:68-84) and the greedy LM head (sampling.cpp:14-20)
+    {
+        const char* path = "test_host_nit1.bin";
+        {
+            std::FILE* f = std::fopen(path, "wb");
+            const int32_t hdr[4] = {1, 2, 4, 64};  // NIT1, bf16 payload, [4, 64]
+            std::fwrite("NIT1", 1, 4, f);
+            std::fwrite(hdr, 4, 4, f);
+            for (int i = 0; i < 4 * 64; ++i) {
+                const float v = (i % 64 == 7 + 11 * (i / 64)) ? 2.5f : 0.0625f * static_cast<float>((i * 7) % 5 - 2);
+                uint32_t bits;
+                std::memcpy(&bits, &v, 4);
+                const uint16_t top = static_cast<uint16_t>(bits >> 16);  // the values are exact in bf16
+                std::fwrite(&top, 2, 1, f);
+            }
+            std::fclose(f);
+        }
+        Tensor dev = load_bin(path);
+        Tensor host = to_host(dev);
+        CHECK(host.ndim() == 2 && host.size(0) == 4 && host.size(1) == 64 && host[7] == 2.5f && host[2] == 0.125f && host[3] == -0.0625f);
+        auto w8 = load_quantized(path, QuantMode::W8A8);
+        auto ref = make_quantized(host, QuantMode::W8A8);
+        Tensor x = to_device(make({2, 64}, std::vector<float>(128, 1.0f)));
+        Tensor a = to_host(w8->linear(x, nullptr)), b = to_host(ref->linear(x, nullptr));
+        for (int64_t i = 0; i < a.numel(); ++i) CHECK(a[i] == b[i]);
+        CHECK(load_quantized(path, QuantMode::Q4G)->format() == Format::Q4G);
+        // rows 0..3 carry a 2.5 spike at columns 7, 18, 29, 40: x = e_29 picks row 2
+        std::vector<float> e(64, 0.0f);
+        e[29] = 1.0f;
+        const std::vector<int64_t> ids = lm_head_argmax(to_device(make({1, 64}, e)), quantize_q8(host));
+        CHECK(ids.size() == 1 && ids[0] == 2);
+        bool threw = false;
+        try { load_bin("missing_weight_file.bin"); } catch (const std::runtime_error&) { threw = true; }
+        CHECK(threw);
+        std::remove(path);
+    }
     std::printf(g_failures ? "test_host: %d failures\n" : "test_host: ok\n", g_failures);
     return g_failures ? 1 : 0;
 }
