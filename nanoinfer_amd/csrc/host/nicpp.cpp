@@ -91,6 +91,16 @@ struct PyBackend {
         if (!q) return py::none();
         return py::cast(PyWeight{std::shared_ptr<Weight>(std::move(q))});
     }
+    // A weight straight from a NIT0/NIT1 file (load_bin + make_quant_weight), quantized on the device.
+    py::object load_quant_weight(const std::string& path, QuantMode mode) const {
+        std::unique_ptr<Weight> q;
+        {
+            py::gil_scoped_release release;
+            q = load_quantized(path, mode);
+        }
+        if (!q) return py::none();
+        return py::cast(PyWeight{std::shared_ptr<Weight>(std::move(q))});
+    }
     PyWeight make_embed_weight(const py::array_t<float, py::array::c_style | py::array::forcecast>& w) const {
         Tensor h = host_from_numpy(w);
         std::unique_ptr<Weight> q;
@@ -137,7 +147,8 @@ PYBIND11_MODULE(nicpp, m) {
         .def(py::init<const std::string&>(), py::arg("device") = "hip")
         .def_readonly("device", &PyBackend::device)
         .def("make_quant_weight", &PyBackend::make_quant_weight, py::arg("w"), py::arg("mode"))
-        .def("make_embed_weight", &PyBackend::make_embed_weight, py::arg("w"));
+        .def("make_embed_weight", &PyBackend::make_embed_weight, py::arg("w"))
+        .def("load_quant_weight", &PyBackend::load_quant_weight, py::arg("path"), py::arg("mode"));
 
     m.def("make_backend", [](const std::string& device) { return PyBackend(device); }, py::arg("device") = "hip");
 }

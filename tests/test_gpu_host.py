@@ -60,3 +60,23 @@ def test_nicpp_embed_and_errors(dev, orc):
     with pytest.raises(ValueError):
         wt.linear(np.zeros((2, 63), np.float32))                    # x cols must match
     assert be.make_quant_weight(table, nicpp.QuantMode.NONE) is None
+
+
+@pytest.mark.parametrize("mode", ["w8a8", "q4g"])
+def test_nicpp_load_quant_weight(dev, tmp_path, mode):
+    """A weight loaded from a NIT1 bf16 file equals make_quant_weight of the
+    same values (quantize-on-load, serialize.cpp:11-72)."""
+    from nanoinfer_amd import nicpp
+    from nit_util import bf16_exact, write_nit1
+    be = nicpp.make_backend("hip")
+    rng = np.random.default_rng(9)
+    w = bf16_exact(rng.normal(0, 0.02, (96, 256)).astype(np.float32))
+    x = rng.normal(0, 1, (3, 256)).astype(np.float32)
+    p = str(tmp_path / "w.bin")
+    write_nit1(p, w, 1)
+    a = be.load_quant_weight(p, nicpp.quant_mode(mode))
+    b = be.make_quant_weight(w, nicpp.quant_mode(mode))
+    assert nicpp.format_name(a.format()) == mode
+    assert np.array_equal(a.linear(x), b.linear(x))
+    with pytest.raises(RuntimeError):
+        be.load_quant_weight(str(tmp_path / "missing.bin"), nicpp.quant_mode(mode))
