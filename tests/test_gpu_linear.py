@@ -388,3 +388,30 @@ def test_w8a8_prefill_plans_exact(dev, nq, orc, m, n, k):
     assert_close_rms(host(y.float())[rows], ref, f"w8a8 prefill {m}x{n}x{k}", fp16_out=True)
     y32 = nq.linear_w8a8(xdv, t, to_dev(b, dev), out_dtype=torch.float32)   # fp32 epilogue path
     assert_close_rms(host(y32)[rows], ref, f"w8a8 prefill fp32-out {m}x{n}x{k}")
+
+
+def _plan_shapes():
+    """Seeded shapes spread over the W8A8 plans for m > 64: wide (256- and
+    128-row tiles), 256x128, 128x128, 64x128 narrow, split K, and k % 64 != 0
+    (the skinny kernel over 64-row blocks)."""
+    rng = np.random.default_rng(2026)
+    shapes = [(2304, 16384, 128), (2048, 8200, 128), (200, 1003, 4096), (96, 5000, 6144)]   # big, wide, split
+    for _ in range(12):
+        m = int(rng.integers(65, 2300))
+        n = int(rng.integers(16, 20000))
+        k = int(rng.choice([64, 128, 192, 320, 1536, 2560, 4096, 48, 208]))
+        if m * n * k > 6e9:
+            n = max(16, int(6e9 / (m * k)))
+        shapes.append((m, n, k))
+    return shapes
+
+
+@pytest.mark.parametrize("m,n,k", _plan_shapes())
+def test_w8a8_plans_random_shapes(dev, nq, m, n, k):
+    """int32 accumulators of the MFMA plans equal the GEMV path's bit for bit."""
+    g = torch.Generator(device=dev).manual_seed(m * 131 + n * 7 + k)
+    xq = torch.randint(-127, 128, (m, k), generator=g, device=dev, dtype=torch.int8)
+    wq = torch.randint(-127, 128, (n, k), generator=g, device=dev, dtype=torch.int8)
+    acc_m = nq.w8a8_acc_i32(xq, wq, nq._lib.NQ_PATH_MFMA)
+    acc_g = nq.w8a8_acc_i32(xq, wq, nq._lib.NQ_PATH_GEMV)
+    assert torch.equal(acc_m, acc_g), (m, n, k)
