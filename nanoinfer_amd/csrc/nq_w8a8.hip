@@ -288,23 +288,29 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_w8a8_prefill_kernel(
 // 4 x 63 tiles of 128 x 288), a single round of tiles beats two rounds of
 // smaller tiles: every output tile costs one pass over its A rows and B rows,
 // and a second round would leave most CUs idle. WM x 2 waves (WM = 4 or 2), each
-// 64 x 16*FN outputs (4 x FN fragments, 4*FN int32 accumulator registers). K advances in 64-byte slabs through a 4-deep LDS ring filled by
-// LDS-DMA as in the prefill kernel; the slab kt + 3 request goes out right
-// after the barrier that frees its slot, so three slabs are in flight while
-// slab kt is multiplied. All fragment reads of a slab are issued before its
-// first MFMA (a scheduling barrier keeps the compiler from sinking them next
-// to their uses, which left LDS latency exposed). The 256 x BN block of
-// DMA requests does not split evenly over the waves; the spare requests read
-// zeros into a 1 KB sink so every wave counts the same number per slab.
+// 64 x 16*FN outputs (4 x FN fragments, 4*FN int32 accumulator registers). K
+// advances in 128-byte slabs (two MFMA K steps) through a 2-slot LDS ring
+// filled by LDS-DMA; the request for slab kt + 1 goes out right after the
+// barrier that frees its slot. A 1 KB DMA request covers 8 rows x 128 bytes,
+// i.e. whole 128-byte cache lines: with 64-byte slabs (16 rows x 64 bytes per
+// request, a 4-slot ring) every request touched twice as many lines and the
+// loads of the same tile took longer even with more slabs in flight. Chunk c
+// of row r sits in slot c ^ ((r >> 1) & 7) of its 128-byte LDS row, so the
+// 16 rows of a fragment read hit distinct banks. All fragment reads of a K
+// step are issued before its first MFMA (a scheduling barrier keeps the
+// compiler from sinking them next to their uses, which left LDS latency
+// exposed). The block of DMA requests does not split evenly over the waves;
+// the spare requests read zeros into a 1 KB sink so every wave counts the same
+// number per slab. When k % 128 == 64 the last slab's upper half reads zeros.
 // fp16 results go through LDS in two halves of the tile's rows and leave as
 // 16-byte row chunks with non-temporal stores (a one-round grid writes its
 // whole output at the end, which no later work overlaps).
 template <int WM, int FN>
 struct WideShape {
-    static constexpr int kWM = WM, kWN = 2, kWaves = WM * 2, kD = 4;
+    static constexpr int kWM = WM, kWN = 2, kWaves = WM * 2, kD = 2, kRow = 128;
     static constexpr int kBM = kWM * 64, kBN = kWN * FN * 16;
-    static constexpr int kXB = kBM / 16, kNB = kXB + kBN / 16, kQ = (kNB + kWaves - 1) / kWaves;
-    static constexpr int kSlab = (kBM + kBN) * kPRow;
+    static constexpr int kXB = kBM / 8, kNB = kXB + kBN / 8, kQ = (kNB + kWaves - 1) / kWaves;
+    static constexpr int kSlab = (kBM + kBN) * kRow;
     static constexpr int kSink = kD * kSlab;  // 1 KB
     static constexpr size_t kLds = std::max<size_t>(size_t(kSink) + 1024, size_t(kBM / 2) * kBN * 2);
 };
@@ -332,36 +338,41 @@ __global__ __launch_bounds__(WM * 2 * 64) void gemm_w8a8_wide_kernel(
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(xq), 0, m * k, 0x00020000);
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(wq), 0, n * k, 0x00020000);
     constexpr int kOob = 0x7FFFFFF0;
-    // Request q of wave w moves 1 KB block b = q * 8 + w of the slab: blocks
-    // [0, XB) are 16 activation rows each, [XB, NB) 16 weight rows, the rest
-    // spares. Lane i writes LDS bytes 16i..16i+15 of the block (row i/4,
-    // slot i%4) and loads the chunk the swizzle puts there.
-    int voff[Q], loff[Q];
+    // Request q of wave w moves 1 KB block b = q * NW + w of the slab: blocks
+    // [0, XB) are 8 activation rows each, [XB, NB) 8 weight rows, the rest
+    // spares. Lane i writes LDS bytes 16i..16i+15 of the block (row i/8,
+    // slot i%8) and loads the chunk the swizzle puts there. vtail: the same
+    // offsets with the upper half of the row (chunks 4..7) out of range.
+    int voff[Q], vtail[Q], loff[Q];
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
         const int b = q * NW + wave;
         const bool real = b < NB, isx = b < XB;
-        const int r = (isx ? b : b - XB) * 16 + (lane >> 2);
-        const int c = (lane & 3) ^ ((r >> 1) & 3);
+        const int r = (isx ? b : b - XB) * 8 + (lane >> 3);
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
         const int grow = (isx ? m0 : n0) + r;
         voff[q] = real && grow < (isx ? m : n) ? grow * k + c * 16 : kOob;
-        loff[q] = real ? (isx ? b * 1024 : BM * kPRow + (b - XB) * 1024) : S::kSink;
+        vtail[q] = c < 4 ? voff[q] : kOob;
+        loff[q] = real ? b * 1024 : S::kSink;
     }
-    const int nk = k / kBK;
+    const int nk = (k + S::kRow - 1) / S::kRow;
+    const bool half_tail = (k % S::kRow) != 0;  // k % 64 == 0 by contract
     const unsigned lds_base = static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds));
     auto issue = [&](int sl) {
         const unsigned slot = static_cast<unsigned>(sl % D) * S::kSlab;
-        const int soff = sl < nk ? sl * kBK : kOob;
+        const int soff = sl < nk ? sl * S::kRow : kOob;
+        const bool tail = half_tail && sl == nk - 1;
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
             const int b = q * NW + wave;  // wave-uniform
             const unsigned dst = lds_base + (b < NB ? slot : 0u) + static_cast<unsigned>(loff[q]);
+            const int vo = tail ? vtail[q] : voff[q];
             if (b < XB)
                 asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                             ::"s"(dst), "v"(voff[q]), "s"(xrs), "s"(soff) : "memory");
+                             ::"s"(dst), "v"(vo), "s"(xrs), "s"(soff) : "memory");
             else
                 asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                             ::"s"(dst), "v"(voff[q]), "s"(wrs), "s"(soff) : "memory");
+                             ::"s"(dst), "v"(vo), "s"(wrs), "s"(soff) : "memory");
         }
     };
 
@@ -371,11 +382,16 @@ __global__ __launch_bounds__(WM * 2 * 64) void gemm_w8a8_wide_kernel(
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
     const int fr = lane & 15, fc = lane >> 4;
-    int fxo[4], fwo[FN];
+    // Fragment byte offsets of MFMA K step t (0, 1) within a slab.
+    auto swz128 = [](int r, int c) { return r * S::kRow + ((c ^ ((r >> 1) & 7)) << 4); };
+    int fxo[2][4], fwo[2][FN];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) fxo[j] = swz(wm * 64 + j * 16 + fr, fc);
+    for (int t = 0; t < 2; ++t) {
 #pragma unroll
-    for (int i = 0; i < FN; ++i) fwo[i] = BM * kPRow + swz(wn * FN * 16 + i * 16 + fr, fc);
+        for (int j = 0; j < 4; ++j) fxo[t][j] = swz128(wm * 64 + j * 16 + fr, t * 4 + fc);
+#pragma unroll
+        for (int i = 0; i < FN; ++i) fwo[t][i] = swz128(BM + wn * FN * 16 + i * 16 + fr, t * 4 + fc);
+    }
 
 #pragma unroll
     for (int sl = 0; sl < D - 1; ++sl) issue(sl);
@@ -384,16 +400,19 @@ __global__ __launch_bounds__(WM * 2 * 64) void gemm_w8a8_wide_kernel(
         __builtin_amdgcn_s_barrier();  // everyone's landed; slot of slab kt - 1 is free
         issue(kt + D - 1);
         const int8_t* base = lds + (kt % D) * S::kSlab;
-        v4i fx[4], fw[FN];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) fx[j] = *reinterpret_cast<const v4i*>(base + fxo[j]);
+        for (int t = 0; t < 2; ++t) {
+            v4i fx[4], fw[FN];
 #pragma unroll
-        for (int i = 0; i < FN; ++i) fw[i] = *reinterpret_cast<const v4i*>(base + fwo[i]);
-        __builtin_amdgcn_sched_barrier(0);
+            for (int j = 0; j < 4; ++j) fx[j] = *reinterpret_cast<const v4i*>(base + fxo[t][j]);
 #pragma unroll
-        for (int i = 0; i < FN; ++i)
+            for (int i = 0; i < FN; ++i) fw[i] = *reinterpret_cast<const v4i*>(base + fwo[t][i]);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fw[i], fx[j], acc[i][j], 0, 0, 0);
+            for (int i = 0; i < FN; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fw[i], fx[j], acc[i][j], 0, 0, 0);
+        }
         // this slab's fragment reads are done before the next barrier frees its slot
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }

@@ -393,9 +393,11 @@ def test_w8a8_prefill_plans_exact(dev, nq, orc, m, n, k):
 def _plan_shapes():
     """Seeded shapes spread over the W8A8 plans for m > 64: wide (256- and
     128-row tiles), 256x128, 128x128, 64x128 narrow, split K, and k % 64 != 0
-    (the skinny kernel over 64-row blocks)."""
+    (the skinny kernel over 64-row blocks); wide shapes whose last 128-byte
+    K slab is half empty."""
     rng = np.random.default_rng(2026)
     shapes = [(2304, 16384, 128), (2048, 8200, 128), (200, 1003, 4096), (96, 5000, 6144)]   # big, wide, split
+    shapes += [(2048, 8200, 192), (512, 17000, 320), (1900, 8900, 64)]   # wide with k % 128 == 64
     for _ in range(12):
         m = int(rng.integers(65, 2300))
         n = int(rng.integers(16, 20000))
