@@ -37,13 +37,17 @@ enum class Out { Y, ACC, PARTIAL };
 
 // ---- prefill W8A8 GEMM (m > 64) ---------------------------------------------------------
 // A workgroup of WM x WN waves owns a (WM*64) x (WN*64) output tile; each wave
-// owns 64 x 64 (4 x 4 MFMA 16x16x64 fragments). K advances in 64-byte slabs
-// that the buffer unit writes straight into a D-deep LDS ring (buffer_load ...
-// lds: no VGPR staging, no ds_write); each lane picks the global chunk that
-// belongs at its LDS slot, which applies an XOR swizzle (16-byte chunk c of
-// row r lands in slot c ^ ((r >> 1) & 3); the MFMA fragment reads are then
-// bank-conflict free). One barrier per slab; the MFMAs of slab kt run while
-// slab kt + D - 1 is requested and the fragments of slab kt + 1 are read.
+// owns 64 x 64 (4 x 4 MFMA 16x16x64 fragments). K advances in SW-byte slabs
+// (SW = 64 or 128) that the buffer unit writes straight into a D-deep LDS ring
+// (buffer_load ... lds: no VGPR staging, no ds_write); each lane picks the
+// global chunk that belongs at its LDS slot, which applies an XOR swizzle
+// (16-byte chunk c of row r lands in slot c ^ ((r >> 1) & (SW/16 - 1)); the
+// MFMA fragment reads are then bank-conflict free). One barrier per slab.
+// SW = 64: the MFMAs of slab kt run while slab kt + D - 1 is requested and the
+// fragments of slab kt + 1 are read. SW = 128 (two MFMA K steps per slab): a
+// 1 KB DMA request covers 8 rows x 128 bytes, whole cache lines, which loads a
+// tile faster than 16 rows x 64 bytes but takes twice the LDS per slab; the
+// fragments of the second K step are read during the first step's MFMAs.
 // The MFMA computes D = W_tile * xq_tile^T (weights as the A operand), so a lane
 // ends with four consecutive output columns of one row. fp16 outputs are staged
 // through LDS and written as whole 16-byte row chunks.
@@ -53,17 +57,17 @@ enum class Out { Y, ACC, PARTIAL };
 // The LDS-DMA loads are issued from inline asm, so the compiler does not track
 // them: the kernel waits for them itself (s_waitcnt vmcnt) before each barrier
 // and before the epilogue.
-constexpr int kPRow = kBK;
+// Byte offset of 16-byte chunk c of row r in a swizzled SW-byte-row LDS tile.
+template <int SW>
+__device__ __forceinline__ int swz(int r, int c) { return r * SW + ((c ^ ((r >> 1) & (SW / 16 - 1))) << 4); }
 
-// Byte offset of 16-byte chunk c of row r in a swizzled 64-byte-row LDS tile.
-__device__ __forceinline__ int swz(int r, int c) { return r * kPRow + ((c ^ ((r >> 1) & 3)) << 4); }
-
-template <int WM, int WN, int D>
+template <int WM, int WN, int D, int SW = 64>
 struct PrefillShape {
     static constexpr int kWaves = WM * WN, kBM = WM * 64, kBN = WN * 64;
-    static constexpr int kXB = kBM / 16, kWB = kBN / 16;   // 1 KB blocks (16 rows x 64 B) per slab
+    static constexpr int kRows = 1024 / SW;                // rows per 1 KB LDS-DMA block
+    static constexpr int kXB = kBM / kRows, kWB = kBN / kRows;  // blocks per slab
     static constexpr int kQ = (kXB + kWB) / kWaves;        // LDS-DMA instructions per wave per slab
-    static constexpr int kSlab = (kBM + kBN) * kPRow;      // bytes per slab
+    static constexpr int kSlab = (kBM + kBN) * SW;         // bytes per slab
     static constexpr int kOutStride = kBN * 2 + 16;        // staged fp16 row stride (bytes)
     static constexpr size_t kLds = std::max<size_t>(size_t(D) * kSlab, size_t(kBM) * kOutStride);
     static_assert((kXB + kWB) % kWaves == 0, "whole LDS-DMA blocks per wave");
@@ -75,13 +79,13 @@ __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int WM, int WN, int D, Out OUT, typename YT>
+template <int WM, int WN, int D, int SW, Out OUT, typename YT>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_w8a8_prefill_kernel(
     const int8_t* __restrict__ xq, const float* __restrict__ as, const int8_t* __restrict__ wq,
     const float* __restrict__ ws, const float* __restrict__ bias, YT* __restrict__ y,
     int32_t* __restrict__ acc_out, int m, int n, int k, int tiles_m, int tiles_n, int k_slabs) {
-    using S = PrefillShape<WM, WN, D>;
-    constexpr int Q = S::kQ, XB = S::kXB, BM = S::kBM, BN = S::kBN;
+    using S = PrefillShape<WM, WN, D, SW>;
+    constexpr int Q = S::kQ, XB = S::kXB, BM = S::kBM, BN = S::kBN, CPR = SW / 16;
     extern __shared__ __attribute__((aligned(16))) int8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -99,35 +103,43 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_w8a8_prefill_kernel(
     constexpr int kOob = 0x7FFFFFF0;
     // Wave w issues blocks w*Q .. w*Q+Q-1 of each slab: blocks [0, XB) are the
     // activation tile, the rest the weight tile. Lane i of a block writes LDS
-    // bytes 16i..16i+15 of it (row i/4, slot i%4) and so loads the chunk that
-    // the swizzle puts in that slot.
-    int voff[Q];
+    // bytes 16i..16i+15 of it (row i / CPR, slot i % CPR) and so loads the
+    // chunk that the swizzle puts in that slot. vtail: the same offsets with
+    // the upper half of a 128-byte row out of range (the last slab when
+    // k % 128 == 64).
+    int voff[Q], vtail[Q];
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
         const int blk = wave * Q + q;
         const bool isx = blk < XB;
-        const int r = (isx ? blk : blk - XB) * 16 + (lane >> 2);
-        const int c = (lane & 3) ^ ((r >> 1) & 3);
+        const int r = (isx ? blk : blk - XB) * S::kRows + lane / CPR;
+        const int c = (lane % CPR) ^ ((r >> 1) & (CPR - 1));
         const int grow = (isx ? m0 : n0) + r;
         voff[q] = grow < (isx ? m : n) ? grow * k + c * 16 : kOob;
+        vtail[q] = c < 4 ? voff[q] : kOob;
     }
     // This workgroup's K range: slabs [s0, s1) (the whole K unless the launch
-    // splits K over gridDim.y; the prefill contract has k % kBK == 0).
-    const int s0 = blockIdx.y * k_slabs, s1 = min(k / kBK, s0 + k_slabs);
+    // splits K over gridDim.y; the prefill contract has k % 64 == 0).
+    const int nslab = (k + SW - 1) / SW;
+    const bool half_tail = SW == 128 && (k % SW) != 0;
+    const int s0 = blockIdx.y * k_slabs, s1 = min(nslab, s0 + k_slabs);
     const unsigned lds_base = static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds));
     auto issue = [&](int sl) {  // sl counts from s0
         const unsigned slot = static_cast<unsigned>(sl % D) * S::kSlab;
-        const int soff = s0 + sl < s1 ? (s0 + sl) * kBK : kOob;
+        const int g = s0 + sl;
+        const int soff = g < s1 ? g * SW : kOob;
+        const bool tail = half_tail && g == nslab - 1;
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
             const int blk = wave * Q + q;
             const unsigned dst = lds_base + slot + blk * 1024;
+            const int vo = tail ? vtail[q] : voff[q];
             if (blk < XB)
                 asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                             ::"s"(dst), "v"(voff[q]), "s"(xrs), "s"(soff) : "memory");
+                             ::"s"(dst), "v"(vo), "s"(xrs), "s"(soff) : "memory");
             else
                 asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                             ::"s"(dst), "v"(voff[q]), "s"(wrs), "s"(soff) : "memory");
+                             ::"s"(dst), "v"(vo), "s"(wrs), "s"(soff) : "memory");
         }
     };
     // Own LDS-DMA of the oldest in-flight slab landed (D - 2 younger slabs may fly).
@@ -139,18 +151,22 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_w8a8_prefill_kernel(
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
     const int fr = lane & 15, fc = lane >> 4;
-    int fxo[4], fwo[4];
+    constexpr int T = SW / 64;  // MFMA K steps per slab
+    int fxo[T][4], fwo[T][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) fxo[j] = swz(wm * 64 + j * 16 + fr, fc);
+    for (int t = 0; t < T; ++t) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fwo[i] = BM * kPRow + swz(wn * 64 + i * 16 + fr, fc);
+        for (int j = 0; j < 4; ++j) fxo[t][j] = swz<SW>(wm * 64 + j * 16 + fr, t * 4 + fc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) fwo[t][i] = swz<SW>(BM + wn * 64 + i * 16 + fr, t * 4 + fc);
+    }
     v4i fw[2][4], fx[2][4];
-    auto read = [&](int sl, v4i (&w)[4], v4i (&x)[4]) {
+    auto read = [&](int sl, int t, v4i (&w)[4], v4i (&x)[4]) {
         const int8_t* base = lds + (sl % D) * S::kSlab;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = *reinterpret_cast<const v4i*>(base + fwo[i]);
+        for (int i = 0; i < 4; ++i) w[i] = *reinterpret_cast<const v4i*>(base + fwo[t][i]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) x[j] = *reinterpret_cast<const v4i*>(base + fxo[j]);
+        for (int j = 0; j < 4; ++j) x[j] = *reinterpret_cast<const v4i*>(base + fxo[t][j]);
     };
     auto mma = [&](const v4i (&w)[4], const v4i (&x)[4]) {
 #pragma unroll
@@ -163,24 +179,39 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_w8a8_prefill_kernel(
     for (int sl = 0; sl < D - 1; ++sl) issue(sl);
     wait_slab();
     __builtin_amdgcn_s_barrier();
-    read(0, fw[0], fx[0]);
-    // The slot refilled at iteration kt held slab kt - 1, whose fragments every
-    // wave read before the previous iteration's barrier.
-    auto iter = [&](int kt, auto par) {
-        constexpr int P = decltype(par)::value;
-        mma(fw[P], fx[P]);
-        issue(kt + D - 1);
-        wait_slab();
-        __builtin_amdgcn_s_barrier();
-        read(kt + 1, fw[P ^ 1], fx[P ^ 1]);
-    };
+    read(0, 0, fw[0], fx[0]);
     const int nk = s1 - s0;
-    int kt = 0;
-    for (; kt + 2 <= nk; kt += 2) {
-        iter(kt, std::integral_constant<int, 0>{});
-        iter(kt + 1, std::integral_constant<int, 1>{});
+    if constexpr (SW == 64) {
+        // The slot refilled at iteration kt held slab kt - 1, whose fragments every
+        // wave read before the previous iteration's barrier.
+        auto iter = [&](int kt, auto par) {
+            constexpr int P = decltype(par)::value;
+            mma(fw[P], fx[P]);
+            issue(kt + D - 1);
+            wait_slab();
+            __builtin_amdgcn_s_barrier();
+            read(kt + 1, 0, fw[P ^ 1], fx[P ^ 1]);
+        };
+        int kt = 0;
+        for (; kt + 2 <= nk; kt += 2) {
+            iter(kt, std::integral_constant<int, 0>{});
+            iter(kt + 1, std::integral_constant<int, 1>{});
+        }
+        if (kt < nk) iter(kt, std::integral_constant<int, 0>{});
+    } else {
+        for (int kt = 0; kt < nk; ++kt) {
+            // The slot refilled here held slab kt - 1, whose fragments every
+            // wave had in registers before the previous barrier.
+            issue(kt + D - 1);
+            read(kt, 1, fw[1], fx[1]);
+            mma(fw[0], fx[0]);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // step-1 fragments of slab kt landed
+            wait_slab();
+            __builtin_amdgcn_s_barrier();
+            read(kt + 1, 0, fw[0], fx[0]);
+            mma(fw[1], fx[1]);
+        }
     }
-    if (kt < nk) iter(kt, std::integral_constant<int, 0>{});
     wait_vmcnt<0>();  // the ring's tail requests (zero reads) have retired
 
     // Lane l holds, for fragment (i, j), output row m0 + wm*64 + j*16 + (l % 16)
@@ -305,22 +336,22 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_w8a8_prefill_kernel(
 // fp16 results go through LDS in two halves of the tile's rows and leave as
 // 16-byte row chunks with non-temporal stores (a one-round grid writes its
 // whole output at the end, which no later work overlaps).
-template <int WM, int FN>
+template <int WM, int FN, int FM>
 struct WideShape {
     static constexpr int kWM = WM, kWN = 2, kWaves = WM * 2, kD = 2, kRow = 128;
-    static constexpr int kBM = kWM * 64, kBN = kWN * FN * 16;
+    static constexpr int kBM = kWM * FM * 16, kBN = kWN * FN * 16;
     static constexpr int kXB = kBM / 8, kNB = kXB + kBN / 8, kQ = (kNB + kWaves - 1) / kWaves;
     static constexpr int kSlab = (kBM + kBN) * kRow;
     static constexpr int kSink = kD * kSlab;  // 1 KB
     static constexpr size_t kLds = std::max<size_t>(size_t(kSink) + 1024, size_t(kBM / 2) * kBN * 2);
 };
 
-template <int WM, int FN, Out OUT, typename YT>
+template <int WM, int FN, int FM, Out OUT, typename YT>
 __global__ __launch_bounds__(WM * 2 * 64) void gemm_w8a8_wide_kernel(
     const int8_t* __restrict__ xq, const float* __restrict__ as, const int8_t* __restrict__ wq,
     const float* __restrict__ ws, const float* __restrict__ bias, YT* __restrict__ y,
     int32_t* __restrict__ acc_out, int m, int n, int k, int tiles_m, int tiles_n) {
-    using S = WideShape<WM, FN>;
+    using S = WideShape<WM, FN, FM>;
     constexpr int NW = S::kWaves, Q = S::kQ, XB = S::kXB, NB = S::kNB, BM = S::kBM, BN = S::kBN, D = S::kD;
     extern __shared__ __attribute__((aligned(16))) int8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -376,19 +407,19 @@ __global__ __launch_bounds__(WM * 2 * 64) void gemm_w8a8_wide_kernel(
         }
     };
 
-    v4i acc[FN][4];  // [n fragment][m fragment]
+    v4i acc[FN][FM];  // [n fragment][m fragment]
 #pragma unroll
     for (int i = 0; i < FN; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+        for (int j = 0; j < FM; ++j) acc[i][j] = v4i{0, 0, 0, 0};
     const int fr = lane & 15, fc = lane >> 4;
     // Fragment byte offsets of MFMA K step t (0, 1) within a slab.
     auto swz128 = [](int r, int c) { return r * S::kRow + ((c ^ ((r >> 1) & 7)) << 4); };
-    int fxo[2][4], fwo[2][FN];
+    int fxo[2][FM], fwo[2][FN];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) fxo[t][j] = swz128(wm * 64 + j * 16 + fr, t * 4 + fc);
+        for (int j = 0; j < FM; ++j) fxo[t][j] = swz128(wm * FM * 16 + j * 16 + fr, t * 4 + fc);
 #pragma unroll
         for (int i = 0; i < FN; ++i) fwo[t][i] = swz128(BM + wn * FN * 16 + i * 16 + fr, t * 4 + fc);
     }
@@ -402,23 +433,23 @@ __global__ __launch_bounds__(WM * 2 * 64) void gemm_w8a8_wide_kernel(
         const int8_t* base = lds + (kt % D) * S::kSlab;
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-            v4i fx[4], fw[FN];
+            v4i fx[FM], fw[FN];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) fx[j] = *reinterpret_cast<const v4i*>(base + fxo[t][j]);
+            for (int j = 0; j < FM; ++j) fx[j] = *reinterpret_cast<const v4i*>(base + fxo[t][j]);
 #pragma unroll
             for (int i = 0; i < FN; ++i) fw[i] = *reinterpret_cast<const v4i*>(base + fwo[t][i]);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < FN; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fw[i], fx[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < FM; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fw[i], fx[j], acc[i][j], 0, 0, 0);
         }
         // this slab's fragment reads are done before the next barrier frees its slot
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
     wait_vmcnt<0>();  // the ring's tail requests (zero reads) have retired
 
-    // Lane l holds, for fragment (i, j), output row m0 + wm*64 + j*16 + (l % 16)
+    // Lane l holds, for fragment (i, j), output row m0 + wm*FM*16 + j*16 + (l % 16)
     // and columns n0 + wn*16*FN + i*16 + 4*(l / 16) + (0..3).
     const int row_in = fr, col_in = fc * 4;
     if constexpr (OUT == Out::Y && sizeof(YT) == 2) {
@@ -431,8 +462,8 @@ __global__ __launch_bounds__(WM * 2 * 64) void gemm_w8a8_wide_kernel(
                 __syncthreads();  // the ring (first half) or the staging rows (second) are free
                 if (wm / HW == half) {
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int rl = (wm % HW) * 64 + j * 16 + row_in;  // row within the half
+                    for (int j = 0; j < FM; ++j) {
+                        const int rl = (wm % HW) * FM * 16 + j * 16 + row_in;  // row within the half
                         const int row = m0 + half * HR + rl;
                         const float a_s = row < m ? as[row] : 0.0f;
 #pragma unroll
@@ -461,8 +492,8 @@ __global__ __launch_bounds__(WM * 2 * 64) void gemm_w8a8_wide_kernel(
         }
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int row = m0 + wm * 64 + j * 16 + row_in;
+    for (int j = 0; j < FM; ++j) {
+        const int row = m0 + wm * FM * 16 + j * 16 + row_in;
         if (row >= m) continue;
         const float a_s = OUT == Out::Y ? as[row] : 0.0f;
 #pragma unroll
@@ -739,6 +770,7 @@ struct PrefillPlan {
     bool narrow;  // 64 x 128 tiles
     int wide_fn;  // 0: not wide
     int wide_wm;  // wide tile rows / 64
+    int sw;       // K slab bytes of the prefill kernel (64 or 128)
     int tiles, splits, k_slabs;
     size_t acc_bytes;
 };
@@ -779,17 +811,24 @@ PrefillPlan plan_prefill(int64_t m, int64_t n, int64_t k) {
     }
     // at most 64 MiB of partial planes
     splits = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(splits, (int64_t(64) << 20) / std::max<int64_t>(1, m * n * 4))));
-    p.k_slabs = (nk + splits - 1) / splits;
-    p.splits = (nk + p.k_slabs - 1) / p.k_slabs;
+    // 128 x 128 tiles that fit one round (split ranges included) take 128-byte
+    // slabs in a 3-slot ring (m = 512, n = 1536, k = 8960 in four ranges: 25.4
+    // -> 23.2 us); where a second workgroup per CU matters, the 64-byte ring
+    // keeps its smaller LDS footprint (the 256 x 128 multi-round tiles ran
+    // slower with 128-byte slabs).
+    p.sw = !p.big && !p.narrow && int64_t(p.tiles) * splits <= 256 ? 128 : 64;
+    const int ns = p.sw == 128 ? static_cast<int>((k + 127) / 128) : nk;
+    p.k_slabs = (ns + splits - 1) / splits;
+    p.splits = (ns + p.k_slabs - 1) / p.k_slabs;
     if (p.splits > 1) p.acc_bytes = round_up(static_cast<size_t>(p.splits) * static_cast<size_t>(m * n) * 4, 256);
     return p;
 }
 
-template <int WM, int WN, int D, Out OUT, typename YT>
+template <int WM, int WN, int D, int SW, Out OUT, typename YT>
 nq_status launch_prefill(const int8_t* xq, const float* as, const int8_t* wq, const float* ws, const float* bias,
                          YT* y, int32_t* acc_out, int m, int n, int k, int splits, int k_slabs, hipStream_t s) {
-    using S = PrefillShape<WM, WN, D>;
-    auto* fn = gemm_w8a8_prefill_kernel<WM, WN, D, OUT, YT>;
+    using S = PrefillShape<WM, WN, D, SW>;
+    auto* fn = gemm_w8a8_prefill_kernel<WM, WN, D, SW, OUT, YT>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                                        static_cast<int>(S::kLds));
@@ -800,11 +839,11 @@ nq_status launch_prefill(const int8_t* xq, const float* as, const int8_t* wq, co
     return launch_status("gemm_w8a8_prefill_kernel");
 }
 
-template <int WM, int FN, Out OUT, typename YT>
+template <int WM, int FN, int FM, Out OUT, typename YT>
 nq_status launch_wide(const int8_t* xq, const float* as, const int8_t* wq, const float* ws, const float* bias,
                       YT* y, int32_t* acc_out, int m, int n, int k, hipStream_t s) {
-    using S = WideShape<WM, FN>;
-    auto* fn = gemm_w8a8_wide_kernel<WM, FN, OUT, YT>;
+    using S = WideShape<WM, FN, FM>;
+    auto* fn = gemm_w8a8_wide_kernel<WM, FN, FM, OUT, YT>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                                        static_cast<int>(S::kLds));
@@ -820,15 +859,16 @@ nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const fl
     const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
     const PrefillPlan p = plan_prefill(m, n, k);
     if (p.wide_fn) {
+        // 256-row tiles: 4 x 2 waves of 64 rows; 128-row tiles: 4 x 2 waves of 32 rows.
         auto wide = [&](auto wmtag, auto fntag) -> nq_status {
-            constexpr int WM = decltype(wmtag)::value, FN = decltype(fntag)::value;
+            constexpr int FM = decltype(wmtag)::value, FN = decltype(fntag)::value;
             if (acc_out)
-                return launch_wide<WM, FN, Out::ACC, float>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, s);
+                return launch_wide<4, FN, FM, Out::ACC, float>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, s);
             if (ydt == NQ_F32)
-                return launch_wide<WM, FN, Out::Y, float>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi,
-                                                          ni, ki, s);
-            return launch_wide<WM, FN, Out::Y, _Float16>(xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr,
-                                                         mi, ni, ki, s);
+                return launch_wide<4, FN, FM, Out::Y, float>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi,
+                                                             ni, ki, s);
+            return launch_wide<4, FN, FM, Out::Y, _Float16>(xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr,
+                                                            mi, ni, ki, s);
         };
         auto by_fn = [&](auto wmtag) -> nq_status {
             if (p.wide_fn == 8) return wide(wmtag, std::integral_constant<int, 8>{});
@@ -844,23 +884,31 @@ nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const fl
         NQ_REQUIRE(aligned(workspace, 256), NQ_BAD_ALIGN, "w8a8 gemm: workspace must be 256-byte aligned");
         parts = static_cast<int32_t*>(workspace);
     }
-    auto go = [&](auto wmtag, auto wntag, auto dtag) -> nq_status {
+    auto go = [&](auto wmtag, auto wntag, auto dtag, auto swtag) -> nq_status {
         constexpr int WM = decltype(wmtag)::value, WN = decltype(wntag)::value, D = decltype(dtag)::value;
+        constexpr int SW = decltype(swtag)::value;
         if (p.splits > 1)
-            return launch_prefill<WM, WN, D, Out::PARTIAL, float>(xq, as, wq, ws, bias, nullptr, parts, mi, ni, ki,
-                                                                 p.splits, p.k_slabs, s);
+            return launch_prefill<WM, WN, D, SW, Out::PARTIAL, float>(xq, as, wq, ws, bias, nullptr, parts, mi, ni,
+                                                                     ki, p.splits, p.k_slabs, s);
         if (acc_out)
-            return launch_prefill<WM, WN, D, Out::ACC, float>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, 1,
-                                                             p.k_slabs, s);
+            return launch_prefill<WM, WN, D, SW, Out::ACC, float>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki,
+                                                                 1, p.k_slabs, s);
         if (ydt == NQ_F32)
-            return launch_prefill<WM, WN, D, Out::Y, float>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi,
-                                                           ni, ki, 1, p.k_slabs, s);
-        return launch_prefill<WM, WN, D, Out::Y, _Float16>(xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr,
-                                                          mi, ni, ki, 1, p.k_slabs, s);
+            return launch_prefill<WM, WN, D, SW, Out::Y, float>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr,
+                                                               mi, ni, ki, 1, p.k_slabs, s);
+        return launch_prefill<WM, WN, D, SW, Out::Y, _Float16>(xq, as, wq, ws, bias, static_cast<_Float16*>(y),
+                                                              nullptr, mi, ni, ki, 1, p.k_slabs, s);
     };
-    const nq_status st = p.big      ? go(std::integral_constant<int, 4>{}, std::integral_constant<int, 2>{}, std::integral_constant<int, 3>{})
-                         : p.narrow ? go(std::integral_constant<int, 1>{}, std::integral_constant<int, 2>{}, std::integral_constant<int, 4>{})
-                                    : go(std::integral_constant<int, 2>{}, std::integral_constant<int, 2>{}, std::integral_constant<int, 4>{});
+    using I = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    using I4 = std::integral_constant<int, 4>;
+    using I64 = std::integral_constant<int, 64>;
+    using I128 = std::integral_constant<int, 128>;
+    const nq_status st = p.big          ? go(I4{}, I2{}, I3{}, I64{})
+                         : p.narrow     ? go(I{}, I2{}, I4{}, I64{})
+                         : p.sw == 128  ? go(I2{}, I2{}, I3{}, I128{})
+                                        : go(I2{}, I2{}, I4{}, I64{});
     if (st != NQ_OK || p.splits == 1) return st;
     return reduce_partials(parts, p.splits, as, ws, bias, y, ydt, acc_out, mi, ni, s);
 }

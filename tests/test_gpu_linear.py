@@ -397,7 +397,7 @@ def _plan_shapes():
     K slab is half empty."""
     rng = np.random.default_rng(2026)
     shapes = [(2304, 16384, 128), (2048, 8200, 128), (200, 1003, 4096), (96, 5000, 6144)]   # big, wide, split
-    shapes += [(2048, 8200, 192), (512, 17000, 320), (1900, 8900, 64)]   # wide with k % 128 == 64
+    shapes += [(2048, 8200, 192), (512, 17000, 320), (1900, 8900, 64), (200, 1003, 4160)]   # last 128-byte slab half empty
     for _ in range(12):
         m = int(rng.integers(65, 2300))
         n = int(rng.integers(16, 20000))
