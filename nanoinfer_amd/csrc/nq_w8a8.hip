@@ -320,8 +320,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_w8a8_prefill_kernel(
 // smaller tiles: every output tile costs one pass over its A rows and B rows,
 // and a second round would leave most CUs idle. WM x 2 waves (WM = 4 or 2), each
 // 64 x 16*FN outputs (4 x FN fragments, 4*FN int32 accumulator registers). K
-// advances in 128-byte slabs (two MFMA K steps) through a 2-slot LDS ring
-// filled by LDS-DMA; the request for slab kt + 1 goes out right after the
+// advances in 128-byte slabs (two MFMA K steps) through an LDS ring of as many
+// slots D as fit (2 for 256 x 288 tiles, 3 for 128 x 288, up to 8 for small
+// tiles) filled by LDS-DMA; the request for slab kt + D - 1 goes out right after the
 // barrier that frees its slot. A 1 KB DMA request covers 8 rows x 128 bytes,
 // i.e. whole 128-byte cache lines: with 64-byte slabs (16 rows x 64 bytes per
 // request, a 4-slot ring) every request touched twice as many lines and the
@@ -338,10 +339,13 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_w8a8_prefill_kernel(
 // whole output at the end, which no later work overlaps).
 template <int WM, int FN, int FM>
 struct WideShape {
-    static constexpr int kWM = WM, kWN = 2, kWaves = WM * 2, kD = 2, kRow = 128;
+    static constexpr int kWM = WM, kWN = 2, kWaves = WM * 2, kRow = 128;
     static constexpr int kBM = kWM * FM * 16, kBN = kWN * FN * 16;
     static constexpr int kXB = kBM / 8, kNB = kXB + kBN / 8, kQ = (kNB + kWaves - 1) / kWaves;
     static constexpr int kSlab = (kBM + kBN) * kRow;
+    // As many ring slots as 160 KB of LDS holds beside the sink (at most 8).
+    static constexpr int kD = std::min(8, (160 * 1024 - 1024) / kSlab);
+    static_assert(kD >= 2, "two slabs must fit");
     static constexpr int kSink = kD * kSlab;  // 1 KB
     static constexpr size_t kLds = std::max<size_t>(size_t(kSink) + 1024, size_t(kBM / 2) * kBN * 2);
 };
@@ -755,47 +759,56 @@ nq_status gemm_skinny(const int8_t* xq, const float* as, const int8_t* wq, const
     return reduce_partials(parts, p.splits, as, ws, bias, y, ydt, acc_out, mi, ni, s);
 }
 
-// Big-m plan. When 256 x (32*fn) tiles, fn = 8..10, or else 128 x (32*fn)
-// tiles number between 192 and 256 (one per CU, one round), the wide-tile
-// kernel runs (smallest fn that fits, 256-row tiles first). Otherwise 256 x 128 tiles
-// (8 waves, 3-slab ring) when they give at least two tiles per CU, else
-// 128 x 128 tiles (4 waves, 4-slab ring; 64 x 128 with 2 waves for short K and
-// few tiles). With fewer than 256 tiles a long K is split over workgroups in
-// ranges of at least 32 slabs: each range stores its int32 partial tile into
-// its own workspace plane and a reduction launch sums the planes and applies
-// the epilogue (device-scope atomics into one plane measured several times
-// slower).
+// Big-m plan. The wide-tile kernel takes every shape that one round of its
+// tiles covers (at most one tile per CU): among the tile shapes below, the one
+// with the most tiles not above 256 (earlier entries win ties). One round of
+// small tiles with a deep ring beat two rounds and beat fewer, larger tiles
+// (m = 512, n = 2048, k = 1536: 64 x 64 tiles 7.7 us, 64 x 128 tiles 9.9,
+// 128 x 128 split-free 2-wave-per-SIMD tiles 13.3). When that round would have
+// fewer than 128 tiles and K is long, the K-split prefill plans below run
+// instead. Otherwise 256 x 128 tiles (8 waves, 3-slab ring) when they give
+// at least two tiles per CU, else 128 x 128 tiles (4 waves, 4-slab ring; 64 x
+// 128 with 2 waves for short K and few tiles). With fewer than 256 tiles a
+// long K is split over workgroups in ranges of at least 32 slabs: each range
+// stores its int32 partial tile into its own workspace plane and a reduction
+// launch sums the planes and applies the epilogue (device-scope atomics into
+// one plane measured several times slower).
+struct WideTile {
+    int fm, fn;  // tile = (64 * fm) x (32 * fn), 8 waves of (16 * fm) x (16 * fn)
+};
+constexpr WideTile kWideTiles[] = {{4, 9}, {4, 8}, {4, 10}, {4, 4}, {2, 9}, {2, 8}, {2, 10},
+                                   {2, 4}, {2, 2}, {1, 4}, {1, 3}, {1, 2}};
 struct PrefillPlan {
     bool big;
     bool narrow;  // 64 x 128 tiles
     int wide_fn;  // 0: not wide
-    int wide_wm;  // wide tile rows / 64
+    int wide_fm;  // wide tile rows / 64
     int sw;       // K slab bytes of the prefill kernel (64 or 128)
     int tiles, splits, k_slabs;
     size_t acc_bytes;
 };
 PrefillPlan plan_prefill(int64_t m, int64_t n, int64_t k) {
     PrefillPlan p{};
-    for (int wm = 4; wm >= 2; wm -= 2) {
-        for (int fn = 8; fn <= 10; ++fn) {
-            const int64_t t = ((m + 64 * wm - 1) / (64 * wm)) * ((n + 32 * fn - 1) / (32 * fn));
-            if (t <= 256) {
-                if (t >= 192) {
-                    p.wide_fn = fn;
-                    p.wide_wm = wm;
-                    p.tiles = static_cast<int>(t);
-                    p.splits = 1;
-                    p.k_slabs = std::max(1, static_cast<int>(k / kBK));
-                    return p;
-                }
-                break;
-            }
+    const int nk = std::max(1, static_cast<int>(k / kBK));  // also sized for shapes outside the contract
+    int64_t best = 0;
+    for (const WideTile& t : kWideTiles) {
+        const int64_t c = ((m + 64 * t.fm - 1) / (64 * t.fm)) * ((n + 32 * t.fn - 1) / (32 * t.fn));
+        if (c <= 256 && c > best) {
+            best = c;
+            p.wide_fm = t.fm;
+            p.wide_fn = t.fn;
         }
     }
+    if (best >= 128 || (best > 0 && nk < 64)) {
+        p.tiles = static_cast<int>(best);
+        p.splits = 1;
+        p.k_slabs = nk;
+        return p;
+    }
+    p.wide_fm = p.wide_fn = 0;
     const int64_t big_tiles = ((m + 255) / 256) * ((n + 127) / 128);
     p.big = big_tiles >= 512;
     p.tiles = static_cast<int>(p.big ? big_tiles : ((m + 127) / 128) * ((n + 127) / 128));
-    const int nk = std::max(1, static_cast<int>(k / kBK));  // also sized for shapes outside the contract
     int splits = 1;
     // Fewer than 256 tiles: K splits into ranges of at least 32 slabs (the
     // partial planes and the reduction launch cost more than a short K loop
@@ -859,9 +872,8 @@ nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const fl
     const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
     const PrefillPlan p = plan_prefill(m, n, k);
     if (p.wide_fn) {
-        // 256-row tiles: 4 x 2 waves of 64 rows; 128-row tiles: 4 x 2 waves of 32 rows.
-        auto wide = [&](auto wmtag, auto fntag) -> nq_status {
-            constexpr int FM = decltype(wmtag)::value, FN = decltype(fntag)::value;
+        auto wide = [&](auto fmtag, auto fntag) -> nq_status {
+            constexpr int FM = decltype(fmtag)::value, FN = decltype(fntag)::value;
             if (acc_out)
                 return launch_wide<4, FN, FM, Out::ACC, float>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, s);
             if (ydt == NQ_F32)
@@ -870,12 +882,22 @@ nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const fl
             return launch_wide<4, FN, FM, Out::Y, _Float16>(xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr,
                                                             mi, ni, ki, s);
         };
-        auto by_fn = [&](auto wmtag) -> nq_status {
-            if (p.wide_fn == 8) return wide(wmtag, std::integral_constant<int, 8>{});
-            if (p.wide_fn == 9) return wide(wmtag, std::integral_constant<int, 9>{});
-            return wide(wmtag, std::integral_constant<int, 10>{});
-        };
-        return p.wide_wm == 4 ? by_fn(std::integral_constant<int, 4>{}) : by_fn(std::integral_constant<int, 2>{});
+        using std::integral_constant;
+        switch (p.wide_fm * 100 + p.wide_fn) {
+            case 409: return wide(integral_constant<int, 4>{}, integral_constant<int, 9>{});
+            case 408: return wide(integral_constant<int, 4>{}, integral_constant<int, 8>{});
+            case 410: return wide(integral_constant<int, 4>{}, integral_constant<int, 10>{});
+            case 404: return wide(integral_constant<int, 4>{}, integral_constant<int, 4>{});
+            case 209: return wide(integral_constant<int, 2>{}, integral_constant<int, 9>{});
+            case 208: return wide(integral_constant<int, 2>{}, integral_constant<int, 8>{});
+            case 210: return wide(integral_constant<int, 2>{}, integral_constant<int, 10>{});
+            case 204: return wide(integral_constant<int, 2>{}, integral_constant<int, 4>{});
+            case 202: return wide(integral_constant<int, 2>{}, integral_constant<int, 2>{});
+            case 104: return wide(integral_constant<int, 1>{}, integral_constant<int, 4>{});
+            case 103: return wide(integral_constant<int, 1>{}, integral_constant<int, 3>{});
+            case 102: return wide(integral_constant<int, 1>{}, integral_constant<int, 2>{});
+            default: return fail(NQ_BAD_ARG, "w8a8 gemm: no wide tile %d x %d", 64 * p.wide_fm, 32 * p.wide_fn);
+        }
     }
     int32_t* parts = nullptr;
     if (p.splits > 1) {

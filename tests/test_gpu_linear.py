@@ -408,6 +408,33 @@ def _plan_shapes():
     return shapes
 
 
+# One shape per wide-kernel tile (rows x cols): 64x64, 64x96, 64x128, 128x64,
+# 128x128, 128x256, 128x320, 256x128, 256x256, 256x320 (256x288 and 128x288 are
+# the config shapes above), each with a half-empty last 128-byte K slab or not.
+WIDE_TILE_SHAPES = [(512, 2048, 1536), (1024, 1536, 1536), (1088, 1920, 320), (1024, 2048, 192),
+                    (1000, 4000, 448), (512, 16384, 320), (512, 20480, 192), (1024, 8192, 448),
+                    (2048, 8192, 256), (2048, 10240, 192)]
+
+
+@pytest.mark.parametrize("m,n,k", WIDE_TILE_SHAPES)
+def test_w8a8_wide_tiles(dev, nq, m, n, k):
+    """Every wide tile: int32 accumulators and the fp32 / fp16 epilogue with
+    bias equal the GEMV path bit for bit."""
+    g = torch.Generator(device=dev).manual_seed(m + 3 * n + 7 * k)
+    xq = torch.randint(-127, 128, (m, k), generator=g, device=dev, dtype=torch.int8)
+    wq = torch.randint(-127, 128, (n, k), generator=g, device=dev, dtype=torch.int8)
+    assert torch.equal(nq.w8a8_acc_i32(xq, wq, nq._lib.NQ_PATH_MFMA), nq.w8a8_acc_i32(xq, wq, nq._lib.NQ_PATH_GEMV))
+    x = torch.randn((m, k), generator=g, device=dev)
+    w = torch.randn((n, k), generator=g, device=dev) * 0.05
+    b = torch.randn(n, generator=g, device=dev)
+    t = nq.quantize_q8(w)
+    yg = nq.linear_w8a8(x, t, b, path=nq._lib.NQ_PATH_GEMV, out_dtype=F32)
+    ym = nq.linear_w8a8(x, t, b, path=nq._lib.NQ_PATH_MFMA, out_dtype=F32)
+    assert torch.equal(ym, yg), (m, n, k)
+    y16 = nq.linear_w8a8(x, t, b, path=nq._lib.NQ_PATH_MFMA, out_dtype=F16)
+    assert torch.equal(y16, ym.half()), (m, n, k)
+
+
 @pytest.mark.parametrize("m,n,k", _plan_shapes())
 def test_w8a8_plans_random_shapes(dev, nq, m, n, k):
     """int32 accumulators of the MFMA plans equal the GEMV path's bit for bit."""
