@@ -866,39 +866,45 @@ nq_status launch_wide(const int8_t* xq, const float* as, const int8_t* wq, const
     return launch_status("gemm_w8a8_wide_kernel");
 }
 
+// One round of wide-kernel tiles of (64 * fm) x (32 * fn).
+nq_status launch_wide_tile(int fm, int fn, const int8_t* xq, const float* as, const int8_t* wq, const float* ws,
+                           const float* bias, void* y, nq_dtype ydt, int32_t* acc_out, int mi, int ni, int ki,
+                           hipStream_t s) {
+    auto wide = [&](auto fmtag, auto fntag) -> nq_status {
+        constexpr int FM = decltype(fmtag)::value, FN = decltype(fntag)::value;
+        if (acc_out)
+            return launch_wide<4, FN, FM, Out::ACC, float>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, s);
+        if (ydt == NQ_F32)
+            return launch_wide<4, FN, FM, Out::Y, float>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi,
+                                                         ni, ki, s);
+        return launch_wide<4, FN, FM, Out::Y, _Float16>(xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr,
+                                                        mi, ni, ki, s);
+    };
+    using std::integral_constant;
+    switch (fm * 100 + fn) {
+        case 409: return wide(integral_constant<int, 4>{}, integral_constant<int, 9>{});
+        case 408: return wide(integral_constant<int, 4>{}, integral_constant<int, 8>{});
+        case 410: return wide(integral_constant<int, 4>{}, integral_constant<int, 10>{});
+        case 404: return wide(integral_constant<int, 4>{}, integral_constant<int, 4>{});
+        case 209: return wide(integral_constant<int, 2>{}, integral_constant<int, 9>{});
+        case 208: return wide(integral_constant<int, 2>{}, integral_constant<int, 8>{});
+        case 210: return wide(integral_constant<int, 2>{}, integral_constant<int, 10>{});
+        case 204: return wide(integral_constant<int, 2>{}, integral_constant<int, 4>{});
+        case 202: return wide(integral_constant<int, 2>{}, integral_constant<int, 2>{});
+        case 104: return wide(integral_constant<int, 1>{}, integral_constant<int, 4>{});
+        case 103: return wide(integral_constant<int, 1>{}, integral_constant<int, 3>{});
+        case 102: return wide(integral_constant<int, 1>{}, integral_constant<int, 2>{});
+        case 101: return wide(integral_constant<int, 1>{}, integral_constant<int, 1>{});
+        default: return fail(NQ_BAD_ARG, "w8a8 gemm: no wide tile %d x %d", 64 * fm, 32 * fn);
+    }
+}
+
 nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const float* ws,
                    const float* bias, void* y, nq_dtype ydt, int32_t* acc_out, int64_t m, int64_t n,
                    int64_t k, void* workspace, size_t ws_bytes, hipStream_t s) {
     const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
     const PrefillPlan p = plan_prefill(m, n, k);
-    if (p.wide_fn) {
-        auto wide = [&](auto fmtag, auto fntag) -> nq_status {
-            constexpr int FM = decltype(fmtag)::value, FN = decltype(fntag)::value;
-            if (acc_out)
-                return launch_wide<4, FN, FM, Out::ACC, float>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, s);
-            if (ydt == NQ_F32)
-                return launch_wide<4, FN, FM, Out::Y, float>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr, mi,
-                                                             ni, ki, s);
-            return launch_wide<4, FN, FM, Out::Y, _Float16>(xq, as, wq, ws, bias, static_cast<_Float16*>(y), nullptr,
-                                                            mi, ni, ki, s);
-        };
-        using std::integral_constant;
-        switch (p.wide_fm * 100 + p.wide_fn) {
-            case 409: return wide(integral_constant<int, 4>{}, integral_constant<int, 9>{});
-            case 408: return wide(integral_constant<int, 4>{}, integral_constant<int, 8>{});
-            case 410: return wide(integral_constant<int, 4>{}, integral_constant<int, 10>{});
-            case 404: return wide(integral_constant<int, 4>{}, integral_constant<int, 4>{});
-            case 209: return wide(integral_constant<int, 2>{}, integral_constant<int, 9>{});
-            case 208: return wide(integral_constant<int, 2>{}, integral_constant<int, 8>{});
-            case 210: return wide(integral_constant<int, 2>{}, integral_constant<int, 10>{});
-            case 204: return wide(integral_constant<int, 2>{}, integral_constant<int, 4>{});
-            case 202: return wide(integral_constant<int, 2>{}, integral_constant<int, 2>{});
-            case 104: return wide(integral_constant<int, 1>{}, integral_constant<int, 4>{});
-            case 103: return wide(integral_constant<int, 1>{}, integral_constant<int, 3>{});
-            case 102: return wide(integral_constant<int, 1>{}, integral_constant<int, 2>{});
-            default: return fail(NQ_BAD_ARG, "w8a8 gemm: no wide tile %d x %d", 64 * p.wide_fm, 32 * p.wide_fn);
-        }
-    }
+    if (p.wide_fn) return launch_wide_tile(p.wide_fm, p.wide_fn, xq, as, wq, ws, bias, y, ydt, acc_out, mi, ni, ki, s);
     int32_t* parts = nullptr;
     if (p.splits > 1) {
         NQ_REQUIRE(workspace && ws_bytes >= p.acc_bytes, NQ_BAD_ARG,
@@ -976,15 +982,38 @@ bool skinny_ok(int64_t m, int64_t n, int64_t k) {
     return std::min<int64_t>(m, kSkinnyMaxM) * k < (int64_t(1) << 31) - 64 && n * k < (int64_t(1) << 31) - 64;
 }
 
+// Decode batches (m <= 64) with a short K and a tall weight: one round of
+// 64 x (32 * fn) wide tiles (64-row tiles, rows past m read zeros without
+// touching memory) when it gives at least 128 tiles; returns fn, or 0 for the
+// skinny kernel. Measured (k = 1536, n = 8960): m = 16 8.6 -> 7.2 us, m = 32
+// 11.1 -> 7.4, m = 64 15.7 -> 8.4; n = 1536 (48 tiles or fewer) stays skinny, as
+// does long K (the skinny plan splits K: k = 8960, n = 1536, m = 16 10.2 us vs
+// 19.1 unsplit).
+int small_wide_fn(int64_t m, int64_t n, int64_t k) {
+    if (m > kSkinnyMaxM || k > 4096 || !prefill_ok(m, n, k)) return 0;
+    int best_fn = 0;
+    int64_t best = 0;
+    for (int fn = 4; fn >= 1; --fn) {
+        const int64_t c = (n + 32 * fn - 1) / (32 * fn);
+        if (c <= 256 && c > best) {
+            best = c;
+            best_fn = fn;
+        }
+    }
+    return best >= 128 ? best_fn : 0;
+}
+
 // AUTO: the v_dot4 GEMV up to m = 4, and up to m = 8 for long K (where the
 // skinny MFMA plan splits K and pays for a reduction launch) or tall weights
-// (n >= 8192: m = 8, n = 8960, k = 1536 GEMV 10.25 us vs MFMA 10.83); the
+// that the small-m wide tiles do not take (m = 8, n = 8960, k = 1536: GEMV
+// 10.25 us, skinny MFMA 10.83, wide tiles 7.1); the
 // GEMV's per-row dot work grows with m while one 16x16x64 MFMA covers 16
 // activation rows, so the MFMA kernels take larger m. Measured on the decode
 // shapes k = 1536 / 8960, n = 256 .. 8960.
 int resolve_path(int path, int64_t m, int64_t n, int64_t k) {
     if (path != NQ_PATH_AUTO) return path;
-    return (m <= 4 || (m <= 8 && (k >= 4096 || n >= 8192))) ? NQ_PATH_GEMV : NQ_PATH_MFMA;
+    return (m <= 4 || (m <= 8 && (k >= 4096 || (n >= 8192 && !small_wide_fn(m, n, k))))) ? NQ_PATH_GEMV
+                                                                                          : NQ_PATH_MFMA;
 }
 
 // Runs the chosen path on pre-quantized activations.
@@ -997,6 +1026,9 @@ nq_status run_gemm(const int8_t* xq, const float* as, const int8_t* wq, const fl
     // the v_dot4 GEMV (64-bit addressing) takes them, in slices of 8 rows.
     if (p == NQ_PATH_MFMA && !skinny_ok(m, n, k)) p = NQ_PATH_GEMV;
     if (p == NQ_PATH_MFMA) {
+        if (const int fn = small_wide_fn(m, n, k))
+            return launch_wide_tile(1, fn, xq, as, wq, ws, bias, y, ydt, acc_out, static_cast<int>(m),
+                                    static_cast<int>(n), static_cast<int>(k), s);
         if (m <= kSkinnyMaxM)
             return gemm_skinny(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, workspace, ws_bytes, s);
         // (The skinny kernel over 64-row blocks in one launch was measured on the

@@ -408,12 +408,14 @@ def _plan_shapes():
     return shapes
 
 
-# One shape per wide-kernel tile (rows x cols): 64x64, 64x96, 64x128, 128x64,
+# One shape per wide-kernel tile (rows x cols): 64x32, 64x64, 64x96, 64x128, 128x64,
 # 128x128, 128x256, 128x320, 256x128, 256x256, 256x320 (256x288 and 128x288 are
 # the config shapes above), each with a half-empty last 128-byte K slab or not.
 WIDE_TILE_SHAPES = [(512, 2048, 1536), (1024, 1536, 1536), (1088, 1920, 320), (1024, 2048, 192),
                     (1000, 4000, 448), (512, 16384, 320), (512, 20480, 192), (1024, 8192, 448),
-                    (2048, 8192, 256), (2048, 10240, 192)]
+                    (2048, 8192, 256), (2048, 10240, 192),
+                    # m <= 64 with a tall weight: 64 x 32..128 tiles, rows past m read as zeros
+                    (16, 8960, 1536), (64, 17920, 1536), (8, 8960, 192), (33, 4100, 320), (64, 16384, 1600)]
 
 
 @pytest.mark.parametrize("m,n,k", WIDE_TILE_SHAPES)
