@@ -354,7 +354,7 @@ template <int WM, int FN, int FM, Out OUT, typename YT>
 __global__ __launch_bounds__(WM * 2 * 64) void gemm_w8a8_wide_kernel(
     const int8_t* __restrict__ xq, const float* __restrict__ as, const int8_t* __restrict__ wq,
     const float* __restrict__ ws, const float* __restrict__ bias, YT* __restrict__ y,
-    int32_t* __restrict__ acc_out, int m, int n, int k, int tiles_m, int tiles_n) {
+    int32_t* __restrict__ acc_out, int m, int n, int k, int tiles_m, int tiles_n, int k_slabs) {
     using S = WideShape<WM, FN, FM>;
     constexpr int NW = S::kWaves, Q = S::kQ, XB = S::kXB, NB = S::kNB, BM = S::kBM, BN = S::kBN, D = S::kD;
     extern __shared__ __attribute__((aligned(16))) int8_t lds[];
@@ -390,13 +390,18 @@ __global__ __launch_bounds__(WM * 2 * 64) void gemm_w8a8_wide_kernel(
         vtail[q] = c < 4 ? voff[q] : kOob;
         loff[q] = real ? b * 1024 : S::kSink;
     }
-    const int nk = (k + S::kRow - 1) / S::kRow;
+    // This workgroup's K range: slabs [s0, s1) (all of K unless the launch
+    // splits K over gridDim.y; OUT == PARTIAL then stores the range's int32
+    // tile into plane blockIdx.y).
+    const int nslab = (k + S::kRow - 1) / S::kRow;
     const bool half_tail = (k % S::kRow) != 0;  // k % 64 == 0 by contract
+    const int s0 = blockIdx.y * k_slabs, s1 = min(nslab, s0 + k_slabs), nk = s1 - s0;
     const unsigned lds_base = static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds));
-    auto issue = [&](int sl) {
+    auto issue = [&](int sl) {  // sl counts from s0
         const unsigned slot = static_cast<unsigned>(sl % D) * S::kSlab;
-        const int soff = sl < nk ? sl * S::kRow : kOob;
-        const bool tail = half_tail && sl == nk - 1;
+        const int g = s0 + sl;
+        const int soff = g < s1 ? g * S::kRow : kOob;
+        const bool tail = half_tail && g == nslab - 1;
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
             const int b = q * NW + wave;  // wave-uniform
@@ -456,6 +461,7 @@ __global__ __launch_bounds__(WM * 2 * 64) void gemm_w8a8_wide_kernel(
     // Lane l holds, for fragment (i, j), output row m0 + wm*FM*16 + j*16 + (l % 16)
     // and columns n0 + wn*16*FN + i*16 + 4*(l / 16) + (0..3).
     const int row_in = fr, col_in = fc * 4;
+    if constexpr (OUT == Out::PARTIAL) acc_out += static_cast<size_t>(blockIdx.y) * m * n;
     if constexpr (OUT == Out::Y && sizeof(YT) == 2) {
         if ((n & 7) == 0) {
             typedef _Float16 h4 __attribute__((ext_vector_type(4)));
@@ -505,7 +511,7 @@ __global__ __launch_bounds__(WM * 2 * 64) void gemm_w8a8_wide_kernel(
             const int col = n0 + wn * FN * 16 + i * 16 + col_in;
             const size_t o = static_cast<size_t>(row) * n + col;
             if (col + 3 < n && (n & 3) == 0) {
-                if constexpr (OUT == Out::ACC) {
+                if constexpr (OUT != Out::Y) {
                     *reinterpret_cast<v4i*>(acc_out + o) = acc[i][j];
                 } else {
                     const f4 w4 = *reinterpret_cast<const f4*>(ws + col);
@@ -527,7 +533,7 @@ __global__ __launch_bounds__(WM * 2 * 64) void gemm_w8a8_wide_kernel(
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     if (col + v >= n) break;
-                    if constexpr (OUT == Out::ACC) acc_out[o + v] = acc[i][j][v];
+                    if constexpr (OUT != Out::Y) acc_out[o + v] = acc[i][j][v];
                     else y[o + v] = from_f32<YT>(w8a8_epilogue(acc[i][j][v], a_s, ws[col + v], bias ? bias[col + v] : 0.0f));
                 }
             }
@@ -854,7 +860,8 @@ nq_status launch_prefill(const int8_t* xq, const float* as, const int8_t* wq, co
 
 template <int WM, int FN, int FM, Out OUT, typename YT>
 nq_status launch_wide(const int8_t* xq, const float* as, const int8_t* wq, const float* ws, const float* bias,
-                      YT* y, int32_t* acc_out, int m, int n, int k, hipStream_t s) {
+                      YT* y, int32_t* acc_out, int m, int n, int k, hipStream_t s, int splits = 1,
+                      int k_slabs = 1 << 30) {
     using S = WideShape<WM, FN, FM>;
     auto* fn = gemm_w8a8_wide_kernel<WM, FN, FM, OUT, YT>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -862,16 +869,25 @@ nq_status launch_wide(const int8_t* xq, const float* as, const int8_t* wq, const
                                                        static_cast<int>(S::kLds));
     if (attr != hipSuccess) return fail(NQ_HIP_ERROR, "gemm_w8a8_wide: LDS attribute: %s", hipGetErrorString(attr));
     const int tm = (m + S::kBM - 1) / S::kBM, tn = (n + S::kBN - 1) / S::kBN;
-    fn<<<tm * tn, S::kWaves * 64, S::kLds, s>>>(xq, as, wq, ws, bias, y, acc_out, m, n, k, tm, tn);
+    const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(splits));
+    fn<<<grid, S::kWaves * 64, S::kLds, s>>>(xq, as, wq, ws, bias, y, acc_out, m, n, k, tm, tn, k_slabs);
     return launch_status("gemm_w8a8_wide_kernel");
 }
 
 // One round of wide-kernel tiles of (64 * fm) x (32 * fn).
+// With splits > 1 each K range of k_slabs 128-byte slabs stores its int32
+// partial tile into plane i of `parts` and a reduction launch applies the epilogue.
 nq_status launch_wide_tile(int fm, int fn, const int8_t* xq, const float* as, const int8_t* wq, const float* ws,
                            const float* bias, void* y, nq_dtype ydt, int32_t* acc_out, int mi, int ni, int ki,
-                           hipStream_t s) {
+                           hipStream_t s, int splits = 1, int k_slabs = 1 << 30, int32_t* parts = nullptr) {
     auto wide = [&](auto fmtag, auto fntag) -> nq_status {
         constexpr int FM = decltype(fmtag)::value, FN = decltype(fntag)::value;
+        if (splits > 1) {
+            const nq_status st = launch_wide<4, FN, FM, Out::PARTIAL, float>(xq, as, wq, ws, bias, nullptr, parts, mi,
+                                                                             ni, ki, s, splits, k_slabs);
+            if (st != NQ_OK) return st;
+            return reduce_partials(parts, splits, as, ws, bias, y, ydt, acc_out, mi, ni, s);
+        }
         if (acc_out)
             return launch_wide<4, FN, FM, Out::ACC, float>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, s);
         if (ydt == NQ_F32)
@@ -941,6 +957,50 @@ nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const fl
     return reduce_partials(parts, p.splits, as, ws, bias, y, ydt, acc_out, mi, ni, s);
 }
 
+bool prefill_ok(int64_t m, int64_t n, int64_t k) {
+    return k % kBK == 0 && m * k < (int64_t(1) << 31) - 64 && n * k < (int64_t(1) << 31) - 64;
+}
+
+// Decode batches (m <= 64): one round of 64 x (32 * fn) wide tiles (rows past
+// m read zeros without touching memory) when the tiles, times the K ranges,
+// number at least 128; otherwise (fn = 0) the skinny kernel. Short K (<= 4096)
+// runs unsplit: k = 1536, n = 8960: m = 16 8.6 -> 7.2 us, m = 32 11.1 -> 7.4,
+// m = 64 15.7 -> 8.4 against the skinny kernel. Longer K splits into up to 8
+// ranges of at least 8 slabs for m > 16 (k = 8960, n = 1536: m = 32 12.9 ->
+// 10.7 us, m = 64 17.1 -> 11.2 in five ranges; at m <= 16 the skinny kernel's
+// own split is as fast).
+struct SmallWidePlan {
+    int fn, splits, k_slabs;
+    size_t acc_bytes;
+};
+SmallWidePlan plan_small_wide(int64_t m, int64_t n, int64_t k) {
+    SmallWidePlan p{};
+    if (m > kSkinnyMaxM || m <= 0 || n <= 0 || k <= 0 || !prefill_ok(m, n, k)) return p;
+    int64_t best = 0;
+    int fn = 0;
+    for (int f = 4; f >= 1; --f) {
+        const int64_t c = (n + 32 * f - 1) / (32 * f);
+        if (c <= 256 && c > best) {
+            best = c;
+            fn = f;
+        }
+    }
+    if (best == 0) return p;
+    const int nslab = static_cast<int>((k + 127) / 128);
+    int splits = 1;
+    if (k > 4096) {
+        if (m <= 16) return p;
+        splits = static_cast<int>(std::min<int64_t>({8, 256 / best, nslab / 8}));
+        splits = std::max(1, splits);
+    }
+    if (best * splits < 128) return p;
+    p.fn = fn;
+    p.k_slabs = (nslab + splits - 1) / splits;
+    p.splits = (nslab + p.k_slabs - 1) / p.k_slabs;
+    if (p.splits > 1) p.acc_bytes = round_up(static_cast<size_t>(p.splits) * static_cast<size_t>(m * n) * 4, 256);
+    return p;
+}
+
 // Workspace of the MFMA GEMM for this shape: a split plan's int32
 // accumulator (skinny plans for m <= 64, the prefill plan above, and the
 // skinny 64-row blocks that shapes outside the prefill contract run).
@@ -952,7 +1012,7 @@ bool skinny_one_launch(int64_t m, int64_t n, int64_t k) {
 
 size_t gemm_ws_bytes(int64_t m, int64_t n, int64_t k) {
     if (m <= 0 || n <= 0 || k <= 0) return 0;
-    if (m <= kSkinnyMaxM) return plan_skinny(m, n, k).acc_bytes;
+    if (m <= kSkinnyMaxM) return std::max(plan_skinny(m, n, k).acc_bytes, plan_small_wide(m, n, k).acc_bytes);
     const size_t sk = skinny_one_launch(m, n, k) ? plan_skinny(m, n, k).acc_bytes : plan_skinny(kSkinnyMaxM, n, k).acc_bytes;
     return std::max(plan_prefill(m, n, k).acc_bytes, sk);
 }
@@ -974,33 +1034,9 @@ bool mfma_ok(const int8_t* xq, const int8_t* wq, int64_t k) {
 }
 
 // The prefill kernel's contract: whole 64-byte K slabs and 32-bit buffer offsets.
-bool prefill_ok(int64_t m, int64_t n, int64_t k) {
-    return k % kBK == 0 && m * k < (int64_t(1) << 31) - 64 && n * k < (int64_t(1) << 31) - 64;
-}
 // The skinny kernel's contract: 32-bit buffer offsets (k % 16 == 0 is mfma_ok's).
 bool skinny_ok(int64_t m, int64_t n, int64_t k) {
     return std::min<int64_t>(m, kSkinnyMaxM) * k < (int64_t(1) << 31) - 64 && n * k < (int64_t(1) << 31) - 64;
-}
-
-// Decode batches (m <= 64) with a short K and a tall weight: one round of
-// 64 x (32 * fn) wide tiles (64-row tiles, rows past m read zeros without
-// touching memory) when it gives at least 128 tiles; returns fn, or 0 for the
-// skinny kernel. Measured (k = 1536, n = 8960): m = 16 8.6 -> 7.2 us, m = 32
-// 11.1 -> 7.4, m = 64 15.7 -> 8.4; n = 1536 (48 tiles or fewer) stays skinny, as
-// does long K (the skinny plan splits K: k = 8960, n = 1536, m = 16 10.2 us vs
-// 19.1 unsplit).
-int small_wide_fn(int64_t m, int64_t n, int64_t k) {
-    if (m > kSkinnyMaxM || k > 4096 || !prefill_ok(m, n, k)) return 0;
-    int best_fn = 0;
-    int64_t best = 0;
-    for (int fn = 4; fn >= 1; --fn) {
-        const int64_t c = (n + 32 * fn - 1) / (32 * fn);
-        if (c <= 256 && c > best) {
-            best = c;
-            best_fn = fn;
-        }
-    }
-    return best >= 128 ? best_fn : 0;
 }
 
 // AUTO: the v_dot4 GEMV up to m = 4, and up to m = 8 for long K (where the
@@ -1012,7 +1048,7 @@ int small_wide_fn(int64_t m, int64_t n, int64_t k) {
 // shapes k = 1536 / 8960, n = 256 .. 8960.
 int resolve_path(int path, int64_t m, int64_t n, int64_t k) {
     if (path != NQ_PATH_AUTO) return path;
-    return (m <= 4 || (m <= 8 && (k >= 4096 || (n >= 8192 && !small_wide_fn(m, n, k))))) ? NQ_PATH_GEMV
+    return (m <= 4 || (m <= 8 && (k >= 4096 || (n >= 8192 && !plan_small_wide(m, n, k).fn)))) ? NQ_PATH_GEMV
                                                                                           : NQ_PATH_MFMA;
 }
 
@@ -1026,9 +1062,18 @@ nq_status run_gemm(const int8_t* xq, const float* as, const int8_t* wq, const fl
     // the v_dot4 GEMV (64-bit addressing) takes them, in slices of 8 rows.
     if (p == NQ_PATH_MFMA && !skinny_ok(m, n, k)) p = NQ_PATH_GEMV;
     if (p == NQ_PATH_MFMA) {
-        if (const int fn = small_wide_fn(m, n, k))
-            return launch_wide_tile(1, fn, xq, as, wq, ws, bias, y, ydt, acc_out, static_cast<int>(m),
-                                    static_cast<int>(n), static_cast<int>(k), s);
+        const SmallWidePlan sw = plan_small_wide(m, n, k);
+        if (sw.fn) {
+            int32_t* parts = nullptr;
+            if (sw.splits > 1) {
+                NQ_REQUIRE(workspace && ws_bytes >= sw.acc_bytes, NQ_BAD_ARG,
+                           "w8a8 gemm: workspace of %zu bytes required, %zu given", sw.acc_bytes, ws_bytes);
+                NQ_REQUIRE(aligned(workspace, 256), NQ_BAD_ALIGN, "w8a8 gemm: workspace must be 256-byte aligned");
+                parts = static_cast<int32_t*>(workspace);
+            }
+            return launch_wide_tile(1, sw.fn, xq, as, wq, ws, bias, y, ydt, acc_out, static_cast<int>(m),
+                                    static_cast<int>(n), static_cast<int>(k), s, sw.splits, sw.k_slabs, parts);
+        }
         if (m <= kSkinnyMaxM)
             return gemm_skinny(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, workspace, ws_bytes, s);
         // (The skinny kernel over 64-row blocks in one launch was measured on the

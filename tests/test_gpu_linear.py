@@ -415,7 +415,9 @@ WIDE_TILE_SHAPES = [(512, 2048, 1536), (1024, 1536, 1536), (1088, 1920, 320), (1
                     (1000, 4000, 448), (512, 16384, 320), (512, 20480, 192), (1024, 8192, 448),
                     (2048, 8192, 256), (2048, 10240, 192),
                     # m <= 64 with a tall weight: 64 x 32..128 tiles, rows past m read as zeros
-                    (16, 8960, 1536), (64, 17920, 1536), (8, 8960, 192), (33, 4100, 320), (64, 16384, 1600)]
+                    (16, 8960, 1536), (64, 17920, 1536), (8, 8960, 192), (33, 4100, 320), (64, 16384, 1600),
+                    # ... and long K in ranges (partial planes + reduction)
+                    (32, 1536, 8960), (64, 1536, 8960), (40, 3000, 6080)]
 
 
 @pytest.mark.parametrize("m,n,k", WIDE_TILE_SHAPES)
