@@ -765,27 +765,29 @@ nq_status gemm_skinny(const int8_t* xq, const float* as, const int8_t* wq, const
     return reduce_partials(parts, p.splits, as, ws, bias, y, ydt, acc_out, mi, ni, s);
 }
 
-// Big-m plan. The wide-tile kernel takes every shape that one round of its
-// tiles covers (at most one tile per CU): among the tile shapes below, the one
-// with the most tiles not above 256 (earlier entries win ties). One round of
-// small tiles with a deep ring beat two rounds and beat fewer, larger tiles
-// (m = 512, n = 2048, k = 1536: 64 x 64 tiles 7.7 us, 64 x 128 tiles 9.9,
-// 128 x 128 split-free 2-wave-per-SIMD tiles 13.3). When that round would have
-// fewer than 128 tiles and K is long, the K-split prefill plans below run
-// instead. Otherwise 256 x 128 tiles (8 waves, 3-slab ring) when they give
-// at least two tiles per CU, else 128 x 128 tiles (4 waves, 4-slab ring; 64 x
-// 128 with 2 waves for short K and few tiles). With fewer than 256 tiles a
-// long K is split over workgroups in ranges of at least 32 slabs: each range
+// Big-m plan. The wide-tile kernel takes every shape except few tiles with a
+// long K. Among the tile shapes below it picks the least (rounds x tile area),
+// rounds = ceil(tiles / 256) (one tile per CU per round): a round costs about
+// the same for every workgroup, and a half-empty last round costs a full one.
+// Ties go to the larger tile. Measured: m = 512, n = 2048, k = 1536: 64 x 64
+// tiles 7.7 us, 64 x 128 9.9, 128 x 128 12.4; m = 4096, n = 8960, k = 1536: 256 x
+// 288 in two rounds 77.1, 256 x 320 (448 tiles) 78.4, 256 x 256 (560) 94.2, 256 x
+// 128 prefill tiles 85.5; m = 8192, n = 1536: 256 x 256 32.2 vs 256 x 288 34.9
+// (the same 192 tiles, less padding). When the chosen round has fewer than 128
+// tiles and K is long (>= 64 slabs of 64 bytes), the K-split prefill plan runs
+// instead: 128 x 128 tiles of 4 waves (64 x 128 with 2 waves when no split
+// applies and tiles are few), K in ranges of at least 32 slabs: each range
 // stores its int32 partial tile into its own workspace plane and a reduction
 // launch sums the planes and applies the epilogue (device-scope atomics into
 // one plane measured several times slower).
 struct WideTile {
     int fm, fn;  // tile = (64 * fm) x (32 * fn), 8 waves of (16 * fm) x (16 * fn)
 };
-constexpr WideTile kWideTiles[] = {{4, 9}, {4, 8}, {4, 10}, {4, 4}, {2, 9}, {2, 8}, {2, 10},
+// By falling area; of two equal areas the 64-row-per-wave tile comes first
+// (m = 1024, n = 8192, k = 4096: 256 x 128 44.0 us, 128 x 256 44.6).
+constexpr WideTile kWideTiles[] = {{4, 10}, {4, 9}, {4, 8}, {2, 10}, {2, 9}, {4, 4}, {2, 8},
                                    {2, 4}, {2, 2}, {1, 4}, {1, 3}, {1, 2}};
 struct PrefillPlan {
-    bool big;
     bool narrow;  // 64 x 128 tiles
     int wide_fn;  // 0: not wide
     int wide_fm;  // wide tile rows / 64
@@ -796,25 +798,25 @@ struct PrefillPlan {
 PrefillPlan plan_prefill(int64_t m, int64_t n, int64_t k) {
     PrefillPlan p{};
     const int nk = std::max(1, static_cast<int>(k / kBK));  // also sized for shapes outside the contract
-    int64_t best = 0;
+    int64_t best_cost = 0, best_tiles = 0;
     for (const WideTile& t : kWideTiles) {
         const int64_t c = ((m + 64 * t.fm - 1) / (64 * t.fm)) * ((n + 32 * t.fn - 1) / (32 * t.fn));
-        if (c <= 256 && c > best) {
-            best = c;
+        const int64_t cost = ((c + 255) / 256) * (64 * t.fm) * (32 * t.fn);
+        if (best_cost == 0 || cost < best_cost) {
+            best_cost = cost;
+            best_tiles = c;
             p.wide_fm = t.fm;
             p.wide_fn = t.fn;
         }
     }
-    if (best >= 128 || (best > 0 && nk < 64)) {
-        p.tiles = static_cast<int>(best);
+    if (best_tiles >= 128 || nk < 64) {
+        p.tiles = static_cast<int>(best_tiles);
         p.splits = 1;
         p.k_slabs = nk;
         return p;
     }
     p.wide_fm = p.wide_fn = 0;
-    const int64_t big_tiles = ((m + 255) / 256) * ((n + 127) / 128);
-    p.big = big_tiles >= 512;
-    p.tiles = static_cast<int>(p.big ? big_tiles : ((m + 127) / 128) * ((n + 127) / 128));
+    p.tiles = static_cast<int>(((m + 127) / 128) * ((n + 127) / 128));
     int splits = 1;
     // Fewer than 256 tiles: K splits into ranges of at least 32 slabs (the
     // partial planes and the reduction launch cost more than a short K loop
@@ -833,9 +835,8 @@ PrefillPlan plan_prefill(int64_t m, int64_t n, int64_t k) {
     // 128 x 128 tiles that fit one round (split ranges included) take 128-byte
     // slabs in a 3-slot ring (m = 512, n = 1536, k = 8960 in four ranges: 25.4
     // -> 23.2 us); where a second workgroup per CU matters, the 64-byte ring
-    // keeps its smaller LDS footprint (the 256 x 128 multi-round tiles ran
-    // slower with 128-byte slabs).
-    p.sw = !p.big && !p.narrow && int64_t(p.tiles) * splits <= 256 ? 128 : 64;
+    // keeps its smaller LDS footprint.
+    p.sw = !p.narrow && int64_t(p.tiles) * splits <= 256 ? 128 : 64;
     const int ns = p.sw == 128 ? static_cast<int>((k + 127) / 128) : nk;
     p.k_slabs = (ns + splits - 1) / splits;
     p.splits = (ns + p.k_slabs - 1) / p.k_slabs;
@@ -949,10 +950,9 @@ nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const fl
     using I4 = std::integral_constant<int, 4>;
     using I64 = std::integral_constant<int, 64>;
     using I128 = std::integral_constant<int, 128>;
-    const nq_status st = p.big          ? go(I4{}, I2{}, I3{}, I64{})
-                         : p.narrow     ? go(I{}, I2{}, I4{}, I64{})
-                         : p.sw == 128  ? go(I2{}, I2{}, I3{}, I128{})
-                                        : go(I2{}, I2{}, I4{}, I64{});
+    const nq_status st = p.narrow    ? go(I{}, I2{}, I4{}, I64{})
+                         : p.sw == 128 ? go(I2{}, I2{}, I3{}, I128{})
+                                       : go(I2{}, I2{}, I4{}, I64{});
     if (st != NQ_OK || p.splits == 1) return st;
     return reduce_partials(parts, p.splits, as, ws, bias, y, ydt, acc_out, mi, ni, s);
 }

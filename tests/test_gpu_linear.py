@@ -391,12 +391,12 @@ def test_w8a8_prefill_plans_exact(dev, nq, orc, m, n, k):
 
 
 def _plan_shapes():
-    """Seeded shapes spread over the W8A8 plans for m > 64: wide (256- and
-    128-row tiles), 256x128, 128x128, 64x128 narrow, split K, and k % 64 != 0
+    """Seeded shapes spread over the W8A8 plans for m > 64: wide tiles in one
+    or more rounds, 128x128 and 64x128 prefill tiles, split K, and k % 64 != 0
     (the skinny kernel over 64-row blocks); wide shapes whose last 128-byte
     K slab is half empty."""
     rng = np.random.default_rng(2026)
-    shapes = [(2304, 16384, 128), (2048, 8200, 128), (200, 1003, 4096), (96, 5000, 6144)]   # big, wide, split
+    shapes = [(2304, 16384, 128), (2048, 8200, 128), (200, 1003, 4096), (96, 5000, 6144)]   # 2 rounds, wide, split
     shapes += [(2048, 8200, 192), (512, 17000, 320), (1900, 8900, 64), (200, 1003, 4160)]   # last 128-byte slab half empty
     for _ in range(12):
         m = int(rng.integers(65, 2300))
@@ -413,7 +413,7 @@ def _plan_shapes():
 # the config shapes above), each with a half-empty last 128-byte K slab or not.
 WIDE_TILE_SHAPES = [(512, 2048, 1536), (1024, 1536, 1536), (1088, 1920, 320), (1024, 2048, 192),
                     (1000, 4000, 448), (512, 16384, 320), (512, 20480, 192), (1024, 8192, 448),
-                    (2048, 8192, 256), (2048, 10240, 192),
+                    (2048, 8192, 256), (2048, 10240, 192), (4096, 8960, 192), (3000, 5000, 320),
                     # m <= 64 with a tall weight: 64 x 32..128 tiles, rows past m read as zeros
                     (16, 8960, 1536), (64, 17920, 1536), (8, 8960, 192), (33, 4100, 320), (64, 16384, 1600),
                     # ... and long K in ranges (partial planes + reduction)
