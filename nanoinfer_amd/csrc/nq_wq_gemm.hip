@@ -32,6 +32,12 @@ namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 constexpr int kWqRing = 4, kOob = 0x7FFFFFF0;
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 // Waves per workgroup: 16 for one 16-row tile of x (more loads in flight per
 // CU), 8 for larger tiles (their prefetch ring needs up to 256 VGPRs).
 template <int TM>
@@ -275,6 +281,345 @@ nq_status launch_wq(const XT* x, const uint8_t* w, const ST* sc, const float* b,
     return launch_status("gemm_wq_kernel");
 }
 
+
+// ---- wide tiles for fp16 activations (m > 64) -------------------------------------------
+// One (64*FM) x (32*FN) output tile per workgroup, 8 waves as 4 x 2, each
+// (16*FM) x (16*FN) outputs, as in the wide W8A8 kernel: K advances in slabs
+// of 128 columns that LDS-DMA (buffer_load ... lds) writes into a ring of as
+// many slots as fit in 160 KB; the request for slab kt + D - 1 goes out after
+// the barrier that frees its slot. A slab holds the activation tile (256-byte
+// fp16 rows: a 1 KB request covers 4 rows), the weight codes (128-byte Q8 rows
+// / 64-byte Q4 rows) and, for Q4G, the tile's group scales of the slab. Each
+// lane loads the chunk an XOR swizzle puts in its LDS slot so the fragment
+// reads are bank-conflict free. Codes become fp16 exactly in registers after
+// the LDS read (the WFrag conversions above); A = activations, B = weights,
+// so a lane's four results share one weight row. Q8: one MFMA chain over K,
+// row scale in the epilogue. Q4G: an MFMA chain over each group's chunks
+// (at most one slab), scaled by the group scale into the fp32 accumulator.
+template <bool Q4, int FM, int FN, typename ST>
+struct WqWide {
+    static constexpr int kBM = 64 * FM, kBN = 32 * FN, kXRow = 256, kWRow = Q4 ? 64 : 128;
+    // Scale bytes per weight row and slab (Q4G): groups of 32 / 64 columns
+    // put 4 / 2 group scales in a slab, larger groups one.
+    template <int GSH>
+    static constexpr int srow() { return Q4 ? (GSH >= 2 ? 1 : 4 >> GSH) * static_cast<int>(sizeof(ST)) : 0; }
+};
+
+template <bool Q4, int FM, int FN, int GSH, typename YT, typename ST>
+struct WqWideShape {
+    using B = WqWide<Q4, FM, FN, ST>;
+    static constexpr int kBM = B::kBM, kBN = B::kBN, kSRow = B::template srow<GSH>();
+    static constexpr int kXB = kBM * 256 / 1024, kWB = kBN * B::kWRow / 1024;  // 1 KB requests
+    static constexpr int kNB = kXB + kWB, kQ = (kNB + 7) / 8;
+    // 256-byte scale requests; the last may run past the tile's rows into the
+    // region's padding.
+    static constexpr int kNS = (kBN * kSRow + 255) / 256, kQS = (kNS + 7) / 8;
+    static constexpr int kXOff = 0, kWOff = kBM * 256, kSOff = kWOff + kBN * B::kWRow;
+    static constexpr int kSlab = kSOff + kNS * 256;
+    static constexpr int kD = std::min(8, (160 * 1024 - 1024) / kSlab);
+    static constexpr int kSink = kD * kSlab;
+    static constexpr size_t kStage = size_t(kBM) * kBN * sizeof(YT);
+    static constexpr size_t kLds = std::max<size_t>(size_t(kSink) + 1024, sizeof(YT) == 2 ? kStage : 0);
+    static_assert(kD >= 2, "two slabs must fit");
+    static_assert(kQ + kQS <= 63, "vmcnt range");
+};
+
+template <bool Q4, int FM, int FN, int GSH, typename YT, typename ST>
+__global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
+    const _Float16* __restrict__ x, const uint8_t* __restrict__ wq, const ST* __restrict__ scale,
+    const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int tiles_m, int tiles_n,
+    int gsh_rt) {
+    using S = WqWideShape<Q4, FM, FN, GSH, YT, ST>;
+    // group = 32 << gsh columns; GSH = 2 stands for every group of at least
+    // one slab (one scale per slab), its shift given at run time.
+    const int gsh = GSH >= 2 ? gsh_rt : GSH;
+    constexpr int BM = S::kBM, BN = S::kBN, D = S::kD, Q = S::kQ, QS = S::kQS, XB = S::kXB, NB = S::kNB;
+    constexpr int WROW = WqWide<Q4, FM, FN, ST>::kWRow;
+    extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int total = tiles_m * tiles_n;
+    const int per = (total + 7) / 8, xcd = blockIdx.x % 8, idx = blockIdx.x / 8;
+    const int full = total - 8 * (per - 1);
+    const int lin = xcd < full ? xcd * per + idx : full * per + (xcd - full) * (per - 1) + idx;
+    const int m0 = (lin % tiles_m) * BM, n0 = (lin / tiles_m) * BN;
+
+    const int wrow_bytes = Q4 ? k / 2 : k;
+    const int groups = Q4 ? k >> (5 + gsh) : 1;
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(x), 0, m * k * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(wq), 0, n * wrow_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<ST*>(scale), 0, Q4 ? n * groups * static_cast<int>(sizeof(ST)) : 0, 0x00020000);
+    // 1 KB request q of wave w = block b = q * 8 + w: blocks [0, XB) hold 4
+    // activation rows each, [XB, NB) 1024 / WROW weight rows, the rest spares.
+    int voff[Q], loff[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const int b = q * 8 + wave;
+        const bool real = b < NB, isx = b < XB;
+        if (isx) {
+            const int r = b * 4 + (lane >> 4), c = (lane & 15) ^ (r & 15);
+            voff[q] = m0 + r < m ? (m0 + r) * k * 2 + c * 16 : kOob;
+        } else if (Q4) {
+            const int r = (b - XB) * 16 + (lane >> 2), c = (lane & 3) ^ ((r >> 2) & 3);
+            voff[q] = real && n0 + r < n ? (n0 + r) * wrow_bytes + c * 16 : kOob;
+        } else {
+            const int r = (b - XB) * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
+            voff[q] = real && n0 + r < n ? (n0 + r) * wrow_bytes + c * 16 : kOob;
+        }
+        loff[q] = real ? b * 1024 : S::kSink;
+    }
+    // 256-byte scale request q of wave w = block b: kSRow / 4 lanes per weight row.
+    int soffv[QS > 0 ? QS : 1], sloff[QS > 0 ? QS : 1];
+#pragma unroll
+    for (int q = 0; q < QS; ++q) {
+        const int b = q * 8 + wave;
+        constexpr int LPR = S::kSRow / 4 > 0 ? S::kSRow / 4 : 1;
+        const int r = b * (64 / LPR) + lane / LPR;
+        soffv[q] = b < S::kNS && n0 + r < n ? (n0 + r) * groups * static_cast<int>(sizeof(ST)) + (lane % LPR) * 4 : kOob;
+        sloff[q] = b < S::kNS ? S::kSOff + b * 256 : S::kSink;
+    }
+    const int nk = k / 128;
+    const unsigned lds_base = static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds));
+    auto issue = [&](int sl) {
+        const unsigned slot = static_cast<unsigned>(sl % D) * S::kSlab;
+        const bool in = sl < nk;
+        const int xo = in ? sl * 256 : kOob, wo = in ? sl * 128 * WROW / 128 : kOob;
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const int b = q * 8 + wave;
+            const unsigned dst = lds_base + (b < NB ? slot : 0u) + static_cast<unsigned>(loff[q]);
+            if (b < XB)
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                             ::"s"(dst), "v"(voff[q]), "s"(xrs), "s"(xo) : "memory");
+            else
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                             ::"s"(dst), "v"(voff[q]), "s"(wrs), "s"(wo) : "memory");
+        }
+        if constexpr (Q4) {
+            // the slab's first group (its groups are consecutive in the row)
+            const int so = in ? ((sl * 4) >> gsh) * static_cast<int>(sizeof(ST)) : kOob;
+#pragma unroll
+            for (int q = 0; q < QS; ++q) {
+                const int b = q * 8 + wave;
+                const unsigned dst = lds_base + (b < S::kNS ? slot : 0u) + static_cast<unsigned>(sloff[q]);
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+                             ::"s"(dst), "v"(soffv[q]), "s"(srs), "s"(so) : "memory");
+            }
+        }
+    };
+
+    f4 acc[FN][FM];
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) acc[i][j] = f4{0, 0, 0, 0};
+    const int fr = lane & 15, fq = lane >> 4;
+    int fxo[FM], fwr[FN];
+#pragma unroll
+    for (int j = 0; j < FM; ++j) fxo[j] = wm * 16 * FM + j * 16 + fr;
+#pragma unroll
+    for (int i = 0; i < FN; ++i) fwr[i] = wn * 16 * FN + i * 16 + fr;
+    constexpr int kChunksPerGroup = GSH >= 2 ? 4 : 1 << GSH;  // MFMA steps per scale (within a slab)
+
+#pragma unroll
+    for (int sl = 0; sl < D - 1; ++sl) issue(sl);
+    for (int kt = 0; kt < nk; ++kt) {
+        wait_vmcnt<(Q + (Q4 ? QS : 0)) * (D - 2)>();
+        __builtin_amdgcn_s_barrier();
+        issue(kt + D - 1);
+        const int8_t* base = lds + (kt % D) * S::kSlab;
+        f4 part[FN][FM];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            h8 xa[FM], wb[FN];
+#pragma unroll
+            for (int j = 0; j < FM; ++j) {
+                const int r = fxo[j], c = t * 4 + fq;
+                XFrag<_Float16> f;
+                f.raw = *reinterpret_cast<const v4i*>(base + S::kXOff + r * 256 + ((c ^ (r & 15)) << 4));
+                h8 lo;
+                f.operands(xa[j], lo);
+            }
+#pragma unroll
+            for (int i = 0; i < FN; ++i) {
+                const int r = fwr[i];
+                if constexpr (Q4) {
+                    WFrag<true> f;
+                    f.w = *reinterpret_cast<const int*>(base + S::kWOff + r * 64 + ((t ^ ((r >> 2) & 3)) << 4) + fq * 4);
+                    wb[i] = f.codes();
+                } else {
+                    typedef int v2i __attribute__((ext_vector_type(2)));
+                    const int c = t * 2 + (fq >> 1);
+                    const v2i v = *reinterpret_cast<const v2i*>(base + S::kWOff + r * 128 + ((c ^ ((r >> 1) & 7)) << 4) + (fq & 1) * 8);
+                    WFrag<false> f;
+                    f.w0 = v[0];
+                    f.w1 = v[1];
+                    wb[i] = f.codes();
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < FN; ++i)
+#pragma unroll
+                for (int j = 0; j < FM; ++j) {
+                    if constexpr (Q4) {
+                        const f4 z = t % kChunksPerGroup == 0 ? f4{0, 0, 0, 0} : part[i][j];
+                        part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], wb[i], z, 0, 0, 0);
+                    } else {
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], wb[i], acc[i][j], 0, 0, 0);
+                    }
+                }
+            if constexpr (Q4) {
+                if (t % kChunksPerGroup == kChunksPerGroup - 1) {
+                    const int gi = GSH >= 2 ? 0 : t >> GSH;  // group within the slab
+#pragma unroll
+                    for (int i = 0; i < FN; ++i) {
+                        const int8_t* sp = base + S::kSOff + fwr[i] * S::kSRow + gi * static_cast<int>(sizeof(ST));
+                        float sc;
+                        if constexpr (sizeof(ST) == 4) sc = *reinterpret_cast<const float*>(sp);
+                        else sc = static_cast<float>(*reinterpret_cast<const _Float16*>(sp));
+#pragma unroll
+                        for (int j = 0; j < FM; ++j)
+#pragma unroll
+                            for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(part[i][j][v], sc, acc[i][j][v]);
+                    }
+                }
+            }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this slab's reads are done
+    }
+    wait_vmcnt<0>();
+
+    // Lane l holds, for fragment (i, j), rows m0 + wm*16*FM + j*16 + 4*(l/16) + v
+    // of column n0 + wn*16*FN + i*16 + l%16.
+    if constexpr (sizeof(YT) == 2) {
+        if ((n & 7) == 0) {
+            __syncthreads();  // every wave is done with the ring
+#pragma unroll
+            for (int i = 0; i < FN; ++i) {
+                const int cl = fwr[i], col = n0 + cl;
+                const float ws = !Q4 && col < n ? to_f32(scale[col]) : 1.0f;
+                const float b = bias && col < n ? bias[col] : 0.0f;
+#pragma unroll
+                for (int j = 0; j < FM; ++j)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const int rl = fxo[j] - fr + 4 * fq + v;
+                        const float val = Q4 ? acc[i][j][v] + b : acc[i][j][v] * ws + b;
+                        *reinterpret_cast<_Float16*>(lds + (rl * BN + cl) * 2) = static_cast<_Float16>(val);
+                    }
+            }
+            __syncthreads();
+            constexpr int CPR = BN / 8;
+            for (int c = tid; c < BM * CPR; c += 512) {
+                const int rl = c / CPR, cc = c % CPR;
+                const int row = m0 + rl, col = n0 + cc * 8;
+                if (row < m && col < n)
+                    __builtin_nontemporal_store(*reinterpret_cast<const v4i*>(lds + (rl * BN + cc * 8) * 2),
+                                                reinterpret_cast<v4i*>(y + static_cast<size_t>(row) * n + col));
+            }
+            return;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+        const int col = n0 + fwr[i];
+        if (col >= n) continue;
+        const float ws = Q4 ? 1.0f : to_f32(scale[col]);
+        const float b = bias ? bias[col] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int row = m0 + fxo[j] - fr + 4 * fq + v;
+                if (row < m) {
+                    const float val = Q4 ? acc[i][j][v] + b : acc[i][j][v] * ws + b;
+                    y[static_cast<size_t>(row) * n + col] = from_f32<YT>(val);
+                }
+            }
+    }
+}
+
+template <bool Q4, int FM, int FN, int GSH, typename YT, typename ST>
+nq_status launch_wq_wide(const _Float16* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n,
+                         int k, int gsh, hipStream_t s) {
+    using S = WqWideShape<Q4, FM, FN, GSH, YT, ST>;
+    auto* fn = gemm_wq_wide_kernel<Q4, FM, FN, GSH, YT, ST>;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       static_cast<int>(S::kLds));
+    if (attr != hipSuccess) return fail(NQ_HIP_ERROR, "gemm_wq_wide: LDS attribute: %s", hipGetErrorString(attr));
+    const int tm = (m + S::kBM - 1) / S::kBM, tn = (n + S::kBN - 1) / S::kBN;
+    fn<<<tm * tn, 512, S::kLds, s>>>(x, w, sc, b, y, m, n, k, tm, tn, gsh);
+    return launch_status("gemm_wq_wide_kernel");
+}
+
+// Tiles of the wide path: (64 * fm) x (32 * fn), by falling area; the plan
+// takes the least (rounds x area), rounds = ceil(tiles / 256).
+struct WqTile {
+    int fm, fn;
+};
+constexpr WqTile kWqTiles[] = {{2, 9}, {2, 8}, {2, 4}, {1, 8}, {1, 4}, {1, 2}};  // 128 x 320 spilled (Q4G)
+
+struct WqPlan {
+    WqTile tile;
+    int64_t tiles;
+};
+WqPlan plan_wq_wide(int64_t m, int64_t n) {
+    int64_t best_cost = 0;
+    WqPlan p{{0, 0}, 0};
+    for (const WqTile& t : kWqTiles) {
+        const int64_t c = ((m + 64 * t.fm - 1) / (64 * t.fm)) * ((n + 32 * t.fn - 1) / (32 * t.fn));
+        const int64_t cost = ((c + 255) / 256) * (64 * t.fm) * (32 * t.fn);
+        if (best_cost == 0 || cost < best_cost) {
+            best_cost = cost;
+            p = {t, c};
+        }
+    }
+    return p;
+}
+
+template <bool Q4, typename YT, typename ST>
+nq_status wq_wide(const _Float16* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n, int k,
+                  int group, hipStream_t s) {
+    const WqTile pick = plan_wq_wide(m, n).tile;
+    const int gsh = Q4 ? __builtin_ctz(static_cast<unsigned>(group >> 5)) : 0;
+    auto with_g = [&](auto fmt, auto fnt) -> nq_status {
+        constexpr int FM = decltype(fmt)::value, FN = decltype(fnt)::value;
+        if constexpr (!Q4) return launch_wq_wide<false, FM, FN, 0, YT, ST>(x, w, sc, b, y, m, n, k, 0, s);
+        else {
+            if (gsh == 0) return launch_wq_wide<true, FM, FN, 0, YT, ST>(x, w, sc, b, y, m, n, k, 0, s);
+            if (gsh == 1) return launch_wq_wide<true, FM, FN, 1, YT, ST>(x, w, sc, b, y, m, n, k, 1, s);
+            return launch_wq_wide<true, FM, FN, 2, YT, ST>(x, w, sc, b, y, m, n, k, gsh, s);
+        }
+    };
+    using std::integral_constant;
+    switch (pick.fm * 100 + pick.fn) {
+        case 209: return with_g(integral_constant<int, 2>{}, integral_constant<int, 9>{});
+        case 208: return with_g(integral_constant<int, 2>{}, integral_constant<int, 8>{});
+        case 204: return with_g(integral_constant<int, 2>{}, integral_constant<int, 4>{});
+        case 108: return with_g(integral_constant<int, 1>{}, integral_constant<int, 8>{});
+        case 104: return with_g(integral_constant<int, 1>{}, integral_constant<int, 4>{});
+        default: return with_g(integral_constant<int, 1>{}, integral_constant<int, 2>{});
+    }
+}
+
+// The wide path's contract: fp16 activations, k % 128 == 0, 32-bit offsets,
+// and for Q4G fp16 scales groups of 32 or 64 columns (a slab's scales are
+// whole dwords), fp32 scales any power-of-two multiple of 32. It runs from
+// m = 32 when its tiles number at least 128, and for every m > 128; otherwise
+// the 16-row kernel, which streams the weight once per 64 rows of x, is faster
+// (measured, k = 1536: m = 64, n = 8960 Q8 23.9 -> 12.0 us, Q4G 29.8 -> 15.0;
+// m = 128 38.4 -> 17.9; m = 64, n = 1536 (24 tiles) 9.2 vs 11.8; long K with
+// few tiles, m = 64, n = 1536, k = 8960: 40.4 vs 53.6).
+template <bool Q4, typename ST>
+bool wq_wide_ok(int64_t m, int64_t n, int64_t k, int64_t group) {
+    if (m < 32 || (m <= 128 && plan_wq_wide(m, n).tiles < 128)) return false;
+    if (k % 128 != 0 || m * k * 2 >= (int64_t(1) << 31) - 64) return false;
+    if (!Q4) return n * k < (int64_t(1) << 31) - 64;
+    if (sizeof(ST) == 2 && group != 32 && group != 64) return false;
+    return n * (k / 2) < (int64_t(1) << 31) - 64 && n * (k / group) * int64_t(sizeof(ST)) < (int64_t(1) << 31) - 64;
+}
 }  // namespace
 
 // Whether the MFMA path takes this call (the caller runs GEMV slices otherwise):
@@ -297,6 +642,11 @@ bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m,
 template <bool Q4, typename XT, typename YT, typename ST>
 nq_status wq_gemm(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int64_t m, int64_t n,
                   int64_t k, int64_t group, hipStream_t s) {
+    if constexpr (std::is_same_v<XT, _Float16>) {
+        if (wq_wide_ok<Q4, ST>(m, n, k, group))
+            return wq_wide<Q4>(x, w, sc, b, y, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
+                               static_cast<int>(group), s);
+    }
     return launch_wq<Q4>(x, w, sc, b, y, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
                          static_cast<int>(group), s);
 }

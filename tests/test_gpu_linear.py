@@ -176,6 +176,14 @@ WQ_GEMM_CASES = [  # m > 8: the fp16 MFMA GEMM (m >= 16 or n >= 4096) or GEMV sl
     ("q4g", 64, 896, 4864, 64, False, F16, F32, F16),  # group 64
     ("q4g", 130, 512, 2048, 128, True, F16, F16, F32),
     ("q4g", 20, 256, 1536, 96, False, F16, F32, F16),  # group 96 (3 chunks): GEMV slices
+    # m > 64, fp16 x, k % 128 == 0: the wide-tile kernel (LDS-DMA ring)
+    ("q4g", 300, 1536, 1536, 32, True, F16, F16, F16),
+    ("q4g", 200, 2000, 1024, 64, False, F16, F16, F32),  # fp32 y: direct stores
+    ("q4g", 130, 1000, 2048, 128, True, F16, F32, F16),  # fp32 scales, one group per slab
+    ("q4g", 96, 700, 1536, 256, False, F16, F32, F16),   # a group spans two slabs
+    ("q8", 257, 2900, 1024, 0, True, F16, F32, F32),
+    ("q4g", 1100, 640, 512, 32, True, F16, F16, F16),
+    ("q4g", 40, 8960, 1536, 64, True, F16, F16, F16),    # m >= 32 with >= 128 tiles
 ]
 
 
