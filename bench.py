@@ -34,6 +34,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA
+FP16_PEAK_TFLOPS = 2500.0      # MI355X dense fp16 MFMA
 ROTATE_BYTES = 512 << 20
 
 
@@ -221,7 +222,8 @@ def main():
         tops = ops / (ms * 1e-3) / 1e12
         e = {"name": name, "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "TOPS": round(tops, 2),
              "bytes": nb, "ops": ops, "bound": bound,
-             "frac": round(gbs / HBM_PEAK_GBS if bound == "hbm" else tops / INT8_PEAK_TOPS, 4),
+             "frac": round(gbs / HBM_PEAK_GBS if bound == "hbm"
+                           else tops / (FP16_PEAK_TFLOPS if bound == "mfma_f16" else INT8_PEAK_TOPS), 4),
              "warmup": sweep_warmup}
         return e
 
@@ -258,6 +260,15 @@ def main():
                                *w8a8_linear(2048, 8960, 1536, gemm_only=True), "mfma"))
             sweep.append(entry("w8a8_linear_cfg5a M=2048 K=1536 N=8960 (incl. act quant)",
                                *w8a8_linear(2048, 8960, 1536), "mfma"))
+        if want("wq_prefill"):
+            # weight-only prefill (fp16 activations, fp16 MFMA): the caller-side
+            # shape of config 5a in the q8 / q4g quant modes
+            sweep.append(entry("q8_weight_only_prefill M=2048 K=1536 N=8960 fp16",
+                               *q8_gemv(2048, 8960, 1536, torch.float16), "mfma_f16"))
+            torch.cuda.empty_cache()
+            sweep.append(entry("q4g_weight_only_prefill M=2048 K=1536 N=8960 g=32 fp16",
+                               *q4g_gemv(2048, 8960, 1536, 32), "mfma_f16"))
+            torch.cuda.empty_cache()
         if want("decoder_cfg4"):
             sweep.append(decoder_layer_cfg4(rnd, time_graph, args, w8a8_linear, entry))
         torch.cuda.empty_cache()
