@@ -187,6 +187,53 @@ WQ_GEMM_CASES = [  # m > 8: the fp16 MFMA GEMM (m >= 16 or n >= 4096) or GEMV sl
 ]
 
 
+def _wq_random_cases():
+    """Seeded shapes over the weight-only wide-tile plans (m >= 32, fp16 x,
+    k % 128 == 0): every tile shape, fp16 / fp32 scales, group 32..256."""
+    rng = np.random.default_rng(77)
+    cases = []
+    for i in range(14):
+        mode = "q8" if i % 3 == 0 else "q4g"
+        m = int(rng.integers(32, 1600))
+        n = int(rng.integers(64, 12000))
+        k = 128 * int(rng.integers(1, 24))
+        if m * n * k > 4e9:
+            n = max(64, int(4e9 / (m * k)))
+        sdt = F16 if i % 2 else F32
+        g = int(rng.choice([32, 64])) if sdt == F16 else int(rng.choice([32, 64, 128, 256]))
+        while k % g:
+            g //= 2
+        cases.append((mode, m, n, k, g, bool(i % 4 == 1), sdt, F16 if i % 5 else F32))
+    return cases
+
+
+def _dequant_q4g(t, g):
+    q = t.q.to(torch.int32)
+    codes = torch.stack([q & 15, q >> 4], dim=-1).reshape(t.out, -1)[:, :t.in_] - 8
+    return codes.float() * t.scale.float().repeat_interleave(g, dim=1)[:, :t.in_]
+
+
+@pytest.mark.parametrize("mode,m,n,k,g,bias,sdt,ydt", _wq_random_cases())
+def test_weight_only_random_shapes(dev, nq, mode, m, n, k, g, bias, sdt, ydt):
+    """Weight-only linears on fp16 activations against a torch fp32 reference
+    on the dequantized weight (the reference's own test_quant.cpp:100-116
+    invariant linear(x, dequant(w)))."""
+    gen = torch.Generator(device=dev).manual_seed(m * 7 + n * 3 + k)
+    x = torch.randn((m, k), generator=gen, device=dev).half()
+    w = torch.randn((n, k), generator=gen, device=dev) * 0.05
+    b = torch.randn(n, generator=gen, device=dev) if bias else None
+    if mode == "q8":
+        t = nq.quantize_q8(w)
+        deq = t.q.float() * t.scale[:, None]
+        y = nq.linear_q8(x, t, b, out_dtype=ydt)
+    else:
+        t = nq.quantize_q4g(w, g, scale_dtype=sdt)
+        deq = _dequant_q4g(t, g)
+        y = nq.linear_q4g(x, t, b, out_dtype=ydt)
+    ref = x.float() @ deq.t() + (b if b is not None else 0.0)
+    assert_close_rms(host(y.float()), host(ref), f"{mode} {m}x{n}x{k} g{g}", fp16_out=(ydt == F16))
+
+
 @pytest.mark.parametrize("mode,m,n,k,g,bias,xdt,sdt,ydt", WQ_GEMM_CASES)
 def test_weight_only_gemm_batched(dev, nq, orc, mode, m, n, k, g, bias, xdt, sdt, ydt):
     x, w, b = data(m, n, k, m * 31 + n + k + g, bias=bias)
