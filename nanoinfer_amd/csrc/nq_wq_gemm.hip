@@ -282,39 +282,46 @@ nq_status launch_wq(const XT* x, const uint8_t* w, const ST* sc, const float* b,
 }
 
 
-// ---- wide tiles for fp16 activations (m > 64) -------------------------------------------
+// ---- wide tiles for fp16 activations -----------------------------------------------------
 // One (64*FM) x (32*FN) output tile per workgroup, 8 waves as 4 x 2, each
 // (16*FM) x (16*FN) outputs, as in the wide W8A8 kernel: K advances in slabs
-// of 128 columns that LDS-DMA (buffer_load ... lds) writes into a ring of as
-// many slots as fit in 160 KB; the request for slab kt + D - 1 goes out after
-// the barrier that frees its slot. A slab holds the activation tile (256-byte
-// fp16 rows: a 1 KB request covers 4 rows), the weight codes (128-byte Q8 rows
-// / 64-byte Q4 rows) and, for Q4G, the tile's group scales of the slab. Each
-// lane loads the chunk an XOR swizzle puts in its LDS slot so the fragment
-// reads are bank-conflict free. Codes become fp16 exactly in registers after
-// the LDS read (the WFrag conversions above); A = activations, B = weights,
-// so a lane's four results share one weight row. Q8: one MFMA chain over K,
-// row scale in the epilogue. Q4G: an MFMA chain over each group's chunks
-// (at most one slab), scaled by the group scale into the fp32 accumulator.
-template <bool Q4, int FM, int FN, typename ST>
-struct WqWide {
-    static constexpr int kBM = 64 * FM, kBN = 32 * FN, kXRow = 256, kWRow = Q4 ? 64 : 128;
-    // Scale bytes per weight row and slab (Q4G): groups of 32 / 64 columns
-    // put 4 / 2 group scales in a slab, larger groups one.
-    template <int GSH>
-    static constexpr int srow() { return Q4 ? (GSH >= 2 ? 1 : 4 >> GSH) * static_cast<int>(sizeof(ST)) : 0; }
-};
+// of SK columns (64 or 128) that LDS-DMA (buffer_load ... lds) writes into a
+// ring of as many slots as fit in 160 KB; the request for slab kt + D - 1 goes
+// out after the barrier that frees its slot. A slab holds the activation tile
+// (fp16 rows of 2*SK bytes), the weight codes (SK or SK/2 bytes per row) and,
+// for Q4G, the tile's group scales of the slab. 256-row tiles take 64-column
+// slabs (three fit: 256 x 288 in one round beat two rounds of 128 x 288 with
+// 128-column slabs); smaller tiles take 128-column slabs. Each lane loads the
+// chunk an XOR swizzle puts in its LDS slot (16-byte chunk c of a row of C
+// chunks at slot c ^ ((r >> log2(16 / C)) & (C - 1))), so the 16 rows of a
+// fragment read hit distinct banks. Codes become fp16 exactly in registers
+// after the LDS read (the WFrag conversions above); A = activations, B =
+// weights, so a lane's four results share one weight row. Q8: one MFMA chain
+// over K, row scale in the epilogue. Q4G: an MFMA chain over each group's
+// chunks (at most one slab), scaled by the group scale into the fp32 accumulator.
+template <int C>
+__device__ __forceinline__ int wq_swz(int r) {  // slot XOR of row r, C 16-byte chunks per row
+    constexpr int S = C >= 16 ? 0 : C == 8 ? 1 : C == 4 ? 2 : 3;
+    return (r >> S) & (C - 1);
+}
 
-template <bool Q4, int FM, int FN, int GSH, typename YT, typename ST>
+template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST>
 struct WqWideShape {
-    using B = WqWide<Q4, FM, FN, ST>;
-    static constexpr int kBM = B::kBM, kBN = B::kBN, kSRow = B::template srow<GSH>();
-    static constexpr int kXB = kBM * 256 / 1024, kWB = kBN * B::kWRow / 1024;  // 1 KB requests
+    static constexpr int kBM = 64 * FM, kBN = 32 * FN, kT = SK / 32;  // MFMA K steps per slab
+    static constexpr int kXRow = 2 * SK, kWRow = Q4 ? SK / 2 : SK;   // bytes per row and slab
+    static constexpr int kXC = kXRow / 16, kWC = kWRow / 16;         // 16-byte chunks per row
+    // Scales per weight row and slab (Q4G): groups of 32 << GSH columns, one per
+    // slab when a group covers the slab (GSH = kGBig stands for all such groups).
+    static constexpr int kGBig = SK == 128 ? 2 : 1;
+    static constexpr int kSPer = Q4 ? (GSH >= kGBig ? 1 : kT >> GSH) : 0;
+    static constexpr int kSRow = kSPer * static_cast<int>(sizeof(ST));
+    static constexpr int kCPG = GSH >= kGBig ? kT : 1 << GSH;  // MFMA steps per scaled chain
+    static constexpr int kXB = kBM * kXRow / 1024, kWB = kBN * kWRow / 1024;  // 1 KB requests
     static constexpr int kNB = kXB + kWB, kQ = (kNB + 7) / 8;
     // 256-byte scale requests; the last may run past the tile's rows into the
     // region's padding.
     static constexpr int kNS = (kBN * kSRow + 255) / 256, kQS = (kNS + 7) / 8;
-    static constexpr int kXOff = 0, kWOff = kBM * 256, kSOff = kWOff + kBN * B::kWRow;
+    static constexpr int kXOff = 0, kWOff = kBM * kXRow, kSOff = kWOff + kBN * kWRow;
     static constexpr int kSlab = kSOff + kNS * 256;
     static constexpr int kD = std::min(8, (160 * 1024 - 1024) / kSlab);
     static constexpr int kSink = kD * kSlab;
@@ -322,19 +329,20 @@ struct WqWideShape {
     static constexpr size_t kLds = std::max<size_t>(size_t(kSink) + 1024, sizeof(YT) == 2 ? kStage : 0);
     static_assert(kD >= 2, "two slabs must fit");
     static_assert(kQ + kQS <= 63, "vmcnt range");
+    static_assert(!Q4 || kSRow % 4 == 0, "scale rows are whole dwords");
 };
 
-template <bool Q4, int FM, int FN, int GSH, typename YT, typename ST>
+template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST>
 __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
     const _Float16* __restrict__ x, const uint8_t* __restrict__ wq, const ST* __restrict__ scale,
     const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int tiles_m, int tiles_n,
     int gsh_rt) {
-    using S = WqWideShape<Q4, FM, FN, GSH, YT, ST>;
-    // group = 32 << gsh columns; GSH = 2 stands for every group of at least
-    // one slab (one scale per slab), its shift given at run time.
-    const int gsh = GSH >= 2 ? gsh_rt : GSH;
+    using S = WqWideShape<Q4, SK, FM, FN, GSH, YT, ST>;
     constexpr int BM = S::kBM, BN = S::kBN, D = S::kD, Q = S::kQ, QS = S::kQS, XB = S::kXB, NB = S::kNB;
-    constexpr int WROW = WqWide<Q4, FM, FN, ST>::kWRow;
+    constexpr int T = S::kT, XROW = S::kXRow, WROW = S::kWRow, XC = S::kXC, WC = S::kWC;
+    // group = 32 << gsh columns; GSH = kGBig stands for every group of at
+    // least one slab (one scale per slab), its shift given at run time.
+    const int gsh = GSH >= S::kGBig ? gsh_rt : GSH;
     extern __shared__ __attribute__((aligned(16))) int8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -350,21 +358,19 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(x), 0, m * k * 2, 0x00020000);
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(wq), 0, n * wrow_bytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<ST*>(scale), 0, Q4 ? n * groups * static_cast<int>(sizeof(ST)) : 0, 0x00020000);
-    // 1 KB request q of wave w = block b = q * 8 + w: blocks [0, XB) hold 4
-    // activation rows each, [XB, NB) 1024 / WROW weight rows, the rest spares.
+    // 1 KB request q of wave w = block b = q * 8 + w: blocks [0, XB) hold
+    // 1024 / XROW activation rows each, [XB, NB) 1024 / WROW weight rows, the
+    // rest spares (they read zeros into the sink).
     int voff[Q], loff[Q];
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
         const int b = q * 8 + wave;
-        const bool real = b < NB, isx = b < XB;
-        if (isx) {
-            const int r = b * 4 + (lane >> 4), c = (lane & 15) ^ (r & 15);
+        const bool real = b < NB;
+        if (b < XB) {
+            const int r = b * (1024 / XROW) + lane / XC, c = (lane % XC) ^ wq_swz<XC>(r);
             voff[q] = m0 + r < m ? (m0 + r) * k * 2 + c * 16 : kOob;
-        } else if (Q4) {
-            const int r = (b - XB) * 16 + (lane >> 2), c = (lane & 3) ^ ((r >> 2) & 3);
-            voff[q] = real && n0 + r < n ? (n0 + r) * wrow_bytes + c * 16 : kOob;
         } else {
-            const int r = (b - XB) * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
+            const int r = (b - XB) * (1024 / WROW) + lane / WC, c = (lane % WC) ^ wq_swz<WC>(r);
             voff[q] = real && n0 + r < n ? (n0 + r) * wrow_bytes + c * 16 : kOob;
         }
         loff[q] = real ? b * 1024 : S::kSink;
@@ -379,12 +385,12 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
         soffv[q] = b < S::kNS && n0 + r < n ? (n0 + r) * groups * static_cast<int>(sizeof(ST)) + (lane % LPR) * 4 : kOob;
         sloff[q] = b < S::kNS ? S::kSOff + b * 256 : S::kSink;
     }
-    const int nk = k / 128;
+    const int nk = k / SK;
     const unsigned lds_base = static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds));
     auto issue = [&](int sl) {
         const unsigned slot = static_cast<unsigned>(sl % D) * S::kSlab;
         const bool in = sl < nk;
-        const int xo = in ? sl * 256 : kOob, wo = in ? sl * 128 * WROW / 128 : kOob;
+        const int xo = in ? sl * XROW : kOob, wo = in ? sl * WROW : kOob;
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
             const int b = q * 8 + wave;
@@ -398,7 +404,7 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
         }
         if constexpr (Q4) {
             // the slab's first group (its groups are consecutive in the row)
-            const int so = in ? ((sl * 4) >> gsh) * static_cast<int>(sizeof(ST)) : kOob;
+            const int so = in ? ((sl * T) >> gsh) * static_cast<int>(sizeof(ST)) : kOob;
 #pragma unroll
             for (int q = 0; q < QS; ++q) {
                 const int b = q * 8 + wave;
@@ -420,7 +426,6 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
     for (int j = 0; j < FM; ++j) fxo[j] = wm * 16 * FM + j * 16 + fr;
 #pragma unroll
     for (int i = 0; i < FN; ++i) fwr[i] = wn * 16 * FN + i * 16 + fr;
-    constexpr int kChunksPerGroup = GSH >= 2 ? 4 : 1 << GSH;  // MFMA steps per scale (within a slab)
 
 #pragma unroll
     for (int sl = 0; sl < D - 1; ++sl) issue(sl);
@@ -431,27 +436,27 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
         const int8_t* base = lds + (kt % D) * S::kSlab;
         f4 part[FN][FM];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int t = 0; t < T; ++t) {
             h8 xa[FM], wb[FN];
 #pragma unroll
             for (int j = 0; j < FM; ++j) {
                 const int r = fxo[j], c = t * 4 + fq;
                 XFrag<_Float16> f;
-                f.raw = *reinterpret_cast<const v4i*>(base + S::kXOff + r * 256 + ((c ^ (r & 15)) << 4));
+                f.raw = *reinterpret_cast<const v4i*>(base + S::kXOff + r * XROW + ((c ^ wq_swz<XC>(r)) << 4));
                 h8 lo;
                 f.operands(xa[j], lo);
             }
 #pragma unroll
             for (int i = 0; i < FN; ++i) {
                 const int r = fwr[i];
-                if constexpr (Q4) {
+                if constexpr (Q4) {  // 8 codes = one dword: chunk t, dword fq
                     WFrag<true> f;
-                    f.w = *reinterpret_cast<const int*>(base + S::kWOff + r * 64 + ((t ^ ((r >> 2) & 3)) << 4) + fq * 4);
+                    f.w = *reinterpret_cast<const int*>(base + S::kWOff + r * WROW + ((t ^ wq_swz<WC>(r)) << 4) + fq * 4);
                     wb[i] = f.codes();
-                } else {
+                } else {  // 8 codes = two dwords: chunk 2t + fq / 2, half fq % 2
                     typedef int v2i __attribute__((ext_vector_type(2)));
                     const int c = t * 2 + (fq >> 1);
-                    const v2i v = *reinterpret_cast<const v2i*>(base + S::kWOff + r * 128 + ((c ^ ((r >> 1) & 7)) << 4) + (fq & 1) * 8);
+                    const v2i v = *reinterpret_cast<const v2i*>(base + S::kWOff + r * WROW + ((c ^ wq_swz<WC>(r)) << 4) + (fq & 1) * 8);
                     WFrag<false> f;
                     f.w0 = v[0];
                     f.w1 = v[1];
@@ -463,15 +468,15 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
 #pragma unroll
                 for (int j = 0; j < FM; ++j) {
                     if constexpr (Q4) {
-                        const f4 z = t % kChunksPerGroup == 0 ? f4{0, 0, 0, 0} : part[i][j];
+                        const f4 z = t % S::kCPG == 0 ? f4{0, 0, 0, 0} : part[i][j];
                         part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], wb[i], z, 0, 0, 0);
                     } else {
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], wb[i], acc[i][j], 0, 0, 0);
                     }
                 }
             if constexpr (Q4) {
-                if (t % kChunksPerGroup == kChunksPerGroup - 1) {
-                    const int gi = GSH >= 2 ? 0 : t >> GSH;  // group within the slab
+                if (t % S::kCPG == S::kCPG - 1) {
+                    const int gi = GSH >= S::kGBig ? 0 : t >> GSH;  // group within the slab
 #pragma unroll
                     for (int i = 0; i < FN; ++i) {
                         const int8_t* sp = base + S::kSOff + fwr[i] * S::kSRow + gi * static_cast<int>(sizeof(ST));
@@ -540,11 +545,11 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
     }
 }
 
-template <bool Q4, int FM, int FN, int GSH, typename YT, typename ST>
+template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST>
 nq_status launch_wq_wide(const _Float16* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n,
                          int k, int gsh, hipStream_t s) {
-    using S = WqWideShape<Q4, FM, FN, GSH, YT, ST>;
-    auto* fn = gemm_wq_wide_kernel<Q4, FM, FN, GSH, YT, ST>;
+    using S = WqWideShape<Q4, SK, FM, FN, GSH, YT, ST>;
+    auto* fn = gemm_wq_wide_kernel<Q4, SK, FM, FN, GSH, YT, ST>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                                        static_cast<int>(S::kLds));
@@ -554,21 +559,23 @@ nq_status launch_wq_wide(const _Float16* x, const uint8_t* w, const ST* sc, cons
     return launch_status("gemm_wq_wide_kernel");
 }
 
-// Tiles of the wide path: (64 * fm) x (32 * fn), by falling area; the plan
-// takes the least (rounds x area), rounds = ceil(tiles / 256).
+// Tiles of the wide path: (64 * fm) x (32 * fn) with sk-column slabs, by
+// falling area; the plan takes the least (rounds x area), rounds =
+// ceil(tiles / 256). 256-row tiles need 64-column slabs.
 struct WqTile {
-    int fm, fn;
+    int fm, fn, sk;
 };
-constexpr WqTile kWqTiles[] = {{2, 9}, {2, 8}, {2, 4}, {1, 8}, {1, 4}, {1, 2}};  // 128 x 320 spilled (Q4G)
-
+constexpr WqTile kWqTiles[] = {{4, 9, 64}, {4, 8, 64}, {2, 9, 128}, {4, 4, 64}, {2, 8, 128},
+                               {2, 4, 128}, {1, 8, 128}, {1, 4, 128}, {1, 2, 128}};
 struct WqPlan {
     WqTile tile;
     int64_t tiles;
 };
-WqPlan plan_wq_wide(int64_t m, int64_t n) {
+WqPlan plan_wq_wide(int64_t m, int64_t n, bool sk64_ok) {
     int64_t best_cost = 0;
-    WqPlan p{{0, 0}, 0};
+    WqPlan p{{0, 0, 0}, 0};
     for (const WqTile& t : kWqTiles) {
+        if (t.sk == 64 && !sk64_ok) continue;
         const int64_t c = ((m + 64 * t.fm - 1) / (64 * t.fm)) * ((n + 32 * t.fn - 1) / (32 * t.fn));
         const int64_t cost = ((c + 255) / 256) * (64 * t.fm) * (32 * t.fn);
         if (best_cost == 0 || cost < best_cost) {
@@ -578,29 +585,50 @@ WqPlan plan_wq_wide(int64_t m, int64_t n) {
     }
     return p;
 }
+// 64-column slabs: Q8, or Q4G in groups of 32 (a scaled chain per MFMA step;
+// longer chains kept the 256-row tiles' partial sums live and spilled).
+template <bool Q4, typename ST>
+bool wq_sk64_ok(int64_t group) {
+    return !Q4 || group == 32;
+}
 
 template <bool Q4, typename YT, typename ST>
 nq_status wq_wide(const _Float16* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n, int k,
                   int group, hipStream_t s) {
-    const WqTile pick = plan_wq_wide(m, n).tile;
+    const WqTile pick = plan_wq_wide(m, n, wq_sk64_ok<Q4, ST>(group)).tile;
     const int gsh = Q4 ? __builtin_ctz(static_cast<unsigned>(group >> 5)) : 0;
-    auto with_g = [&](auto fmt, auto fnt) -> nq_status {
-        constexpr int FM = decltype(fmt)::value, FN = decltype(fnt)::value;
-        if constexpr (!Q4) return launch_wq_wide<false, FM, FN, 0, YT, ST>(x, w, sc, b, y, m, n, k, 0, s);
-        else {
-            if (gsh == 0) return launch_wq_wide<true, FM, FN, 0, YT, ST>(x, w, sc, b, y, m, n, k, 0, s);
-            if (gsh == 1) return launch_wq_wide<true, FM, FN, 1, YT, ST>(x, w, sc, b, y, m, n, k, 1, s);
-            return launch_wq_wide<true, FM, FN, 2, YT, ST>(x, w, sc, b, y, m, n, k, gsh, s);
+    auto with_g = [&](auto skt, auto fmt, auto fnt) -> nq_status {
+        constexpr int SK = decltype(skt)::value, FM = decltype(fmt)::value, FN = decltype(fnt)::value;
+        constexpr int BIG = SK == 128 ? 2 : 1;  // one scale per slab from this shift on
+        if constexpr (!Q4) {
+            return launch_wq_wide<false, SK, FM, FN, 0, YT, ST>(x, w, sc, b, y, m, n, k, 0, s);
+        } else {
+            if (gsh == 0) return launch_wq_wide<true, SK, FM, FN, 0, YT, ST>(x, w, sc, b, y, m, n, k, 0, s);
+            if constexpr (SK == 64) {  // excluded by wq_sk64_ok
+                return fail(NQ_BAD_ARG, "gemm_wq_wide: 64-column slabs take groups of 32 only (got %d)", group);
+            } else {
+                if (gsh == 1) return launch_wq_wide<true, SK, FM, FN, 1, YT, ST>(x, w, sc, b, y, m, n, k, 1, s);
+                if constexpr (sizeof(ST) == 2) {  // excluded by wq_wide_ok
+                    return fail(NQ_BAD_ARG, "gemm_wq_wide: fp16 scales in groups of %d are not supported", group);
+                } else {
+                    return launch_wq_wide<true, SK, FM, FN, BIG, YT, ST>(x, w, sc, b, y, m, n, k, gsh, s);
+                }
+            }
         }
     };
     using std::integral_constant;
+    using I64 = integral_constant<int, 64>;
+    using I128 = integral_constant<int, 128>;
     switch (pick.fm * 100 + pick.fn) {
-        case 209: return with_g(integral_constant<int, 2>{}, integral_constant<int, 9>{});
-        case 208: return with_g(integral_constant<int, 2>{}, integral_constant<int, 8>{});
-        case 204: return with_g(integral_constant<int, 2>{}, integral_constant<int, 4>{});
-        case 108: return with_g(integral_constant<int, 1>{}, integral_constant<int, 8>{});
-        case 104: return with_g(integral_constant<int, 1>{}, integral_constant<int, 4>{});
-        default: return with_g(integral_constant<int, 1>{}, integral_constant<int, 2>{});
+        case 409: return with_g(I64{}, integral_constant<int, 4>{}, integral_constant<int, 9>{});
+        case 408: return with_g(I64{}, integral_constant<int, 4>{}, integral_constant<int, 8>{});
+        case 404: return with_g(I64{}, integral_constant<int, 4>{}, integral_constant<int, 4>{});
+        case 209: return with_g(I128{}, integral_constant<int, 2>{}, integral_constant<int, 9>{});
+        case 208: return with_g(I128{}, integral_constant<int, 2>{}, integral_constant<int, 8>{});
+        case 204: return with_g(I128{}, integral_constant<int, 2>{}, integral_constant<int, 4>{});
+        case 108: return with_g(I128{}, integral_constant<int, 1>{}, integral_constant<int, 8>{});
+        case 104: return with_g(I128{}, integral_constant<int, 1>{}, integral_constant<int, 4>{});
+        default: return with_g(I128{}, integral_constant<int, 1>{}, integral_constant<int, 2>{});
     }
 }
 
@@ -614,7 +642,7 @@ nq_status wq_wide(const _Float16* x, const uint8_t* w, const ST* sc, const float
 // few tiles, m = 64, n = 1536, k = 8960: 40.4 vs 53.6).
 template <bool Q4, typename ST>
 bool wq_wide_ok(int64_t m, int64_t n, int64_t k, int64_t group) {
-    if (m < 32 || (m <= 128 && plan_wq_wide(m, n).tiles < 128)) return false;
+    if (m < 32 || (m <= 128 && plan_wq_wide(m, n, wq_sk64_ok<Q4, ST>(group)).tiles < 128)) return false;
     if (k % 128 != 0 || m * k * 2 >= (int64_t(1) << 31) - 64) return false;
     if (!Q4) return n * k < (int64_t(1) << 31) - 64;
     if (sizeof(ST) == 2 && group != 32 && group != 64) return false;
