@@ -560,8 +560,12 @@ nq_status launch_wq_wide(const _Float16* x, const uint8_t* w, const ST* sc, cons
 }
 
 // Tiles of the wide path: (64 * fm) x (32 * fn) with sk-column slabs, by
-// falling area; the plan takes the least (rounds x area), rounds =
-// ceil(tiles / 256). 256-row tiles need 64-column slabs.
+// falling area. 256-row tiles need 64-column slabs. The plan takes the least
+// rounds x (area + 21504), rounds = ceil(tiles / 256): a round of tiles took
+// about 14 us + 0.65 us per 1024 outputs of the tile at k = 1536 (m = 512, n =
+// 8960: 256 x 128 tiles 34.3 us, 128 x 256 39.0, 128 x 288 44.3, 256 x 256
+// 55.6, 256 x 288 61.2; m = 2048: 256 x 288 in one round 67.0 us, 128 x 288 in
+// two 91.9, 256 x 128 in three 100).
 struct WqTile {
     int fm, fn, sk;
 };
@@ -577,7 +581,7 @@ WqPlan plan_wq_wide(int64_t m, int64_t n, bool sk64_ok) {
     for (const WqTile& t : kWqTiles) {
         if (t.sk == 64 && !sk64_ok) continue;
         const int64_t c = ((m + 64 * t.fm - 1) / (64 * t.fm)) * ((n + 32 * t.fn - 1) / (32 * t.fn));
-        const int64_t cost = ((c + 255) / 256) * (64 * t.fm) * (32 * t.fn);
+        const int64_t cost = ((c + 255) / 256) * ((64 * t.fm) * (32 * t.fn) + 21504);
         if (best_cost == 0 || cost < best_cost) {
             best_cost = cost;
             p = {t, c};
