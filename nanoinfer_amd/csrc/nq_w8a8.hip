@@ -766,14 +766,16 @@ nq_status gemm_skinny(const int8_t* xq, const float* as, const int8_t* wq, const
 }
 
 // Big-m plan. The wide-tile kernel takes every shape except few tiles with a
-// long K. Among the tile shapes below it picks the least (rounds x tile area),
-// rounds = ceil(tiles / 256) (one tile per CU per round): a round costs about
-// the same for every workgroup, and a half-empty last round costs a full one.
-// Ties go to the larger tile. Measured: m = 512, n = 2048, k = 1536: 64 x 64
-// tiles 7.7 us, 64 x 128 9.9, 128 x 128 12.4; m = 4096, n = 8960, k = 1536: 256 x
-// 288 in two rounds 77.1, 256 x 320 (448 tiles) 78.4, 256 x 256 (560) 94.2, 256 x
-// 128 prefill tiles 85.5; m = 8192, n = 1536: 256 x 256 32.2 vs 256 x 288 34.9
-// (the same 192 tiles, less padding). When the chosen round has fewer than 128
+// long K. Among the tile shapes below it picks the least modeled time
+// rounds x (3.5 + 1.32 (BM + BN) / 100 + 3.24 BM BN / 10^4) us (k = 1536),
+// rounds = ceil(tiles / 256) (one tile per CU per round; a half-empty last
+// round costs a full one): a least-squares fit to 50 measured shape x tile
+// points (within 20%) that picks the measured best tile, or one within 3%, on
+// all of them. Examples: m = 512, n = 8960: 256 x 128 tiles 19.7 us, 64 x 96
+// in three rounds 25.2, 256 x 288 31.9; m = 768: 256 x 128 19.9, 64 x 64 44.2;
+// m = 512, n = 2048: 64 x 64 7.7, 64 x 128 9.9, 128 x 128 12.4; m = 4096, n =
+// 8960: 256 x 288 in two rounds 77.1, 256 x 256 (560 tiles) 94.2; m = 8192, n =
+// 1536: 256 x 256 32.2 vs 256 x 288 34.9 (the same 192 tiles, less padding). When the chosen round has fewer than 128
 // tiles and K is long (>= 64 slabs of 64 bytes), the K-split prefill plan runs
 // instead: 128 x 128 tiles of 4 waves (64 x 128 with 2 waves when no split
 // applies and tiles are few), K in ranges of at least 32 slabs: each range
@@ -801,7 +803,8 @@ PrefillPlan plan_prefill(int64_t m, int64_t n, int64_t k) {
     int64_t best_cost = 0, best_tiles = 0;
     for (const WideTile& t : kWideTiles) {
         const int64_t c = ((m + 64 * t.fm - 1) / (64 * t.fm)) * ((n + 32 * t.fn - 1) / (32 * t.fn));
-        const int64_t cost = ((c + 255) / 256) * (64 * t.fm) * (32 * t.fn);
+        const int64_t bm = 64 * t.fm, bn = 32 * t.fn;
+        const int64_t cost = ((c + 255) / 256) * (35000 + 132 * (bm + bn) + 324 * bm * bn / 100);
         if (best_cost == 0 || cost < best_cost) {
             best_cost = cost;
             best_tiles = c;
