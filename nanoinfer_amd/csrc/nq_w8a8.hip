@@ -7,10 +7,13 @@
 // (l % 16) and of B column (l % 16) for K slice (l / 16); the 16x16 int32
 // result lands as rows 4*(l/16)+v, column l%16, v = 0..3.
 //
-// Two MFMA kernels: a skinny one for batched decode (m <= 64: operands loaded
-// straight into the MFMA lane layout, K steps interleaved over waves) and an
-// LDS-tiled prefill GEMM (m > 64). When a launch would have too few
-// workgroups, both split K: each K range writes its int32 partial tile to its
+// Three MFMA kernels: a skinny one for batched decode (m <= 64: operands
+// loaded straight into the MFMA lane layout, K steps interleaved over waves);
+// the wide-tile kernel (one round of up to 256 tiles of 64 x 32 .. 256 x 320,
+// LDS-DMA ring of 128-byte K slabs), which takes most shapes with m > 64 and
+// decode batches with tall weights; and the LDS-tiled prefill kernel for m > 64
+// shapes with few tiles and a long K. When a launch would have too few
+// workgroups, they split K: each K range writes its int32 partial tile to its
 // own workspace plane and a reduction launch sums the planes in a fixed order
 // (integer addition is exact, so the result is bit-identical to a single pass)
 // and applies the epilogue.
@@ -35,7 +38,7 @@ constexpr int kLdsRow = kBK + 16;  // padded LDS row stride (bytes)
 
 enum class Out { Y, ACC, PARTIAL };
 
-// ---- prefill W8A8 GEMM (m > 64) ---------------------------------------------------------
+// ---- prefill W8A8 GEMM (m > 64, few tiles and long K) -------------------------------------
 // A workgroup of WM x WN waves owns a (WM*64) x (WN*64) output tile; each wave
 // owns 64 x 64 (4 x 4 MFMA 16x16x64 fragments). K advances in SW-byte slabs
 // (SW = 64 or 128) that the buffer unit writes straight into a D-deep LDS ring
@@ -960,6 +963,8 @@ nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const fl
     return reduce_partials(parts, p.splits, as, ws, bias, y, ydt, acc_out, mi, ni, s);
 }
 
+// The wide and prefill kernels' contract: whole 64-byte K slabs and 32-bit
+// buffer offsets.
 bool prefill_ok(int64_t m, int64_t n, int64_t k) {
     return k % kBK == 0 && m * k < (int64_t(1) << 31) - 64 && n * k < (int64_t(1) << 31) - 64;
 }
@@ -1036,7 +1041,6 @@ bool mfma_ok(const int8_t* xq, const int8_t* wq, int64_t k) {
     return k > 0 && k % 16 == 0 && aligned(xq, 16) && aligned(wq, 16);
 }
 
-// The prefill kernel's contract: whole 64-byte K slabs and 32-bit buffer offsets.
 // The skinny kernel's contract: 32-bit buffer offsets (k % 16 == 0 is mfma_ok's).
 bool skinny_ok(int64_t m, int64_t n, int64_t k) {
     return std::min<int64_t>(m, kSkinnyMaxM) * k < (int64_t(1) << 31) - 64 && n * k < (int64_t(1) << 31) - 64;
