@@ -350,7 +350,11 @@ struct WideShape {
     static constexpr int kD = std::min(8, (160 * 1024 - 1024) / kSlab);
     static_assert(kD >= 2, "two slabs must fit");
     static constexpr int kSink = kD * kSlab;  // 1 KB
-    static constexpr size_t kLds = std::max<size_t>(size_t(kSink) + 1024, size_t(kBM / 2) * kBN * 2);
+    // fp16 staging rows of the epilogue: 16 bytes of padding make the stride an
+    // odd multiple of 16, so the 16 rows of a fragment store hit distinct banks
+    // (an unpadded 576-byte stride put 4 rows on each bank group).
+    static constexpr int kStg = kBN * 2 + 16;
+    static constexpr size_t kLds = std::max<size_t>(size_t(kSink) + 1024, size_t(kBM / 2) * kStg);
 };
 
 template <int WM, int FN, int FM, Out OUT, typename YT>
@@ -488,7 +492,7 @@ __global__ __launch_bounds__(WM * 2 * 64) void gemm_w8a8_wide_kernel(
                             h4 r;
 #pragma unroll
                             for (int v = 0; v < 4; ++v) r[v] = from_f32<_Float16>(w8a8_epilogue(acc[i][j][v], a_s, w4[v], b4[v]));
-                            *reinterpret_cast<h4*>(lds + (rl * BN + cl) * 2) = r;
+                            *reinterpret_cast<h4*>(lds + rl * S::kStg + cl * 2) = r;
                         }
                     }
                 }
@@ -497,7 +501,7 @@ __global__ __launch_bounds__(WM * 2 * 64) void gemm_w8a8_wide_kernel(
                     const int rl = c / CPR, cc = c % CPR;
                     const int row = m0 + half * HR + rl, col = n0 + cc * 8;
                     if (row < m && col < n)
-                        __builtin_nontemporal_store(*reinterpret_cast<const v4i*>(lds + (rl * BN + cc * 8) * 2),
+                        __builtin_nontemporal_store(*reinterpret_cast<const v4i*>(lds + rl * S::kStg + cc * 16),
                                                     reinterpret_cast<v4i*>(y + static_cast<size_t>(row) * n + col));
                 }
             }

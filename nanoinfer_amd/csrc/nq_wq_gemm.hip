@@ -325,7 +325,10 @@ struct WqWideShape {
     static constexpr int kSlab = kSOff + kNS * 256;
     static constexpr int kD = std::min(8, (160 * 1024 - 1024) / kSlab);
     static constexpr int kSink = kD * kSlab;
-    static constexpr size_t kStage = size_t(kBM) * kBN * sizeof(YT);
+    // fp16 staging rows padded by 16 bytes (an odd multiple of 16: the rows a
+    // store instruction touches fall on distinct banks).
+    static constexpr int kStg = kBN * 2 + 16;
+    static constexpr size_t kStage = size_t(kBM) * kStg;
     static constexpr size_t kLds = std::max<size_t>(size_t(kSink) + 1024, sizeof(YT) == 2 ? kStage : 0);
     static_assert(kD >= 2, "two slabs must fit");
     static_assert(kQ + kQS <= 63, "vmcnt range");
@@ -511,7 +514,7 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
                     for (int v = 0; v < 4; ++v) {
                         const int rl = fxo[j] - fr + 4 * fq + v;
                         const float val = Q4 ? acc[i][j][v] + b : acc[i][j][v] * ws + b;
-                        *reinterpret_cast<_Float16*>(lds + (rl * BN + cl) * 2) = static_cast<_Float16>(val);
+                        *reinterpret_cast<_Float16*>(lds + rl * S::kStg + cl * 2) = static_cast<_Float16>(val);
                     }
             }
             __syncthreads();
@@ -520,7 +523,7 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
                 const int rl = c / CPR, cc = c % CPR;
                 const int row = m0 + rl, col = n0 + cc * 8;
                 if (row < m && col < n)
-                    __builtin_nontemporal_store(*reinterpret_cast<const v4i*>(lds + (rl * BN + cc * 8) * 2),
+                    __builtin_nontemporal_store(*reinterpret_cast<const v4i*>(lds + rl * S::kStg + cc * 16),
                                                 reinterpret_cast<v4i*>(y + static_cast<size_t>(row) * n + col));
             }
             return;
