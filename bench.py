@@ -235,6 +235,16 @@ def main():
     torch.cuda.empty_cache()
     gbs = nbytes / (ms * 1e-3) / 1e9
 
+    # Context for the headline: one device-to-device copy of the same number of
+    # bytes (torch's copy kernel; it reads and writes them), rotated and timed
+    # the same way. A single launch that touches ~8 MB is bound by launch and
+    # memory latency, not by bandwidth.
+    srcs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(copies_for(2 * nbytes))]
+    dsts = [torch.empty_like(t) for t in srcs]
+    copy_ms = time_graph([lambda i=i: dsts[i].copy_(srcs[i]) for i in range(len(srcs))], args.steps, args.warmup)
+    del srcs, dsts
+    torch.cuda.empty_cache()
+
     sweep = []
     if not args.no_sweep:
         only = set(filter(None, args.only.split(",")))
@@ -298,6 +308,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic("q4g_gemv_cfg2")},
         "cpu_baseline": cpu,
+        "context": {"copy_same_bytes_us": round(copy_ms * 1e3, 3),
+                    "copy_same_bytes_note": "device copy of the headline's algorithmic bytes (read + write), "
+                                            "same graph timing: the single-launch latency floor at this size"},
     }
     if sweep:
         out["sweep"] = sweep
