@@ -1,6 +1,9 @@
 // Library identification and error reporting for the C ABI.
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
+#include <set>
+#include <utility>
 
 #include "nq_internal.hpp"
 
@@ -21,6 +24,20 @@ nq_status fail(nq_status st, const char* fmt, ...) {
 nq_status launch_status(const char* what) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(NQ_HIP_ERROR, "%s: %s", what, hipGetErrorString(e));
+    return NQ_OK;
+}
+
+nq_status set_dynamic_lds(const void* fn, size_t bytes, const char* who) {
+    static std::mutex mu;
+    static std::set<std::pair<const void*, int>> done;
+    int dev = 0;
+    if (hipError_t e = hipGetDevice(&dev); e != hipSuccess)
+        return fail(NQ_HIP_ERROR, "%s: hipGetDevice: %s", who, hipGetErrorString(e));
+    std::lock_guard<std::mutex> lock(mu);
+    if (done.count({fn, dev})) return NQ_OK;
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+    if (e != hipSuccess) return fail(NQ_HIP_ERROR, "%s: LDS attribute: %s", who, hipGetErrorString(e));
+    done.insert({fn, dev});
     return NQ_OK;
 }
 

@@ -20,6 +20,11 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 // Checks hipGetLastError after a launch: a failed launch is NQ_HIP_ERROR.
 nq_status launch_status(const char* what);
 
+// Raises kernel `fn`'s dynamic LDS limit to `bytes` on the current device, once
+// per (kernel, device) pair (the attribute is a property of the kernel on each
+// device).
+nq_status set_dynamic_lds(const void* fn, size_t bytes, const char* who);
+
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 constexpr int64_t kMaxIndex = (int64_t(1) << 31) - 1;

@@ -859,10 +859,7 @@ nq_status launch_prefill(const int8_t* xq, const float* as, const int8_t* wq, co
                          YT* y, int32_t* acc_out, int m, int n, int k, int splits, int k_slabs, hipStream_t s) {
     using S = PrefillShape<WM, WN, D, SW>;
     auto* fn = gemm_w8a8_prefill_kernel<WM, WN, D, SW, OUT, YT>;
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                       static_cast<int>(S::kLds));
-    if (attr != hipSuccess) return fail(NQ_HIP_ERROR, "gemm_w8a8_prefill: LDS attribute: %s", hipGetErrorString(attr));
+    if (nq_status st = set_dynamic_lds(reinterpret_cast<const void*>(fn), S::kLds, "gemm_w8a8_prefill")) return st;
     const int tm = (m + S::kBM - 1) / S::kBM, tn = (n + S::kBN - 1) / S::kBN;
     const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(splits));
     fn<<<grid, S::kWaves * 64, S::kLds, s>>>(xq, as, wq, ws, bias, y, acc_out, m, n, k, tm, tn, k_slabs);
@@ -875,10 +872,7 @@ nq_status launch_wide(const int8_t* xq, const float* as, const int8_t* wq, const
                       int k_slabs = 1 << 30) {
     using S = WideShape<WM, FN, FM>;
     auto* fn = gemm_w8a8_wide_kernel<WM, FN, FM, OUT, YT>;
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                       static_cast<int>(S::kLds));
-    if (attr != hipSuccess) return fail(NQ_HIP_ERROR, "gemm_w8a8_wide: LDS attribute: %s", hipGetErrorString(attr));
+    if (nq_status st = set_dynamic_lds(reinterpret_cast<const void*>(fn), S::kLds, "gemm_w8a8_wide")) return st;
     const int tm = (m + S::kBM - 1) / S::kBM, tn = (n + S::kBN - 1) / S::kBN;
     const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(splits));
     fn<<<grid, S::kWaves * 64, S::kLds, s>>>(xq, as, wq, ws, bias, y, acc_out, m, n, k, tm, tn, k_slabs);

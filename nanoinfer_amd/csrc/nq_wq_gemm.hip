@@ -553,10 +553,7 @@ nq_status launch_wq_wide(const _Float16* x, const uint8_t* w, const ST* sc, cons
                          int k, int gsh, hipStream_t s) {
     using S = WqWideShape<Q4, SK, FM, FN, GSH, YT, ST>;
     auto* fn = gemm_wq_wide_kernel<Q4, SK, FM, FN, GSH, YT, ST>;
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                       static_cast<int>(S::kLds));
-    if (attr != hipSuccess) return fail(NQ_HIP_ERROR, "gemm_wq_wide: LDS attribute: %s", hipGetErrorString(attr));
+    if (nq_status st = set_dynamic_lds(reinterpret_cast<const void*>(fn), S::kLds, "gemm_wq_wide")) return st;
     const int tm = (m + S::kBM - 1) / S::kBM, tn = (n + S::kBN - 1) / S::kBN;
     fn<<<tm * tn, 512, S::kLds, s>>>(x, w, sc, b, y, m, n, k, tm, tn, gsh);
     return launch_status("gemm_wq_wide_kernel");
