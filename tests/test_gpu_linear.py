@@ -406,6 +406,25 @@ def test_w8a8_workspace_reuse_and_gemm_entry(dev, nq, orc):
         assert same_bits(host(y2), host(y))
 
 
+@pytest.mark.parametrize("m,n,k", [(32, 1536, 8960), (200, 1003, 4096), (16, 1536, 8960)])
+def test_w8a8_split_workspace_too_small(dev, nq, m, n, k):
+    """Plans with K ranges need their partial planes: one byte short of the
+    reported size is NQ_BAD_ARG, before anything is launched."""
+    from nanoinfer_amd import _lib
+    lib = _lib.load()
+    need = lib.nq_gemm_w8a8_workspace_size(m, n, k)
+    assert need > 0
+    xq = torch.zeros((m, k), dtype=torch.int8, device=dev)
+    a_s = torch.ones(m, device=dev)
+    wq = torch.zeros((n, k), dtype=torch.int8, device=dev)
+    w_s = torch.ones(n, device=dev)
+    y = torch.empty((m, n), dtype=torch.float16, device=dev)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    st = lib.nq_gemm_w8a8(xq.data_ptr(), a_s.data_ptr(), wq.data_ptr(), w_s.data_ptr(), None, y.data_ptr(), 1,
+                          m, n, k, ws.data_ptr(), need - 256, 0, torch.cuda.current_stream().cuda_stream)
+    assert st == _lib.NQ_BAD_ARG, st
+
+
 @pytest.mark.parametrize("m,n,k", [(512, 256, 1536), (512, 1536, 1536), (512, 1536, 8960), (300, 1000, 960),
                                    (2048, 8960, 1536), (200, 1003, 192), (77, 517, 1024), (129, 36, 2048),
                                    # wide-tile plans: 256 x 256 / 288 / 320 tiles, ragged m and n, n % 8 != 0
