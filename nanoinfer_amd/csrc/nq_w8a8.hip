@@ -1007,9 +1007,10 @@ SmallWidePlan plan_small_wide(int64_t m, int64_t n, int64_t k) {
     return p;
 }
 
-// Workspace of the MFMA GEMM for this shape: a split plan's int32
-// accumulator (skinny plans for m <= 64, the prefill plan above, and the
-// skinny 64-row blocks that shapes outside the prefill contract run).
+// Workspace of the MFMA GEMM for this shape: the int32 partial planes of the
+// plan run_gemm picks (the small-m wide tiles or the skinny plan for m <= 64,
+// the wide / prefill plan for m > 64, the skinny 64-row blocks for shapes
+// outside the prefill contract); zero when the plan does not split K.
 // One skinny launch covers all m rows (64-row blocks over gridDim.z) when its
 // split planes stay within 64 MiB.
 bool skinny_one_launch(int64_t m, int64_t n, int64_t k) {
@@ -1018,9 +1019,12 @@ bool skinny_one_launch(int64_t m, int64_t n, int64_t k) {
 
 size_t gemm_ws_bytes(int64_t m, int64_t n, int64_t k) {
     if (m <= 0 || n <= 0 || k <= 0) return 0;
-    if (m <= kSkinnyMaxM) return std::max(plan_skinny(m, n, k).acc_bytes, plan_small_wide(m, n, k).acc_bytes);
-    const size_t sk = skinny_one_launch(m, n, k) ? plan_skinny(m, n, k).acc_bytes : plan_skinny(kSkinnyMaxM, n, k).acc_bytes;
-    return std::max(plan_prefill(m, n, k).acc_bytes, sk);
+    if (m <= kSkinnyMaxM) {
+        const SmallWidePlan sw = plan_small_wide(m, n, k);
+        return sw.fn ? sw.acc_bytes : plan_skinny(m, n, k).acc_bytes;
+    }
+    if (prefill_ok(m, n, k)) return plan_prefill(m, n, k).acc_bytes;
+    return skinny_one_launch(m, n, k) ? plan_skinny(m, n, k).acc_bytes : plan_skinny(kSkinnyMaxM, n, k).acc_bytes;
 }
 
 nq_status check_w8a8(int64_t m, int64_t n, int64_t k, int path, const char* who) {
