@@ -464,6 +464,32 @@ def test_w8a8_prefill_plans_exact(dev, nq, orc, m, n, k):
     assert_close_rms(host(y32)[rows], ref, f"w8a8 prefill fp32-out {m}x{n}x{k}")
 
 
+def _small_m_shapes():
+    """Seeded decode-batch shapes (m <= 64) over the skinny kernel, the 64-row
+    wide tiles (tall weights) and their K ranges (long K), k % 128 == 64 tails."""
+    rng = np.random.default_rng(4242)
+    shapes = []
+    for _ in range(14):
+        m = int(rng.integers(3, 65))
+        n = int(rng.choice([int(rng.integers(16, 3000)), int(rng.integers(4096, 20000))]))
+        k = int(rng.choice([64, 192, 1536, 1600, 4160, 6080, 8960]))
+        if m * n * k > 3e9:
+            n = max(16, int(3e9 / (m * k)))
+        shapes.append((m, n, k))
+    return shapes
+
+
+@pytest.mark.parametrize("m,n,k", _small_m_shapes())
+def test_w8a8_small_m_random_shapes(dev, nq, m, n, k):
+    """int32 accumulators of the m <= 64 MFMA plans equal the GEMV path's bit for bit."""
+    g = torch.Generator(device=dev).manual_seed(m * 17 + n * 5 + k)
+    xq = torch.randint(-127, 128, (m, k), generator=g, device=dev, dtype=torch.int8)
+    wq = torch.randint(-127, 128, (n, k), generator=g, device=dev, dtype=torch.int8)
+    acc_m = nq.w8a8_acc_i32(xq, wq, nq._lib.NQ_PATH_MFMA)
+    acc_g = nq.w8a8_acc_i32(xq, wq, nq._lib.NQ_PATH_GEMV)
+    assert torch.equal(acc_m, acc_g), (m, n, k)
+
+
 def _plan_shapes():
     """Seeded shapes spread over the W8A8 plans for m > 64: wide tiles in one
     or more rounds, 128x128 and 64x128 prefill tiles, split K, and k % 64 != 0
