@@ -22,6 +22,7 @@
 // reduced through LDS in wave order, so results are deterministic.
 #include <hip/hip_runtime.h>
 
+#include <iterator>
 #include <type_traits>
 
 #include "nq_device.hpp"
@@ -305,10 +306,10 @@ __device__ __forceinline__ int wq_swz(int r) {  // slot XOR of row r, C 16-byte 
     return (r >> S) & (C - 1);
 }
 
-template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST>
+template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST, typename XT = _Float16>
 struct WqWideShape {
     static constexpr int kBM = 64 * FM, kBN = 32 * FN, kT = SK / 32;  // MFMA K steps per slab
-    static constexpr int kXRow = 2 * SK, kWRow = Q4 ? SK / 2 : SK;   // bytes per row and slab
+    static constexpr int kXRow = static_cast<int>(sizeof(XT)) * SK, kWRow = Q4 ? SK / 2 : SK;  // bytes per row and slab
     static constexpr int kXC = kXRow / 16, kWC = kWRow / 16;         // 16-byte chunks per row
     // Scales per weight row and slab (Q4G): groups of 32 << GSH columns, one per
     // slab when a group covers the slab (GSH = kGBig stands for all such groups).
@@ -335,12 +336,13 @@ struct WqWideShape {
     static_assert(!Q4 || kSRow % 4 == 0, "scale rows are whole dwords");
 };
 
-template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST>
+template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST, typename XT>
 __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
-    const _Float16* __restrict__ x, const uint8_t* __restrict__ wq, const ST* __restrict__ scale,
+    const XT* __restrict__ x, const uint8_t* __restrict__ wq, const ST* __restrict__ scale,
     const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int tiles_m, int tiles_n,
     int gsh_rt) {
-    using S = WqWideShape<Q4, SK, FM, FN, GSH, YT, ST>;
+    using S = WqWideShape<Q4, SK, FM, FN, GSH, YT, ST, XT>;
+    constexpr bool F32X = sizeof(XT) == 4;  // fp32 activations: fp16 high part + fp16 remainder, two MFMAs
     constexpr int BM = S::kBM, BN = S::kBN, D = S::kD, Q = S::kQ, QS = S::kQS, XB = S::kXB, NB = S::kNB;
     constexpr int T = S::kT, XROW = S::kXRow, WROW = S::kWRow, XC = S::kXC, WC = S::kWC;
     // group = 32 << gsh columns; GSH = kGBig stands for every group of at
@@ -358,7 +360,7 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
 
     const int wrow_bytes = Q4 ? k / 2 : k;
     const int groups = Q4 ? k >> (5 + gsh) : 1;
-    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(x), 0, m * k * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<XT*>(x), 0, m * k * static_cast<int>(sizeof(XT)), 0x00020000);
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(wq), 0, n * wrow_bytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<ST*>(scale), 0, Q4 ? n * groups * static_cast<int>(sizeof(ST)) : 0, 0x00020000);
     // 1 KB request q of wave w = block b = q * 8 + w: blocks [0, XB) hold
@@ -371,7 +373,7 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
         const bool real = b < NB;
         if (b < XB) {
             const int r = b * (1024 / XROW) + lane / XC, c = (lane % XC) ^ wq_swz<XC>(r);
-            voff[q] = m0 + r < m ? (m0 + r) * k * 2 + c * 16 : kOob;
+            voff[q] = m0 + r < m ? (m0 + r) * k * static_cast<int>(sizeof(XT)) + c * 16 : kOob;
         } else {
             const int r = (b - XB) * (1024 / WROW) + lane / WC, c = (lane % WC) ^ wq_swz<WC>(r);
             voff[q] = real && n0 + r < n ? (n0 + r) * wrow_bytes + c * 16 : kOob;
@@ -440,14 +442,22 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
         f4 part[FN][FM];
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            h8 xa[FM], wb[FN];
+            h8 xa[FM], xl[FM], wb[FN];
 #pragma unroll
             for (int j = 0; j < FM; ++j) {
-                const int r = fxo[j], c = t * 4 + fq;
-                XFrag<_Float16> f;
-                f.raw = *reinterpret_cast<const v4i*>(base + S::kXOff + r * XROW + ((c ^ wq_swz<XC>(r)) << 4));
-                h8 lo;
-                f.operands(xa[j], lo);
+                const int r = fxo[j];
+                if constexpr (F32X) {  // 8 floats = chunks 8t + 2 fq and the next
+                    const int c = t * 8 + fq * 2;
+                    XFrag<float> f;
+                    f.a = *reinterpret_cast<const v4i*>(base + S::kXOff + r * XROW + ((c ^ wq_swz<XC>(r)) << 4));
+                    f.b = *reinterpret_cast<const v4i*>(base + S::kXOff + r * XROW + (((c + 1) ^ wq_swz<XC>(r)) << 4));
+                    f.operands(xa[j], xl[j]);
+                } else {  // 8 halves = chunk 4t + fq
+                    const int c = t * 4 + fq;
+                    XFrag<_Float16> f;
+                    f.raw = *reinterpret_cast<const v4i*>(base + S::kXOff + r * XROW + ((c ^ wq_swz<XC>(r)) << 4));
+                    f.operands(xa[j], xl[j]);
+                }
             }
 #pragma unroll
             for (int i = 0; i < FN; ++i) {
@@ -473,8 +483,10 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
                     if constexpr (Q4) {
                         const f4 z = t % S::kCPG == 0 ? f4{0, 0, 0, 0} : part[i][j];
                         part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], wb[i], z, 0, 0, 0);
+                        if constexpr (F32X) part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[j], wb[i], part[i][j], 0, 0, 0);
                     } else {
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], wb[i], acc[i][j], 0, 0, 0);
+                        if constexpr (F32X) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[j], wb[i], acc[i][j], 0, 0, 0);
                     }
                 }
             if constexpr (Q4) {
@@ -548,11 +560,11 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
     }
 }
 
-template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST>
-nq_status launch_wq_wide(const _Float16* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n,
+template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST, typename XT>
+nq_status launch_wq_wide(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n,
                          int k, int gsh, hipStream_t s) {
-    using S = WqWideShape<Q4, SK, FM, FN, GSH, YT, ST>;
-    auto* fn = gemm_wq_wide_kernel<Q4, SK, FM, FN, GSH, YT, ST>;
+    using S = WqWideShape<Q4, SK, FM, FN, GSH, YT, ST, XT>;
+    auto* fn = gemm_wq_wide_kernel<Q4, SK, FM, FN, GSH, YT, ST, XT>;
     if (nq_status st = set_dynamic_lds(reinterpret_cast<const void*>(fn), S::kLds, "gemm_wq_wide")) return st;
     const int tm = (m + S::kBM - 1) / S::kBM, tn = (n + S::kBN - 1) / S::kBN;
     fn<<<tm * tn, 512, S::kLds, s>>>(x, w, sc, b, y, m, n, k, tm, tn, gsh);
@@ -571,14 +583,19 @@ struct WqTile {
 };
 constexpr WqTile kWqTiles[] = {{4, 9, 64}, {4, 8, 64}, {2, 9, 128}, {4, 4, 64}, {2, 8, 128},
                                {2, 4, 128}, {1, 8, 128}, {1, 4, 128}, {1, 2, 128}};
+// fp32 activations take twice the LDS per row: 64-column slabs and at most 128-row tiles.
+constexpr WqTile kWqTilesF32[] = {{2, 9, 64}, {2, 8, 64}, {2, 4, 64}, {1, 8, 64}, {1, 4, 64}, {1, 2, 64}};
 struct WqPlan {
     WqTile tile;
     int64_t tiles;
 };
-WqPlan plan_wq_wide(int64_t m, int64_t n, bool sk64_ok) {
+WqPlan plan_wq_wide(int64_t m, int64_t n, bool sk64_ok, bool f32x) {
     int64_t best_cost = 0;
     WqPlan p{{0, 0, 0}, 0};
-    for (const WqTile& t : kWqTiles) {
+    const WqTile* tiles = f32x ? kWqTilesF32 : kWqTiles;
+    const int count = f32x ? static_cast<int>(std::size(kWqTilesF32)) : static_cast<int>(std::size(kWqTiles));
+    for (int ti = 0; ti < count; ++ti) {
+        const WqTile& t = tiles[ti];
         if (t.sk == 64 && !sk64_ok) continue;
         const int64_t c = ((m + 64 * t.fm - 1) / (64 * t.fm)) * ((n + 32 * t.fn - 1) / (32 * t.fn));
         const int64_t cost = ((c + 255) / 256) * ((64 * t.fm) * (32 * t.fn) + 21504);
@@ -596,26 +613,27 @@ bool wq_sk64_ok(int64_t group) {
     return !Q4 || group == 32;
 }
 
-template <bool Q4, typename YT, typename ST>
-nq_status wq_wide(const _Float16* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n, int k,
+template <bool Q4, typename XT, typename YT, typename ST>
+nq_status wq_wide(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n, int k,
                   int group, hipStream_t s) {
-    const WqTile pick = plan_wq_wide(m, n, wq_sk64_ok<Q4, ST>(group)).tile;
+    constexpr bool F32X = sizeof(XT) == 4;
+    const WqTile pick = plan_wq_wide(m, n, wq_sk64_ok<Q4, ST>(group), F32X).tile;
     const int gsh = Q4 ? __builtin_ctz(static_cast<unsigned>(group >> 5)) : 0;
     auto with_g = [&](auto skt, auto fmt, auto fnt) -> nq_status {
         constexpr int SK = decltype(skt)::value, FM = decltype(fmt)::value, FN = decltype(fnt)::value;
         constexpr int BIG = SK == 128 ? 2 : 1;  // one scale per slab from this shift on
         if constexpr (!Q4) {
-            return launch_wq_wide<false, SK, FM, FN, 0, YT, ST>(x, w, sc, b, y, m, n, k, 0, s);
+            return launch_wq_wide<false, SK, FM, FN, 0, YT, ST, XT>(x, w, sc, b, y, m, n, k, 0, s);
         } else {
-            if (gsh == 0) return launch_wq_wide<true, SK, FM, FN, 0, YT, ST>(x, w, sc, b, y, m, n, k, 0, s);
+            if (gsh == 0) return launch_wq_wide<true, SK, FM, FN, 0, YT, ST, XT>(x, w, sc, b, y, m, n, k, 0, s);
             if constexpr (SK == 64) {  // excluded by wq_sk64_ok
                 return fail(NQ_BAD_ARG, "gemm_wq_wide: 64-column slabs take groups of 32 only (got %d)", group);
             } else {
-                if (gsh == 1) return launch_wq_wide<true, SK, FM, FN, 1, YT, ST>(x, w, sc, b, y, m, n, k, 1, s);
+                if (gsh == 1) return launch_wq_wide<true, SK, FM, FN, 1, YT, ST, XT>(x, w, sc, b, y, m, n, k, 1, s);
                 if constexpr (sizeof(ST) == 2) {  // excluded by wq_wide_ok
                     return fail(NQ_BAD_ARG, "gemm_wq_wide: fp16 scales in groups of %d are not supported", group);
                 } else {
-                    return launch_wq_wide<true, SK, FM, FN, BIG, YT, ST>(x, w, sc, b, y, m, n, k, gsh, s);
+                    return launch_wq_wide<true, SK, FM, FN, BIG, YT, ST, XT>(x, w, sc, b, y, m, n, k, gsh, s);
                 }
             }
         }
@@ -623,31 +641,46 @@ nq_status wq_wide(const _Float16* x, const uint8_t* w, const ST* sc, const float
     using std::integral_constant;
     using I64 = integral_constant<int, 64>;
     using I128 = integral_constant<int, 128>;
-    switch (pick.fm * 100 + pick.fn) {
-        case 409: return with_g(I64{}, integral_constant<int, 4>{}, integral_constant<int, 9>{});
-        case 408: return with_g(I64{}, integral_constant<int, 4>{}, integral_constant<int, 8>{});
-        case 404: return with_g(I64{}, integral_constant<int, 4>{}, integral_constant<int, 4>{});
-        case 209: return with_g(I128{}, integral_constant<int, 2>{}, integral_constant<int, 9>{});
-        case 208: return with_g(I128{}, integral_constant<int, 2>{}, integral_constant<int, 8>{});
-        case 204: return with_g(I128{}, integral_constant<int, 2>{}, integral_constant<int, 4>{});
-        case 108: return with_g(I128{}, integral_constant<int, 1>{}, integral_constant<int, 8>{});
-        case 104: return with_g(I128{}, integral_constant<int, 1>{}, integral_constant<int, 4>{});
-        default: return with_g(I128{}, integral_constant<int, 1>{}, integral_constant<int, 2>{});
+    if constexpr (F32X) {
+        switch (pick.fm * 100 + pick.fn) {
+            case 209: return with_g(I64{}, integral_constant<int, 2>{}, integral_constant<int, 9>{});
+            case 208: return with_g(I64{}, integral_constant<int, 2>{}, integral_constant<int, 8>{});
+            case 204: return with_g(I64{}, integral_constant<int, 2>{}, integral_constant<int, 4>{});
+            case 108: return with_g(I64{}, integral_constant<int, 1>{}, integral_constant<int, 8>{});
+            case 104: return with_g(I64{}, integral_constant<int, 1>{}, integral_constant<int, 4>{});
+            default: return with_g(I64{}, integral_constant<int, 1>{}, integral_constant<int, 2>{});
+        }
+    } else {
+        switch (pick.fm * 100 + pick.fn) {
+            case 409: return with_g(I64{}, integral_constant<int, 4>{}, integral_constant<int, 9>{});
+            case 408: return with_g(I64{}, integral_constant<int, 4>{}, integral_constant<int, 8>{});
+            case 404: return with_g(I64{}, integral_constant<int, 4>{}, integral_constant<int, 4>{});
+            case 209: return with_g(I128{}, integral_constant<int, 2>{}, integral_constant<int, 9>{});
+            case 208: return with_g(I128{}, integral_constant<int, 2>{}, integral_constant<int, 8>{});
+            case 204: return with_g(I128{}, integral_constant<int, 2>{}, integral_constant<int, 4>{});
+            case 108: return with_g(I128{}, integral_constant<int, 1>{}, integral_constant<int, 8>{});
+            case 104: return with_g(I128{}, integral_constant<int, 1>{}, integral_constant<int, 4>{});
+            default: return with_g(I128{}, integral_constant<int, 1>{}, integral_constant<int, 2>{});
+        }
     }
 }
 
-// The wide path's contract: fp16 activations, k % 128 == 0, 32-bit offsets,
-// and for Q4G fp16 scales groups of 32 or 64 columns (a slab's scales are
-// whole dwords), fp32 scales any power-of-two multiple of 32. It runs from
+// The wide path's contract: k % 128 == 0, 32-bit offsets, for Q4G fp16 scales
+// groups of 32 or 64 columns (a slab's scales are whole dwords), fp32 scales
+// any power-of-two multiple of 32; fp32 activations (split into an fp16 high
+// part and an fp16 remainder after the LDS read, two MFMAs) take 64-column
+// slabs, so Q4G only in groups of 32 there. It runs from
 // m = 32 when its tiles number at least 128, and for every m > 128; otherwise
 // the 16-row kernel, which streams the weight once per 64 rows of x, is faster
 // (measured, k = 1536: m = 64, n = 8960 Q8 23.9 -> 12.0 us, Q4G 29.8 -> 15.0;
 // m = 128 38.4 -> 17.9; m = 64, n = 1536 (24 tiles) 9.2 vs 11.8; long K with
 // few tiles, m = 64, n = 1536, k = 8960: 40.4 vs 53.6).
-template <bool Q4, typename ST>
+template <bool Q4, typename XT, typename ST>
 bool wq_wide_ok(int64_t m, int64_t n, int64_t k, int64_t group) {
-    if (m < 32 || (m <= 128 && plan_wq_wide(m, n, wq_sk64_ok<Q4, ST>(group)).tiles < 128)) return false;
-    if (k % 128 != 0 || m * k * 2 >= (int64_t(1) << 31) - 64) return false;
+    constexpr bool F32X = sizeof(XT) == 4;
+    if (F32X && !wq_sk64_ok<Q4, ST>(group)) return false;
+    if (m < 32 || (m <= 128 && plan_wq_wide(m, n, wq_sk64_ok<Q4, ST>(group), F32X).tiles < 128)) return false;
+    if (k % 128 != 0 || m * k * static_cast<int64_t>(sizeof(XT)) >= (int64_t(1) << 31) - 64) return false;
     if (!Q4) return n * k < (int64_t(1) << 31) - 64;
     if (sizeof(ST) == 2 && group != 32 && group != 64) return false;
     return n * (k / 2) < (int64_t(1) << 31) - 64 && n * (k / group) * int64_t(sizeof(ST)) < (int64_t(1) << 31) - 64;
@@ -674,11 +707,9 @@ bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m,
 template <bool Q4, typename XT, typename YT, typename ST>
 nq_status wq_gemm(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int64_t m, int64_t n,
                   int64_t k, int64_t group, hipStream_t s) {
-    if constexpr (std::is_same_v<XT, _Float16>) {
-        if (wq_wide_ok<Q4, ST>(m, n, k, group))
-            return wq_wide<Q4>(x, w, sc, b, y, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
-                               static_cast<int>(group), s);
-    }
+    if (wq_wide_ok<Q4, XT, ST>(m, n, k, group))
+        return wq_wide<Q4>(x, w, sc, b, y, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
+                           static_cast<int>(group), s);
     return launch_wq<Q4>(x, w, sc, b, y, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
                          static_cast<int>(group), s);
 }

@@ -184,6 +184,10 @@ WQ_GEMM_CASES = [  # m > 8: the fp16 MFMA GEMM (m >= 16 or n >= 4096) or GEMV sl
     ("q8", 257, 2900, 1024, 0, True, F16, F32, F32),
     ("q4g", 1100, 640, 512, 32, True, F16, F16, F16),
     ("q4g", 40, 8960, 1536, 64, True, F16, F16, F16),    # m >= 32 with >= 128 tiles
+    # fp32 x on the wide tiles: fp16 high part + remainder, 64-column slabs
+    ("q8", 300, 1536, 1536, 0, True, F32, F32, F32),
+    ("q4g", 200, 2000, 1024, 32, False, F32, F16, F16),
+    ("q4g", 130, 9000, 512, 32, True, F32, F32, F32),
 ]
 
 
@@ -203,7 +207,7 @@ def _wq_random_cases():
         g = int(rng.choice([32, 64])) if sdt == F16 else int(rng.choice([32, 64, 128, 256]))
         while k % g:
             g //= 2
-        cases.append((mode, m, n, k, g, bool(i % 4 == 1), sdt, F16 if i % 5 else F32))
+        cases.append((mode, m, n, k, g, bool(i % 4 == 1), sdt, F16 if i % 5 else F32, F32 if i % 3 == 1 else F16))
     return cases
 
 
@@ -213,13 +217,13 @@ def _dequant_q4g(t, g):
     return codes.float() * t.scale.float().repeat_interleave(g, dim=1)[:, :t.in_]
 
 
-@pytest.mark.parametrize("mode,m,n,k,g,bias,sdt,ydt", _wq_random_cases())
-def test_weight_only_random_shapes(dev, nq, mode, m, n, k, g, bias, sdt, ydt):
-    """Weight-only linears on fp16 activations against a torch fp32 reference
+@pytest.mark.parametrize("mode,m,n,k,g,bias,sdt,ydt,xdt", _wq_random_cases())
+def test_weight_only_random_shapes(dev, nq, mode, m, n, k, g, bias, sdt, ydt, xdt):
+    """Weight-only linears on fp16 or fp32 activations against a torch fp32 reference
     on the dequantized weight (the reference's own test_quant.cpp:100-116
     invariant linear(x, dequant(w)))."""
     gen = torch.Generator(device=dev).manual_seed(m * 7 + n * 3 + k)
-    x = torch.randn((m, k), generator=gen, device=dev).half()
+    x = torch.randn((m, k), generator=gen, device=dev).to(xdt)
     w = torch.randn((n, k), generator=gen, device=dev) * 0.05
     b = torch.randn(n, generator=gen, device=dev) if bias else None
     if mode == "q8":
