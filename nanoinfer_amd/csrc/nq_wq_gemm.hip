@@ -306,9 +306,10 @@ __device__ __forceinline__ int wq_swz(int r) {  // slot XOR of row r, C 16-byte 
     return (r >> S) & (C - 1);
 }
 
-template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST, typename XT = _Float16>
+template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST, typename XT = _Float16, int WN = 2>
 struct WqWideShape {
-    static constexpr int kBM = 64 * FM, kBN = 32 * FN, kT = SK / 32;  // MFMA K steps per slab
+    static constexpr int kNW = 4 * WN;  // waves: 4 along m, WN along n
+    static constexpr int kBM = 64 * FM, kBN = WN * 16 * FN, kT = SK / 32;  // MFMA K steps per slab
     static constexpr int kXRow = static_cast<int>(sizeof(XT)) * SK, kWRow = Q4 ? SK / 2 : SK;  // bytes per row and slab
     static constexpr int kXC = kXRow / 16, kWC = kWRow / 16;         // 16-byte chunks per row
     // Scales per weight row and slab (Q4G): groups of 32 << GSH columns, one per
@@ -318,10 +319,10 @@ struct WqWideShape {
     static constexpr int kSRow = kSPer * static_cast<int>(sizeof(ST));
     static constexpr int kCPG = GSH >= kGBig ? kT : 1 << GSH;  // MFMA steps per scaled chain
     static constexpr int kXB = kBM * kXRow / 1024, kWB = kBN * kWRow / 1024;  // 1 KB requests
-    static constexpr int kNB = kXB + kWB, kQ = (kNB + 7) / 8;
+    static constexpr int kNB = kXB + kWB, kQ = (kNB + kNW - 1) / kNW;
     // 256-byte scale requests; the last may run past the tile's rows into the
     // region's padding.
-    static constexpr int kNS = (kBN * kSRow + 255) / 256, kQS = (kNS + 7) / 8;
+    static constexpr int kNS = (kBN * kSRow + 255) / 256, kQS = (kNS + kNW - 1) / kNW;
     static constexpr int kXOff = 0, kWOff = kBM * kXRow, kSOff = kWOff + kBN * kWRow;
     static constexpr int kSlab = kSOff + kNS * 256;
     static constexpr int kD = std::min(8, (160 * 1024 - 1024) / kSlab);
@@ -336,12 +337,13 @@ struct WqWideShape {
     static_assert(!Q4 || kSRow % 4 == 0, "scale rows are whole dwords");
 };
 
-template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST, typename XT>
-__global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
+template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST, typename XT, int WN>
+__global__ __launch_bounds__(4 * WN * 64) void gemm_wq_wide_kernel(
     const XT* __restrict__ x, const uint8_t* __restrict__ wq, const ST* __restrict__ scale,
     const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int tiles_m, int tiles_n,
     int gsh_rt) {
-    using S = WqWideShape<Q4, SK, FM, FN, GSH, YT, ST, XT>;
+    using S = WqWideShape<Q4, SK, FM, FN, GSH, YT, ST, XT, WN>;
+    constexpr int NW = S::kNW;
     constexpr bool F32X = sizeof(XT) == 4;  // fp32 activations: fp16 high part + fp16 remainder, two MFMAs
     constexpr int BM = S::kBM, BN = S::kBN, D = S::kD, Q = S::kQ, QS = S::kQS, XB = S::kXB, NB = S::kNB;
     constexpr int T = S::kT, XROW = S::kXRow, WROW = S::kWRow, XC = S::kXC, WC = S::kWC;
@@ -351,7 +353,7 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
     extern __shared__ __attribute__((aligned(16))) int8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
     const int total = tiles_m * tiles_n;
     const int per = (total + 7) / 8, xcd = blockIdx.x % 8, idx = blockIdx.x / 8;
     const int full = total - 8 * (per - 1);
@@ -369,7 +371,7 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
     int voff[Q], loff[Q];
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
-        const int b = q * 8 + wave;
+        const int b = q * NW + wave;
         const bool real = b < NB;
         if (b < XB) {
             const int r = b * (1024 / XROW) + lane / XC, c = (lane % XC) ^ wq_swz<XC>(r);
@@ -384,7 +386,7 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
     int soffv[QS > 0 ? QS : 1], sloff[QS > 0 ? QS : 1];
 #pragma unroll
     for (int q = 0; q < QS; ++q) {
-        const int b = q * 8 + wave;
+        const int b = q * NW + wave;
         constexpr int LPR = S::kSRow / 4 > 0 ? S::kSRow / 4 : 1;
         const int r = b * (64 / LPR) + lane / LPR;
         soffv[q] = b < S::kNS && n0 + r < n ? (n0 + r) * groups * static_cast<int>(sizeof(ST)) + (lane % LPR) * 4 : kOob;
@@ -398,7 +400,7 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
         const int xo = in ? sl * XROW : kOob, wo = in ? sl * WROW : kOob;
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
-            const int b = q * 8 + wave;
+            const int b = q * NW + wave;
             const unsigned dst = lds_base + (b < NB ? slot : 0u) + static_cast<unsigned>(loff[q]);
             if (b < XB)
                 asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
@@ -412,7 +414,7 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
             const int so = in ? ((sl * T) >> gsh) * static_cast<int>(sizeof(ST)) : kOob;
 #pragma unroll
             for (int q = 0; q < QS; ++q) {
-                const int b = q * 8 + wave;
+                const int b = q * NW + wave;
                 const unsigned dst = lds_base + (b < S::kNS ? slot : 0u) + static_cast<unsigned>(sloff[q]);
                 asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
                              ::"s"(dst), "v"(soffv[q]), "s"(srs), "s"(so) : "memory");
@@ -531,7 +533,7 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
             }
             __syncthreads();
             constexpr int CPR = BN / 8;
-            for (int c = tid; c < BM * CPR; c += 512) {
+            for (int c = tid; c < BM * CPR; c += NW * 64) {
                 const int rl = c / CPR, cc = c % CPR;
                 const int row = m0 + rl, col = n0 + cc * 8;
                 if (row < m && col < n)
@@ -560,14 +562,14 @@ __global__ __launch_bounds__(512) void gemm_wq_wide_kernel(
     }
 }
 
-template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST, typename XT>
+template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST, typename XT, int WN>
 nq_status launch_wq_wide(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n,
                          int k, int gsh, hipStream_t s) {
-    using S = WqWideShape<Q4, SK, FM, FN, GSH, YT, ST, XT>;
-    auto* fn = gemm_wq_wide_kernel<Q4, SK, FM, FN, GSH, YT, ST, XT>;
+    using S = WqWideShape<Q4, SK, FM, FN, GSH, YT, ST, XT, WN>;
+    auto* fn = gemm_wq_wide_kernel<Q4, SK, FM, FN, GSH, YT, ST, XT, WN>;
     if (nq_status st = set_dynamic_lds(reinterpret_cast<const void*>(fn), S::kLds, "gemm_wq_wide")) return st;
     const int tm = (m + S::kBM - 1) / S::kBM, tn = (n + S::kBN - 1) / S::kBN;
-    fn<<<tm * tn, 512, S::kLds, s>>>(x, w, sc, b, y, m, n, k, tm, tn, gsh);
+    fn<<<tm * tn, S::kNW * 64, S::kLds, s>>>(x, w, sc, b, y, m, n, k, tm, tn, gsh);
     return launch_status("gemm_wq_wide_kernel");
 }
 
@@ -619,21 +621,25 @@ nq_status wq_wide(const XT* x, const uint8_t* w, const ST* sc, const float* b, Y
     constexpr bool F32X = sizeof(XT) == 4;
     const WqTile pick = plan_wq_wide(m, n, wq_sk64_ok<Q4, ST>(group), F32X).tile;
     const int gsh = Q4 ? __builtin_ctz(static_cast<unsigned>(group >> 5)) : 0;
+    // Q8 tile widths that split in three 16-column multiples run 12 waves (4 x 3),
+    // as in the W8A8 wide kernel (m = 2048: 74.3 -> 71.7 us); Q4G keeps 8 waves
+    // (its group-scaled partial sums do not fit 170 registers: 106.9 vs 128.9 us).
     auto with_g = [&](auto skt, auto fmt, auto fnt) -> nq_status {
-        constexpr int SK = decltype(skt)::value, FM = decltype(fmt)::value, FN = decltype(fnt)::value;
+        constexpr int SK = decltype(skt)::value, FM = decltype(fmt)::value, FN2 = decltype(fnt)::value;
+        constexpr int WN = !Q4 && FN2 % 3 == 0 ? 3 : 2, FN = FN2 * 2 / WN;
         constexpr int BIG = SK == 128 ? 2 : 1;  // one scale per slab from this shift on
         if constexpr (!Q4) {
-            return launch_wq_wide<false, SK, FM, FN, 0, YT, ST, XT>(x, w, sc, b, y, m, n, k, 0, s);
+            return launch_wq_wide<false, SK, FM, FN, 0, YT, ST, XT, WN>(x, w, sc, b, y, m, n, k, 0, s);
         } else {
-            if (gsh == 0) return launch_wq_wide<true, SK, FM, FN, 0, YT, ST, XT>(x, w, sc, b, y, m, n, k, 0, s);
+            if (gsh == 0) return launch_wq_wide<true, SK, FM, FN, 0, YT, ST, XT, WN>(x, w, sc, b, y, m, n, k, 0, s);
             if constexpr (SK == 64) {  // excluded by wq_sk64_ok
                 return fail(NQ_BAD_ARG, "gemm_wq_wide: 64-column slabs take groups of 32 only (got %d)", group);
             } else {
-                if (gsh == 1) return launch_wq_wide<true, SK, FM, FN, 1, YT, ST, XT>(x, w, sc, b, y, m, n, k, 1, s);
+                if (gsh == 1) return launch_wq_wide<true, SK, FM, FN, 1, YT, ST, XT, WN>(x, w, sc, b, y, m, n, k, 1, s);
                 if constexpr (sizeof(ST) == 2) {  // excluded by wq_wide_ok
                     return fail(NQ_BAD_ARG, "gemm_wq_wide: fp16 scales in groups of %d are not supported", group);
                 } else {
-                    return launch_wq_wide<true, SK, FM, FN, BIG, YT, ST, XT>(x, w, sc, b, y, m, n, k, gsh, s);
+                    return launch_wq_wide<true, SK, FM, FN, BIG, YT, ST, XT, WN>(x, w, sc, b, y, m, n, k, gsh, s);
                 }
             }
         }
