@@ -885,12 +885,15 @@ nq_status launch_wide(const int8_t* xq, const float* as, const int8_t* wq, const
 nq_status launch_wide_tile(int fm, int fn, const int8_t* xq, const float* as, const int8_t* wq, const float* ws,
                            const float* bias, void* y, nq_dtype ydt, int32_t* acc_out, int mi, int ni, int ki,
                            hipStream_t s, int splits = 1, int k_slabs = 1 << 30, int32_t* parts = nullptr) {
-    // Tiles whose width splits into three 16-column multiples run 12 waves (4 x 3)
-    // instead of 8 (4 x 2): three waves per SIMD hide more of the LDS latency
-    // (config 5a, 256 x 288: 64 x 96 per wave 34.8 us vs 64 x 144 37.5).
+    // More waves along n where the tile width allows: widths that split in three
+    // 16-column multiples run 12 waves (4 x 3), in four 16 waves (4 x 4), else 8
+    // (4 x 2). Three or four waves per SIMD hide more of the LDS latency (config
+    // 5a, 256 x 288: 64 x 96 per wave 34.8 us vs 64 x 144 37.5; m = 8192, n =
+    // 1536, 256 x 256: 16 waves 27.1 us vs 8 waves 32.2; m = 512, n = 8960,
+    // 128 x 256: 16.8 vs 19.5).
     auto wide = [&](auto fmtag, auto fntag) -> nq_status {
         constexpr int FM = decltype(fmtag)::value, FN2 = decltype(fntag)::value;
-        constexpr int WN = FN2 % 3 == 0 ? 3 : 2, FN = FN2 * 2 / WN;  // 16-column fragments per wave
+        constexpr int WN = FN2 % 3 == 0 ? 3 : FN2 % 4 == 0 ? 4 : 2, FN = FN2 * 2 / WN;  // 16-column fragments per wave
         if (splits > 1) {
             const nq_status st = launch_wide<4, FN, FM, Out::PARTIAL, float, WN>(xq, as, wq, ws, bias, nullptr, parts,
                                                                                  mi, ni, ki, s, splits, k_slabs);
