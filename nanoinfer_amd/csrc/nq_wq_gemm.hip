@@ -621,12 +621,13 @@ nq_status wq_wide(const XT* x, const uint8_t* w, const ST* sc, const float* b, Y
     constexpr bool F32X = sizeof(XT) == 4;
     const WqTile pick = plan_wq_wide(m, n, wq_sk64_ok<Q4, ST>(group), F32X).tile;
     const int gsh = Q4 ? __builtin_ctz(static_cast<unsigned>(group >> 5)) : 0;
-    // Q8 tile widths that split in three 16-column multiples run 12 waves (4 x 3),
-    // as in the W8A8 wide kernel (m = 2048: 74.3 -> 71.7 us); Q4G keeps 8 waves
-    // (its group-scaled partial sums do not fit 170 registers: 106.9 vs 128.9 us).
+    // Q8 tile widths that split in three (four) 16-column multiples run 12 (16)
+    // waves, as in the W8A8 wide kernel (m = 2048: 74.3 -> 71.7 us); Q4G keeps 8
+    // waves (its group-scaled partial sums do not fit 170 registers: 106.9 vs
+    // 128.9 us).
     auto with_g = [&](auto skt, auto fmt, auto fnt) -> nq_status {
         constexpr int SK = decltype(skt)::value, FM = decltype(fmt)::value, FN2 = decltype(fnt)::value;
-        constexpr int WN = !Q4 && FN2 % 3 == 0 ? 3 : 2, FN = FN2 * 2 / WN;
+        constexpr int WN = Q4 ? 2 : FN2 % 3 == 0 ? 3 : FN2 % 4 == 0 ? 4 : 2, FN = FN2 * 2 / WN;
         constexpr int BIG = SK == 128 ? 2 : 1;  // one scale per slab from this shift on
         if constexpr (!Q4) {
             return launch_wq_wide<false, SK, FM, FN, 0, YT, ST, XT, WN>(x, w, sc, b, y, m, n, k, 0, s);
