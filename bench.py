@@ -162,6 +162,26 @@ def main():
             return lambda: lib.nq_linear_q8(P(x), dt, P(qs[i]), P(ss[i]), None, P(y), dt, m, n, k, stream_ptr())
         return [mk(i) for i in range(len(qs))], nb, 2 * m * n * k
 
+    def quantize(kind, n, k, g=32):
+        """Load-time weight quantize (quant.cpp:88-108 / :295-321): fp32 [n, k]
+        read once, codes + scales written once (q4g: fp16 scales)."""
+        ws = [rnd((n, k), 0.02) for _ in range(copies_for(n * k * 4))]
+        if kind == "q8":
+            q = torch.empty((n, k), dtype=torch.int8, device=dev)
+            s = torch.empty(n, dtype=torch.float32, device=dev)
+            nb = n * k * 4 + n * k + n * 4
+
+            def mk(i):
+                return lambda: lib.nq_quantize_q8(P(ws[i]), n, k, P(q), P(s), stream_ptr())
+        else:
+            q = torch.empty((n, (k + 1) // 2), dtype=torch.uint8, device=dev)
+            s = torch.empty((n, (k + g - 1) // g), dtype=torch.float16, device=dev)
+            nb = n * k * 4 + q.numel() + s.numel() * 2
+
+            def mk(i):
+                return lambda: lib.nq_quantize_q4g(P(ws[i]), n, k, g, P(q), P(s), 1, stream_ptr())
+        return [mk(i) for i in range(len(ws))], nb, 0
+
     def q8_lmhead_argmax(m, n, k, xdt):
         """LM head with the greedy argmax fused in: no logits are written, so
         the algorithmic bytes are weights + scales + x + the int64 ids."""
@@ -279,6 +299,12 @@ def main():
             sweep.append(entry("q4g_weight_only_prefill M=2048 K=1536 N=8960 g=32 fp16",
                                *q4g_gemv(2048, 8960, 1536, 32), "mfma_f16"))
             torch.cuda.empty_cache()
+        if want("quantize"):
+            # load-time quantize of the configs' weights, HBM-bound (fp32 in)
+            for kind, n, k, nm in (("q8", 151936, 1536, "lm head cfg5b"), ("q8", 8960, 1536, "gate/up cfg5a"),
+                                   ("q4g", 1536, 8960, "down cfg2, g=32")):
+                sweep.append(entry(f"quantize_{kind} {nm} N={n} K={k} fp32 in", *quantize(kind, n, k), "hbm"))
+                torch.cuda.empty_cache()
         if want("decoder_cfg4"):
             sweep.append(decoder_layer_cfg4(rnd, time_graph, args, w8a8_linear, entry))
         torch.cuda.empty_cache()

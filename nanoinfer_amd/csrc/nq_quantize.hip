@@ -76,6 +76,43 @@ __global__ void quantize_q4g_even_kernel(const float* __restrict__ w, uint8_t* _
     }
 }
 
+// Vector path (group = 8 G with G a power of two <= 64, in % 8 == 0): lane t
+// owns 8 consecutive columns (two 16-byte loads) of a row whose chunks are
+// padded to a multiple of G, so the G lanes of one block are an aligned run of
+// a wave; the block absmax is a G-lane shuffle reduction (order-free), and the
+// lane writes its 4 packed bytes with one 32-bit store. Lanes past the row's
+// end (a partial last block) contribute 0 to the absmax and store nothing.
+template <typename ST, int G>
+__global__ __launch_bounds__(256) void quantize_q4g_vec_kernel(const float* __restrict__ w, uint32_t* __restrict__ q,
+                                                               ST* __restrict__ scale, int out, int in, int blocks,
+                                                               int cpr) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const bool live = t < static_cast<int64_t>(out) * cpr;
+    const int o = live ? static_cast<int>(t / cpr) : 0, cc = live ? static_cast<int>(t % cpr) : 0;
+    const bool act = live && cc * 8 < in;
+    const f4* src = reinterpret_cast<const f4*>(w + static_cast<size_t>(o) * in + (act ? cc * 8 : 0));
+    const f4 a = src[0], b = src[1];
+    const float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    float am = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) am = absmax_step(am, v[j]);
+    am = act ? am : 0.0f;
+#pragma unroll
+    for (int off = 1; off < G; off <<= 1) am = absmax_step(am, __shfl_xor(am, off));
+    const float s = am / 7.0f;
+    if (!act) return;
+    if (cc % G == 0) store_scale(scale + static_cast<size_t>(o) * blocks + cc / G, s);
+    const RowQuantizer rq(s);
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t lo = static_cast<uint32_t>(static_cast<int>(rq.code(v[2 * j], 7.0f)) + 8);
+        const uint32_t hi = static_cast<uint32_t>(static_cast<int>(rq.code(v[2 * j + 1], 7.0f)) + 8);
+        word |= (lo | (hi << 4)) << (8 * j);
+    }
+    q[static_cast<size_t>(o) * (in / 8) + cc] = word;
+}
+
 // Odd group: one thread per packed byte; each of its two columns recomputes its
 // block's absmax (blocks can straddle bytes). The thread owning a block's first
 // column writes that block's scale.
@@ -232,9 +269,9 @@ extern "C" nq_status nq_quantize_q8(const float* w, int64_t out, int64_t in, int
     if (out == 0) return NQ_OK;
     NQ_REQUIRE(scale && (in == 0 || (w && q)), NQ_BAD_ARG, "nq_quantize_q8: null pointer");
     NQ_REQUIRE(aligned(w, 4) && aligned(scale, 4), NQ_BAD_ALIGN, "nq_quantize_q8: misaligned fp32");
-    quantize_rows_i8_kernel<float><<<static_cast<unsigned>(out), kRowThreads, 0, as_stream(stream)>>>(
-        w, q, scale, static_cast<int>(in));
-    return launch_status("quantize_rows_i8_kernel");
+    // The weight quantizer is the activation quantizer's arithmetic
+    // (quant.cpp:88-108 and :179-193 both take absmax / 127 and round_clamp).
+    return act_quant(w, NQ_F32, out, in, q, scale, as_stream(stream));
 }
 
 extern "C" nq_status nq_act_quant_i8_heads(const void* x, nq_dtype x_dtype, int64_t heads, int64_t s,
@@ -295,7 +332,29 @@ extern "C" nq_status nq_quantize_q4g(const float* w, int64_t out, int64_t in, in
     const int blocks = static_cast<int>((in + group - 1) / group);
     const int threads = 256;
     hipStream_t s = as_stream(stream);
-    if (g % 2 == 0) {
+    const int gl = g / 8;  // lanes per block on the vector path
+    if (g % 8 == 0 && gl <= 64 && (gl & (gl - 1)) == 0 && k % 8 == 0 && aligned(w, 16) && aligned(q, 4)) {
+        const int cpr = ((k / 8 + gl - 1) / gl) * gl;
+        const unsigned grid = static_cast<unsigned>((out * cpr + 255) / 256);
+        auto go = [&](auto gtag, auto* sp) {
+            constexpr int G = decltype(gtag)::value;
+            using ST = std::remove_pointer_t<decltype(sp)>;
+            quantize_q4g_vec_kernel<ST, G><<<grid, 256, 0, s>>>(w, reinterpret_cast<uint32_t*>(q), sp, o, k, blocks, cpr);
+        };
+        auto with_g = [&](auto* sp) {
+            switch (gl) {
+                case 1: go(std::integral_constant<int, 1>{}, sp); break;
+                case 2: go(std::integral_constant<int, 2>{}, sp); break;
+                case 4: go(std::integral_constant<int, 4>{}, sp); break;
+                case 8: go(std::integral_constant<int, 8>{}, sp); break;
+                case 16: go(std::integral_constant<int, 16>{}, sp); break;
+                case 32: go(std::integral_constant<int, 32>{}, sp); break;
+                default: go(std::integral_constant<int, 64>{}, sp); break;
+            }
+        };
+        if (scale_dtype == NQ_F32) with_g(static_cast<float*>(scale));
+        else with_g(static_cast<_Float16*>(scale));
+    } else if (g % 2 == 0) {
         const int64_t total = out * blocks;
         const unsigned grid = static_cast<unsigned>((total + threads - 1) / threads);
         if (scale_dtype == NQ_F32)

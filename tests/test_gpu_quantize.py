@@ -42,10 +42,18 @@ def test_quantize_q4g_golden(dev, nq, golden):
         assert same_bits(host(t.scale).reshape(-1), g[n + "_s"]), n
 
 
-@pytest.mark.parametrize("shape,group", [((1536, 8960), 32), ((64, 896), 64), ((33, 137), 32), ((17, 45), 5)])
+# The vector path (group = 8 * 2^j <= 512, in % 8 == 0) and the scalar ones:
+# partial last blocks (1000 % 32, 200 % 128), 64-lane blocks (g = 512), g = 8,
+# a non-power-of-two lane count (g = 96) and in % 8 != 0 take the scalar kernels.
+@pytest.mark.parametrize("shape,group", [((1536, 8960), 32), ((64, 896), 64), ((33, 137), 32), ((17, 45), 5),
+                                         ((40, 1000), 32), ((9, 1024), 8), ((5, 4096), 512), ((11, 200), 128),
+                                         ((7, 960), 96), ((3, 8192), 256)])
 def test_quantize_q4g_full(dev, nq, orc, shape, group):
-    rng = np.random.default_rng(shape[0])
+    rng = np.random.default_rng(shape[0] * 7 + shape[1])
     w = rng.normal(0, 0.02, shape).astype(np.float32)
+    w[0, 1] = np.nan                              # skipped by the absmax, code 0 (nibble 8)
+    w[-1, -3:] = 0
+    w[shape[0] // 2, 0] = 3.0                     # one block dominated by an outlier
     q, s = orc.quantize_q4g(w, group)
     t = nq.quantize_q4g(to_dev(w, dev), group)
     assert same_bits(host(t.q), q) and same_bits(host(t.scale), s)
