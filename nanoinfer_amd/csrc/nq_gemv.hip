@@ -664,7 +664,8 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
                 int k, int g, hipStream_t s) {
     // Two rows per workgroup: the workgroup's 5..9 waves split K, which spreads
     // the unpack math over many SIMDs, and each activation chunk serves two rows
-    // (measured at k = 8960, n = 1536: 1 row 4.83 us, 2 rows 4.46, 4 rows 4.82).
+    // (measured at k = 8960, n = 1536: 1 row 4.83 us, 2 rows 4.46, 3 rows (512
+    // workgroups, two per CU) 4.51, 4 rows 4.82, 6 rows 5.21, 8 rows 4.98).
     constexpr int R = 2;
     const int chunks = k >> 5;
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
