@@ -420,10 +420,22 @@ def cpu_baseline(m, n, k, g, nbytes, seconds):
         impl.linear_q4g(x, q, s, g)
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
+    # The load-time quantize of the same weight (quant.cpp:295-321, serial in
+    # the reference): fp32 read once, packed codes + fp32 scales written once.
+    qtimes = []
+    q_end = time.perf_counter() + max(1.0, seconds / 5)
+    while time.perf_counter() < q_end or len(qtimes) < 3:
+        t0 = time.perf_counter()
+        impl.quantize_q4g(w, g)
+        qtimes.append(time.perf_counter() - t0)
+    qmed = float(np.median(qtimes))
+    qbytes = n * k * 4 + n * ((k + 1) // 2) + n * ((k + g - 1) // g) * 4
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": impl.max_threads(),
             "kind": kind,
             "sample": f"{len(times)} calls of linear_q4g M={m} K={k} N={n} g={g} (median {med * 1e3:.2f} ms), "
-                      f"~{seconds:.0f}s of CPU work, same algorithmic bytes; nproc={os.cpu_count()}"}
+                      f"~{seconds:.0f}s of CPU work, same algorithmic bytes; nproc={os.cpu_count()}",
+            "quantize": {"op": f"quantize_q4g N={n} K={k} g={g} (load time)", "ms": round(qmed * 1e3, 3),
+                         "GB/s": round(qbytes / qmed / 1e9, 3), "calls": len(qtimes)}}
 
 
 if __name__ == "__main__":
