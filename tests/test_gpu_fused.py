@@ -29,7 +29,8 @@ def check(xq, s, y_ref):
 
 
 @pytest.mark.parametrize("m,k,dt", [(1, 1536, torch.float16), (7, 1536, torch.float32), (512, 1536, torch.float16),
-                                    (3, 8960, torch.float16), (5, 100, torch.float32), (2, 40000, torch.float16)])
+                                    (3, 8960, torch.float16), (5, 100, torch.float32), (2, 40000, torch.float16),
+                                    (256, 8960, torch.float16)])
 def test_rmsnorm_quant(dev, nq, m, k, dt):
     rng = np.random.default_rng(m * 7 + k)
     x = rng.normal(0, 1, (m, k)).astype(np.float32)
@@ -42,7 +43,7 @@ def test_rmsnorm_quant(dev, nq, m, k, dt):
 
 
 @pytest.mark.parametrize("m,k,dt", [(1, 8960, torch.float16), (16, 8960, torch.float32), (512, 8960, torch.float16),
-                                    (4, 72, torch.float32)])
+                                    (4, 72, torch.float32), (300, 16384, torch.float32), (256, 8200, torch.float16)])
 def test_silu_mul_quant_on_fused_halves(dev, nq, m, k, dt):
     rng = np.random.default_rng(m + k)
     gu = rng.normal(0, 2, (m, 2 * k)).astype(np.float32)
