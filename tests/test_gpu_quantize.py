@@ -68,7 +68,8 @@ def test_q4_byte_layout_known_answer(dev, nq):
     assert host(t.q).tolist() == [[0x1F]] and host(t.scale).tolist() == [[1.0]]
 
 
-@pytest.mark.parametrize("m,k", [(1, 896), (8, 1536), (16, 8960), (64, 1536), (512, 1536), (3, 90), (2, 0)])
+@pytest.mark.parametrize("m,k", [(1, 896), (8, 1536), (16, 8960), (64, 1536), (512, 1536), (3, 90), (2, 0),
+                                 (300, 8960), (256, 16384)])
 @pytest.mark.parametrize("xdt", [torch.float32, torch.float16])
 def test_act_quant(dev, nq, orc, m, k, xdt):
     rng = np.random.default_rng(m * 31 + k)
