@@ -97,32 +97,63 @@ def main():
         return (torch.randn(shape, generator=gen, device=dev, dtype=torch.float32) * std).to(dtype)
 
     def copies_for(nbytes):
-        return max(2, math.ceil(ROTATE_BYTES / max(nbytes, 1)))
+        """Weight copies that make >= 512 MiB; a multiple of --steps when there
+        are more copies than steps, so time_graph's windows tile the rotation."""
+        c = max(2, math.ceil(ROTATE_BYTES / max(nbytes, 1)))
+        if c > args.steps:
+            c = math.ceil(c / args.steps) * args.steps
+        return c
 
-    def time_graph(launches, steps, warmup):
-        """launches: list of zero-arg callables (rotating weight copies).
-        Returns ms per launch over a graph of `steps` back-to-back launches."""
+    def time_graph(launches, steps, warmup, replays=None):
+        """launches: zero-arg callables over rotating weight copies (each copy
+        one launch's operands). Returns the median ms per launch over timed
+        replays of a HIP graph of exactly `steps` back-to-back launches.
+
+        The copies are split into windows of `steps` consecutive launches (one
+        graph each; a single window of launches[i % r] when steps >= r) and the
+        graphs replay in a cycle, so every launch reads a copy last touched a
+        whole rotation (>= 512 MiB of other weights) earlier: the timed reads
+        come from HBM, not from the 256 MiB Infinity Cache, whatever `steps`
+        is. Each replay is timed on its own between two events on the launch
+        stream; at least 5 replays and 50 timed launches."""
         r = len(launches)
+        warmup = max(warmup, 10)
+        if replays is None:
+            replays = max(5, math.ceil(50 / steps))
         s = torch.cuda.Stream()
         with torch.cuda.stream(s):
-            for i in range(warmup):
+            for i in range(max(warmup, r)):
                 launches[i % r]()
         torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=s):
-            for i in range(steps):
-                launches[i % r]()
+        if steps >= r:
+            windows = [[launches[i % r] for i in range(steps)]]
+        else:
+            nw = math.ceil(r / steps)
+            windows = [[launches[(j * steps + i) % r] for i in range(steps)] for j in range(nw)]
+        graphs = []
+        for win in windows:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                for f in win:
+                    f()
+            graphs.append(g)
         torch.cuda.synchronize()
         with torch.cuda.stream(s):
-            g.replay()                                   # untimed replay (first-replay setup)
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            torch.cuda.synchronize()
-            e0.record(s)
-            g.replay()
-            e1.record(s)
+            for g in graphs:                             # untimed cycle (first-replay setup)
+                g.replay()
         torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / steps
+        times = []
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(replays)]
+        with torch.cuda.stream(s):
+            for t in range(replays):
+                e0, e1 = ev[t]
+                e0.record(s)
+                graphs[t % len(graphs)].replay()
+                e1.record(s)
+        torch.cuda.synchronize()
+        times = sorted(e0.elapsed_time(e1) / steps for e0, e1 in ev)
+        del graphs
+        return times[len(times) // 2]
 
     def stream_ptr():
         return torch.cuda.current_stream().cuda_stream
@@ -263,6 +294,14 @@ def main():
     dsts = [torch.empty_like(t) for t in srcs]
     copy_ms = time_graph([lambda i=i: dsts[i].copy_(srcs[i]) for i in range(len(srcs))], args.steps, args.warmup)
     del srcs, dsts
+    # The read floor: one streaming read of the same bytes (nq_probe_read, the
+    # GEMV's 16-byte non-temporal loads, nothing written), rotated the same way.
+    rbytes = (nbytes + 15) // 16 * 16
+    rsrc = [torch.empty(rbytes, dtype=torch.uint8, device=dev) for _ in range(copies_for(rbytes))]
+    sink = torch.zeros(64, dtype=torch.int32, device=dev)
+    read_ms = time_graph([lambda i=i: lib.nq_probe_read(P(rsrc[i]), rbytes, P(sink), stream_ptr())
+                          for i in range(len(rsrc))], args.steps, args.warmup)
+    del rsrc
     torch.cuda.empty_cache()
 
     sweep = []
@@ -320,14 +359,15 @@ def main():
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": max(args.warmup, 10),
         "ms_per_step": round(ms, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int4 weights, fp16 x/y, fp32 accumulate",
         "data": "synthetic (weights N(0,0.02) quantized on device, x N(0,1)); weights rotated over "
-                f">= {ROTATE_BYTES >> 20} MiB of copies",
+                f">= {ROTATE_BYTES >> 20} MiB of copies, every timed launch on a copy last read a full "
+                "rotation earlier",
         "config": {"workload": "configs[1]: int4 group GEMV, Qwen2.5-1.5B down-proj",
                    "M": M, "K": K, "N": N, "group": G, "scale_dtype": "fp16", "x_dtype": "fp16",
                    "algorithmic_bytes": nbytes, "parallelism": "single GPU"},
@@ -336,7 +376,16 @@ def main():
         "cpu_baseline": cpu,
         "context": {"copy_same_bytes_us": round(copy_ms * 1e3, 3),
                     "copy_same_bytes_note": "device copy of the headline's algorithmic bytes (read + write), "
-                                            "same graph timing: the single-launch latency floor at this size"},
+                                            "same graph timing",
+                    "read_same_bytes_us": round(read_ms * 1e3, 3),
+                    "read_same_bytes_GB/s": round(rbytes / (read_ms * 1e-3) / 1e9, 1),
+                    "read_same_bytes_note": "nq_probe_read: one streaming read of the headline's algorithmic "
+                                            "bytes with 16-byte non-temporal loads, same graph timing: the "
+                                            "single-launch floor at this size"},
+        "timing": {"method": "HIP graph of exactly `steps` launches, windows of distinct weight copies "
+                             "replayed in a cycle (each copy last read >= 512 MiB earlier); median over timed "
+                             "replays, each between two events on the launch stream",
+                   "timed_replays": max(5, math.ceil(50 / args.steps)), "warmup_launches": max(args.warmup, 10)},
     }
     if sweep:
         out["sweep"] = sweep
@@ -397,8 +446,36 @@ def decoder_layer_cfg4(rnd, time_graph, args, w8a8_linear, entry):
     return e
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _time_calls(fn, seconds, min_calls=3):
+    """Median wall time of repeated fn() calls over about `seconds` (after one warm call)."""
+    import numpy as np
+    fn()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < min_calls:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
 def cpu_baseline(m, n, k, g, nbytes, seconds):
-    """Time the reference's CPU linear_q4g (quant.cpp:337-389) on the same shape."""
+    """Time the reference's CPU path (oracle/_ref: the reference's own quant.cpp,
+    AVX2 + OpenMP) — or the C restatement where that build is absent — on this
+    host's cores: the headline linear_q4g (quant.cpp:337-389) on the same shape,
+    plus bounded samples of the other configs' CPU ops (linear_q8 :136-163 at
+    config 1 and the LM head, linear_w8a8 :165-210 at configs 3 and 5a)."""
     import numpy as np
 
     import oracle
@@ -412,30 +489,52 @@ def cpu_baseline(m, n, k, g, nbytes, seconds):
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
     q, s = impl.quantize_q4g(w, g)
     s = s.astype(np.float16).astype(np.float32)      # the fp16 storage variant's scales, widened
-    impl.linear_q4g(x, q, s, g)                      # warm
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        impl.linear_q4g(x, q, s, g)
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
+    med, calls = _time_calls(lambda: impl.linear_q4g(x, q, s, g), seconds)
     # The load-time quantize of the same weight (quant.cpp:295-321, serial in
     # the reference): fp32 read once, packed codes + fp32 scales written once.
-    qtimes = []
-    q_end = time.perf_counter() + max(1.0, seconds / 5)
-    while time.perf_counter() < q_end or len(qtimes) < 3:
-        t0 = time.perf_counter()
-        impl.quantize_q4g(w, g)
-        qtimes.append(time.perf_counter() - t0)
-    qmed = float(np.median(qtimes))
+    qmed, qcalls = _time_calls(lambda: impl.quantize_q4g(w, g), max(1.0, seconds / 5))
     qbytes = n * k * 4 + n * ((k + 1) // 2) + n * ((k + g - 1) // g) * 4
+    del w, q, s
+
+    # Other configs, same algorithmic-byte / op accounting as the GPU sweep.
+    others = []
+    per = max(1.0, seconds / 4)
+
+    def q8_case(name, mm, nn, kk, xdt):
+        xx = rng.standard_normal((mm, kk), dtype=np.float32).astype(xdt).astype(np.float32)
+        ww = rng.standard_normal((nn, kk), dtype=np.float32) * np.float32(0.02)
+        qq, ss = impl.quantize_q8(ww)
+        del ww
+        t, c = _time_calls(lambda: impl.linear_q8(xx, qq, ss), per)
+        esz = 2 if xdt == np.float16 else 4
+        nb = nn * kk + 4 * nn + esz * mm * kk + esz * mm * nn
+        others.append({"op": f"linear_q8 {name} M={mm} K={kk} N={nn}", "ms": round(t * 1e3, 3),
+                       "GB/s": round(nb / t / 1e9, 3), "calls": c})
+
+    def w8a8_case(name, mm, nn, kk, bound):
+        xx = rng.standard_normal((mm, kk), dtype=np.float32).astype(np.float16).astype(np.float32)
+        ww = rng.standard_normal((nn, kk), dtype=np.float32) * np.float32(0.02)
+        qq, ss = impl.quantize_q8(ww)
+        del ww
+        t, c = _time_calls(lambda: impl.linear_w8a8(xx, qq, ss), per, min_calls=1)
+        nb = nn * kk + 4 * nn + 2 * mm * kk + 2 * mm * nn
+        e = {"op": f"linear_w8a8 {name} M={mm} K={kk} N={nn}", "ms": round(t * 1e3, 3), "calls": c,
+             "TOPS": round(2 * mm * nn * kk / t / 1e12, 4)}
+        if bound == "hbm":
+            e["GB/s"] = round(nb / t / 1e9, 3)
+        others.append(e)
+
+    q8_case("cfg1", 1, 4864, 896, np.float32)
+    q8_case("lm head cfg5b", 1, 151936, 1536, np.float16)
+    w8a8_case("gate/up cfg3", 8, 8960, 1536, "hbm")
+    w8a8_case("prefill cfg5a", 2048, 8960, 1536, "mfma")
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": impl.max_threads(),
-            "kind": kind,
-            "sample": f"{len(times)} calls of linear_q4g M={m} K={k} N={n} g={g} (median {med * 1e3:.2f} ms), "
-                      f"~{seconds:.0f}s of CPU work, same algorithmic bytes; nproc={os.cpu_count()}",
+            "kind": kind, "cpu_model": cpu_model(), "nproc": os.cpu_count(),
+            "sample": f"{calls} calls of linear_q4g M={m} K={k} N={n} g={g} (median {med * 1e3:.2f} ms), "
+                      f"~{seconds:.0f}s of CPU work, same algorithmic bytes",
             "quantize": {"op": f"quantize_q4g N={n} K={k} g={g} (load time)", "ms": round(qmed * 1e3, 3),
-                         "GB/s": round(qbytes / qmed / 1e9, 3), "calls": len(qtimes)}}
+                         "GB/s": round(qbytes / qmed / 1e9, 3), "calls": qcalls},
+            "other_configs": others}
 
 
 if __name__ == "__main__":

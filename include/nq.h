@@ -69,6 +69,16 @@ nq_status nq_quantize_q8(const float* w, int64_t out, int64_t in, int8_t* q, flo
 nq_status nq_quantize_q4g(const float* w, int64_t out, int64_t in, int64_t group, uint8_t* q,
                           void* scale, nq_dtype scale_dtype, void* stream);
 
+/* Replace the reference's dequantize_q8 (quant.cpp:110-119) and dequantize_q4g
+ * (quant.cpp:323-335), test helpers there: w[o,j] = float(q[o,j]) * scale[o] and
+ * w[o,j] = float(nib(o,j) - 8) * scale[o, j / group], one fp32 multiply per
+ * element (fp16 scales widened exactly first). w: [out, in] fp32 (the reference's
+ * output) or fp16 (that value rounded). Bit-exact with the reference for fp32. */
+nq_status nq_dequantize_q8(const int8_t* q, const float* scale, int64_t out, int64_t in, void* w,
+                           nq_dtype w_dtype, void* stream);
+nq_status nq_dequantize_q4g(const uint8_t* q, const void* scale, nq_dtype scale_dtype, int64_t group,
+                            int64_t out, int64_t in, void* w, nq_dtype w_dtype, void* stream);
+
 /* Replaces activation_quant_kernel (cuda_quant.cu:38-58) / the act-quant loop of
  * linear_w8a8 (quant.cpp:179-193): per-row a_scale = absmax/127 and int8 codes,
  * computed on the fp32 value of x (fp16 x is widened exactly first). */
@@ -194,6 +204,13 @@ nq_status nq_w8a8_acc_i32(const int8_t* xq, const int8_t* wq, int32_t* acc, int6
 nq_status nq_embedding_q8(const int8_t* codes, const float* scale, int64_t vocab, int64_t hidden,
                           const int64_t* ids, int64_t n, void* out, nq_dtype out_dtype,
                           void* stream);
+
+/* ---- measurement helper ---------------------------------------------------------
+ * No reference counterpart: one streaming read of `bytes` (16-byte aligned, a
+ * multiple of 16) with the 16-byte non-temporal loads the decode GEMVs use,
+ * for the benchmark's read-floor context. sink: >= 64 ints, written only in a
+ * case the data never produces. */
+nq_status nq_probe_read(const void* p, size_t bytes, int* sink, void* stream);
 
 #ifdef __cplusplus
 }

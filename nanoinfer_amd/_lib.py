@@ -27,6 +27,8 @@ SIGNATURES = {
     "nq_last_error": (ctypes.c_char_p, []),
     "nq_quantize_q8": (_D, [_P, _I, _I, _P, _P, _P]),
     "nq_quantize_q4g": (_D, [_P, _I, _I, _I, _P, _P, _D, _P]),
+    "nq_dequantize_q8": (_D, [_P, _P, _I, _I, _P, _D, _P]),
+    "nq_dequantize_q4g": (_D, [_P, _P, _D, _I, _I, _I, _P, _D, _P]),
     "nq_act_quant_i8": (_D, [_P, _D, _I, _I, _P, _P, _P]),
     "nq_act_quant_i8_heads": (_D, [_P, _D, _I, _I, _I, _P, _P, _P]),
     "nq_rmsnorm_quant_i8": (_D, [_P, _D, _P, ctypes.c_float, _I, _I, _P, _P, _P]),
@@ -43,6 +45,7 @@ SIGNATURES = {
     "nq_w8a8_acc_i32": (_D, [_P, _P, _P, _I, _I, _I, _P, _Z, ctypes.c_int, _P]),
     "nq_embedding_q8": (_D, [_P, _P, _I, _I, _P, _I, _P, _D, _P]),
     "nq_rope_qkv": (_D, [_P, _D, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
+    "nq_probe_read": (_D, [_P, _Z, _P, _P]),
     "nq_nit_info": (_D, [ctypes.c_char_p, _P, _P, _P, ctypes.c_int32]),
     "nq_nit_load_f32": (_D, [ctypes.c_char_p, _P, _I, _P]),
     "nq_nit_load_q8": (_D, [ctypes.c_char_p, _P, _P, _I, _I, _P]),

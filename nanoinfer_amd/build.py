@@ -23,7 +23,7 @@ HOST_TEST = os.path.join(ROOT, "tests", "cpp", "test_host.bin")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["nq_abi.cpp", "nq_quantize.hip", "nq_gemv.hip", "nq_w8a8.hip", "nq_embed.hip", "nq_fused.hip", "nq_wq_gemm.hip", "nq_nit.hip", "nq_rope.hip"]
+SOURCES = ["nq_abi.cpp", "nq_quantize.hip", "nq_gemv.hip", "nq_w8a8.hip", "nq_embed.hip", "nq_fused.hip", "nq_wq_gemm.hip", "nq_nit.hip", "nq_rope.hip", "nq_dequant.hip", "nq_probe.hip"]
 
 # -packed-fp32-ops: keep hipcc from forming v_pk_{add,mul,fma}_f32 (the host
 # pass prints that it does not know the feature; that is harmless).

@@ -105,9 +105,10 @@ struct Vec8<_Float16> {
 // ADD: the row is first h = x + r (the residual add that precedes the norm),
 // stored to h as a tensor add would, and the norm runs on h.
 template <typename XT, int CPT, int NT, bool ADD = false>
-__global__ __launch_bounds__(NT) void rmsnorm_quant_kernel(const XT* __restrict__ x, const float* __restrict__ w,
+// x and r are not __restrict__: the in-place add passes h == x.
+__global__ __launch_bounds__(NT) void rmsnorm_quant_kernel(const XT* x, const float* __restrict__ w,
                                                            float eps, int k, int8_t* __restrict__ xq,
-                                                           float* __restrict__ a_scale, const XT* __restrict__ r = nullptr,
+                                                           float* __restrict__ a_scale, const XT* r = nullptr,
                                                            XT* h = nullptr) {
     __shared__ float red[NT / 64];
     const int row = blockIdx.x, tid = threadIdx.x, steps = k >> 3;

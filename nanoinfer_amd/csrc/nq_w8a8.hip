@@ -610,8 +610,9 @@ __global__ __launch_bounds__(1024) void gemm_w8a8_skinny_kernel(
     const int steps = wave < S ? (S - wave + nw - 1) / nw : 0;
     const int rot = S > 0 ? static_cast<int>((blockIdx.x * 5u) % static_cast<unsigned>(S)) : 0;
     auto load = [&](int t, v4i (&a)[TM], v4i (&b)[TN]) {
-        // Steps past the wave's last one (the ring's tail prefetch) read as
-        // zeros without touching memory.
+        // Steps past the wave's last one (the ring's tail prefetch) and rows
+        // past m / n read as zeros without touching memory (the offset stays
+        // kOob: no arithmetic on it, so no signed overflow).
         const int st = wave + t * nw;
         int sr = st + rot;
         sr = sr >= S ? sr - S : sr;
@@ -619,10 +620,10 @@ __global__ __launch_bounds__(1024) void gemm_w8a8_skinny_kernel(
         const bool kin = st < S && kc + fk < ke;
 #pragma unroll
         for (int i = 0; i < TM; ++i)
-            a[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xrs, kin ? xo[i] + kc : kOob, 0, 0));
+            a[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xrs, kin && xo[i] != kOob ? xo[i] + kc : kOob, 0, 0));
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-            b[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wrs, kin ? wo[j] + kc : kOob, 0, 0));
+            b[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wrs, kin && wo[j] != kOob ? wo[j] + kc : kOob, 0, 0));
     };
     v4i a[PD][TM], b[PD][TN];
 #pragma unroll

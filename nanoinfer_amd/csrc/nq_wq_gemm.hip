@@ -3,8 +3,14 @@
 // (quant.cpp:136-163, :337-389; its CUDA tiled Q8 kernel cuda_quant.cu:165-204
 // is the m > 16 counterpart). Codes are converted to fp16 exactly in registers
 // and multiplied with fp16 activations by v_mfma_f32_16x16x32_f16 (fp32
-// accumulation); fp32 activations are split into an fp16 high part and an fp16
-// remainder, two MFMAs, so they keep ~22 bits.
+// accumulation). fp32 activations take the bf16 matrix cores instead: each value
+// is split exactly into three bf16 parts (the top 8 significant bits by
+// truncation, the next 8 the same way, and the remainder, which has at most 8
+// bits left), the codes become bf16 exactly, and three
+// v_mfma_f32_16x16x32_bf16 multiply them. bf16 has fp32's exponent range, so
+// every finite fp32 activation with |x| >= 2^-110 (all three parts normal) is
+// represented exactly and each product is exact in fp32: no overflow above
+// 65504 and no precision lost to fp16 subnormals.
 //
 // Operands: A = activations (16 rows of m), B = weights (16 rows of n), so a
 // lane's four results share one weight row (n = lane % 16) and that row's scale.
@@ -32,6 +38,16 @@ namespace nq {
 namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ unsigned f32_bits(float f) { return __builtin_bit_cast(unsigned, f); }
+// Eight fp32 values whose low 16 bits are zero (each exactly a bf16) as eight bf16.
+__device__ __forceinline__ b8 pack_bf16(const float (&f)[8]) {
+    v4i r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = static_cast<int>(__builtin_amdgcn_perm(f32_bits(f[2 * i + 1]), f32_bits(f[2 * i]), 0x07060302u));
+    return __builtin_bit_cast(b8, r);
+}
 constexpr int kWqRing = 4, kOob = 0x7FFFFFF0;
 
 template <int N>
@@ -44,7 +60,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 template <int TM>
 constexpr int wq_waves() { return TM == 1 ? 16 : 8; }
 
-// Activation fragment of one chunk: 8 values of one row, as fp16 pairs (c, c+4).
+// Activation fragment of one chunk: 8 values of one row.
 template <typename XT>
 struct XFrag;
 template <>
@@ -53,14 +69,16 @@ struct XFrag<_Float16> {
     __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, int off) {
         raw = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
     }
-    __device__ __forceinline__ void operands(h8& hi, h8& lo) const {
+    // The 8 halves as pairs (c, c+4), the order the int4 nibble trick gives the codes.
+    __device__ __forceinline__ h8 operands() const {
         const h8 v = __builtin_bit_cast(h8, raw);
+        h8 hi;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             hi[2 * j] = v[j];
             hi[2 * j + 1] = v[j + 4];
         }
-        lo = h8{};
+        return hi;
     }
 };
 template <>
@@ -70,17 +88,25 @@ struct XFrag<float> {
         a = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
         b = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, off == kOob ? kOob : off + 16, 0, 0));
     }
-    __device__ __forceinline__ void operands(h8& hi, h8& lo) const {
+    // Exact split v = hi + mid + lo of the 8 values in column order: hi and mid
+    // truncate to 8 significant bits, so v - hi and (v - hi) - mid are exact and
+    // the remainder fits a bf16. A non-finite v keeps its value in hi and zero
+    // in the other parts (inf - inf would make them NaN).
+    __device__ __forceinline__ void split3(b8& hi, b8& mid, b8& lo) const {
         const f4 fa = __builtin_bit_cast(f4, a), fb = __builtin_bit_cast(f4, b);
+        float h[8], md[8], l[8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float v0 = fa[j], v1 = fb[j];  // columns j and j + 4
-            const _Float16 h0 = static_cast<_Float16>(v0), h1 = static_cast<_Float16>(v1);
-            hi[2 * j] = h0;
-            hi[2 * j + 1] = h1;
-            lo[2 * j] = static_cast<_Float16>(v0 - static_cast<float>(h0));
-            lo[2 * j + 1] = static_cast<_Float16>(v1 - static_cast<float>(h1));
+        for (int e = 0; e < 8; ++e) {
+            const float v = e < 4 ? fa[e] : fb[e - 4];
+            h[e] = __builtin_bit_cast(float, f32_bits(v) & 0xFFFF0000u);
+            float r1 = v - h[e];
+            r1 = r1 == r1 ? r1 : 0.0f;
+            md[e] = __builtin_bit_cast(float, f32_bits(r1) & 0xFFFF0000u);
+            l[e] = r1 - md[e];
         }
+        hi = pack_bf16(h);
+        mid = pack_bf16(md);
+        lo = pack_bf16(l);
     }
 };
 
@@ -104,6 +130,14 @@ struct WFrag<true> {  // 8 nibbles = one dword, nibble e = column e
             r[2 * j + 1] = p[1];
         }
         return r;
+    }
+    // The 8 codes in column order as bf16 (nib - 8 is exact).
+    __device__ __forceinline__ b8 codes_bf16() const {
+        const unsigned u = static_cast<unsigned>(w);
+        float f[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = static_cast<float>((u >> (4 * e)) & 0xFu) - 8.0f;
+        return pack_bf16(f);
     }
 };
 template <>
@@ -129,6 +163,17 @@ struct WFrag<false> {  // 8 int8 codes = two dwords, byte t of dword d = column 
             r[2 * t + 1] = p[1];
         }
         return r;
+    }
+    // The 8 codes in column order as bf16: byte + 128 as a float, minus 128 (exact).
+    __device__ __forceinline__ b8 codes_bf16() const {
+        const unsigned u0 = static_cast<unsigned>(w0) ^ 0x80808080u, u1 = static_cast<unsigned>(w1) ^ 0x80808080u;
+        float f[8];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            f[t] = static_cast<float>((u0 >> (8 * t)) & 0xFFu) - 128.0f;
+            f[4 + t] = static_cast<float>((u1 >> (8 * t)) & 0xFFu) - 128.0f;
+        }
+        return pack_bf16(f);
     }
 };
 
@@ -198,27 +243,49 @@ __global__ __launch_bounds__(wq_waves<TM>() * 64) void gemm_wq_kernel(
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f4{0, 0, 0, 0};
     auto compute = [&](const Stage& st) {
-        h8 b[TN];
+        if constexpr (sizeof(XT) == 4) {  // fp32 x: three bf16 MFMAs per chunk
+            b8 b[TN];
 #pragma unroll
-        for (int j = 0; j < TN; ++j) b[j] = st.wf[j].codes();
+            for (int j = 0; j < TN; ++j) b[j] = st.wf[j].codes_bf16();
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            h8 hi, lo;
-            st.xf[i].operands(hi, lo);
+            for (int i = 0; i < TM; ++i) {
+                b8 hi, mid, lo;
+                st.xf[i].split3(hi, mid, lo);
 #pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                if constexpr (Q4) {
-                    f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi, b[j], f4{0, 0, 0, 0}, 0, 0, 0);
-                    if constexpr (sizeof(XT) == 4) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(lo, b[j], d, 0, 0, 0);
+                for (int j = 0; j < TN; ++j) {
+                    const f4 c0 = Q4 ? f4{0, 0, 0, 0} : acc[i][j];
+                    f4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b[j], c0, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mid, b[j], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b[j], d, 0, 0, 0);
+                    if constexpr (Q4) {
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(d[v], st.s[j], acc[i][j][v]);
-                } else {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi, b[j], acc[i][j], 0, 0, 0);
-                    if constexpr (sizeof(XT) == 4) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(lo, b[j], acc[i][j], 0, 0, 0);
+                        for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(d[v], st.s[j], acc[i][j][v]);
+                    } else {
+                        acc[i][j] = d;
+                    }
+                }
+            }
+        } else {
+            h8 b[TN];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) b[j] = st.wf[j].codes();
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const h8 hi = st.xf[i].operands();
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    if constexpr (Q4) {
+                        const f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi, b[j], f4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(d[v], st.s[j], acc[i][j][v]);
+                    } else {
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi, b[j], acc[i][j], 0, 0, 0);
+                    }
                 }
             }
         }
     };
+
     Stage ring[kWqRing];
 #pragma unroll
     for (int p = 0; p < kWqRing; ++p) load(p, ring[p]);
@@ -344,7 +411,7 @@ __global__ __launch_bounds__(4 * WN * 64) void gemm_wq_wide_kernel(
     int gsh_rt) {
     using S = WqWideShape<Q4, SK, FM, FN, GSH, YT, ST, XT, WN>;
     constexpr int NW = S::kNW;
-    constexpr bool F32X = sizeof(XT) == 4;  // fp32 activations: fp16 high part + fp16 remainder, two MFMAs
+    constexpr bool F32X = sizeof(XT) == 4;  // fp32 activations: three bf16 parts, three bf16 MFMAs
     constexpr int BM = S::kBM, BN = S::kBN, D = S::kD, Q = S::kQ, QS = S::kQS, XB = S::kXB, NB = S::kNB;
     constexpr int T = S::kT, XROW = S::kXRow, WROW = S::kWRow, XC = S::kXC, WC = S::kWC;
     // group = 32 << gsh columns; GSH = kGBig stands for every group of at
@@ -444,7 +511,9 @@ __global__ __launch_bounds__(4 * WN * 64) void gemm_wq_wide_kernel(
         f4 part[FN][FM];
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            h8 xa[FM], xl[FM], wb[FN];
+            // fp16 x: one fp16 MFMA per fragment pair; fp32 x: three bf16 ones.
+            using XOp = std::conditional_t<F32X, b8, h8>;
+            XOp xa[FM], xm[FM], xl[FM], wb[FN];
 #pragma unroll
             for (int j = 0; j < FM; ++j) {
                 const int r = fxo[j];
@@ -453,12 +522,12 @@ __global__ __launch_bounds__(4 * WN * 64) void gemm_wq_wide_kernel(
                     XFrag<float> f;
                     f.a = *reinterpret_cast<const v4i*>(base + S::kXOff + r * XROW + ((c ^ wq_swz<XC>(r)) << 4));
                     f.b = *reinterpret_cast<const v4i*>(base + S::kXOff + r * XROW + (((c + 1) ^ wq_swz<XC>(r)) << 4));
-                    f.operands(xa[j], xl[j]);
+                    f.split3(xa[j], xm[j], xl[j]);
                 } else {  // 8 halves = chunk 4t + fq
                     const int c = t * 4 + fq;
                     XFrag<_Float16> f;
                     f.raw = *reinterpret_cast<const v4i*>(base + S::kXOff + r * XROW + ((c ^ wq_swz<XC>(r)) << 4));
-                    f.operands(xa[j], xl[j]);
+                    xa[j] = f.operands();
                 }
             }
 #pragma unroll
@@ -467,7 +536,8 @@ __global__ __launch_bounds__(4 * WN * 64) void gemm_wq_wide_kernel(
                 if constexpr (Q4) {  // 8 codes = one dword: chunk t, dword fq
                     WFrag<true> f;
                     f.w = *reinterpret_cast<const int*>(base + S::kWOff + r * WROW + ((t ^ wq_swz<WC>(r)) << 4) + fq * 4);
-                    wb[i] = f.codes();
+                    if constexpr (F32X) wb[i] = f.codes_bf16();
+                    else wb[i] = f.codes();
                 } else {  // 8 codes = two dwords: chunk 2t + fq / 2, half fq % 2
                     typedef int v2i __attribute__((ext_vector_type(2)));
                     const int c = t * 2 + (fq >> 1);
@@ -475,20 +545,24 @@ __global__ __launch_bounds__(4 * WN * 64) void gemm_wq_wide_kernel(
                     WFrag<false> f;
                     f.w0 = v[0];
                     f.w1 = v[1];
-                    wb[i] = f.codes();
+                    if constexpr (F32X) wb[i] = f.codes_bf16();
+                    else wb[i] = f.codes();
                 }
             }
+            auto mma = [&](const XOp& a, const XOp& b, const f4& c) {
+                if constexpr (F32X) return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+                else return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+            };
 #pragma unroll
             for (int i = 0; i < FN; ++i)
 #pragma unroll
                 for (int j = 0; j < FM; ++j) {
-                    if constexpr (Q4) {
-                        const f4 z = t % S::kCPG == 0 ? f4{0, 0, 0, 0} : part[i][j];
-                        part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], wb[i], z, 0, 0, 0);
-                        if constexpr (F32X) part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[j], wb[i], part[i][j], 0, 0, 0);
-                    } else {
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], wb[i], acc[i][j], 0, 0, 0);
-                        if constexpr (F32X) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[j], wb[i], acc[i][j], 0, 0, 0);
+                    f4& d = Q4 ? part[i][j] : acc[i][j];
+                    const f4 c0 = Q4 && t % S::kCPG == 0 ? f4{0, 0, 0, 0} : d;
+                    d = mma(xa[j], wb[i], c0);
+                    if constexpr (F32X) {
+                        d = mma(xm[j], wb[i], d);
+                        d = mma(xl[j], wb[i], d);
                     }
                 }
             if constexpr (Q4) {

@@ -404,9 +404,22 @@ def embedding_q8(table: QTensor, ids, out_dtype=torch.float32) -> torch.Tensor:
     return out
 
 
-def dequantize_q8(w: QTensor) -> torch.Tensor:
-    """quant.cpp:110-119: the gather of every row is the dequantized table."""
-    return embedding_q8(w, range(w.out))
+def dequantize_q8(w: QTensor, out_dtype=torch.float32) -> torch.Tensor:
+    """quant.cpp:110-119: w[o, j] = float(q[o, j]) * scale[o] (nq_dequantize_q8)."""
+    w.check()
+    y = torch.empty((w.out, w.in_), dtype=out_dtype, device=w.q.device)
+    check(_lib.load().nq_dequantize_q8(_ptr(w.q), _ptr(w.scale), w.out, w.in_, _ptr(y),
+                                       _dtype_code(y, "out"), _stream()))
+    return y
+
+
+def dequantize_q4g(w: Q4GTensor, out_dtype=torch.float32) -> torch.Tensor:
+    """quant.cpp:323-335: w[o, j] = float(nib - 8) * scale[o, j / group] (nq_dequantize_q4g)."""
+    w.check()
+    y = torch.empty((w.out, w.in_), dtype=out_dtype, device=w.q.device)
+    check(_lib.load().nq_dequantize_q4g(_ptr(w.q), _ptr(w.scale), _dtype_code(w.scale, "scale"), w.group,
+                                        w.out, w.in_, _ptr(y), _dtype_code(y, "out"), _stream()))
+    return y
 
 
 # ---- Weight / factory (quant.hpp:120-141, backend.hpp:109-114) -------------------------

@@ -239,3 +239,68 @@ def reference() -> CpuQuant | None:
             return None
         _cache["reference"] = CpuQuant(REF_SO, "nqr_", "reference")
     return _cache["reference"]
+
+
+class RefOps:
+    """The reference's own ops.cpp functions (rmsnorm, RoPE, attention, silu)
+    from the reference build, used only by tests/golden/gen_golden.py to write
+    the fixtures that pin tests/model_ref.py's numpy restatements."""
+
+    def __init__(self, path: str):
+        L = ctypes.CDLL(path)
+        F = ctypes.c_float
+        sig = {
+            "nqr_rmsnorm": [_P, _I, _I, _P, F, _P],
+            "nqr_rope_cache": [_I, _I, F, _P, _P],
+            "nqr_apply_rope": [_P, _I, _I, _I, _P, _P, _I, _I, _P],
+            "nqr_attention": [_P, _P, _P, _I, _I, _I, _I, ctypes.c_int, _I, _P],
+            "nqr_silu": [_P, _I, _P],
+        }
+        self._f = {}
+        for name, args in sig.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = ctypes.c_int
+            self._f[name] = f
+
+    def _call(self, name, *args):
+        if self._f[name](*args) != 0:
+            raise OracleError(f"reference.{name}: invalid argument")
+
+    def rmsnorm(self, x, w, eps):
+        x, w = _f32(x), _f32(w)
+        y = np.empty_like(x)
+        self._call("nqr_rmsnorm", _ptr(x), x.shape[0], x.shape[1], _ptr(w), float(eps), _ptr(y))
+        return y
+
+    def rope_cache(self, seq, head_dim, theta):
+        c = np.empty((seq, head_dim), np.float32)
+        s = np.empty((seq, head_dim), np.float32)
+        self._call("nqr_rope_cache", seq, head_dim, float(theta), _ptr(c), _ptr(s))
+        return c, s
+
+    def apply_rope(self, x, cos, sin, pos_offset=0):
+        x, cos, sin = _f32(x), _f32(cos), _f32(sin)
+        y = np.empty_like(x)
+        self._call("nqr_apply_rope", _ptr(x), *x.shape, _ptr(cos), _ptr(sin), cos.shape[0], pos_offset, _ptr(y))
+        return y
+
+    def attention(self, q, k, v, causal=True, query_offset=0):
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        y = np.empty_like(q)
+        self._call("nqr_attention", _ptr(q), _ptr(k), _ptr(v), q.shape[0], q.shape[1], k.shape[1], q.shape[2],
+                   int(causal), query_offset, _ptr(y))
+        return y
+
+    def silu(self, x):
+        x = _f32(x)
+        y = np.empty_like(x)
+        self._call("nqr_silu", _ptr(x), x.size, _ptr(y))
+        return y
+
+
+def reference_ops() -> RefOps | None:
+    """ops.cpp from the reference build, or None where it was not built."""
+    if not os.path.exists(REF_SO):
+        return None
+    return RefOps(REF_SO)

@@ -173,4 +173,42 @@ int nqr_linear_f32(const float* x, int64_t m, const float* w, int64_t out, int64
     })
 }
 
+// ---- ops.cpp functions the greedy-token reference decoder restates ---------
+// (tests/model_ref.py): rmsnorm ops.cpp:272-290, build_rope_cache / apply_rope
+// :120-166, attention :206-270, silu :86-92. Exported so that fixtures written
+// from the reference's own build pin those numpy restatements.
+static Tensor host3d(const float* p, int64_t a, int64_t b, int64_t c) {
+    Tensor t({a, b, c});
+    if (a * b * c) std::memcpy(t.data(), p, sizeof(float) * size_t(a * b * c));
+    return t;
+}
+
+int nqr_rmsnorm(const float* x, int64_t rows, int64_t d, const float* w, float eps, float* y) {
+    NQR_TRY(out2d(ni::rmsnorm(host2d(x, rows, d), host1d(w, d), eps), y))
+}
+
+int nqr_rope_cache(int64_t seq, int64_t head_dim, float theta, float* cos, float* sin) {
+    NQR_TRY({
+        ni::RopeCache c = ni::build_rope_cache(seq, head_dim, theta);
+        out2d(c.cos, cos);
+        out2d(c.sin, sin);
+    })
+}
+
+int nqr_apply_rope(const float* x, int64_t heads, int64_t seq, int64_t dim, const float* cos,
+                   const float* sin, int64_t table_len, int64_t pos_offset, float* y) {
+    NQR_TRY(out2d(ni::apply_rope(host3d(x, heads, seq, dim), host2d(cos, table_len, dim),
+                                 host2d(sin, table_len, dim), pos_offset),
+                  y))
+}
+
+int nqr_attention(const float* q, const float* k, const float* v, int64_t heads, int64_t sq,
+                  int64_t sk, int64_t dim, int causal, int64_t query_offset, float* y) {
+    NQR_TRY(out2d(ni::attention(host3d(q, heads, sq, dim), host3d(k, heads, sk, dim),
+                                host3d(v, heads, sk, dim), causal != 0, query_offset),
+                  y))
+}
+
+int nqr_silu(const float* x, int64_t n, float* y) { NQR_TRY(out2d(ni::silu(host1d(x, n)), y)) }
+
 }  // extern "C"

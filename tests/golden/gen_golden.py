@@ -11,6 +11,7 @@ zero rows, clamps, odd widths, partial groups, both Q4 m-paths) plus seeded
 random cases at small versions of the benchmark shapes and non-finite inputs.
 
 Usage:  python tests/golden/gen_golden.py     (rewrites tests/golden/*.npz)
+        python tests/golden/gen_golden.py --ops-only   (only ops.npz)
 """
 import os
 import sys
@@ -139,5 +140,65 @@ def main():
     print("golden fixtures written to", OUT)
 
 
+def ops_fixtures():
+    """ops.cpp fixtures for tests/model_ref.py (rmsnorm :272-290, build_rope_cache /
+    apply_rope :120-166, attention :206-270, silu :86-92) and for the oracle's
+    linear_f32 (ops.cpp:42-69), written from the reference build."""
+    oracle.build(ref=True)
+    ref, ops = oracle.reference(), oracle.reference_ops()
+    assert ref is not None and ops is not None, "reference build missing"
+    rng = np.random.default_rng(20261202)
+    o = {}
+    for i, (rows, d, eps) in enumerate([(2, 1536, 1e-6), (3, 256, 1e-5), (2, 7, 1e-6)]):
+        x = rng.normal(0, 1, (rows, d)).astype(np.float32)
+        if i == 1:
+            x[1] = 0.0                                       # zero row: scale = 1/sqrt(eps)
+        w = (1 + rng.normal(0, 0.02, d)).astype(np.float32)
+        o[f"rms{i}_x"], o[f"rms{i}_w"], o[f"rms{i}_eps"] = x, w, np.float32(eps)
+        o[f"rms{i}_y"] = ops.rmsnorm(x, w, eps)
+    for i, (seq, dim, theta) in enumerate([(40, 128, 1e6), (32, 64, 1e4)]):
+        c, s = ops.rope_cache(seq, dim, theta)
+        o[f"ropec{i}_seq"], o[f"ropec{i}_dim"], o[f"ropec{i}_theta"] = np.int64(seq), np.int64(dim), np.float32(theta)
+        o[f"ropec{i}_cos"], o[f"ropec{i}_sin"] = c, s
+        x = rng.normal(0, 1, (2, 16, dim)).astype(np.float32)
+        o[f"rope{i}_x"] = x
+        for off in (0, 9):
+            o[f"rope{i}_{off}_y"] = ops.apply_rope(x, c, s, off)
+    for i, (h, sq, sk, d, causal) in enumerate([(2, 21, 21, 64, True), (2, 5, 19, 64, True), (3, 4, 17, 32, False),
+                                                 (1, 1, 1, 16, True)]):
+        q = rng.normal(0, 1, (h, sq, d)).astype(np.float32)
+        k = rng.normal(0, 1, (h, sk, d)).astype(np.float32)
+        v = rng.normal(0, 1, (h, sk, d)).astype(np.float32)
+        off = sk - sq if causal else 0
+        for key, val in dict(q=q, k=k, v=v, causal=np.int64(causal), off=np.int64(off),
+                             y=ops.attention(q, k, v, causal, off)).items():
+            o[f"attn{i}_{key}"] = val
+    g = np.concatenate([rng.normal(0, 4, 2000), [0.0, -0.0, 1e-30, -90.0, 90.0, 88.7, -88.7]]).astype(np.float32)
+    o["silu_x"], o["silu_y"] = g, ops.silu(g)
+    for i, (m, n, k, bias) in enumerate([(1, 24, 896, False), (3, 17, 40, True), (4, 9, 1536, True)]):
+        x = rng.normal(0, 1, (m, k)).astype(np.float32)
+        w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+        b = rng.normal(0, 1, n).astype(np.float32) if bias else None
+        o[f"lin{i}_x"], o[f"lin{i}_w"] = x, w
+        if b is not None:
+            o[f"lin{i}_b"] = b
+        o[f"lin{i}_y"] = ref.linear_f32(x, w, b)
+    # dequantize_q8 / dequantize_q4g (quant.cpp:110-119, 323-335) of reference-quantized weights
+    for i, (n, k) in enumerate([(5, 24), (3, 37)]):
+        w = rng.normal(0, 0.05, (n, k)).astype(np.float32)
+        q, s = ref.quantize_q8(w)
+        o[f"dq8_{i}_q"], o[f"dq8_{i}_s"], o[f"dq8_{i}_w"] = q, s, ref.dequantize_q8(q, s)
+    for i, (n, k, g) in enumerate([(4, 64, 32), (3, 37, 5), (2, 40, 16)]):
+        w = rng.normal(0, 0.05, (n, k)).astype(np.float32)
+        q, s = ref.quantize_q4g(w, g)
+        q[0, 0] = 0x0F if k > 1 else q[0, 0]             # nibbles 15 and 0: codes +7 and -8
+        o[f"dq4_{i}_q"], o[f"dq4_{i}_s"], o[f"dq4_{i}_g"] = q, s, np.int64(g)
+        o[f"dq4_{i}_k"], o[f"dq4_{i}_w"] = np.int64(k), ref.dequantize_q4g(q, s, k, g)
+    np.savez_compressed(os.path.join(OUT, "ops.npz"), **o)
+    print("ops fixtures written to", OUT)
+
+
 if __name__ == "__main__":
-    main()
+    if "--ops-only" not in sys.argv:
+        main()
+    ops_fixtures()

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_util import assert_close_rms, host, to_dev
+from gpu_util import assert_close_rms, host, rms, to_dev
 from test_oracle import same_bits
 
 pytestmark = pytest.mark.gpu
@@ -168,7 +168,7 @@ WQ_GEMM_CASES = [  # m > 8: the fp16 MFMA GEMM (m >= 16 or n >= 4096) or GEMV sl
     ("q8", 9, 896, 896, 0, True, F16, F16, F16),       # GEMV slices 8 + 1
     ("q8", 9, 4608, 896, 0, True, F16, F16, F16),      # GEMM, tall weight
     ("q4g", 12, 4104, 512, 32, False, F32, F16, F32),  # GEMM, ragged last tile
-    ("q8", 64, 4864, 896, 0, False, F32, F32, F32),    # fp32 x: hi/lo split
+    ("q8", 64, 4864, 896, 0, False, F32, F32, F32),    # fp32 x: exact three-part bf16 split
     ("q8", 300, 1536, 1536, 0, True, F16, F32, F16),   # several 64-row blocks
     ("q8", 33, 8960, 1536, 0, False, F16, F32, F16),   # 32 rows per workgroup
     ("q4g", 16, 1536, 8960, 32, False, F16, F16, F16),
@@ -184,7 +184,7 @@ WQ_GEMM_CASES = [  # m > 8: the fp16 MFMA GEMM (m >= 16 or n >= 4096) or GEMV sl
     ("q8", 257, 2900, 1024, 0, True, F16, F32, F32),
     ("q4g", 1100, 640, 512, 32, True, F16, F16, F16),
     ("q4g", 40, 8960, 1536, 64, True, F16, F16, F16),    # m >= 32 with >= 128 tiles
-    # fp32 x on the wide tiles: fp16 high part + remainder, 64-column slabs
+    # fp32 x on the wide tiles: three exact bf16 parts, 64-column slabs
     ("q8", 300, 1536, 1536, 0, True, F32, F32, F32),
     ("q4g", 200, 2000, 1024, 32, False, F32, F16, F16),
     ("q4g", 130, 9000, 512, 32, True, F32, F32, F32),
@@ -254,6 +254,37 @@ def test_weight_only_gemm_batched(dev, nq, orc, mode, m, n, k, g, bias, xdt, sdt
         y = nq.linear_q4g(xd, t, bd, out_dtype=ydt)
         ref = orc.linear_q4g(xo, host(t.q), host(t.scale.float()), g, b)
     assert_close_rms(host(y.float()), ref, f"{mode} gemm {m}x{n}x{k}", fp16_out=(ydt == F16))
+
+
+# fp32 activations far outside fp16's range and deep in its subnormals, on both
+# weight-only MFMA kernels (16-row tiles: k % 128 != 0 or small m; wide tiles:
+# m > 128, k % 128 == 0): the exact bf16 split keeps every row at the accuracy of
+# an fp32 dot product, so each row is held to 1e-5 of its own RMS.
+@pytest.mark.parametrize("mode,m,n,k,g", [("q8", 24, 4864, 896, 0), ("q4g", 40, 1536, 960, 32),
+                                          ("q8", 300, 1536, 1536, 0), ("q4g", 200, 2000, 1024, 32)])
+def test_weight_only_fp32_x_extreme_range(dev, nq, orc, mode, m, n, k, g):
+    rng = np.random.default_rng(m + n + k)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    x[0::4] *= 1e5            # |x| up to ~5e5 > 65504
+    x[1::4] *= 1e-6           # fp16 subnormal range
+    x[2::4, 7] = 3e5          # one large outlier among ordinary values
+    x[3::4] *= np.float32(2.0 ** -100)
+    w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    xd = to_dev(x, dev)
+    if mode == "q8":
+        t = nq.quantize_q8(to_dev(w, dev))
+        y = host(nq.linear_q8(xd, t, out_dtype=F32))
+        q, s = orc.quantize_q8(w)
+        ref = orc.linear_q8(x, q, s)
+    else:
+        t = nq.quantize_q4g(to_dev(w, dev), g)
+        y = host(nq.linear_q4g(xd, t, out_dtype=F32))
+        ref = orc.linear_q4g(x, host(t.q), host(t.scale), g)
+    assert np.isfinite(y).all()
+    for r in range(m):
+        rr = rms(ref[r])
+        err = np.abs(y[r].astype(np.float64) - ref[r]).max()
+        assert err <= 1e-5 * rr, (mode, r, err, rr)
 
 
 def test_linear_q4g_golden(dev, nq, golden):
@@ -436,6 +467,9 @@ def test_w8a8_split_workspace_too_small(dev, nq, m, n, k):
                                    (1537, 9000, 64),
                                    # 128-row wide tiles (m = 512 class), ragged m and n, n odd
                                    (512, 17920, 192), (400, 15000, 64), (450, 16001, 64),
+                                   # config 4 gate|up at its real k (12 slabs through the 3-slot ring),
+                                   # and ragged m and n on the same plan
+                                   (512, 17920, 1536), (500, 17917, 1536),
                                    # k % 64 != 0: the skinny kernel over 64-row blocks in one launch,
                                    # with split K and its partial planes for the long k
                                    (200, 1000, 528), (130, 512, 6160)])

@@ -127,3 +127,47 @@ def test_act_quant_ties_and_extremes(dev, nq, orc):
     assert same_bits(host(xq), q_ref) and same_bits(host(s), s_ref)
     t = nq.quantize_q8(to_dev(x, dev))
     assert same_bits(host(t.q), q_ref) and same_bits(host(t.scale), s_ref)
+
+
+# ---- dequantize (quant.cpp:110-119, 323-335) ------------------------------------------
+def test_dequantize_golden(dev, nq, golden):
+    g = golden("ops")
+    for i in range(2):
+        q, s = g[f"dq8_{i}_q"], g[f"dq8_{i}_s"]
+        t = nq.QTensor(to_dev(q, dev), to_dev(s, dev), *q.shape)
+        assert same_bits(host(nq.dequantize_q8(t)), g[f"dq8_{i}_w"]), i
+    for i in range(3):
+        q, s, k, gr = g[f"dq4_{i}_q"], g[f"dq4_{i}_s"], int(g[f"dq4_{i}_k"]), int(g[f"dq4_{i}_g"])
+        t = nq.Q4GTensor(to_dev(q, dev), to_dev(s, dev), q.shape[0], k, gr)
+        assert same_bits(host(nq.dequantize_q4g(t)), g[f"dq4_{i}_w"]), i
+
+
+@pytest.mark.parametrize("shape", [(4864, 896), (151936, 1536), (7, 90), (3, 0), (0, 5)])
+def test_dequantize_q8_full(dev, nq, orc, shape):
+    rng = np.random.default_rng(shape[0] + 3 * shape[1])
+    w = rng.normal(0, 0.02, shape).astype(np.float32)
+    t = nq.quantize_q8(to_dev(w, dev))
+    q, s = host(t.q), host(t.scale)
+    ref = orc.dequantize_q8(q, s)
+    assert same_bits(host(nq.dequantize_q8(t)), ref)
+    h = host(nq.dequantize_q8(t, torch.float16))
+    assert same_bits(h, ref.astype(np.float16))
+
+
+@pytest.mark.parametrize("shape,group", [((1536, 8960), 32), ((33, 137), 32), ((17, 45), 5), ((9, 1024), 3),
+                                         ((5, 96), 96), ((4, 64), 200)])
+def test_dequantize_q4g_full(dev, nq, orc, shape, group):
+    rng = np.random.default_rng(shape[0] * 5 + shape[1])
+    w = rng.normal(0, 0.02, shape).astype(np.float32)
+    q = rng.integers(0, 256, (shape[0], (shape[1] + 1) // 2), dtype=np.uint8)   # all 16 nibbles
+    nb = (shape[1] + group - 1) // group
+    s = np.abs(rng.normal(0, 0.01, (shape[0], nb))).astype(np.float32)
+    t = nq.Q4GTensor(to_dev(q, dev), to_dev(s, dev), shape[0], shape[1], group)
+    ref = orc.dequantize_q4g(q, s, shape[1], group)
+    assert same_bits(host(nq.dequantize_q4g(t)), ref)
+    # fp16 scale storage: the oracle on the widened fp16 scales
+    s16 = s.astype(np.float16)
+    t16 = nq.Q4GTensor(to_dev(q, dev), to_dev(s16, dev), shape[0], shape[1], group)
+    ref16 = orc.dequantize_q4g(q, s16.astype(np.float32), shape[1], group)
+    assert same_bits(host(nq.dequantize_q4g(t16)), ref16)
+    assert same_bits(host(nq.dequantize_q4g(t16, torch.float16)), ref16.astype(np.float16))

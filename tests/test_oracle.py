@@ -233,3 +233,33 @@ def test_reference_build_matches_when_present(orc):
     assert same_bits(orc.linear_w8a8(x, q, s), ref.linear_w8a8(x, q, s))
     p, t = orc.quantize_q4g(w, 40)
     assert same_bits(orc.linear_q4g(x, p, t, 40), ref.linear_q4g(x, p, t, 40))
+
+
+# ---- linear_f32 (ops.cpp:42-69, the dequant-matmul reference of test_quant.cpp) ----------
+def test_linear_f32_golden(orc, golden):
+    g = golden("ops")
+    for i in range(3):
+        b = g[f"lin{i}_b"] if f"lin{i}_b" in g.files else None
+        y = orc.linear_f32(g[f"lin{i}_x"], g[f"lin{i}_w"], b)
+        assert same_bits(y, g[f"lin{i}_y"]), i
+
+
+def test_linear_f32_closed_form(orc):
+    rng = np.random.default_rng(5)
+    x = rng.normal(0, 1, (5, 77)).astype(np.float32)
+    w = rng.normal(0, 1, (9, 77)).astype(np.float32)
+    b = rng.normal(0, 1, 9).astype(np.float32)
+    y = orc.linear_f32(x, w, b)
+    ref = x.astype(np.float64) @ w.astype(np.float64).T + b
+    assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
+    # a transposed operand or a dropped bias fails this
+    assert not np.allclose(orc.linear_f32(x, w), ref, atol=1e-3)
+
+
+def test_dequantize_golden(orc, golden):
+    g = golden("ops")
+    for i in range(2):
+        assert same_bits(orc.dequantize_q8(g[f"dq8_{i}_q"], g[f"dq8_{i}_s"]), g[f"dq8_{i}_w"]), i
+    for i in range(3):
+        w = orc.dequantize_q4g(g[f"dq4_{i}_q"], g[f"dq4_{i}_s"], int(g[f"dq4_{i}_k"]), int(g[f"dq4_{i}_g"]))
+        assert same_bits(w, g[f"dq4_{i}_w"]), i
