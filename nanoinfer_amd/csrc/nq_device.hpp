@@ -87,17 +87,62 @@ __device__ __forceinline__ int dpp(int v) {
     return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
 }
 
-// Full wave64 sum, result in every lane. The in-row steps use DPP; the two
-// cross-row steps use ds_swizzle-free bpermutes. Integer adds are exact, so the
-// int32 variant is order-independent; the float variant fixes one order.
+// Cross-row exchanges without the LDS unit (gfx950 v_permlane{16,32}_swap):
+// swap_sum16(a, b) returns, in every lane, its own row pair's combination: in
+// rows 0 and 2 (lane bit 4 clear) a + (the partner row's a), in rows 1 and 3
+// b + (the partner row's b)... precisely: the instruction swaps the odd rows of
+// a with the even rows of b, so r[0] + r[1] is a_even + a_odd' in even rows and
+// b_even' + b_odd in odd rows, where ' marks the partner lane (lane ^ 16).
+// With a == b this is the pair sum v_even + v_odd, bit-identical in both lanes.
+// swap_sum32 is the same for lane ^ 32 (lower and upper half of the wave).
+//
+// row_swap returns the two swapped registers as (first, second). Each element
+// of the builtin's vector result is copied into a named unsigned before any
+// other use: read as __builtin_bit_cast(T, r[1]), this toolchain's front end
+// extracted element 0 for both (r[0] + r[1] became 2 * r[0]).
+struct SwapPair {
+    unsigned first, second;
+};
+template <int O>
+__device__ __forceinline__ SwapPair row_swap(unsigned a, unsigned b) {
+    static_assert(O == 16 || O == 32, "row swaps");
+    if constexpr (O == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+        const unsigned r0 = r[0], r1 = r[1];
+        return SwapPair{r0, r1};
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+        const unsigned r0 = r[0], r1 = r[1];
+        return SwapPair{r0, r1};
+    }
+}
+template <int O, typename T>
+__device__ __forceinline__ T swap_sum(T a, T b) {
+    const SwapPair r = row_swap<O>(__builtin_bit_cast(unsigned, a), __builtin_bit_cast(unsigned, b));
+    return __builtin_bit_cast(T, r.first) + __builtin_bit_cast(T, r.second);
+}
+template <typename T>
+__device__ __forceinline__ T swap_sum16(T a, T b) { return swap_sum<16>(a, b); }
+template <typename T>
+__device__ __forceinline__ T swap_sum32(T a, T b) { return swap_sum<32>(a, b); }
+// The partner of a lane in the other row half (lane ^ 16) or wave half (lane ^ 32).
+template <int O>
+__device__ __forceinline__ unsigned swap_partner(unsigned v, int lane) {
+    const SwapPair r = row_swap<O>(v, v);
+    return (lane & O) ? r.first : r.second;
+}
+
+// Full wave64 sum, result in every lane, all VALU (no LDS round trips): DPP
+// inside each 16-lane row, then the two row swaps. Each step adds two values
+// that are identical across the lanes that combine them, so every lane ends
+// with the same bits. Integer adds are exact; the float variant fixes one order.
 __device__ __forceinline__ int wave_sum_i32(int v) {
     v += dpp<0xB1>(v);
     v += dpp<0x4E>(v);
     v += dpp<0x141>(v);
     v += dpp<0x140>(v);
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    return v;
+    v = swap_sum16(v, v);
+    return swap_sum32(v, v);
 }
 
 __device__ __forceinline__ float wave_sum_f32(float v) {
@@ -105,21 +150,36 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
     v += __int_as_float(dpp<0x4E>(__float_as_int(v)));
     v += __int_as_float(dpp<0x141>(__float_as_int(v)));
     v += __int_as_float(dpp<0x140>(__float_as_int(v)));
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    return v;
+    v = swap_sum16(v, v);
+    return swap_sum32(v, v);
 }
 
 // absmax reduction over the wave (max is order-free, so this equals the serial
-// std::max scan bit for bit; NaN never wins, as in absmax_step).
+// std::max scan bit for bit; NaN never wins, as in absmax_step). The running
+// values are never NaN, so combining them is symmetric.
 __device__ __forceinline__ float wave_absmax(float v) {
     v = absmax_step(v, __int_as_float(dpp<0xB1>(__float_as_int(v))));
     v = absmax_step(v, __int_as_float(dpp<0x4E>(__float_as_int(v))));
     v = absmax_step(v, __int_as_float(dpp<0x141>(__float_as_int(v))));
     v = absmax_step(v, __int_as_float(dpp<0x140>(__float_as_int(v))));
-    v = absmax_step(v, __shfl_xor(v, 16));
-    v = absmax_step(v, __shfl_xor(v, 32));
+    v = absmax_step(v, __uint_as_float(swap_partner<16>(__float_as_uint(v), __lane_id())));
+    v = absmax_step(v, __uint_as_float(swap_partner<32>(__float_as_uint(v), __lane_id())));
     return v;
+}
+
+// The exchange partner of stage O of wave_reduce_multi: a lane that shares
+// every lane bit above O and differs in bit O (quad_perm for 1 and 2, the
+// 8- and 16-lane mirrors for 4 and 8, the row swaps for 16 and 32).
+template <int O, typename T>
+__device__ __forceinline__ T xchg(T v, int lane) {
+    const int b = __builtin_bit_cast(int, v);
+    int r;
+    if constexpr (O == 1) r = dpp<0xB1>(b);
+    else if constexpr (O == 2) r = dpp<0x4E>(b);
+    else if constexpr (O == 4) r = dpp<0x141>(b);
+    else if constexpr (O == 8) r = dpp<0x140>(b);
+    else r = static_cast<int>(swap_partner<O>(static_cast<unsigned>(b), lane));
+    return __builtin_bit_cast(T, r);
 }
 
 // Sums NV per-lane values (NV a power of two <= 64) over the wave with NV - 1
@@ -127,23 +187,45 @@ __device__ __forceinline__ float wave_absmax(float v) {
 // lane keeps (the half selected by its lane bit) and adds the partner's copy.
 // On return v[0] of lane l is the wave total of value index l / (64 / NV),
 // identical in the 64 / NV lanes of that group. Fixed order, deterministic.
+// All exchanges are VALU (DPP and the gfx950 row swaps): no LDS round trips on
+// the tail of the kernels that end with this reduction.
 template <int CNT, int O, int NV, typename T>
 __device__ __forceinline__ void wave_reduce_stage(T (&v)[NV], int lane) {
     if constexpr (O >= 1) {
         if constexpr (CNT > 1) {
             constexpr int half = CNT / 2;
-            const bool hi = (lane & O) != 0;
+            if constexpr (O >= 16) {
+                // one swap moves both halves: even side keeps v[j], odd side v[j + half]
 #pragma unroll
-            for (int j = 0; j < half; ++j) {
-                const T keep = hi ? v[j + half] : v[j];
-                const T send = hi ? v[j] : v[j + half];
-                v[j] = keep + __shfl_xor(send, O);
+                for (int j = 0; j < half; ++j)
+                    v[j] = O == 16 ? swap_sum16(v[j], v[j + half]) : swap_sum32(v[j], v[j + half]);
+            } else {
+                const bool hi = (lane & O) != 0;
+#pragma unroll
+                for (int j = 0; j < half; ++j) {
+                    const T keep = hi ? v[j + half] : v[j];
+                    const T send = hi ? v[j] : v[j + half];
+                    v[j] = keep + xchg<O>(send, lane);
+                }
             }
             wave_reduce_stage<half, O / 2>(v, lane);
         } else {
-            v[0] += __shfl_xor(v[0], O);
+            if constexpr (O >= 16) v[0] = O == 16 ? swap_sum16(v[0], v[0]) : swap_sum32(v[0], v[0]);
+            else v[0] += xchg<O>(v[0], lane);
             wave_reduce_stage<1, O / 2>(v, lane);
         }
+    }
+}
+
+// absmax over aligned groups of G lanes (G a power of two <= 64), result in
+// every lane of the group: the stage-O partners stay inside the group.
+template <int G, int O = 1>
+__device__ __forceinline__ float group_absmax(float am, int lane) {
+    if constexpr (O < G) {
+        am = absmax_step(am, xchg<O>(am, lane));
+        return group_absmax<G, 2 * O>(am, lane);
+    } else {
+        return am;
     }
 }
 

@@ -6,7 +6,7 @@
 // the R rows, so each lane issues R independent global_load_dwordx4 up front
 // (coalesced: the 64 lanes of a wave read 1 KiB contiguous per row) and reuses
 // the activation chunk it loads for all R rows. Per-lane partials are reduced
-// across the wave with DPP + two bpermutes, across waves through LDS in a fixed
+// across the wave with DPP and the gfx950 row swaps, across waves through LDS in a fixed
 // order (deterministic), then scaled once per row at the store — the reference
 // "accumulate then scale" order (quant.cpp:155-161, cuda_quant.cu:217-235).
 //
@@ -543,18 +543,24 @@ __global__ void gemv_w8a8_generic_kernel(const int8_t* __restrict__ xq, const fl
 // Wave then workgroup reduction of (value, index) pairs by arg_better; the
 // order is a total one on distinct indices, so the result does not depend on
 // the reduction tree.
+template <int O>
+__device__ __forceinline__ void arg_step(float& bv, int& bi, int lane) {
+    const float ov = xchg<O>(bv, lane);
+    const int oi = xchg<O>(bi, lane);
+    if (arg_better(ov, oi, bv, bi)) {
+        bv = ov;
+        bi = oi;
+    }
+}
 template <int NT>
 __device__ __forceinline__ void arg_reduce_block(float& bv, int& bi, float* sv, int* si) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(bv, off);
-        const int oi = __shfl_xor(bi, off);
-        if (arg_better(ov, oi, bv, bi)) {
-            bv = ov;
-            bi = oi;
-        }
-    }
     const int tid = threadIdx.x;
+    arg_step<32>(bv, bi, tid & 63);
+    arg_step<16>(bv, bi, tid & 63);
+    arg_step<8>(bv, bi, tid & 63);
+    arg_step<4>(bv, bi, tid & 63);
+    arg_step<2>(bv, bi, tid & 63);
+    arg_step<1>(bv, bi, tid & 63);
     if ((tid & 63) == 0) {
         sv[tid >> 6] = bv;
         si[tid >> 6] = bi;

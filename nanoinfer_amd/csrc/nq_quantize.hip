@@ -97,8 +97,7 @@ __global__ __launch_bounds__(256) void quantize_q4g_vec_kernel(const float* __re
 #pragma unroll
     for (int j = 0; j < 8; ++j) am = absmax_step(am, v[j]);
     am = act ? am : 0.0f;
-#pragma unroll
-    for (int off = 1; off < G; off <<= 1) am = absmax_step(am, __shfl_xor(am, off));
+    am = group_absmax<G>(am, static_cast<int>(threadIdx.x & 63));
     const float s = am / 7.0f;
     if (!act) return;
     if (cc % G == 0) store_scale(scale + static_cast<size_t>(o) * blocks + cc / G, s);
