@@ -189,6 +189,20 @@ nq_status nq_gemm_w8a8(const int8_t* xq, const float* a_scale, const int8_t* wq,
                        int64_t m, int64_t n, int64_t k, void* workspace, size_t workspace_bytes,
                        int path, void* stream);
 
+/* No counterpart in the reference. nq_linear_w8a8 for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the same kernels and results, with the workspace taken
+ * from a static device array of nq_linear_w8a8_noalloc_max_scratch() bytes
+ * (32 MiB) that each GPU holds for the life of the process. A shape whose
+ * nq_linear_w8a8_workspace_size() exceeds it returns NQ_BAD_SHAPE before
+ * anything is enqueued. The call allocates nothing. Every call on one GPU uses
+ * that GPU's array: calls that overlap on one GPU (other streams, other host
+ * threads) race. */
+size_t nq_linear_w8a8_noalloc_max_scratch(void);
+nq_status nq_linear_w8a8_noalloc(const void* x, nq_dtype x_dtype, const int8_t* wq, const float* w_scale,
+                                 const float* bias, void* y, nq_dtype y_dtype, int64_t m, int64_t n, int64_t k,
+                                 int path, void* stream);
+
 /* Debug/parity entry: the exact int32 accumulators acc[i,o] = sum_j xq[i,j]*wq[o,j]
  * of the chosen path (the integer core of simd::dot_qq, simd.hpp:160-197, which
  * the reference never exposes). Same workspace rule as nq_gemm_w8a8. */

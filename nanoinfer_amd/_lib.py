@@ -40,6 +40,8 @@ SIGNATURES = {
     "nq_lm_head_argmax_q8": (_D, [_P, _D, _P, _P, _P, _P, _I, _I, _I, _P, _Z, _P]),
     "nq_linear_w8a8_workspace_size": (_Z, [_I, _I, _I]),
     "nq_linear_w8a8": (_D, [_P, _D, _P, _P, _P, _P, _D, _I, _I, _I, _P, _Z, ctypes.c_int, _P]),
+    "nq_linear_w8a8_noalloc_max_scratch": (_Z, []),
+    "nq_linear_w8a8_noalloc": (_D, [_P, _D, _P, _P, _P, _P, _D, _I, _I, _I, ctypes.c_int, _P]),
     "nq_gemm_w8a8_workspace_size": (_Z, [_I, _I, _I]),
     "nq_gemm_w8a8": (_D, [_P, _P, _P, _P, _P, _P, _D, _I, _I, _I, _P, _Z, ctypes.c_int, _P]),
     "nq_w8a8_acc_i32": (_D, [_P, _P, _P, _I, _I, _I, _P, _Z, ctypes.c_int, _P]),

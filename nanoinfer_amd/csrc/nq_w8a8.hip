@@ -20,6 +20,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "nq_device.hpp"
@@ -1205,4 +1206,63 @@ extern "C" nq_status nq_linear_w8a8(const void* x, nq_dtype x_dtype, const int8_
     const size_t rest_bytes = workspace_bytes - static_cast<size_t>(rest - base);
     if (nq_status st = act_quant(x, x_dtype, m, k, xq, as, s)) return st;
     return run_gemm(xq, as, wq, w_scale, bias, y, y_dtype, nullptr, m, n, k, rest, rest_bytes, p, s);
+}
+
+// ---- the allocation-free W8A8 linear -------------------------------------------------------
+// nq_linear_w8a8 with its workspace in a static device array instead of a
+// caller buffer, for callers that cannot allocate (graph capture, serving
+// loops). Each GPU holds its own copy of `scratch` for the life of the
+// process; its address is looked up once per device with hipGetSymbolAddress
+// (host code never passes the array's name itself). The workspace holds the
+// activation codes, the row scales and the split-K partial planes, each fully
+// written before it is read, so it needs no clearing between calls. Calls that
+// overlap on one GPU share the array and race.
+namespace nq {
+namespace {
+constexpr size_t kScratchBytes = size_t(32) << 20;
+constexpr int kScratchDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+struct ScratchSlot {
+    std::once_flag once;
+    void* ptr = nullptr;
+    hipError_t err = hipSuccess;
+};
+ScratchSlot g_scratch[kScratchDevices];
+
+// The device address of this device's `scratch` (nullptr + message on failure).
+nq_status scratch_for_current_device(void** out) {
+    int dev = 0;
+    NQ_REQUIRE(hipGetDevice(&dev) == hipSuccess, NQ_HIP_ERROR, "linear_w8a8_noalloc: hipGetDevice failed");
+    NQ_REQUIRE(dev >= 0 && dev < kScratchDevices, NQ_HIP_ERROR, "linear_w8a8_noalloc: device %d beyond %d", dev,
+               kScratchDevices);
+    ScratchSlot& sl = g_scratch[dev];
+    std::call_once(sl.once, [&sl] {
+        void* p = nullptr;
+        sl.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        sl.ptr = sl.err == hipSuccess ? p : nullptr;
+    });
+    NQ_REQUIRE(sl.err == hipSuccess && sl.ptr, NQ_HIP_ERROR, "linear_w8a8_noalloc: hipGetSymbolAddress failed (%s)",
+               hipGetErrorString(sl.err));
+    *out = sl.ptr;
+    return NQ_OK;
+}
+}  // namespace
+}  // namespace nq
+
+extern "C" size_t nq_linear_w8a8_noalloc_max_scratch(void) { return nq::kScratchBytes; }
+
+extern "C" nq_status nq_linear_w8a8_noalloc(const void* x, nq_dtype x_dtype, const int8_t* wq,
+                                            const float* w_scale, const float* bias, void* y, nq_dtype y_dtype,
+                                            int64_t m, int64_t n, int64_t k, int path, void* stream) {
+    if (nq_status st = check_w8a8(m, n, k, path, "linear_w8a8_noalloc")) return st;
+    if (m == 0 || n == 0) return nq_linear_w8a8(x, x_dtype, wq, w_scale, bias, y, y_dtype, m, n, k, nullptr, 0,
+                                                path, stream);
+    const size_t need = nq_linear_w8a8_workspace_size(m, n, k);
+    NQ_REQUIRE(need <= kScratchBytes, NQ_BAD_SHAPE,
+               "linear_w8a8_noalloc: m=%lld n=%lld k=%lld needs %zu bytes of scratch, the static buffer holds %zu",
+               (long long)m, (long long)n, (long long)k, need, kScratchBytes);
+    void* ws = nullptr;
+    if (nq_status st = scratch_for_current_device(&ws)) return st;
+    return nq_linear_w8a8(x, x_dtype, wq, w_scale, bias, y, y_dtype, m, n, k, ws, kScratchBytes, path, stream);
 }
