@@ -128,6 +128,20 @@ nq_status nq_rope_qkv(const void* qkv, nq_dtype dtype, int64_t s, int64_t ld, in
                       int64_t head_dim, const float* cos, const float* sin, void* q, void* k, void* v,
                       void* stream);
 
+/* fp32 ops the C++ decoder caller runs between its quantized projections, with
+ * the reference's arithmetic (ops.cpp): rmsnorm (ops.cpp:272-290; the sum of
+ * squares in double) on rows x [m, k], optionally after the residual add
+ * h = x + r (stored to h, which may be x; r == NULL skips it); silu(gate) * up
+ * (ops.cpp:86-100) on rows at stride ld; causal GQA attention (ops.cpp:206-270,
+ * repeat_kv :190-204) of head-major q [heads, s, d], k / v [kv_heads, s, d]
+ * into token-major out [s, heads * d], s <= 16384. */
+nq_status nq_rmsnorm_f32(const float* x, const float* r, float* h, const float* w, float eps, int64_t m, int64_t k,
+                         float* y, void* stream);
+nq_status nq_silu_mul_f32(const float* gate, const float* up, int64_t ld, int64_t m, int64_t k, float* y,
+                          void* stream);
+nq_status nq_attention_causal_f32(const float* q, const float* k, const float* v, int64_t heads, int64_t kv_heads,
+                                  int64_t s, int64_t head_dim, float* out, void* stream);
+
 /* ---- weight files: quantize on load -------------------------------------------
  * NIT0 / NIT1 files (serialize.hpp:1-23; load_bin serialize.cpp:11-72): the same
  * header checks as load_bin (bad magic, unknown dtype, negative ndim or dim,

@@ -23,7 +23,7 @@ HOST_TEST = os.path.join(ROOT, "tests", "cpp", "test_host.bin")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["nq_abi.cpp", "nq_quantize.hip", "nq_gemv.hip", "nq_w8a8.hip", "nq_embed.hip", "nq_fused.hip", "nq_wq_gemm.hip", "nq_nit.hip", "nq_rope.hip", "nq_dequant.hip", "nq_probe.hip"]
+SOURCES = ["nq_abi.cpp", "nq_quantize.hip", "nq_gemv.hip", "nq_w8a8.hip", "nq_embed.hip", "nq_fused.hip", "nq_wq_gemm.hip", "nq_nit.hip", "nq_rope.hip", "nq_dequant.hip", "nq_probe.hip", "nq_ops.hip"]
 
 # -packed-fp32-ops: keep hipcc from forming v_pk_{add,mul,fma}_f32 (the host
 # pass prints that it does not know the feature; that is harmless).
@@ -64,6 +64,7 @@ def _host_artifacts():
     rpath = "-Wl,-rpath,$ORIGIN"
     cxx = [HIPCC, "-std=c++17", "-O2", "-fPIC", "-Wall", "-I", os.path.join(ROOT, "include")]
     _run([*cxx, "-shared", "-o", HOST_LIB + ".tmp", os.path.join(host_src, "nq_host.cpp"),
+          os.path.join(host_src, "nq_model.cpp"),
           "-L", PKG, "-lnq_hip", rpath], "libnq_host link")
     os.replace(HOST_LIB + ".tmp", HOST_LIB)
     ext = sysconfig.get_config_var("EXT_SUFFIX") or ".so"

@@ -112,6 +112,20 @@ struct PyBackend {
     }
 };
 
+// The greedy pick over one row of logits: the reference's left-to-right scan
+// with a strict > from element 0 (sampling.cpp:13-19; a NaN element 0 is
+// never beaten, later NaNs never win).
+int64_t greedy_pick(const float* row, int64_t n) {
+    int64_t best = 0;
+    float bv = row[0];
+    for (int64_t i = 1; i < n; ++i)
+        if (row[i] > bv) {
+            bv = row[i];
+            best = i;
+        }
+    return best;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(nicpp, m) {
@@ -151,4 +165,73 @@ PYBIND11_MODULE(nicpp, m) {
         .def("load_quant_weight", &PyBackend::load_quant_weight, py::arg("path"), py::arg("mode"));
 
     m.def("make_backend", [](const std::string& device) { return PyBackend(device); }, py::arg("device") = "hip");
+
+    py::class_<Config>(m, "Config", "Model dimensions read from config.txt.")
+        .def_readonly("vocab_size", &Config::vocab_size)
+        .def_readonly("hidden_size", &Config::hidden_size)
+        .def_readonly("intermediate_size", &Config::intermediate_size)
+        .def_readonly("num_layers", &Config::num_layers)
+        .def_readonly("num_attention_heads", &Config::num_attention_heads)
+        .def_readonly("num_kv_heads", &Config::num_kv_heads)
+        .def_readonly("head_dim", &Config::head_dim)
+        .def_readonly("max_position_embeddings", &Config::max_position_embeddings)
+        .def_readonly("rms_norm_eps", &Config::rms_norm_eps)
+        .def_readonly("rope_theta", &Config::rope_theta)
+        .def_readonly("tie_word_embeddings", &Config::tie_word_embeddings)
+        .def_readonly("eos_token_id", &Config::eos_token_id)
+        .def_readonly("qkv_bias", &Config::qkv_bias)
+        .def_property_readonly("n_rep", &Config::n_rep);
+
+    // The reference's Model binding (nicpp.cpp:207-233, 317): the same
+    // constructor arguments, forward with the GIL released, config and
+    // weight_bytes. device must be "hip" and mode a quant mode.
+    py::class_<Model>(m, "Model")
+        .def(py::init([](const std::string& weights_dir, QuantMode mode, const std::string& device) {
+                 if (device != "hip")
+                     throw std::invalid_argument("device must be 'hip' (the CPU path is the reference's own)");
+                 std::unique_ptr<Model> mdl;
+                 {
+                     py::gil_scoped_release release;
+                     mdl = std::make_unique<Model>(weights_dir, mode, Device::HIP);
+                 }
+                 return mdl;
+             }),
+             py::arg("weights_dir"), py::arg("mode") = QuantMode::W8A8, py::arg("device") = "hip",
+             "Load config.txt + every <name>.bin (NIT0 / NIT1) from weights_dir; the projections are "
+             "quantized on the GPU in `mode`, the embedding / LM head to int8.")
+        .def_property_readonly("config", [](const Model& self) { return self.config(); })
+        .def(
+            "forward",
+            [](const Model& self, const std::vector<int64_t>& ids, py::object cache) {
+                if (!cache.is_none())
+                    throw std::invalid_argument("forward: the hip model recomputes the sequence (no KV cache)");
+                Tensor logits;
+                {
+                    py::gil_scoped_release release;
+                    logits = self.forward(ids);
+                }
+                return numpy_from_host(logits);
+            },
+            py::arg("ids"), py::arg("cache") = py::none(), "Token ids -> logits [seq, vocab] (numpy fp32).")
+        .def(
+            "generate",
+            [](const Model& self, const std::vector<int64_t>& prompt, int max_tokens, int64_t eos_id) {
+                if (prompt.empty()) throw std::invalid_argument("generate: empty prompt");
+                std::vector<int64_t> ids = prompt, out;
+                {
+                    py::gil_scoped_release release;
+                    for (int t = 0; t < max_tokens; ++t) {
+                        const Tensor lg = self.forward(ids);
+                        const int64_t v = lg.size(1);
+                        const int64_t nxt = greedy_pick(lg.data() + (lg.size(0) - 1) * v, v);
+                        out.push_back(nxt);
+                        if (nxt == eos_id) break;
+                        ids.push_back(nxt);
+                    }
+                }
+                return out;
+            },
+            py::arg("prompt"), py::arg("max_tokens") = 20, py::arg("eos_id") = -1,
+            "Greedy continuation of prompt by full recompute; returns the new ids.")
+        .def("weight_bytes", &Model::weight_bytes, "(actual_bytes, fp32_bytes) of the weights.");
 }

@@ -25,6 +25,7 @@
 #include <cstdint>
 #include <memory>
 #include <string>
+#include <utility>
 #include <vector>
 
 namespace ni {
@@ -140,6 +141,56 @@ public:
     std::unique_ptr<Weight> make_quant_weight(const Tensor& host, QuantMode mode) const;
     std::unique_ptr<Weight> make_embed_weight(const Tensor& host) const;
     const char* name() const { return "hip"; }
+};
+
+// Model dimensions from the exporter's config.txt (config.hpp:18-60, the
+// key/value format of config.cpp:8-80). The architecture fields this path does
+// not implement (qk_norm, MoE, sliding window, gelu, rope scaling, muP
+// multipliers) are accepted only at their identity values; otherwise
+// load_config throws std::runtime_error.
+struct Config {
+    int64_t vocab_size = 0;
+    int64_t hidden_size = 0;
+    int64_t intermediate_size = 0;
+    int64_t num_layers = 0;
+    int64_t num_attention_heads = 0;
+    int64_t num_kv_heads = 0;
+    int64_t head_dim = 0;
+    int64_t max_position_embeddings = 0;
+    float rms_norm_eps = 1e-6f;
+    float rope_theta = 10000.0f;
+    int64_t tie_word_embeddings = 0;
+    int64_t eos_token_id = -1;
+    int64_t qkv_bias = 1;
+    int64_t n_rep() const { return num_attention_heads / num_kv_heads; }
+};
+Config load_config(const std::string& path);
+
+// The decoder on the GPU (model.hpp:22-131): config.txt + every <name>.bin
+// (NIT0 / NIT1) from weights_dir; the projections are device Weights of `mode`
+// (make_quantized), the embedding and LM head the int8 embed Weight
+// (make_q8_embed, the reference's quantize_embed). forward() recomputes the
+// whole sequence (model.cpp:166-193 without a KV cache) and returns the fp32
+// logits [seq, vocab] on the host. Only Device::HIP and a quant mode are
+// accepted (std::invalid_argument otherwise).
+class Model {
+public:
+    explicit Model(const std::string& weights_dir, QuantMode mode = QuantMode::W8A8, Device device = Device::HIP);
+    Tensor forward(const std::vector<int64_t>& ids) const;
+    const Config& config() const { return cfg_; }
+    Device device() const { return Device::HIP; }
+    // {actual weight bytes, bytes if everything were fp32} (model.cpp:298-322).
+    std::pair<int64_t, int64_t> weight_bytes() const;
+
+private:
+    struct Layer {
+        std::unique_ptr<Weight> qkv, o, gate_up, down;  // q|k|v and gate|up fused by output rows
+        Tensor qkv_bias, in_norm, post_norm;             // device fp32
+    };
+    Config cfg_;
+    std::vector<Layer> layers_;
+    Tensor final_norm_, cos_, sin_;
+    std::unique_ptr<Weight> embed_, lm_head_;  // lm_head_ only for an untied checkpoint
 };
 
 }  // namespace hip
