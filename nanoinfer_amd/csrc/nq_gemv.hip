@@ -465,6 +465,180 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_fused_kernel(
     }
 }
 
+// ---- W8A8 decode in one launch: act quant into LDS, then the weight stream ---------------
+// For m <= 8 activation rows. Workgroups of 16 waves, at most one per CU: the
+// workgroup quantizes all m rows into LDS (every workgroup does; the m * k
+// activations are L2-resident and small next to the weights), with the same
+// absmax, divide and rounding as nq_act_quant_i8 (RowQuantizer), so codes and
+// scales are identical. Each wave takes groups of R weight rows (group g =
+// blockIdx.x + gridDim.x * (wave + 16 * i)); with short K its first group's
+// weight loads go out before the quantization, so HBM latency overlaps it. Lane l owns 16-byte
+// chunk positions l, l + 64, ... of the rows, reads the m code chunks of each
+// position from LDS once (shared by the R rows) and accumulates exact int32
+// sums with v_dot4_i32_i8; with short K the next group's loads are issued
+// before the current group's math. The int32 sums are order independent and
+// the epilogue is w8a8_epilogue: outputs equal the GEMV and MFMA paths bit for bit.
+constexpr int kDecThreads = 1024;
+constexpr int kDecMaxCodes = 128 * 1024;  // m * k bytes of codes in LDS
+
+template <typename XT>
+struct Vec8x;
+template <>
+struct Vec8x<_Float16> {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    h8 v;
+    __device__ __forceinline__ void load(const _Float16* p) { v = *reinterpret_cast<const h8*>(p); }
+    __device__ __forceinline__ float at(int j) const { return static_cast<float>(v[j]); }
+};
+template <>
+struct Vec8x<float> {
+    f4 a, b;
+    __device__ __forceinline__ void load(const float* p) {
+        a = reinterpret_cast<const f4*>(p)[0];
+        b = reinterpret_cast<const f4*>(p)[1];
+    }
+    __device__ __forceinline__ float at(int j) const { return j < 4 ? a[j] : b[j - 4]; }
+};
+
+// PRE: x holds codes already (int8 [m, k] from nq_act_quant_i8, scales in
+// pre_scale); phase 1 then only copies them into LDS.
+template <int M, int R, int T, typename XT, typename YT, bool PRE = false>
+__global__ __launch_bounds__(kDecThreads) void w8a8_decode_kernel(const XT* __restrict__ x,
+                                                                  const int8_t* __restrict__ w,
+                                                                  const float* __restrict__ ws,
+                                                                  const float* __restrict__ bias,
+                                                                  YT* __restrict__ y, int m, int n, int k,
+                                                                  const float* __restrict__ pre_scale = nullptr) {
+    extern __shared__ __attribute__((aligned(16))) int8_t xq[];  // [M][k] codes
+    __shared__ float amax_red[kDecThreads / 64][M];
+    __shared__ float a_scale[M];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int cpr = k >> 4;  // 16-byte code chunks per row
+    const int vpr = k >> 3;  // 8-element activation vectors per row
+
+    // This wave's first group of weights, requested before anything else.
+    const int groups = (n + R - 1) / R;
+    const int wstride = gridDim.x * (kDecThreads / 64);
+    int g = blockIdx.x + gridDim.x * wave;
+    const v4i* wv = reinterpret_cast<const v4i*>(w);
+    constexpr bool DB = T <= 2;
+    v4i cur[T][R], nxt[DB ? T : 1][DB ? R : 1];
+    auto load = [&](int grp, auto& buf) {
+        const int r0 = min(grp, groups - 1) * R;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int c = min(lane + 64 * t, cpr - 1);
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                buf[t][r] = __builtin_nontemporal_load(wv + static_cast<size_t>(min(r0 + r, n - 1)) * cpr + c);
+        }
+    };
+    // (Long K: not held across phase 1, whose activation vectors need the registers.)
+    if constexpr (DB)
+        if (g < groups) load(g, cur);
+
+    if constexpr (PRE) {
+        // Phase 1 for pre-quantized codes: 16-byte copies into LDS (rows past m zero).
+        const int8_t* xc = reinterpret_cast<const int8_t*>(x);
+        for (int v = tid; v < M * cpr; v += kDecThreads) {
+            const int i = v / cpr;
+            reinterpret_cast<v4i*>(xq)[v] =
+                i < m ? *reinterpret_cast<const v4i*>(xc + static_cast<size_t>(i) * k + 16 * (v - i * cpr)) : v4i{0, 0, 0, 0};
+        }
+        if (tid < M) a_scale[tid] = tid < m ? pre_scale[tid] : 0.0f;
+        __syncthreads();
+    } else {
+    // Phase 1: each thread's activation vectors (v = tid + 1024 u) in registers,
+    // per-row absmax, the row scales, then the codes into LDS.
+    const int nv = M * vpr;
+    constexpr int U = (M * T + 7) / 8;  // k <= 1024 T, so M * k / 8 <= 1024 U vectors
+    Vec8x<XT> xv[U];
+    float am[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) am[i] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int v = tid + kDecThreads * u;
+        if (v < nv) {
+            const int i = v / vpr;
+            xv[u].load(x + static_cast<size_t>(min(i, m - 1)) * k + 8 * (v - i * vpr));
+            float a = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) a = absmax_step(a, xv[u].at(j));
+#pragma unroll
+            for (int r = 0; r < M; ++r) am[r] = (r == i) ? absmax_step(am[r], a) : am[r];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        const float a = wave_absmax(am[i]);
+        if (lane == 0) amax_red[wave][i] = a;
+    }
+    __syncthreads();
+    if (tid < M) {
+        float a = 0.0f;
+        for (int w2 = 0; w2 < kDecThreads / 64; ++w2) a = absmax_step(a, amax_red[w2][tid]);
+        a_scale[tid] = a / 127.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int v = tid + kDecThreads * u;
+        if (v < nv) {
+            const int i = v / vpr;
+            int lo = 0, hi = 0;
+            if (i < m) {
+                const RowQuantizer rq(a_scale[i]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    lo |= (static_cast<int>(rq.code(xv[u].at(j), 127.0f)) & 0xFF) << (8 * j);
+                    hi |= (static_cast<int>(rq.code(xv[u].at(4 + j), 127.0f)) & 0xFF) << (8 * j);
+                }
+            }
+            typedef int v2i __attribute__((ext_vector_type(2)));
+            reinterpret_cast<v2i*>(xq)[v] = v2i{lo, hi};  // rows past m hold zero codes
+        }
+    }
+    __syncthreads();
+    }
+
+    // Phase 2: groups of R weight rows; T passes of 64 chunk positions.
+    for (; g < groups; g += wstride) {
+        if constexpr (DB) load(g + wstride, nxt);
+        else load(g, cur);
+        int acc[R * M];
+#pragma unroll
+        for (int j = 0; j < R * M; ++j) acc[j] = 0;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int c = lane + 64 * t;
+            if (c < cpr) {
+#pragma unroll
+                for (int i = 0; i < M; ++i) {
+                    const v4i a = reinterpret_cast<const v4i*>(xq)[i * cpr + c];
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+#pragma unroll
+                        for (int d = 0; d < 4; ++d) acc[r * M + i] = __builtin_amdgcn_sdot4(a[d], cur[t][r][d], acc[r * M + i], false);
+                }
+            }
+        }
+        wave_reduce_multi<R * M>(acc, lane);
+        constexpr int G = 64 / (R * M);
+        const int idx = lane / G, r = idx / M, i = idx % M, row = g * R + r;
+        if (lane % G == 0 && row < n && i < m) {
+            const float b = bias ? bias[row] : 0.0f;
+            y[static_cast<size_t>(i) * n + row] = from_f32<YT>(w8a8_epilogue(acc[0], a_scale[i], ws[row], b));
+        }
+        if constexpr (DB) {
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int r = 0; r < R; ++r) cur[t][r] = nxt[t][r];
+        }
+    }
+}
+
 // ---- generic bounds-checked kernels (any k, any alignment) -----------------------------
 // One wave per output row; lanes stride K one element at a time; rows of x loop.
 template <typename XT, typename YT>
@@ -740,6 +914,79 @@ nq_status gemv_w8a8_launch(const int8_t* xq, const float* as, const int8_t* w, c
         default: go(std::integral_constant<int, 8>{}); break;
     }
     return launch_status("gemv_w8a8_kernel");
+}
+
+// The decode kernel for m <= 8 (see w8a8_decode_kernel): with pre_scale ==
+// nullptr it quantizes x itself (one launch), else x is the int8 codes of
+// nq_act_quant_i8 and pre_scale their row scales. Returns false (nothing
+// launched) outside its contract: k % 16 == 0, k <= 9216, m * k codes within
+// 128 KB of LDS, 16-byte aligned x and w.
+bool w8a8_decode_launch(const void* x, nq_dtype xdt, const int8_t* w, const float* ws, const float* bias,
+                        void* y, nq_dtype ydt, int64_t m, int64_t n, int64_t k, hipStream_t s, nq_status* st,
+                        const float* pre_scale) {
+    const int mb = m_bucket(m);
+    if (!(m >= 1 && m <= 8 && k > 0 && k % 16 == 0 && (k + 1023) / 1024 <= 9 &&
+          static_cast<int64_t>(mb) * k <= kDecMaxCodes &&
+          aligned(w, 16) && aligned(x, 16) && n <= kMaxIndex))
+        return false;
+    const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
+    const int T = (ki / 16 + 63) / 64;
+    const size_t lds = static_cast<size_t>(mb) * ki;
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    *st = NQ_OK;
+    auto go = [&](auto mtag, auto rtag, auto ttag, auto* xp, auto* yp) {
+        constexpr int M = decltype(mtag)::value, R = decltype(rtag)::value, TT = decltype(ttag)::value;
+        using XT = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
+        using YT = std::remove_pointer_t<decltype(yp)>;
+        const int groups = (ni + R - 1) / R;
+        const unsigned grid = static_cast<unsigned>(std::max(1, std::min(cus, groups)));
+        if (pre_scale) {
+            auto* fn = w8a8_decode_kernel<M, R, TT, int8_t, YT, true>;
+            if ((*st = set_dynamic_lds(reinterpret_cast<const void*>(fn), lds, "w8a8_decode"))) return;
+            fn<<<grid, kDecThreads, lds, s>>>(static_cast<const int8_t*>(x), w, ws, bias, yp, mi, ni, ki, pre_scale);
+        } else {
+            auto* fn = w8a8_decode_kernel<M, R, TT, XT, YT>;
+            if ((*st = set_dynamic_lds(reinterpret_cast<const void*>(fn), lds, "w8a8_decode"))) return;
+            fn<<<grid, kDecThreads, lds, s>>>(xp, w, ws, bias, yp, mi, ni, ki, nullptr);
+        }
+    };
+    // Passes padded up to 2, 4 or 9 (a masked extra pass re-loads the last
+    // chunk). R rows per group: the m code chunks read from LDS per pass serve R
+    // rows; long K keeps R <= 2 for registers, and weights with fewer rows than
+    // about four groups per CU take single-row groups so that every CU streams.
+    const bool few = n < 4 * static_cast<int64_t>(cus);
+    auto with_t = [&](auto mtag, auto* xp, auto* yp) {
+        constexpr int M = decltype(mtag)::value;
+        constexpr int RS = M == 8 ? 4 : M == 4 ? 2 : M;  // short K
+        constexpr int RL = RS < 2 ? RS : 2;                // long K
+        using One = std::integral_constant<int, 1>;
+        if (T <= 2) {
+            if (few) go(mtag, One{}, std::integral_constant<int, 2>{}, xp, yp);
+            else go(mtag, std::integral_constant<int, RS>{}, std::integral_constant<int, 2>{}, xp, yp);
+        } else if (T <= 4) {
+            go(mtag, std::integral_constant<int, RL>{}, std::integral_constant<int, 4>{}, xp, yp);
+        } else {
+            go(mtag, std::integral_constant<int, RL>{}, std::integral_constant<int, 9>{}, xp, yp);
+        }
+    };
+    auto with_m = [&](auto* xp, auto* yp) {
+        switch (mb) {
+            case 1: with_t(std::integral_constant<int, 1>{}, xp, yp); break;
+            case 2: with_t(std::integral_constant<int, 2>{}, xp, yp); break;
+            case 4: with_t(std::integral_constant<int, 4>{}, xp, yp); break;
+            default: with_t(std::integral_constant<int, 8>{}, xp, yp); break;
+        }
+    };
+    auto with_y = [&](auto* xp) {
+        if (ydt == NQ_F32) with_m(xp, static_cast<float*>(y));
+        else with_m(xp, static_cast<_Float16*>(y));
+    };
+    // (with pre_scale the activation type only picks an instantiation; x is int8)
+    if (xdt == NQ_F32 && !pre_scale) with_y(static_cast<const float*>(x));
+    else with_y(static_cast<const _Float16*>(x));
+    if (*st == NQ_OK) *st = launch_status("w8a8_decode_kernel");
+    return true;
 }
 
 // Fused act-quant + GEMV for m <= 2 (larger m re-quantizes too many activation

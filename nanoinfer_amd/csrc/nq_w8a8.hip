@@ -1133,10 +1133,21 @@ nq_status run_gemm(const int8_t* xq, const float* as, const int8_t* wq, const fl
 using namespace nq;
 
 namespace nq {
+// m * k up to which a decode batch quantizes its activations inside the GEMV
+// kernel (each workgroup quantizes them again, so long rows pay more in VALU
+// than the separate launch costs).
+constexpr int64_t kDecodeFuseMax = 4096;
+// Shapes on which the decode kernel over pre-quantized codes beat the GEMV /
+// MFMA paths (m = 8: k/v 7.45 -> 6.37 us, q/o 7.46 -> 7.07); wide (n = 8960)
+// and long-K (k = 8960) weights stay on those (10.3 vs 10.3, 12.5 vs 11.2).
+constexpr int64_t kDecodePreMaxN = 2048, kDecodePreMaxK = 2048;
 nq_status act_quant(const void* x, nq_dtype xdt, int64_t m, int64_t k, int8_t* xq, float* as, hipStream_t s);
 bool gemv_w8a8_fused_launch(const void* x, nq_dtype xdt, const int8_t* w, const float* ws,
                             const float* bias, void* y, nq_dtype ydt, int64_t m, int64_t n,
                             int64_t k, hipStream_t s, nq_status* st);
+bool w8a8_decode_launch(const void* x, nq_dtype xdt, const int8_t* w, const float* ws, const float* bias,
+                        void* y, nq_dtype ydt, int64_t m, int64_t n, int64_t k, hipStream_t s, nq_status* st,
+                        const float* pre_scale);
 
 }  // namespace nq
 
@@ -1195,6 +1206,15 @@ extern "C" nq_status nq_linear_w8a8(const void* x, nq_dtype x_dtype, const int8_
     NQ_REQUIRE(aligned(workspace, 256), NQ_BAD_ALIGN, "linear_w8a8: workspace must be 256-byte aligned");
     hipStream_t s = as_stream(stream);
     const int p = resolve_path(path, m, n, k);
+    // Decode batches (AUTO, m <= 8): the activation quant inside the GEMV
+    // kernel while the rows are short (every workgroup quantizes all m rows, a
+    // VALU cost that grows with m * k), else one act-quant launch and the
+    // decode kernel on its codes.
+    const bool decode = path == NQ_PATH_AUTO && m <= 8;
+    if (decode && m * k <= kDecodeFuseMax) {
+        nq_status st = NQ_OK;
+        if (w8a8_decode_launch(x, x_dtype, wq, w_scale, bias, y, y_dtype, m, n, k, s, &st, nullptr)) return st;
+    }
     if (p == NQ_PATH_GEMV) {
         nq_status st = NQ_OK;
         if (gemv_w8a8_fused_launch(x, x_dtype, wq, w_scale, bias, y, y_dtype, m, n, k, s, &st)) return st;
@@ -1205,6 +1225,10 @@ extern "C" nq_status nq_linear_w8a8(const void* x, nq_dtype x_dtype, const int8_
     char* rest = reinterpret_cast<char*>(as) + round_up(static_cast<size_t>(m) * 4, 256);
     const size_t rest_bytes = workspace_bytes - static_cast<size_t>(rest - base);
     if (nq_status st = act_quant(x, x_dtype, m, k, xq, as, s)) return st;
+    if (decode && n <= kDecodePreMaxN && k <= kDecodePreMaxK) {
+        nq_status st = NQ_OK;
+        if (w8a8_decode_launch(xq, NQ_F16, wq, w_scale, bias, y, y_dtype, m, n, k, s, &st, as)) return st;
+    }
     return run_gemm(xq, as, wq, w_scale, bias, y, y_dtype, nullptr, m, n, k, rest, rest_bytes, p, s);
 }
 

@@ -586,3 +586,25 @@ def test_w8a8_plans_random_shapes(dev, nq, m, n, k):
     acc_m = nq.w8a8_acc_i32(xq, wq, nq._lib.NQ_PATH_MFMA)
     acc_g = nq.w8a8_acc_i32(xq, wq, nq._lib.NQ_PATH_GEMV)
     assert torch.equal(acc_m, acc_g), (m, n, k)
+
+
+# The decode-batch routes of nq_linear_w8a8 (AUTO, m <= 8): the act quant fused
+# into the decode kernel (m * k <= 4096), the decode kernel over pre-quantized
+# codes (n, k <= 2048), and the GEMV / MFMA paths otherwise. All share the act
+# quant's codes, exact int32 sums and the epilogue, so every route's output
+# equals the forced MFMA path's bit for bit.
+@pytest.mark.parametrize("m,n,k", [(1, 256, 1536), (2, 8960, 1536), (2, 1536, 2048), (1, 1, 16), (2, 3, 2048),
+                                   (8, 1536, 1536), (8, 256, 1536), (5, 2000, 1024), (3, 1000, 2048),
+                                   (7, 129, 528), (8, 2048, 2048), (4, 8960, 1536), (8, 1536, 8960)])
+@pytest.mark.parametrize("xdt,ydt", [(torch.float16, torch.float16), (torch.float32, torch.float32),
+                                     (torch.float16, torch.float32)])
+def test_w8a8_decode_routes_equal_mfma(dev, nq, m, n, k, xdt, ydt):
+    g = torch.Generator(device=dev).manual_seed(m * 1000 + n + k)
+    x = torch.randn((m, k), generator=g, device=dev).to(xdt)
+    w = torch.randn((n, k), generator=g, device=dev) * 0.02
+    b = torch.randn(n, generator=g, device=dev)
+    t = nq.quantize_q8(w)
+    y = nq.linear_w8a8(x, t, b, out_dtype=ydt)
+    y_mfma = nq.linear_w8a8(x, t, b, out_dtype=ydt, path=nq._lib.NQ_PATH_MFMA)
+    assert torch.isfinite(y).all()
+    assert torch.equal(y, y_mfma), (m, n, k, float((y.float() - y_mfma.float()).abs().max()))
