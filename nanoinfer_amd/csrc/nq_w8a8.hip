@@ -348,14 +348,22 @@ struct WideShape {
     static constexpr int kXB = kBM / 8, kNB = kXB + kBN / 8, kQ = (kNB + kWaves - 1) / kWaves;
     static constexpr int kSlab = (kBM + kBN) * kRow;
     // As many ring slots as 160 KB of LDS holds beside the sink (at most 8).
-    static constexpr int kD = std::min(8, (160 * 1024 - 1024) / kSlab);
+    static constexpr int kEpsBytes = (kBM + 2 * ((kBN + 63) / 64) * 64) * 4;
+    static constexpr int kD = std::min(8, (160 * 1024 - 1024 - kEpsBytes) / kSlab);
     static_assert(kD >= 2, "two slabs must fit");
     static constexpr int kSink = kD * kSlab;  // 1 KB
     // fp16 staging rows of the epilogue: 16 bytes of padding make the stride an
     // odd multiple of 16, so the 16 rows of a fragment store hit distinct banks
     // (an unpadded 576-byte stride put 4 rows on each bank group).
     static constexpr int kStg = kBN * 2 + 16;
-    static constexpr size_t kLds = std::max<size_t>(size_t(kSink) + 1024, size_t(kBM / 2) * kStg);
+    // The tile's activation row scales, weight scales and bias (fp16 epilogue
+    // only): fetched into LDS at the start, after the ring and the staging rows;
+    // loaded in the epilogue instead, their latency sat between the last MFMA
+    // and the first store (config 5a 34.2 -> 31.7 us).
+    static constexpr size_t kEps = (std::max<size_t>(size_t(kSink) + 1024, size_t(kBM / 2) * kStg) + 15) / 16 * 16;
+    static constexpr int kEpsReq = (kBM + 63) / 64 + 2 * ((kBN + 63) / 64);
+    static constexpr size_t kLds = kEps + kEpsBytes;
+    static_assert(kLds <= 160 * 1024, "LDS");
 };
 
 template <int WM, int FN, int FM, Out OUT, typename YT, int WN = 2>
@@ -441,6 +449,30 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_w8a8_wide_kernel(
         for (int i = 0; i < FN; ++i) fwo[t][i] = swz128(BM + wn * FN * 16 + i * 16 + fr, t * 4 + fc);
     }
 
+    constexpr bool kStaged = OUT == Out::Y && sizeof(YT) == 2;
+    if constexpr (kStaged) {
+        // Epilogue operands into LDS by dword DMA: request e of the tile is
+        // 64 values of as (rows m0..), ws (columns n0..) or bias; past m / n
+        // (or without bias) the loads read zeros. Issued before the ring, so
+        // the slab waits below also cover them.
+        constexpr int NA = (BM + 63) / 64, NC = (BN + 63) / 64;
+        const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(as), 0, m * 4, 0x00020000);
+        const __amdgpu_buffer_rsrc_t wsr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(ws), 0, n * 4, 0x00020000);
+        const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(bias ? bias : ws), 0, bias ? n * 4 : 0, 0x00020000);
+        for (int e = wave; e < S::kEpsReq; e += NW) {
+            const unsigned dst = lds_base + static_cast<unsigned>(S::kEps) + static_cast<unsigned>(e < NA ? e * 256 : BM * 4 + (e - NA) * 256);
+            if (e < NA) {
+                const int vo = (m0 + e * 64 + lane) * 4;
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(dst), "v"(vo), "s"(ars) : "memory");
+            } else if (e < NA + NC) {
+                const int vo = (n0 + (e - NA) * 64 + lane) * 4;
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(dst), "v"(vo), "s"(wsr) : "memory");
+            } else {
+                const int vo = (n0 + (e - NA - NC) * 64 + lane) * 4;
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(dst), "v"(vo), "s"(brs) : "memory");
+            }
+        }
+    }
 #pragma unroll
     for (int sl = 0; sl < D - 1; ++sl) issue(sl);
     for (int kt = 0; kt < nk; ++kt) {
@@ -482,14 +514,13 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_w8a8_wide_kernel(
 #pragma unroll
                     for (int j = 0; j < FM; ++j) {
                         const int rl = (wm % HW) * FM * 16 + j * 16 + row_in;  // row within the half
-                        const int row = m0 + half * HR + rl;
-                        const float a_s = row < m ? as[row] : 0.0f;
+                        const float* eps = reinterpret_cast<const float*>(lds + S::kEps);
+                        const float a_s = eps[half * HR + rl];
 #pragma unroll
                         for (int i = 0; i < FN; ++i) {
-                            const int cl = wn * FN * 16 + i * 16 + col_in, col = n0 + cl;
-                            const bool cin = col < n;  // n % 8 == 0: a 4-column group is all in or all out
-                            const f4 w4 = cin ? *reinterpret_cast<const f4*>(ws + col) : f4{0, 0, 0, 0};
-                            const f4 b4 = cin && bias ? *reinterpret_cast<const f4*>(bias + col) : f4{0, 0, 0, 0};
+                            const int cl = wn * FN * 16 + i * 16 + col_in;
+                            const f4 w4 = *reinterpret_cast<const f4*>(eps + BM + cl);
+                            const f4 b4 = *reinterpret_cast<const f4*>(eps + BM + ((BN + 63) / 64) * 64 + cl);
                             h4 r;
 #pragma unroll
                             for (int v = 0; v < 4; ++v) r[v] = from_f32<_Float16>(w8a8_epilogue(acc[i][j][v], a_s, w4[v], b4[v]));
