@@ -312,6 +312,7 @@ def main():
             return not only or n in only
         if want("q8_gemv_cfg1"):
             sweep.append(entry("q8_gemv_cfg1 M=1 K=896 N=4864 fp32", *q8_gemv(1, 4864, 896, torch.float32), "hbm"))
+            torch.cuda.empty_cache()
         if want("lmhead_cfg5b"):
             sweep.append(entry("q8_lmhead_cfg5b M=1 K=1536 N=151936 fp16", *q8_gemv(1, 151936, 1536, torch.float16), "hbm"))
             torch.cuda.empty_cache()
