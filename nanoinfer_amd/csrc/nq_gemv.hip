@@ -112,6 +112,17 @@ __device__ __forceinline__ bool arg_better(float v, int i, float bv, int bi) {
     return v > bv || (v == bv && i < bi);
 }
 
+// Row group of this workgroup. Workgroup ids are dealt round-robin over the 8
+// XCDs; numbering the groups so that XCD x takes a contiguous run of them keeps
+// each output line written by one XCD (its L2 holds whole dirty lines instead
+// of eight partial copies that meet at write-back): int4 GEMV at k = 8960,
+// n = 1536 4.65 -> 4.56 us. Block 0 keeps group 0.
+__device__ __forceinline__ int xcd_row_group() {
+    const int g = gridDim.x, per = (g + 7) / 8, xcd = blockIdx.x % 8, idx = blockIdx.x / 8;
+    const int full = g - 8 * (per - 1);  // XCDs [0, full) take `per` groups, the rest per - 1
+    return xcd < full ? xcd * per + idx : full * per + (xcd - full) * (per - 1) + idx;
+}
+
 // ---- weight-only int8 ------------------------------------------------------------
 // AM: instead of storing y, reduce this workgroup's R logits of each activation
 // row to an ArgPart (part[i * gridDim.x + blockIdx.x]); the logits are the same
@@ -124,7 +135,7 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q8_kernel(
     const int tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6;
     const int chunks = k >> 4;
     const bool act = tid < chunks;
-    const int row0 = blockIdx.x * R;
+    const int row0 = xcd_row_group() * R;
 
     const int c = act ? tid : 0;
     v4i wv[R];
@@ -253,7 +264,7 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q4g_kernel(
     const int chunks = k >> 5;  // 32 codes per 16-byte chunk
     const int rb = k >> 1, blocks = k / group;
     const bool act = tid < chunks;
-    const int row0 = blockIdx.x * R;
+    const int row0 = xcd_row_group() * R;
 
     const int c = act ? tid : 0;
     const int blk = group == 32 ? c : (c * 32) / group;
@@ -335,7 +346,7 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_kernel(
     const int tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6;
     const int chunks = k >> 4;
     const bool act = tid < chunks;
-    const int row0 = blockIdx.x * R;
+    const int row0 = xcd_row_group() * R;
 
     const int c = act ? tid : 0;
     v4i wv[R];
@@ -390,7 +401,7 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_fused_kernel(
     const int tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6;
     const int chunks = k >> 4;
     const bool act = tid < chunks;
-    const int row0 = blockIdx.x * R;
+    const int row0 = xcd_row_group() * R;
 
     const int c = act ? tid : 0;
     v4i wv[R];
