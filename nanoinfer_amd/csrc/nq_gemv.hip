@@ -929,14 +929,15 @@ nq_status gemv_w8a8_launch(const int8_t* xq, const float* as, const int8_t* w, c
 
 // The decode kernel for m <= 8 (see w8a8_decode_kernel): with pre_scale ==
 // nullptr it quantizes x itself (one launch), else x is the int8 codes of
-// nq_act_quant_i8 and pre_scale their row scales. Returns false (nothing
-// launched) outside its contract: k % 16 == 0, k <= 9216, m * k codes within
-// 128 KB of LDS, 16-byte aligned x and w.
+// nq_act_quant_i8 and pre_scale their row scales (then also m <= 16, as one
+// batch of 16). Returns false (nothing launched) outside its contract:
+// k % 16 == 0, k <= 9216, the padded m * k codes within 128 KB of LDS, 16-byte
+// aligned x and w.
 bool w8a8_decode_launch(const void* x, nq_dtype xdt, const int8_t* w, const float* ws, const float* bias,
                         void* y, nq_dtype ydt, int64_t m, int64_t n, int64_t k, hipStream_t s, nq_status* st,
                         const float* pre_scale) {
-    const int mb = m_bucket(m);
-    if (!(m >= 1 && m <= 8 && k > 0 && k % 16 == 0 && (k + 1023) / 1024 <= 9 &&
+    const int mb = m > 8 ? 16 : m_bucket(m);  // 9..16 rows: pre-quantized codes only
+    if (!(m >= 1 && m <= (pre_scale ? 16 : 8) && k > 0 && k % 16 == 0 && (k + 1023) / 1024 <= 9 &&
           static_cast<int64_t>(mb) * k <= kDecMaxCodes &&
           aligned(w, 16) && aligned(x, 16) && n <= kMaxIndex))
         return false;
@@ -956,7 +957,7 @@ bool w8a8_decode_launch(const void* x, nq_dtype xdt, const int8_t* w, const floa
             auto* fn = w8a8_decode_kernel<M, R, TT, int8_t, YT, true>;
             if ((*st = set_dynamic_lds(reinterpret_cast<const void*>(fn), lds, "w8a8_decode"))) return;
             fn<<<grid, kDecThreads, lds, s>>>(static_cast<const int8_t*>(x), w, ws, bias, yp, mi, ni, ki, pre_scale);
-        } else {
+        } else if constexpr (M <= 8) {
             auto* fn = w8a8_decode_kernel<M, R, TT, XT, YT>;
             if ((*st = set_dynamic_lds(reinterpret_cast<const void*>(fn), lds, "w8a8_decode"))) return;
             fn<<<grid, kDecThreads, lds, s>>>(xp, w, ws, bias, yp, mi, ni, ki, nullptr);
@@ -969,8 +970,8 @@ bool w8a8_decode_launch(const void* x, nq_dtype xdt, const int8_t* w, const floa
     const bool few = n < 4 * static_cast<int64_t>(cus);
     auto with_t = [&](auto mtag, auto* xp, auto* yp) {
         constexpr int M = decltype(mtag)::value;
-        constexpr int RS = M == 8 ? 4 : M == 4 ? 2 : M;  // short K
-        constexpr int RL = RS < 2 ? RS : 2;                // long K
+        constexpr int RS = M == 16 ? 2 : M == 8 ? 4 : M == 4 ? 2 : M;  // short K
+        constexpr int RL = M == 16 ? 1 : RS < 2 ? RS : 2;                // long K
         using One = std::integral_constant<int, 1>;
         if (T <= 2) {
             if (few) go(mtag, One{}, std::integral_constant<int, 2>{}, xp, yp);
@@ -986,7 +987,8 @@ bool w8a8_decode_launch(const void* x, nq_dtype xdt, const int8_t* w, const floa
             case 1: with_t(std::integral_constant<int, 1>{}, xp, yp); break;
             case 2: with_t(std::integral_constant<int, 2>{}, xp, yp); break;
             case 4: with_t(std::integral_constant<int, 4>{}, xp, yp); break;
-            default: with_t(std::integral_constant<int, 8>{}, xp, yp); break;
+            case 8: with_t(std::integral_constant<int, 8>{}, xp, yp); break;
+            default: with_t(std::integral_constant<int, 16>{}, xp, yp); break;
         }
     };
     auto with_y = [&](auto* xp) {

@@ -1169,8 +1169,9 @@ namespace nq {
 // than the separate launch costs).
 constexpr int64_t kDecodeFuseMax = 4096;
 // Shapes on which the decode kernel over pre-quantized codes beat the GEMV /
-// MFMA paths (m = 8: k/v 7.45 -> 6.37 us, q/o 7.46 -> 7.07); wide (n = 8960)
-// and long-K (k = 8960) weights stay on those (10.3 vs 10.3, 12.5 vs 11.2).
+// MFMA paths (m = 8: k/v 7.45 -> 6.37 us, q/o 7.46 -> 7.07; m = 16: k/v 7.77 ->
+// 6.86, q/o 7.81 -> 7.49); wide (n = 8960) and long-K (k = 8960) weights stay
+// on those (m = 8: 10.3 vs 10.3, 12.5 vs 11.2; m = 16: 12.4 vs 10.3, 15.9 vs 14.6).
 constexpr int64_t kDecodePreMaxN = 2048, kDecodePreMaxK = 2048;
 nq_status act_quant(const void* x, nq_dtype xdt, int64_t m, int64_t k, int8_t* xq, float* as, hipStream_t s);
 bool gemv_w8a8_fused_launch(const void* x, nq_dtype xdt, const int8_t* w, const float* ws,
@@ -1237,11 +1238,12 @@ extern "C" nq_status nq_linear_w8a8(const void* x, nq_dtype x_dtype, const int8_
     NQ_REQUIRE(aligned(workspace, 256), NQ_BAD_ALIGN, "linear_w8a8: workspace must be 256-byte aligned");
     hipStream_t s = as_stream(stream);
     const int p = resolve_path(path, m, n, k);
-    // Decode batches (AUTO, m <= 8): the activation quant inside the GEMV
+    // Decode batches (AUTO): for m <= 8 the activation quant inside the decode
     // kernel while the rows are short (every workgroup quantizes all m rows, a
-    // VALU cost that grows with m * k), else one act-quant launch and the
-    // decode kernel on its codes.
+    // VALU cost that grows with m * k); else, up to m = 16, one act-quant launch
+    // and the decode kernel on its codes where the weight is small.
     const bool decode = path == NQ_PATH_AUTO && m <= 8;
+    const bool decode16 = path == NQ_PATH_AUTO && m <= 16;
     if (decode && m * k <= kDecodeFuseMax) {
         nq_status st = NQ_OK;
         if (w8a8_decode_launch(x, x_dtype, wq, w_scale, bias, y, y_dtype, m, n, k, s, &st, nullptr)) return st;
@@ -1256,7 +1258,7 @@ extern "C" nq_status nq_linear_w8a8(const void* x, nq_dtype x_dtype, const int8_
     char* rest = reinterpret_cast<char*>(as) + round_up(static_cast<size_t>(m) * 4, 256);
     const size_t rest_bytes = workspace_bytes - static_cast<size_t>(rest - base);
     if (nq_status st = act_quant(x, x_dtype, m, k, xq, as, s)) return st;
-    if (decode && n <= kDecodePreMaxN && k <= kDecodePreMaxK) {
+    if (decode16 && n <= kDecodePreMaxN && k <= kDecodePreMaxK) {
         nq_status st = NQ_OK;
         if (w8a8_decode_launch(xq, NQ_F16, wq, w_scale, bias, y, y_dtype, m, n, k, s, &st, as)) return st;
     }
