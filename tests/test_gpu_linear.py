@@ -256,6 +256,24 @@ def test_weight_only_gemm_batched(dev, nq, orc, mode, m, n, k, g, bias, xdt, sdt
     assert_close_rms(host(y.float()), ref, f"{mode} gemm {m}x{n}x{k}", fp16_out=(ydt == F16))
 
 
+# 256 x 288 Q8 tiles (one round at m ~ 2048, n in (8192, 9216]) run as 2 x 6
+# waves of 128 x 48; ragged m and n, with and without bias, sampled rows against
+# the oracle and the whole output against the 16-row kernel's (fp32 y).
+@pytest.mark.parametrize("m,n,k,bias", [(1900, 8800, 512, True), (2048, 8960, 256, False)])
+def test_weight_only_q8_wide_2x6(dev, nq, orc, m, n, k, bias):
+    x, w, b = data(m, n, k, m + n + k, bias=bias)
+    xd = to_dev(x, dev, F16)
+    bd = None if b is None else to_dev(b, dev)
+    t = nq.quantize_q8(to_dev(w, dev))
+    y = nq.linear_q8(xd, t, bd, out_dtype=F32)
+    rows = np.random.default_rng(m).choice(m, 16, replace=False)
+    q, s = orc.quantize_q8(w)
+    ref = orc.linear_q8(host(xd.float())[rows], q, s, b)
+    assert_close_rms(host(y)[rows], ref, f"q8 wide 2x6 {m}x{n}x{k}")
+    y16 = torch.cat([nq.linear_q8(xd[i:i + 64], t, bd, out_dtype=F32) for i in range(0, 128, 64)])
+    assert_close_rms(host(y[:128]), host(y16), f"q8 wide 2x6 vs 16-row kernel {m}x{n}x{k}")
+
+
 # fp32 activations far outside fp16's range and deep in its subnormals, on both
 # weight-only MFMA kernels (16-row tiles: k % 128 != 0 or small m; wide tiles:
 # m > 128, k % 128 == 0): the exact bf16 split keeps every row at the accuracy of
