@@ -394,13 +394,19 @@ struct WqWideShape {
     static constexpr int kNS = (kBN * kSRow + 255) / 256, kQS = (kNS + kNW - 1) / kNW;
     static constexpr int kXOff = 0, kWOff = kBM * kXRow, kSOff = kWOff + kBN * kWRow;
     static constexpr int kSlab = kSOff + kNS * 256;
-    static constexpr int kD = std::min(8, (160 * 1024 - 1024) / kSlab);
+    // fp16 epilogue: the tile's weight scales (Q8) and bias in LDS, DMA'd at the
+    // start, after the ring and the staging rows.
+    static constexpr int kEpsN = (kBN + 63) / 64 * 64;
+    static constexpr int kEpsBytes = sizeof(YT) == 2 ? 2 * kEpsN * 4 : 0;
+    static constexpr int kD = std::min(8, (160 * 1024 - 1024 - kEpsBytes) / kSlab);
     static constexpr int kSink = kD * kSlab;
     // fp16 staging rows padded by 16 bytes (an odd multiple of 16: the rows a
     // store instruction touches fall on distinct banks).
     static constexpr int kStg = kBN * 2 + 16;
     static constexpr size_t kStage = size_t(kBM) * kStg;
-    static constexpr size_t kLds = std::max<size_t>(size_t(kSink) + 1024, sizeof(YT) == 2 ? kStage : 0);
+    static constexpr size_t kEps = (std::max<size_t>(size_t(kSink) + 1024, sizeof(YT) == 2 ? kStage : 0) + 15) / 16 * 16;
+    static constexpr size_t kLds = kEps + kEpsBytes;
+    static_assert(kLds <= 160 * 1024, "LDS");
     static_assert(kD >= 2, "two slabs must fit");
     static_assert(kQ + kQS <= 63, "vmcnt range");
     static_assert(!Q4 || kSRow % 4 == 0, "scale rows are whole dwords");
@@ -503,6 +509,22 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_wq_wide_kernel(
 #pragma unroll
     for (int i = 0; i < FN; ++i) fwr[i] = wn * 16 * FN + i * 16 + fr;
 
+    if constexpr (sizeof(YT) == 2) {
+        // Epilogue operands by dword DMA, ahead of the ring (the slab waits cover
+        // them): request e < NC is 64 weight scales (Q8; Q4G reads ones), the
+        // rest 64 bias values; past n or without bias the loads read zeros.
+        constexpr int NC = S::kEpsN / 64;
+        const __amdgpu_buffer_rsrc_t wsr = __builtin_amdgcn_make_buffer_rsrc(const_cast<ST*>(scale), 0, Q4 ? 0 : n * 4, 0x00020000);
+        const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(bias ? bias : reinterpret_cast<const float*>(scale)), 0, bias ? n * 4 : 0, 0x00020000);
+        for (int e = wave; e < 2 * NC; e += NW) {
+            const unsigned dst = lds_base + static_cast<unsigned>(S::kEps) + static_cast<unsigned>(e * 256);
+            const int vo = (n0 + (e % NC) * 64 + lane) * 4;
+            if (e < NC)
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(dst), "v"(vo), "s"(wsr) : "memory");
+            else
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(dst), "v"(vo), "s"(brs) : "memory");
+        }
+    }
 #pragma unroll
     for (int sl = 0; sl < D - 1; ++sl) issue(sl);
     for (int kt = 0; kt < nk; ++kt) {
@@ -595,9 +617,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_wq_wide_kernel(
             __syncthreads();  // every wave is done with the ring
 #pragma unroll
             for (int i = 0; i < FN; ++i) {
-                const int cl = fwr[i], col = n0 + cl;
-                const float ws = !Q4 && col < n ? to_f32(scale[col]) : 1.0f;
-                const float b = bias && col < n ? bias[col] : 0.0f;
+                const int cl = fwr[i];
+                const float* eps = reinterpret_cast<const float*>(lds + S::kEps);
+                const float ws = Q4 ? 1.0f : eps[cl];
+                const float b = eps[S::kEpsN + cl];
 #pragma unroll
                 for (int j = 0; j < FM; ++j)
 #pragma unroll
