@@ -229,6 +229,31 @@ __device__ __forceinline__ float group_absmax(float am, int lane) {
     }
 }
 
+// The same reduction with ds_bpermute (__shfl_xor) exchanges at every stage:
+// for many values (NV >= 8) the all-VALU exchanges above left the compiler
+// free to interleave all stages with the producing math, which spilled up to
+// 150 VGPRs in the int4 GEMV at m = 8; the LDS-routed exchanges keep the
+// stages in order at the cost of an LDS round trip each.
+template <int CNT, int O, int NV, typename T>
+__device__ __forceinline__ void wave_reduce_stage_bperm(T (&v)[NV], int lane) {
+    if constexpr (O >= 1) {
+        if constexpr (CNT > 1) {
+            constexpr int half = CNT / 2;
+            const bool hi = (lane & O) != 0;
+#pragma unroll
+            for (int j = 0; j < half; ++j) {
+                const T keep = hi ? v[j + half] : v[j];
+                const T send = hi ? v[j] : v[j + half];
+                v[j] = keep + __shfl_xor(send, O);
+            }
+            wave_reduce_stage_bperm<half, O / 2>(v, lane);
+        } else {
+            v[0] += __shfl_xor(v[0], O);
+            wave_reduce_stage_bperm<1, O / 2>(v, lane);
+        }
+    }
+}
+
 template <int NV, typename T>
 __device__ __forceinline__ T wave_reduce_multi(T (&v)[NV], int lane) {
     static_assert(NV >= 1 && NV <= 64 && (NV & (NV - 1)) == 0, "power of two");

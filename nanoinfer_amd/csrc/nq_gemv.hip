@@ -48,7 +48,9 @@ constexpr int w8a8_rows_for() {
 
 // Wave-reduces the R x M accumulators and leaves the wave totals in
 // red[wave][r * M + i] (one exchange network for all of them).
-template <int R, int M, typename T>
+// BPERM: exchanges through ds_bpermute instead of DPP / row swaps (see
+// wave_reduce_stage_bperm), for the kernels whose all-VALU reduction spilled.
+template <int R, int M, bool BPERM = false, typename T>
 __device__ __forceinline__ void reduce_to_lds(T (&acc)[R][M], T* red, int wave, int lane) {
     constexpr int NV = R * M;
     if constexpr (NV == 1) {
@@ -62,7 +64,8 @@ __device__ __forceinline__ void reduce_to_lds(T (&acc)[R][M], T* red, int wave, 
         for (int r = 0; r < R; ++r)
 #pragma unroll
             for (int i = 0; i < M; ++i) v[r * M + i] = acc[r][i];
-        wave_reduce_multi<NV>(v, lane);
+        if constexpr (BPERM) wave_reduce_stage_bperm<NV, 32>(v, lane);
+        else wave_reduce_multi<NV>(v, lane);
         constexpr int G = 64 / NV;
         if (lane % G == 0) red[wave * NV + lane / G] = v[0];
     }
@@ -322,7 +325,10 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q4g_kernel(
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r][i] = act ? acc[r][i] : 0.0f;
     }
-    reduce_to_lds<R, M>(acc, red, wave, tid & 63);
+    // int4 batches of 8 rows (and 4 fp16 rows) spilled with the all-VALU
+    // exchanges (m = 8, k = 8960, n = 1536: 96 -> 12 us with ds_bpermute)
+    constexpr bool kBperm = R * M >= 16 || (M == 4 && sizeof(XT) == 2);
+    reduce_to_lds<R, M, kBperm>(acc, red, wave, tid & 63);
     __syncthreads();
     if (tid < R * M) {
         const int r = tid / M, i = tid % M, row = row0 + r;
@@ -832,9 +838,11 @@ void launch_q8(const XT* x, const int8_t* w, const float* ws, const float* b, YT
     const int chunks = k >> 4;
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
     constexpr int R = rows_for<M>();
-    if (q8_rows<M>(n) == 8 && R != 8) {
-        gemv_q8_kernel<8, M, XT, YT, AM><<<(n + 7) / 8, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part);
-        return;
+    if constexpr (M <= 2) {  // q8_rows: 8-row groups only for m <= 2
+        if (q8_rows<M>(n) == 8 && R != 8) {
+            gemv_q8_kernel<8, M, XT, YT, AM><<<(n + 7) / 8, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part);
+            return;
+        }
     }
     gemv_q8_kernel<R, M, XT, YT, AM><<<(n + R - 1) / R, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part);
 }
