@@ -121,6 +121,20 @@ nq_status nq_linear_q8(const void* x, nq_dtype x_dtype, const int8_t* q, const f
                        const float* bias, void* y, nq_dtype y_dtype, int64_t m, int64_t n,
                        int64_t k, void* stream);
 
+/* The same linears with a caller workspace: batched activations whose weight
+ * has too few rows to fill the GPU (small n, long k: m = 64, n = 1536, k = 8960)
+ * split K into ranges whose fp32 partial sums (one [m, n] plane per range) the
+ * workspace holds, then sum the planes in range order (deterministic). The
+ * split changes the fp32 summation order, not the arithmetic: the results
+ * agree with nq_linear_q8 / nq_linear_q4g to rounding. workspace: >=
+ * nq_linear_wq_workspace_size(m, n, k) bytes (0: the shape does not split, and
+ * NULL is accepted), 256-byte aligned. No counterpart in the reference, whose
+ * cuda_linear_q8 (cuda_quant.cu:300-322) takes no workspace. */
+size_t nq_linear_wq_workspace_size(int64_t m, int64_t n, int64_t k);
+nq_status nq_linear_q8_ws(const void* x, nq_dtype x_dtype, const int8_t* q, const float* w_scale,
+                          const float* bias, void* y, nq_dtype y_dtype, int64_t m, int64_t n, int64_t k,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- decoder-caller support (outside the quantized matrix path) ----------------
  * RoPE of the q and k heads of a fused q|k|v output (ops.cpp:120-166: half-split
  * tables, x*cos + rotate_half(x)*sin in fp32) written head-major q [heads, s, d],
@@ -183,6 +197,11 @@ nq_status nq_lm_head_argmax_q8(const void* x, nq_dtype x_dtype, const int8_t* q,
 nq_status nq_linear_q4g(const void* x, nq_dtype x_dtype, const uint8_t* q, const void* scale,
                         nq_dtype scale_dtype, int64_t group, const float* bias, void* y,
                         nq_dtype y_dtype, int64_t m, int64_t n, int64_t k, void* stream);
+/* nq_linear_q4g with the split-K workspace of nq_linear_q8_ws (same size rule). */
+nq_status nq_linear_q4g_ws(const void* x, nq_dtype x_dtype, const uint8_t* q, const void* scale,
+                           nq_dtype scale_dtype, int64_t group, const float* bias, void* y,
+                           nq_dtype y_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
+                           size_t workspace_bytes, void* stream);
 
 /* ---- W8A8 ------------------------------------------------------------------------
  * Replaces cuda_linear_w8a8 (cuda/cuda.hpp:41, cuda_quant.cu:250-284) and the CPU

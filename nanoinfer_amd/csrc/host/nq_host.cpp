@@ -48,7 +48,8 @@ nq_dtype abi_dtype(DType d) {
     return d == DType::F32 ? NQ_F32 : NQ_F16;
 }
 
-// Grow-only device workspace per (thread, device) for the W8A8 entry points.
+// Grow-only device workspace per (thread, device) for the W8A8 and split-K
+// weight-only entry points.
 struct Workspace {
     std::shared_ptr<void> buf;
     size_t bytes = 0;
@@ -250,9 +251,11 @@ Tensor linear_q8(const Tensor& x, const QTensor& w, const Tensor* bias, DType ou
     require(x.size(1) == w.in, "linear_q8: x cols must match weight in-features");
     const float* b = bias_ptr(bias, w.out, "linear_q8: bias must be a device fp32 tensor");
     Tensor y({x.size(0), w.out}, out_dtype, Device::HIP);
-    nq_check(nq_linear_q8(x.device_ptr(), abi_dtype(x.dtype()), static_cast<const int8_t*>(w.q.device_ptr()),
-                          static_cast<const float*>(w.scale.device_ptr()), b, y.device_ptr(),
-                          abi_dtype(out_dtype), x.size(0), w.out, w.in, g_stream));
+    const size_t need = nq_linear_wq_workspace_size(x.size(0), w.out, w.in);
+    void* ws = need ? workspace(need) : nullptr;
+    nq_check(nq_linear_q8_ws(x.device_ptr(), abi_dtype(x.dtype()), static_cast<const int8_t*>(w.q.device_ptr()),
+                             static_cast<const float*>(w.scale.device_ptr()), b, y.device_ptr(),
+                             abi_dtype(out_dtype), x.size(0), w.out, w.in, ws, need, g_stream));
     return y;
 }
 
@@ -274,9 +277,11 @@ Tensor linear_q4g(const Tensor& x, const Q4GTensor& w, const Tensor* bias, DType
     require(x.size(1) == w.in, "linear_q4g: x cols must match weight in-features");
     const float* b = bias_ptr(bias, w.out, "linear_q4g: bias must be a device fp32 tensor");
     Tensor y({x.size(0), w.out}, out_dtype, Device::HIP);
-    nq_check(nq_linear_q4g(x.device_ptr(), abi_dtype(x.dtype()), static_cast<const uint8_t*>(w.q.device_ptr()),
-                           w.scale.device_ptr(), abi_dtype(w.scale.dtype()), w.group, b, y.device_ptr(),
-                           abi_dtype(out_dtype), x.size(0), w.out, w.in, g_stream));
+    const size_t need = nq_linear_wq_workspace_size(x.size(0), w.out, w.in);
+    void* ws = need ? workspace(need) : nullptr;
+    nq_check(nq_linear_q4g_ws(x.device_ptr(), abi_dtype(x.dtype()), static_cast<const uint8_t*>(w.q.device_ptr()),
+                              w.scale.device_ptr(), abi_dtype(w.scale.dtype()), w.group, b, y.device_ptr(),
+                              abi_dtype(out_dtype), x.size(0), w.out, w.in, ws, need, g_stream));
     return y;
 }
 

@@ -25,7 +25,8 @@ bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m,
                 int64_t group);
 template <bool Q4, typename XT, typename YT, typename ST>
 nq_status wq_gemm(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int64_t m, int64_t n,
-                  int64_t k, int64_t group, hipStream_t s);
+                  int64_t k, int64_t group, void* workspace, size_t workspace_bytes, hipStream_t s);
+size_t wq_workspace_bytes(int64_t m, int64_t n, int64_t k);
 
 namespace {
 
@@ -1040,15 +1041,19 @@ bool gemv_w8a8_fused_launch(const void* x, nq_dtype xdt, const int8_t* w, const 
     return true;
 }
 
-}  // namespace nq
+namespace {
+// A workspace passed to the *_ws linears must hold the split-K planes the
+// shape plans (NULL / 0 bytes only where it plans none).
+nq_status check_wq_workspace(const void* ws, size_t bytes, int64_t m, int64_t n, int64_t k, const char* who) {
+    const size_t need = m > 0 && n > 0 ? wq_workspace_bytes(m, n, k) : 0;
+    NQ_REQUIRE(bytes >= need && (need == 0 || ws), NQ_BAD_ARG, "%s: workspace of %zu bytes, %zu needed", who, bytes, need);
+    NQ_REQUIRE(aligned(ws, 256), NQ_BAD_ALIGN, "%s: workspace must be 256-byte aligned", who);
+    return NQ_OK;
+}
 
-using namespace nq;
-
-extern "C" nq_status nq_linear_q8(const void* x, nq_dtype x_dtype, const int8_t* q,
-                                  const float* w_scale, const float* bias, void* y,
-                                  nq_dtype y_dtype, int64_t m, int64_t n, int64_t k,
-                                  void* stream) {
-    if (nq_status st = check_linear(x, q, y, m, n, k, "linear_q8")) return st;
+nq_status linear_q8_impl(const void* x, nq_dtype x_dtype, const int8_t* q, const float* w_scale, const float* bias,
+                         void* y, nq_dtype y_dtype, int64_t m, int64_t n, int64_t k, void* ws, size_t ws_bytes,
+                         void* stream) {
     NQ_REQUIRE(dtype_ok(x_dtype) && dtype_ok(y_dtype), NQ_BAD_ARG, "linear_q8: unknown dtype");
     if (m == 0 || n == 0) return NQ_OK;
     NQ_REQUIRE(w_scale, NQ_BAD_ARG, "linear_q8: null w_scale");
@@ -1062,12 +1067,12 @@ extern "C" nq_status nq_linear_q8(const void* x, nq_dtype x_dtype, const int8_t*
     if (wq_gemm_ok(false, x, dtype_size(x_dtype), q, m, n, k, 32)) {
         const uint8_t* w = reinterpret_cast<const uint8_t*>(q);
         if (x_dtype == NQ_F32 && y_dtype == NQ_F32)
-            return wq_gemm<false>(static_cast<const float*>(x), w, w_scale, bias, static_cast<float*>(y), m, n, k, 32, s);
+            return wq_gemm<false>(static_cast<const float*>(x), w, w_scale, bias, static_cast<float*>(y), m, n, k, 32, ws, ws_bytes, s);
         if (x_dtype == NQ_F32)
-            return wq_gemm<false>(static_cast<const float*>(x), w, w_scale, bias, static_cast<_Float16*>(y), m, n, k, 32, s);
+            return wq_gemm<false>(static_cast<const float*>(x), w, w_scale, bias, static_cast<_Float16*>(y), m, n, k, 32, ws, ws_bytes, s);
         if (y_dtype == NQ_F32)
-            return wq_gemm<false>(static_cast<const _Float16*>(x), w, w_scale, bias, static_cast<float*>(y), m, n, k, 32, s);
-        return wq_gemm<false>(static_cast<const _Float16*>(x), w, w_scale, bias, static_cast<_Float16*>(y), m, n, k, 32, s);
+            return wq_gemm<false>(static_cast<const _Float16*>(x), w, w_scale, bias, static_cast<float*>(y), m, n, k, 32, ws, ws_bytes, s);
+        return wq_gemm<false>(static_cast<const _Float16*>(x), w, w_scale, bias, static_cast<_Float16*>(y), m, n, k, 32, ws, ws_bytes, s);
     }
     const bool fast = k % 16 == 0 && k > 0 && k / 16 <= kMaxGemvThreads && aligned(q, 16) && aligned(x, 16);
     // Otherwise x rows beyond 8 run in slices of 8 (each slice re-streams the weight).
@@ -1099,11 +1104,9 @@ extern "C" nq_status nq_linear_q8(const void* x, nq_dtype x_dtype, const int8_t*
     return NQ_OK;
 }
 
-extern "C" nq_status nq_linear_q4g(const void* x, nq_dtype x_dtype, const uint8_t* q,
-                                   const void* scale, nq_dtype scale_dtype, int64_t group,
-                                   const float* bias, void* y, nq_dtype y_dtype, int64_t m,
-                                   int64_t n, int64_t k, void* stream) {
-    if (nq_status st = check_linear(x, q, y, m, n, k, "linear_q4g")) return st;
+nq_status linear_q4g_impl(const void* x, nq_dtype x_dtype, const uint8_t* q, const void* scale,
+                          nq_dtype scale_dtype, int64_t group, const float* bias, void* y, nq_dtype y_dtype,
+                          int64_t m, int64_t n, int64_t k, void* ws, size_t ws_bytes, void* stream) {
     NQ_REQUIRE(group > 0 && group <= kMaxIndex, NQ_BAD_SHAPE, "linear_q4g: group must be positive");
     NQ_REQUIRE(dtype_ok(x_dtype) && dtype_ok(y_dtype) && dtype_ok(scale_dtype), NQ_BAD_ARG,
                "linear_q4g: unknown dtype");
@@ -1119,8 +1122,8 @@ extern "C" nq_status nq_linear_q4g(const void* x, nq_dtype x_dtype, const uint8_
     if (wq_gemm_ok(true, x, dtype_size(x_dtype), q, m, n, k, group)) {
         auto go = [&](auto* xp, auto* yp) {
             if (scale_dtype == NQ_F32)
-                return wq_gemm<true>(xp, q, static_cast<const float*>(scale), bias, yp, m, n, k, group, s);
-            return wq_gemm<true>(xp, q, static_cast<const _Float16*>(scale), bias, yp, m, n, k, group, s);
+                return wq_gemm<true>(xp, q, static_cast<const float*>(scale), bias, yp, m, n, k, group, ws, ws_bytes, s);
+            return wq_gemm<true>(xp, q, static_cast<const _Float16*>(scale), bias, yp, m, n, k, group, ws, ws_bytes, s);
         };
         auto with_y = [&](auto* xp) {
             if (y_dtype == NQ_F32) return go(xp, static_cast<float*>(y));
@@ -1154,6 +1157,46 @@ extern "C" nq_status nq_linear_q4g(const void* x, nq_dtype x_dtype, const uint8_
         if (nq_status st = launch_status("gemv_q4g_kernel")) return st;
     }
     return NQ_OK;
+}
+}  // namespace
+}  // namespace nq
+
+using namespace nq;
+
+extern "C" nq_status nq_linear_q8(const void* x, nq_dtype x_dtype, const int8_t* q, const float* w_scale,
+                                  const float* bias, void* y, nq_dtype y_dtype, int64_t m, int64_t n, int64_t k,
+                                  void* stream) {
+    if (nq_status st = check_linear(x, q, y, m, n, k, "linear_q8")) return st;
+    return linear_q8_impl(x, x_dtype, q, w_scale, bias, y, y_dtype, m, n, k, nullptr, 0, stream);
+}
+
+extern "C" nq_status nq_linear_q4g(const void* x, nq_dtype x_dtype, const uint8_t* q, const void* scale,
+                                   nq_dtype scale_dtype, int64_t group, const float* bias, void* y,
+                                   nq_dtype y_dtype, int64_t m, int64_t n, int64_t k, void* stream) {
+    if (nq_status st = check_linear(x, q, y, m, n, k, "linear_q4g")) return st;
+    return linear_q4g_impl(x, x_dtype, q, scale, scale_dtype, group, bias, y, y_dtype, m, n, k, nullptr, 0, stream);
+}
+
+extern "C" size_t nq_linear_wq_workspace_size(int64_t m, int64_t n, int64_t k) {
+    return m > 0 && n > 0 && k > 0 && k <= kMaxIndex && n <= kMaxIndex ? wq_workspace_bytes(m, n, k) : 0;
+}
+
+extern "C" nq_status nq_linear_q8_ws(const void* x, nq_dtype x_dtype, const int8_t* q, const float* w_scale,
+                                     const float* bias, void* y, nq_dtype y_dtype, int64_t m, int64_t n, int64_t k,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+    if (nq_status st = check_linear(x, q, y, m, n, k, "linear_q8_ws")) return st;
+    if (nq_status st = check_wq_workspace(workspace, workspace_bytes, m, n, k, "linear_q8_ws")) return st;
+    return linear_q8_impl(x, x_dtype, q, w_scale, bias, y, y_dtype, m, n, k, workspace, workspace_bytes, stream);
+}
+
+extern "C" nq_status nq_linear_q4g_ws(const void* x, nq_dtype x_dtype, const uint8_t* q, const void* scale,
+                                      nq_dtype scale_dtype, int64_t group, const float* bias, void* y,
+                                      nq_dtype y_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+    if (nq_status st = check_linear(x, q, y, m, n, k, "linear_q4g_ws")) return st;
+    if (nq_status st = check_wq_workspace(workspace, workspace_bytes, m, n, k, "linear_q4g_ws")) return st;
+    return linear_q4g_impl(x, x_dtype, q, scale, scale_dtype, group, bias, y, y_dtype, m, n, k, workspace,
+                           workspace_bytes, stream);
 }
 
 // ---- LM head with fused greedy argmax ----------------------------------------------------

@@ -180,7 +180,8 @@ struct WFrag<false> {  // 8 int8 codes = two dwords, byte t of dword d = column 
 template <bool Q4, int TM, int TN, typename XT, typename YT, typename ST>
 __global__ __launch_bounds__(wq_waves<TM>() * 64) void gemm_wq_kernel(
     const XT* __restrict__ x, const uint8_t* __restrict__ wq, const ST* __restrict__ scale,
-    const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int group) {
+    const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int group, float* __restrict__ planes,
+    int split_chunks) {
     constexpr int kWqWaves = wq_waves<TM>();
     __shared__ f4 part[kWqWaves][TM][TN][64];
     // group / 32 is a power of two (checked on the host): chunk c uses group c >> gsh.
@@ -188,11 +189,14 @@ __global__ __launch_bounds__(wq_waves<TM>() * 64) void gemm_wq_kernel(
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, q = lane >> 4;
     const int n0 = blockIdx.x * (16 * TN);
+    const int m_all = m;
     // gridDim.y blocks of 64 activation rows
     x += static_cast<size_t>(blockIdx.y) * 64 * k;
     y += static_cast<size_t>(blockIdx.y) * 64 * n;
     m = min(64, m - static_cast<int>(blockIdx.y) * 64);
-    const int chunks = k >> 5;
+    // gridDim.z ranges of split_chunks chunks of K (one range without a split)
+    const int c_begin = blockIdx.z * split_chunks;
+    const int chunks = min(k >> 5, c_begin + split_chunks) - c_begin;
     const int rowb = Q4 ? (k >> 1) : k;  // weight bytes per row
     const int groups = Q4 ? k / group : 1;
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<XT*>(x), 0, m * k * static_cast<int>(sizeof(XT)), 0x00020000);
@@ -212,7 +216,7 @@ __global__ __launch_bounds__(wq_waves<TM>() * 64) void gemm_wq_kernel(
         so[j] = row < n ? row * groups * static_cast<int>(sizeof(ST)) : kOob;
     }
 
-    // Wave w takes chunks w, w + W, ...; steps = its count.
+    // Wave w takes chunks c_begin + w, + W, ...; steps = its count.
     const int steps = wave < chunks ? (chunks - wave + kWqWaves - 1) / kWqWaves : 0;
     struct Stage {
         XFrag<XT> xf[TM];
@@ -220,7 +224,7 @@ __global__ __launch_bounds__(wq_waves<TM>() * 64) void gemm_wq_kernel(
         float s[TN];
     };
     auto load = [&](int t, Stage& st) {
-        const int c = wave + t * kWqWaves;
+        const int c = c_begin + wave + t * kWqWaves;
         const bool in = t < steps;
 #pragma unroll
         for (int i = 0; i < TM; ++i)
@@ -317,38 +321,98 @@ __global__ __launch_bounds__(wq_waves<TM>() * 64) void gemm_wq_kernel(
         if (mm >= m || nn >= n) continue;
         float s = 0.0f;
         for (int w = 0; w < kWqWaves; ++w) s += part[w][i][j][l][v];
+        if (planes) {  // split K: this range's raw sum (Q8 before its row scale)
+            planes[(static_cast<size_t>(blockIdx.z) * m_all + blockIdx.y * 64 + mm) * n + nn] = s;
+            continue;
+        }
         if constexpr (!Q4) s *= to_f32(scale[nn]);
         y[static_cast<size_t>(mm) * n + nn] = from_f32<YT>(s + (bias ? bias[nn] : 0.0f));
     }
 }
 
+// Sums the split-K planes part[splits][m][n] (splits <= kWqMaxSplits) in plane
+// order, then the Q8 row scale and the bias, as the unsplit epilogue applies
+// them. All plane loads are issued before the first add (one latency, not one
+// per plane); four outputs per thread when n % 4 == 0.
+constexpr int kWqMaxSplits = 8;
+template <bool Q4, bool V4, typename YT, typename ST>
+__global__ __launch_bounds__(256) void wq_reduce_kernel(const float* __restrict__ part, int splits,
+                                                        const ST* __restrict__ scale, const float* __restrict__ bias,
+                                                        YT* __restrict__ y, int m, int n) {
+    const size_t mn = static_cast<size_t>(m) * n;
+    constexpr int V = V4 ? 4 : 1;
+    const size_t i0 = (static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x) * V;
+    if (i0 >= mn) return;
+    using VT = std::conditional_t<V4, f4, float>;
+    VT a[kWqMaxSplits];
+#pragma unroll
+    for (int sp = 0; sp < kWqMaxSplits; ++sp)
+        if (sp < splits) a[sp] = *reinterpret_cast<const VT*>(part + sp * mn + i0);
+    VT t = a[0];
+#pragma unroll
+    for (int sp = 1; sp < kWqMaxSplits; ++sp)
+        if (sp < splits) t += a[sp];
+    const int c0 = static_cast<int>(i0 % n);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        float r;
+        if constexpr (V4) r = t[v];
+        else r = t;
+        if constexpr (!Q4) r *= to_f32(scale[c0 + v]);
+        y[i0 + v] = from_f32<YT>(r + (bias ? bias[c0 + v] : 0.0f));
+    }
+}
+
+template <bool Q4, typename YT, typename ST>
+nq_status launch_wq_reduce(const float* planes, int splits, const ST* sc, const float* b, YT* y, int m, int n,
+                           hipStream_t s) {
+    const size_t mn = static_cast<size_t>(m) * n;
+    if (n % 4 == 0)
+        wq_reduce_kernel<Q4, true><<<static_cast<unsigned>((mn / 4 + 255) / 256), 256, 0, s>>>(planes, splits, sc, b, y, m, n);
+    else
+        wq_reduce_kernel<Q4, false><<<static_cast<unsigned>((mn + 255) / 256), 256, 0, s>>>(planes, splits, sc, b, y, m, n);
+    return launch_status("wq_reduce_kernel");
+}
+
+// Launch plan of the 16-row kernel: tm 16-row tiles of x (1..4), tn 16-row
+// tiles of the weight (1, 2), K in `splits` ranges of `per` chunks.
+struct WqRowPlan {
+    int tm, tn, splits, per;
+};
+
 template <bool Q4, typename XT, typename YT, typename ST>
 nq_status launch_wq(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n, int k,
-                    int g, hipStream_t s) {
+                    int g, WqRowPlan p, float* planes, hipStream_t s) {
     // 16 weight rows per workgroup, 32 for tall weights at m <= 32 (the LDS
     // tile of per-wave partials stays within 32 KB); 64-row blocks of x over
-    // gridDim.y.
+    // gridDim.y; K ranges over gridDim.z when planes are given.
+    if (!planes || p.splits <= 1) {
+        planes = nullptr;
+        p.splits = 1;
+        p.per = k / 32;
+    }
     const unsigned mblocks = static_cast<unsigned>((m + 63) / 64);
     auto go = [&](auto tmtag, auto tntag) {
         constexpr int TM = decltype(tmtag)::value, TN = decltype(tntag)::value;
-        const dim3 grid(static_cast<unsigned>((n + 16 * TN - 1) / (16 * TN)), mblocks);
-        gemm_wq_kernel<Q4, TM, TN, XT, YT, ST><<<grid, wq_waves<TM>() * 64, 0, s>>>(x, w, sc, b, y, m, n, k, g);
+        const dim3 grid(static_cast<unsigned>((n + 16 * TN - 1) / (16 * TN)), mblocks, static_cast<unsigned>(p.splits));
+        gemm_wq_kernel<Q4, TM, TN, XT, YT, ST><<<grid, wq_waves<TM>() * 64, 0, s>>>(x, w, sc, b, y, m, n, k, g, planes,
+                                                                                   p.per);
     };
     auto with_tn = [&](auto tmtag) {
         if constexpr (decltype(tmtag)::value <= 2) {
-            if (n > 4096) return go(tmtag, std::integral_constant<int, 2>{});
+            if (p.tn == 2) return go(tmtag, std::integral_constant<int, 2>{});
         }
         go(tmtag, std::integral_constant<int, 1>{});
     };
-    switch (m > 64 ? 4 : (m + 15) / 16) {
+    switch (p.tm) {
         case 1: with_tn(std::integral_constant<int, 1>{}); break;
         case 2: with_tn(std::integral_constant<int, 2>{}); break;
         case 3: with_tn(std::integral_constant<int, 3>{}); break;
         default: with_tn(std::integral_constant<int, 4>{}); break;
     }
-    return launch_status("gemm_wq_kernel");
+    if (nq_status st = launch_status("gemm_wq_kernel")) return st;
+    return planes ? launch_wq_reduce<Q4>(planes, p.splits, sc, b, y, m, n, s) : NQ_OK;
 }
-
 
 // ---- wide tiles for fp16 activations -----------------------------------------------------
 // One (16*WM*FM) x (16*WN*FN) output tile per workgroup, WM x WN waves (4 x 2,
@@ -416,7 +480,7 @@ template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST, ty
 __global__ __launch_bounds__(WM * WN * 64) void gemm_wq_wide_kernel(
     const XT* __restrict__ x, const uint8_t* __restrict__ wq, const ST* __restrict__ scale,
     const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int tiles_m, int tiles_n,
-    int gsh_rt) {
+    int gsh_rt, float* __restrict__ planes, int split_slabs) {
     using S = WqWideShape<Q4, SK, FM, FN, GSH, YT, ST, XT, WN, WM>;
     constexpr int NW = S::kNW;
     constexpr bool F32X = sizeof(XT) == 4;  // fp32 activations: three bf16 parts, three bf16 MFMAs
@@ -467,12 +531,14 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_wq_wide_kernel(
         soffv[q] = b < S::kNS && n0 + r < n ? (n0 + r) * groups * static_cast<int>(sizeof(ST)) + (lane % LPR) * 4 : kOob;
         sloff[q] = b < S::kNS ? S::kSOff + b * 256 : S::kSink;
     }
-    const int nk = k / SK;
+    // gridDim.y ranges of split_slabs slabs of K (one range without a split)
+    const int kb = blockIdx.y * split_slabs;
+    const int nk = min(k / SK, kb + split_slabs) - kb;
     const unsigned lds_base = static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds));
     auto issue = [&](int sl) {
         const unsigned slot = static_cast<unsigned>(sl % D) * S::kSlab;
         const bool in = sl < nk;
-        const int xo = in ? sl * XROW : kOob, wo = in ? sl * WROW : kOob;
+        const int xo = in ? (kb + sl) * XROW : kOob, wo = in ? (kb + sl) * WROW : kOob;
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
             const int b = q * NW + wave;
@@ -486,7 +552,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_wq_wide_kernel(
         }
         if constexpr (Q4) {
             // the slab's first group (its groups are consecutive in the row)
-            const int so = in ? ((sl * T) >> gsh) * static_cast<int>(sizeof(ST)) : kOob;
+            const int so = in ? (((kb + sl) * T) >> gsh) * static_cast<int>(sizeof(ST)) : kOob;
 #pragma unroll
             for (int q = 0; q < QS; ++q) {
                 const int b = q * NW + wave;
@@ -612,6 +678,22 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_wq_wide_kernel(
 
     // Lane l holds, for fragment (i, j), rows m0 + wm*16*FM + j*16 + 4*(l/16) + v
     // of column n0 + wn*16*FN + i*16 + l%16.
+    if (planes) {  // split K: this range's raw sums (Q8 before its row scale) into plane blockIdx.y
+        float* pl = planes + static_cast<size_t>(blockIdx.y) * m * n;
+#pragma unroll
+        for (int i = 0; i < FN; ++i) {
+            const int col = n0 + fwr[i];
+            if (col >= n) continue;
+#pragma unroll
+            for (int j = 0; j < FM; ++j)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int row = m0 + fxo[j] - fr + 4 * fq + v;
+                    if (row < m) pl[static_cast<size_t>(row) * n + col] = acc[i][j][v];
+                }
+        }
+        return;
+    }
     if constexpr (sizeof(YT) == 2) {
         if ((n & 7) == 0) {
             __syncthreads();  // every wave is done with the ring
@@ -663,12 +745,12 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_wq_wide_kernel(
 
 template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST, typename XT, int WN, int WM = 4>
 nq_status launch_wq_wide(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n,
-                         int k, int gsh, hipStream_t s) {
+                         int k, int gsh, float* planes, int splits, int split_slabs, hipStream_t s) {
     using S = WqWideShape<Q4, SK, FM, FN, GSH, YT, ST, XT, WN, WM>;
     auto* fn = gemm_wq_wide_kernel<Q4, SK, FM, FN, GSH, YT, ST, XT, WN, WM>;
     if (nq_status st = set_dynamic_lds(reinterpret_cast<const void*>(fn), S::kLds, "gemm_wq_wide")) return st;
     const int tm = (m + S::kBM - 1) / S::kBM, tn = (n + S::kBN - 1) / S::kBN;
-    fn<<<tm * tn, S::kNW * 64, S::kLds, s>>>(x, w, sc, b, y, m, n, k, tm, tn, gsh);
+    fn<<<dim3(tm * tn, splits), S::kNW * 64, S::kLds, s>>>(x, w, sc, b, y, m, n, k, tm, tn, gsh, planes, split_slabs);
     return launch_status("gemm_wq_wide_kernel");
 }
 
@@ -715,10 +797,9 @@ bool wq_sk64_ok(int64_t group) {
 }
 
 template <bool Q4, typename XT, typename YT, typename ST>
-nq_status wq_wide(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n, int k,
-                  int group, hipStream_t s) {
+nq_status wq_wide_tiles(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n, int k,
+                        int group, WqTile pick, float* planes, int splits, int split_slabs, hipStream_t s) {
     constexpr bool F32X = sizeof(XT) == 4;
-    const WqTile pick = plan_wq_wide(m, n, wq_sk64_ok<Q4, ST>(group), F32X).tile;
     const int gsh = Q4 ? __builtin_ctz(static_cast<unsigned>(group >> 5)) : 0;
     // Q8 tile widths that split in three (four) 16-column multiples run 12 (16)
     // waves, as in the W8A8 wide kernel (m = 2048: 74.3 -> 71.7 us); Q4G keeps 8
@@ -732,20 +813,20 @@ nq_status wq_wide(const XT* x, const uint8_t* w, const ST* sc, const float* b, Y
             // 256-row Q8 tiles as 2 x 6 waves of (128 x 16 * FN2 / 3): each
             // weight fragment is converted to fp16 by two waves instead of four
             // (the conversion is a third of the MFMA time; m = 2048: 66.1 -> 63.7 us).
-            return launch_wq_wide<false, SK, 8, FN2 / 3, 0, YT, ST, XT, 6, 2>(x, w, sc, b, y, m, n, k, 0, s);
+            return launch_wq_wide<false, SK, 8, FN2 / 3, 0, YT, ST, XT, 6, 2>(x, w, sc, b, y, m, n, k, 0, planes, splits, split_slabs, s);
         }
         if constexpr (!Q4) {
-            return launch_wq_wide<false, SK, FM, FN, 0, YT, ST, XT, WN>(x, w, sc, b, y, m, n, k, 0, s);
+            return launch_wq_wide<false, SK, FM, FN, 0, YT, ST, XT, WN>(x, w, sc, b, y, m, n, k, 0, planes, splits, split_slabs, s);
         } else {
-            if (gsh == 0) return launch_wq_wide<true, SK, FM, FN, 0, YT, ST, XT, WN>(x, w, sc, b, y, m, n, k, 0, s);
+            if (gsh == 0) return launch_wq_wide<true, SK, FM, FN, 0, YT, ST, XT, WN>(x, w, sc, b, y, m, n, k, 0, planes, splits, split_slabs, s);
             if constexpr (SK == 64) {  // excluded by wq_sk64_ok
                 return fail(NQ_BAD_ARG, "gemm_wq_wide: 64-column slabs take groups of 32 only (got %d)", group);
             } else {
-                if (gsh == 1) return launch_wq_wide<true, SK, FM, FN, 1, YT, ST, XT, WN>(x, w, sc, b, y, m, n, k, 1, s);
+                if (gsh == 1) return launch_wq_wide<true, SK, FM, FN, 1, YT, ST, XT, WN>(x, w, sc, b, y, m, n, k, 1, planes, splits, split_slabs, s);
                 if constexpr (sizeof(ST) == 2) {  // excluded by wq_wide_ok
                     return fail(NQ_BAD_ARG, "gemm_wq_wide: fp16 scales in groups of %d are not supported", group);
                 } else {
-                    return launch_wq_wide<true, SK, FM, FN, BIG, YT, ST, XT, WN>(x, w, sc, b, y, m, n, k, gsh, s);
+                    return launch_wq_wide<true, SK, FM, FN, BIG, YT, ST, XT, WN>(x, w, sc, b, y, m, n, k, gsh, planes, splits, split_slabs, s);
                 }
             }
         }
@@ -777,6 +858,20 @@ nq_status wq_wide(const XT* x, const uint8_t* w, const ST* sc, const float* b, Y
     }
 }
 
+template <bool Q4, typename XT, typename YT, typename ST>
+nq_status wq_wide(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n, int k,
+                  int group, WqTile pick, float* planes, int splits, int split_slabs, hipStream_t s) {
+    if (!planes || splits <= 1) {  // no planes: one range over all of K
+        planes = nullptr;
+        splits = 1;
+        split_slabs = k / pick.sk;
+    }
+    if (nq_status st = wq_wide_tiles<Q4>(x, w, sc, b, y, m, n, k, group, pick, splits > 1 ? planes : nullptr, splits,
+                                         split_slabs, s))
+        return st;
+    return splits > 1 ? launch_wq_reduce<Q4>(planes, splits, sc, b, y, m, n, s) : NQ_OK;
+}
+
 // The wide path's contract: k % 128 == 0, 32-bit offsets, for Q4G fp16 scales
 // groups of 32 or 64 columns (a slab's scales are whole dwords), fp32 scales
 // any power-of-two multiple of 32; fp32 activations (split into an fp16 high
@@ -788,16 +883,85 @@ nq_status wq_wide(const XT* x, const uint8_t* w, const ST* sc, const float* b, Y
 // m = 128 38.4 -> 17.9; m = 64, n = 1536 (24 tiles) 9.2 vs 11.8; long K with
 // few tiles, m = 64, n = 1536, k = 8960: 40.4 vs 53.6).
 template <bool Q4, typename XT, typename ST>
-bool wq_wide_ok(int64_t m, int64_t n, int64_t k, int64_t group) {
+bool wq_wide_contract(int64_t m, int64_t n, int64_t k, int64_t group) {
     constexpr bool F32X = sizeof(XT) == 4;
     if (F32X && !wq_sk64_ok<Q4, ST>(group)) return false;
-    if (m < 32 || (m <= 128 && plan_wq_wide(m, n, wq_sk64_ok<Q4, ST>(group), F32X).tiles < 128)) return false;
     if (k % 128 != 0 || m * k * static_cast<int64_t>(sizeof(XT)) >= (int64_t(1) << 31) - 64) return false;
     if (!Q4) return n * k < (int64_t(1) << 31) - 64;
     if (sizeof(ST) == 2 && group != 32 && group != 64) return false;
     return n * (k / 2) < (int64_t(1) << 31) - 64 && n * (k / group) * int64_t(sizeof(ST)) < (int64_t(1) << 31) - 64;
 }
+template <bool Q4, typename XT, typename ST>
+bool wq_wide_ok(int64_t m, int64_t n, int64_t k, int64_t group) {
+    if (m < 32 || (m <= 128 && plan_wq_wide(m, n, wq_sk64_ok<Q4, ST>(group), sizeof(XT) == 4).tiles < 128)) return false;
+    return wq_wide_contract<Q4, XT, ST>(m, n, k, group);
+}
+
+// Split-K, when the caller gives a workspace for the fp32 partial planes. A
+// weight with few rows leaves most CUs idle, each workgroup walking all of K,
+// so long K splits into up to kWqMaxSplits ranges summed by wq_reduce_kernel
+// (about 3 us more: a second launch and the planes' traffic). Measured with
+// fp16 x (us, unsplit -> split): n = 1536, k = 8960: m = 16 20.6 -> 14.9
+// (16-row kernel), m = 64 43.5 -> 17.3 (wide 64 x 64 tiles, 8 ranges), m = 128
+// 42.7 -> 21.3 (64 x 128 tiles); n = 896, k = 4864, m = 64: 25.1 -> 13.7; n =
+// 256, k = 1536, m = 64: 10.5 -> 9.3. Short K with a hundred or more
+// workgroups lost (n = 1536, k = 1536, m = 64: 10.7 -> 11.6), and so did a
+// 16-row grid that already fills the CUs (n = 4096, k = 4096, m = 16: 11.8 ->
+// 16.0): those stay whole. Wide split: m > 32, k >= 4096, at most 256
+// workgroups (one per CU, as their LDS ring takes) of at least kWqMinSlabs
+// slabs each. 16-row split: under 256 workgroups unsplit, k >= 4096 (or at
+// most 32 workgroups and m > 32 or fp32 x), about kWqRowSplitWgs workgroups,
+// each wave with at least two chunks of its range.
+constexpr int kWqRowSplitWgs = 1024, kWqWideSplitWgs = 256, kWqMinSlabs = 4;
+struct WqRoute {
+    bool wide;
+    WqTile tile;         // wide
+    int splits, per;     // K ranges and slabs (wide) or chunks (16-row) per range
+    WqRowPlan row;       // 16-row
+};
+WqRoute plan_wq_route(int64_t m, int64_t n, int64_t k, bool wide_ok, bool wide_contract, bool sk64_ok, bool f32x,
+                      bool allow_split) {
+    WqRoute r{};
+    if (wide_ok) {
+        r.wide = true;
+        r.tile = plan_wq_wide(m, n, sk64_ok, f32x).tile;
+        r.splits = 1;
+        r.per = static_cast<int>(k / r.tile.sk);
+        return r;
+    }
+    if (allow_split && wide_contract && m > 32 && m <= 128 && k >= 4096) {
+        const WqTile t{1, m <= 64 ? 2 : 4, f32x ? 64 : 128};
+        const int64_t tiles = ((m + 63) / 64) * ((n + 32 * t.fn - 1) / (32 * t.fn)), nk = k / t.sk;
+        const int64_t sp = std::min<int64_t>({kWqMaxSplits, kWqWideSplitWgs / tiles, nk / kWqMinSlabs});
+        if (sp >= 2) {
+            const int64_t per = (nk + sp - 1) / sp;
+            r.wide = true;
+            r.tile = t;
+            r.per = static_cast<int>(per);
+            r.splits = static_cast<int>((nk + per - 1) / per);
+            return r;
+        }
+    }
+    WqRowPlan& p = r.row;
+    p.tm = m > 64 ? 4 : static_cast<int>((m + 15) / 16);
+    p.tn = p.tm <= 2 && n > 4096 ? 2 : 1;
+    const int64_t chunks = k / 32, waves = p.tm == 1 ? 16 : 8;
+    const int64_t wgs = (n + 16 * p.tn - 1) / (16 * p.tn) * ((m + 63) / 64);
+    int64_t sp = 1;
+    if (allow_split && wgs < 256 && (k >= 4096 || (wgs <= 32 && (m > 32 || f32x))))
+        sp = std::max<int64_t>(1, std::min<int64_t>({(kWqRowSplitWgs + wgs - 1) / wgs, kWqMaxSplits, chunks / (2 * waves)}));
+    p.per = static_cast<int>((chunks + sp - 1) / sp);
+    p.splits = static_cast<int>((chunks + p.per - 1) / p.per);
+    r.splits = p.splits;
+    r.per = p.per;
+    return r;
+}
+size_t wq_route_bytes(const WqRoute& r, int64_t m, int64_t n) {
+    return r.splits > 1 ? round_up(static_cast<size_t>(r.splits) * static_cast<size_t>(m) * static_cast<size_t>(n) * 4, 256) : 0;
+}
 }  // namespace
+
+bool wq_gemm_shape_ok(int64_t m, int64_t n) { return m > 8 && (m >= 16 || n >= 4096); }
 
 // Whether the MFMA path takes this call (the caller runs GEMV slices otherwise):
 // whole 32-column chunks, groups of a power-of-two number of chunks, 16-byte aligned operands and
@@ -808,7 +972,7 @@ bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m,
     // Shape rule (measured): the GEMM runs one workgroup per 16 (or 32) weight
     // rows, each reading all of x, so below 4096 rows it fills under 256 CUs; a
     // GEMV slice of 8 rows plus a remainder slice is then faster up to m = 15.
-    if (m <= 8 || (m < 16 && n < 4096)) return false;
+    if (!wq_gemm_shape_ok(m, n)) return false;
     return k > 0 && k % 32 == 0 && (!q4 || (group % 32 == 0 && ((group / 32) & (group / 32 - 1)) == 0)) && aligned(x, 16) && aligned(w, 16) &&
            m <= (int64_t(65535) * 64) && std::min<int64_t>(m, 64) * k * static_cast<int64_t>(x_elem) < (int64_t(1) << 31) - 64 &&
            n * rowb < (int64_t(1) << 31) - 64;
@@ -818,17 +982,32 @@ bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m,
 // streams the weight once).
 template <bool Q4, typename XT, typename YT, typename ST>
 nq_status wq_gemm(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int64_t m, int64_t n,
-                  int64_t k, int64_t group, hipStream_t s) {
-    if (wq_wide_ok<Q4, XT, ST>(m, n, k, group))
-        return wq_wide<Q4>(x, w, sc, b, y, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
-                           static_cast<int>(group), s);
-    return launch_wq<Q4>(x, w, sc, b, y, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
-                         static_cast<int>(group), s);
+                  int64_t k, int64_t group, void* workspace, size_t workspace_bytes, hipStream_t s) {
+    const bool sk64 = wq_sk64_ok<Q4, ST>(group), f32x = sizeof(XT) == 4;
+    const bool wide_ok = wq_wide_ok<Q4, XT, ST>(m, n, k, group), contract = wq_wide_contract<Q4, XT, ST>(m, n, k, group);
+    WqRoute r = plan_wq_route(m, n, k, wide_ok, contract, sk64, f32x, workspace != nullptr);
+    if (r.splits > 1 && workspace_bytes < wq_route_bytes(r, m, n))
+        r = plan_wq_route(m, n, k, wide_ok, contract, sk64, f32x, false);
+    float* planes = r.splits > 1 ? static_cast<float*>(workspace) : nullptr;
+    const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k), gi = static_cast<int>(group);
+    if (r.wide) return wq_wide<Q4>(x, w, sc, b, y, mi, ni, ki, gi, r.tile, planes, r.splits, r.per, s);
+    return launch_wq<Q4>(x, w, sc, b, y, mi, ni, ki, gi, r.row, planes, s);
+}
+
+// Workspace the split-K planes take at this shape (0: no split): the most any
+// activation dtype or group size can plan, so one size serves every call.
+size_t wq_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+    if (m <= 0 || n <= 0 || k <= 0 || !wq_gemm_shape_ok(m, n)) return 0;
+    size_t most = 0;
+    for (int f32x = 0; f32x < 2; ++f32x)
+        for (int contract = 0; contract < 2; ++contract)
+            most = std::max(most, wq_route_bytes(plan_wq_route(m, n, k, false, contract, true, f32x, true), m, n));
+    return most;
 }
 
 #define NQ_WQ_INST(Q4, XT, YT, ST)                                                                          \
     template nq_status wq_gemm<Q4, XT, YT, ST>(const XT*, const uint8_t*, const ST*, const float*, YT*, \
-                                               int64_t, int64_t, int64_t, int64_t, hipStream_t);
+                                               int64_t, int64_t, int64_t, int64_t, void*, size_t, hipStream_t);
 NQ_WQ_INST(false, float, float, float)
 NQ_WQ_INST(false, float, _Float16, float)
 NQ_WQ_INST(false, _Float16, float, float)

@@ -247,25 +247,34 @@ def _x2d(x, w_in, who):
 
 
 def linear_q8(x: torch.Tensor, w: QTensor, bias=None, out_dtype=None) -> torch.Tensor:
-    """quant.cpp:136-163 / cuda_quant.cu:300-322."""
+    """quant.cpp:136-163 / cuda_quant.cu:300-322. Batched shapes whose weight
+    has too few rows to fill the GPU split K over a workspace from torch's
+    allocator (nq_linear_q8_ws)."""
     w.check()
     x = _x2d(x, w.in_, "linear_q8")
     b = _bias(bias, w.out)
     y = torch.empty((x.shape[0], w.out), dtype=out_dtype or x.dtype, device=x.device)
-    check(_lib.load().nq_linear_q8(_ptr(x), _dtype_code(x, "x"), _ptr(w.q), _ptr(w.scale), _ptr(b),
-                                   _ptr(y), _dtype_code(y, "y"), x.shape[0], w.out, w.in_, _stream()))
+    lib = _lib.load()
+    nbytes = lib.nq_linear_wq_workspace_size(x.shape[0], w.out, w.in_)
+    ws = _workspace(nbytes, x.device) if nbytes else None
+    check(lib.nq_linear_q8_ws(_ptr(x), _dtype_code(x, "x"), _ptr(w.q), _ptr(w.scale), _ptr(b), _ptr(y),
+                              _dtype_code(y, "y"), x.shape[0], w.out, w.in_, _ptr(ws), nbytes, _stream()))
     return y
 
 
 def linear_q4g(x: torch.Tensor, w: Q4GTensor, bias=None, out_dtype=None) -> torch.Tensor:
-    """quant.cpp:337-389 (no GPU counterpart in the reference)."""
+    """quant.cpp:337-389 (no GPU counterpart in the reference); split K as
+    linear_q8 does (nq_linear_q4g_ws)."""
     w.check()
     x = _x2d(x, w.in_, "linear_q4g")
     b = _bias(bias, w.out)
     y = torch.empty((x.shape[0], w.out), dtype=out_dtype or x.dtype, device=x.device)
-    check(_lib.load().nq_linear_q4g(_ptr(x), _dtype_code(x, "x"), _ptr(w.q), _ptr(w.scale),
-                                    _dtype_code(w.scale, "scale"), w.group, _ptr(b), _ptr(y),
-                                    _dtype_code(y, "y"), x.shape[0], w.out, w.in_, _stream()))
+    lib = _lib.load()
+    nbytes = lib.nq_linear_wq_workspace_size(x.shape[0], w.out, w.in_)
+    ws = _workspace(nbytes, x.device) if nbytes else None
+    check(lib.nq_linear_q4g_ws(_ptr(x), _dtype_code(x, "x"), _ptr(w.q), _ptr(w.scale),
+                               _dtype_code(w.scale, "scale"), w.group, _ptr(b), _ptr(y), _dtype_code(y, "y"),
+                               x.shape[0], w.out, w.in_, _ptr(ws), nbytes, _stream()))
     return y
 
 

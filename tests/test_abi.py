@@ -81,6 +81,29 @@ def test_w8a8_workspace_too_small(lib):
     assert lib.nq_linear_w8a8_workspace_size(0, 5, 5) == 0
 
 
+def test_weight_only_split_workspace_rules(lib):
+    """The split-K linears need the planes nq_linear_wq_workspace_size gives
+    (checked before any launch); shapes that do not split take none."""
+    from nanoinfer_amd import _lib as L
+    fake = ctypes.c_void_p(0x1000)
+    need = lib.nq_linear_wq_workspace_size(64, 1536, 8960)
+    assert need >= 2 * 64 * 1536 * 4 and need % 256 == 0
+    assert lib.nq_linear_q8_ws(fake, 1, fake, fake, None, fake, 1, 64, 1536, 8960, fake, need - 256,
+                               None) == L.NQ_BAD_ARG
+    assert b"workspace" in lib.nq_last_error()
+    assert lib.nq_linear_q4g_ws(fake, 1, fake, fake, 1, 32, None, fake, 1, 64, 1536, 8960, None, 0,
+                                None) == L.NQ_BAD_ARG
+    odd = ctypes.c_void_p(0x1010)
+    assert lib.nq_linear_q8_ws(fake, 1, fake, fake, None, fake, 1, 64, 1536, 8960, odd, need,
+                               None) == L.NQ_BAD_ALIGN
+    # decode-sized m and short K with a full grid: no planes
+    assert lib.nq_linear_wq_workspace_size(1, 1536, 8960) == 0
+    assert lib.nq_linear_wq_workspace_size(8, 1536, 8960) == 0
+    assert lib.nq_linear_wq_workspace_size(64, 1536, 1536) == 0
+    assert lib.nq_linear_wq_workspace_size(0, 1536, 8960) == 0
+    assert lib.nq_linear_q8_ws(fake, 1, fake, fake, None, fake, 1, 0, 1536, 8960, None, 0, None) == L.NQ_OK
+
+
 def test_embedding_rejects_out_of_range_id(lib):
     from nanoinfer_amd import _lib as L
     fake = ctypes.c_void_p(0x1000)

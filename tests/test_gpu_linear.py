@@ -274,6 +274,56 @@ def test_weight_only_q8_wide_2x6(dev, nq, orc, m, n, k, bias):
     assert_close_rms(host(y[:128]), host(y16), f"q8 wide 2x6 vs 16-row kernel {m}x{n}x{k}")
 
 
+# Split K over a workspace (nq_linear_q8_ws / nq_linear_q4g_ws, which the
+# Python linears call): weights with few rows at batched m run K in ranges whose
+# fp32 planes a reduce kernel sums in order. 16-row kernel splits (m <= 32, or
+# short K with a tiny grid), wide 64-row tile splits (32 < m <= 128, k >= 4096;
+# fp32 x takes 64-column slabs), ragged m and n (n % 4 != 0: the scalar reduce),
+# fp16 / fp32 scales, group 128 (one scale per slab). Against the oracle, and
+# against the unsplit entry point on the same inputs.
+WQ_SPLIT_CASES = [
+    ("q8", 16, 896, 4864, 0, False, F16, F32, F16),
+    ("q4g", 24, 1536, 8960, 32, True, F32, F16, F32),
+    ("q8", 48, 896, 4864, 0, True, F32, F32, F16),
+    ("q4g", 64, 1536, 8960, 32, False, F16, F16, F32),
+    ("q4g", 100, 896, 4864, 128, True, F16, F32, F16),
+    ("q8", 128, 2048, 8192, 0, False, F16, F32, F32),
+    ("q8", 40, 256, 1536, 0, True, F32, F32, F32),
+    ("q4g", 72, 202, 1536, 64, False, F16, F16, F16),
+    ("q8", 97, 1001, 4096, 0, True, F16, F32, F16),
+]
+
+
+@pytest.mark.parametrize("mode,m,n,k,g,bias,xdt,sdt,ydt", WQ_SPLIT_CASES)
+def test_weight_only_split_k(dev, nq, orc, mode, m, n, k, g, bias, xdt, sdt, ydt):
+    from nanoinfer_amd import _lib
+    lib = _lib.load()
+    nbytes = lib.nq_linear_wq_workspace_size(m, n, k)
+    assert nbytes > 0, "shape must plan a split"
+    x, w, b = data(m, n, k, m * 13 + n + k, bias=bias)
+    xd = to_dev(x, dev, xdt)
+    bd = None if b is None else to_dev(b, dev)
+    xo = host(xd.float())
+    y0 = torch.empty((m, n), dtype=ydt, device=dev)
+    xc, yc = (1 if xdt == F16 else 0), (1 if ydt == F16 else 0)
+    s = torch.cuda.current_stream().cuda_stream
+    P = lambda t: None if t is None else t.data_ptr()
+    if mode == "q8":
+        t = nq.quantize_q8(to_dev(w, dev))
+        y = nq.linear_q8(xd, t, bd, out_dtype=ydt)
+        _lib.check(lib.nq_linear_q8(P(xd), xc, P(t.q), P(t.scale), P(bd), P(y0), yc, m, n, k, s))
+        q, sc = orc.quantize_q8(w)
+        ref = orc.linear_q8(xo, q, sc, b)
+    else:
+        t = nq.quantize_q4g(to_dev(w, dev), g, scale_dtype=sdt)
+        y = nq.linear_q4g(xd, t, bd, out_dtype=ydt)
+        _lib.check(lib.nq_linear_q4g(P(xd), xc, P(t.q), P(t.scale), 0 if sdt == F32 else 1, g, P(bd), P(y0),
+                                     yc, m, n, k, s))
+        ref = orc.linear_q4g(xo, host(t.q), host(t.scale.float()), g, b)
+    assert_close_rms(host(y.float()), ref, f"{mode} split {m}x{n}x{k}", fp16_out=(ydt == F16))
+    assert_close_rms(host(y.float()), host(y0.float()), f"{mode} split vs whole {m}x{n}x{k}", fp16_out=(ydt == F16))
+
+
 # fp32 activations far outside fp16's range and deep in its subnormals, on both
 # weight-only MFMA kernels (16-row tiles: k % 128 != 0 or small m; wide tiles:
 # m > 128, k % 128 == 0): the exact bf16 split keeps every row at the accuracy of
