@@ -830,8 +830,22 @@ inline int m_bucket(int64_t m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8
 // Rows per workgroup of the q8 GEMV. Very tall weights (an LM head) have
 // workgroups to spare: 8 rows per workgroup halves the activation re-reads
 // (measured 38.5 -> 36 us at n = 151936, k = 1536; 4 rows stay best at n = 4864).
-template <int M>
-int q8_rows(int n) { return (M <= 2 && n >= 32768) ? 8 : rows_for<M>(); }
+//
+// fp32 activations at m = 5..8: each workgroup reads all m rows of x (16 bytes
+// of codes per lane meet 8 x 64 bytes of x), so the x re-reads rather than the
+// weight bound the 2-row grid; 4 or 8 rows per workgroup cut them (measured, us,
+// 2 -> 4 -> 8 rows, m = 8: n = 1536, k = 8960 24.1 -> 19.8 -> 15.6; n = 8960, k =
+// 1536 20.2 -> 14.7 -> 13.4; n = 4864, k = 896 7.38 -> 6.35 -> 6.55; n = 896, k =
+// 4864 8.42 -> 7.61 -> 9.38; n = k = 1536 5.52 -> 5.65 -> 6.15). fp16 x keeps 2.
+template <int M, typename XT>
+int q8_rows(int n, int k) {
+    if (M <= 2 && n >= 32768) return 8;
+    if (M == 8 && sizeof(XT) == 4) {
+        const int64_t nk = static_cast<int64_t>(n) * k;
+        return nk >= (int64_t(8) << 20) ? 8 : nk >= (int64_t(3) << 20) ? 4 : 2;
+    }
+    return rows_for<M>();
+}
 
 template <int M, bool AM = false, typename XT, typename YT>
 void launch_q8(const XT* x, const int8_t* w, const float* ws, const float* b, YT* y, int m, int n,
@@ -839,9 +853,16 @@ void launch_q8(const XT* x, const int8_t* w, const float* ws, const float* b, YT
     const int chunks = k >> 4;
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
     constexpr int R = rows_for<M>();
-    if constexpr (M <= 2) {  // q8_rows: 8-row groups only for m <= 2
-        if (q8_rows<M>(n) == 8 && R != 8) {
+    const int rows = q8_rows<M, XT>(n, k);
+    if constexpr (M <= 2 || (M == 8 && sizeof(XT) == 4)) {  // the other row counts q8_rows picks
+        if (rows == 8 && R != 8) {
             gemv_q8_kernel<8, M, XT, YT, AM><<<(n + 7) / 8, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part);
+            return;
+        }
+    }
+    if constexpr (M == 8 && sizeof(XT) == 4) {
+        if (rows == 4) {
+            gemv_q8_kernel<4, M, XT, YT, AM><<<(n + 3) / 4, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part);
             return;
         }
     }
@@ -1262,10 +1283,10 @@ extern "C" nq_status nq_lm_head_argmax_q8(const void* x, nq_dtype x_dtype, const
             const XT* xs = xp + static_cast<size_t>(r0) * k;
             float* none = nullptr;
             switch (m_bucket(mi)) {
-                case 1: nwg = (ni + q8_rows<1>(ni) - 1) / q8_rows<1>(ni); launch_q8<1, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part); break;
-                case 2: nwg = (ni + q8_rows<2>(ni) - 1) / q8_rows<2>(ni); launch_q8<2, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part); break;
-                case 4: nwg = (ni + q8_rows<4>(ni) - 1) / q8_rows<4>(ni); launch_q8<4, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part); break;
-                default: nwg = (ni + q8_rows<8>(ni) - 1) / q8_rows<8>(ni); launch_q8<8, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part); break;
+                case 1: nwg = (ni + q8_rows<1, XT>(ni, ki) - 1) / q8_rows<1, XT>(ni, ki); launch_q8<1, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part); break;
+                case 2: nwg = (ni + q8_rows<2, XT>(ni, ki) - 1) / q8_rows<2, XT>(ni, ki); launch_q8<2, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part); break;
+                case 4: nwg = (ni + q8_rows<4, XT>(ni, ki) - 1) / q8_rows<4, XT>(ni, ki); launch_q8<4, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part); break;
+                default: nwg = (ni + q8_rows<8, XT>(ni, ki) - 1) / q8_rows<8, XT>(ni, ki); launch_q8<8, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part); break;
             }
         };
         if (x_dtype == NQ_F32) go(static_cast<const float*>(x));

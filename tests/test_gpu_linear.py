@@ -35,6 +35,9 @@ Q8_CASES = [
     (16, 896, 896, True, F32, F16),       # m > 8: slices of 8 rows
     (100, 896, 4864, False, F32, F32),    # :440 ragged m, wide k
     (5, 64, 16384, False, F32, F32),      # k beyond one workgroup (generic)
+    (8, 1536, 8960, True, F32, F32),      # fp32 x, m = 5..8: 8 rows per workgroup
+    (6, 4864, 896, False, F32, F16),      # fp32 x, m = 5..8: 4 rows per workgroup
+    (7, 1001, 2048, True, F32, F32),      # fp32 x, m = 5..8, small: 2 rows, ragged n
 ]
 
 
@@ -70,6 +73,9 @@ def gemv_logits(nq, xd, t, b):
     (3, 8192, 896, False, F16),       # 2 rows per workgroup
     (8, 1000, 512, True, F32),
     (11, 5000, 256, False, F16),      # two slices of 8
+    (8, 9000, 1024, True, F32),       # fp32 x: 8 rows per workgroup
+    (6, 4864, 896, False, F32),       # fp32 x: 4 rows per workgroup
+    (13, 20000, 512, True, F32),      # a slice of 8 and one of 5, 8 rows per workgroup
     (3, 700, 90, True, F32),          # ragged k: logits in the workspace, then argmax
 ])
 def test_lm_head_argmax(dev, nq, orc, m, n, k, bias, xdt):
