@@ -836,10 +836,14 @@ inline int m_bucket(int64_t m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8
 // weight bound the 2-row grid; 4 or 8 rows per workgroup cut them (measured, us,
 // 2 -> 4 -> 8 rows, m = 8: n = 1536, k = 8960 24.1 -> 19.8 -> 15.6; n = 8960, k =
 // 1536 20.2 -> 14.7 -> 13.4; n = 4864, k = 896 7.38 -> 6.35 -> 6.55; n = 896, k =
-// 4864 8.42 -> 7.61 -> 9.38; n = k = 1536 5.52 -> 5.65 -> 6.15). fp16 x keeps 2.
+// 4864 8.42 -> 7.61 -> 9.38; n = k = 1536 5.52 -> 5.65 -> 6.15); at m = 3..4 4
+// rows (2 -> 4: 15.8 -> 11.0, 11.1 -> 8.4, 5.07 -> 4.43, 6.26 -> 4.94; n = k =
+// 1536 4.18 -> 4.30). fp16 x keeps 2 (its x chunks are half the bytes; 4 rows
+// measured slower on four of the five shapes).
 template <int M, typename XT>
 int q8_rows(int n, int k) {
     if (M <= 2 && n >= 32768) return 8;
+    if (M == 4 && sizeof(XT) == 4) return static_cast<int64_t>(n) * k >= (int64_t(3) << 20) ? 4 : 2;
     if (M == 8 && sizeof(XT) == 4) {
         const int64_t nk = static_cast<int64_t>(n) * k;
         return nk >= (int64_t(8) << 20) ? 8 : nk >= (int64_t(3) << 20) ? 4 : 2;
@@ -860,7 +864,7 @@ void launch_q8(const XT* x, const int8_t* w, const float* ws, const float* b, YT
             return;
         }
     }
-    if constexpr (M == 8 && sizeof(XT) == 4) {
+    if constexpr (M >= 4 && sizeof(XT) == 4) {
         if (rows == 4) {
             gemv_q8_kernel<4, M, XT, YT, AM><<<(n + 3) / 4, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part);
             return;

@@ -38,6 +38,8 @@ Q8_CASES = [
     (8, 1536, 8960, True, F32, F32),      # fp32 x, m = 5..8: 8 rows per workgroup
     (6, 4864, 896, False, F32, F16),      # fp32 x, m = 5..8: 4 rows per workgroup
     (7, 1001, 2048, True, F32, F32),      # fp32 x, m = 5..8, small: 2 rows, ragged n
+    (4, 4864, 896, True, F32, F32),       # fp32 x, m = 3..4: 4 rows per workgroup
+    (3, 1537, 2048, False, F32, F16),     # fp32 x, m = 3..4: 4 rows, ragged n
 ]
 
 
@@ -75,6 +77,7 @@ def gemv_logits(nq, xd, t, b):
     (11, 5000, 256, False, F16),      # two slices of 8
     (8, 9000, 1024, True, F32),       # fp32 x: 8 rows per workgroup
     (6, 4864, 896, False, F32),       # fp32 x: 4 rows per workgroup
+    (4, 9000, 1024, False, F32),      # fp32 x, m = 3..4: 4 rows per workgroup
     (13, 20000, 512, True, F32),      # a slice of 8 and one of 5, 8 rows per workgroup
     (3, 700, 90, True, F32),          # ragged k: logits in the workspace, then argmax
 ])
