@@ -171,9 +171,12 @@ def main():
         qs = [t.q] + [t.q.clone() for _ in range(copies_for(wbytes) - 1)]
         ss = [t.scale] + [t.scale.clone() for _ in range(len(qs) - 1)]
         y = torch.empty((m, n), dtype=torch.float16, device=dev)
+        wsb = lib.nq_linear_wq_workspace_size(m, n, k)  # split-K planes (0: none)
+        work = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev) if wsb else None
 
         def mk(i):
-            return lambda: lib.nq_linear_q4g(P(x), 1, P(qs[i]), P(ss[i]), 1, g, None, P(y), 1, m, n, k, stream_ptr())
+            return lambda: lib.nq_linear_q4g_ws(P(x), 1, P(qs[i]), P(ss[i]), 1, g, None, P(y), 1, m, n, k,
+                                                P(work), wsb, stream_ptr())
         return [mk(i) for i in range(len(qs))], nb, 2 * m * n * k
 
     def q8_gemv(m, n, k, xdt):
@@ -188,9 +191,12 @@ def main():
         ss = [t.scale] + [t.scale.clone() for _ in range(len(qs) - 1)]
         y = torch.empty((m, n), dtype=xdt, device=dev)
         dt = 1 if xdt == torch.float16 else 0
+        wsb = lib.nq_linear_wq_workspace_size(m, n, k)
+        work = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev) if wsb else None
 
         def mk(i):
-            return lambda: lib.nq_linear_q8(P(x), dt, P(qs[i]), P(ss[i]), None, P(y), dt, m, n, k, stream_ptr())
+            return lambda: lib.nq_linear_q8_ws(P(x), dt, P(qs[i]), P(ss[i]), None, P(y), dt, m, n, k, P(work), wsb,
+                                               stream_ptr())
         return [mk(i) for i in range(len(qs))], nb, 2 * m * n * k
 
     def quantize(kind, n, k, g=32):
@@ -338,6 +344,15 @@ def main():
             torch.cuda.empty_cache()
             sweep.append(entry("q4g_weight_only_prefill M=2048 K=1536 N=8960 g=32 fp16",
                                *q4g_gemv(2048, 8960, 1536, 32), "mfma_f16"))
+            torch.cuda.empty_cache()
+        if want("wq_batched"):
+            # weight-only at a batch of 64 on config 2's weight shape: few weight
+            # rows and long K, split K over the workspace
+            sweep.append(entry("q8_weight_only_batched M=64 K=8960 N=1536 fp16 (split K)",
+                               *q8_gemv(64, 1536, 8960, torch.float16), "hbm"))
+            torch.cuda.empty_cache()
+            sweep.append(entry("q4g_weight_only_batched M=64 K=8960 N=1536 g=32 fp16 (split K)",
+                               *q4g_gemv(64, 1536, 8960, 32), "hbm"))
             torch.cuda.empty_cache()
         if want("quantize"):
             # load-time quantize of the configs' weights, HBM-bound (fp32 in)
