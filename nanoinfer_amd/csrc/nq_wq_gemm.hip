@@ -334,7 +334,7 @@ __global__ __launch_bounds__(wq_waves<TM>() * 64) void gemm_wq_kernel(
 // order, then the Q8 row scale and the bias, as the unsplit epilogue applies
 // them. All plane loads are issued before the first add (one latency, not one
 // per plane); four outputs per thread when n % 4 == 0.
-constexpr int kWqMaxSplits = 8;
+constexpr int kWqMaxSplits = 16;
 template <bool Q4, bool V4, typename YT, typename ST>
 __global__ __launch_bounds__(256) void wq_reduce_kernel(const float* __restrict__ part, int splits,
                                                         const ST* __restrict__ scale, const float* __restrict__ bias,
@@ -439,7 +439,7 @@ __device__ __forceinline__ int wq_swz(int r) {  // slot XOR of row r, C 16-byte 
 }
 
 template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST, typename XT = _Float16, int WN = 2,
-          int WM = 4>
+          int WM = 4, int DMAX = 8>
 struct WqWideShape {
     static constexpr int kNW = WM * WN;  // waves: WM along m, WN along n
     static constexpr int kBM = WM * 16 * FM, kBN = WN * 16 * FN, kT = SK / 32;  // MFMA K steps per slab
@@ -462,7 +462,7 @@ struct WqWideShape {
     // start, after the ring and the staging rows.
     static constexpr int kEpsN = (kBN + 63) / 64 * 64;
     static constexpr int kEpsBytes = sizeof(YT) == 2 ? 2 * kEpsN * 4 : 0;
-    static constexpr int kD = std::min(8, (160 * 1024 - 1024 - kEpsBytes) / kSlab);
+    static constexpr int kD = std::min(DMAX, (160 * 1024 - 1024 - kEpsBytes) / kSlab);
     static constexpr int kSink = kD * kSlab;
     // fp16 staging rows padded by 16 bytes (an odd multiple of 16: the rows a
     // store instruction touches fall on distinct banks).
@@ -476,12 +476,12 @@ struct WqWideShape {
     static_assert(!Q4 || kSRow % 4 == 0, "scale rows are whole dwords");
 };
 
-template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST, typename XT, int WN, int WM>
+template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST, typename XT, int WN, int WM, int DMAX>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_wq_wide_kernel(
     const XT* __restrict__ x, const uint8_t* __restrict__ wq, const ST* __restrict__ scale,
     const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int tiles_m, int tiles_n,
     int gsh_rt, float* __restrict__ planes, int split_slabs) {
-    using S = WqWideShape<Q4, SK, FM, FN, GSH, YT, ST, XT, WN, WM>;
+    using S = WqWideShape<Q4, SK, FM, FN, GSH, YT, ST, XT, WN, WM, DMAX>;
     constexpr int NW = S::kNW;
     constexpr bool F32X = sizeof(XT) == 4;  // fp32 activations: three bf16 parts, three bf16 MFMAs
     constexpr int BM = S::kBM, BN = S::kBN, D = S::kD, Q = S::kQ, QS = S::kQS, XB = S::kXB, NB = S::kNB;
@@ -743,11 +743,12 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_wq_wide_kernel(
     }
 }
 
-template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST, typename XT, int WN, int WM = 4>
+template <bool Q4, int SK, int FM, int FN, int GSH, typename YT, typename ST, typename XT, int WN, int WM = 4,
+          int DMAX = 8>
 nq_status launch_wq_wide(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n,
                          int k, int gsh, float* planes, int splits, int split_slabs, hipStream_t s) {
-    using S = WqWideShape<Q4, SK, FM, FN, GSH, YT, ST, XT, WN, WM>;
-    auto* fn = gemm_wq_wide_kernel<Q4, SK, FM, FN, GSH, YT, ST, XT, WN, WM>;
+    using S = WqWideShape<Q4, SK, FM, FN, GSH, YT, ST, XT, WN, WM, DMAX>;
+    auto* fn = gemm_wq_wide_kernel<Q4, SK, FM, FN, GSH, YT, ST, XT, WN, WM, DMAX>;
     if (nq_status st = set_dynamic_lds(reinterpret_cast<const void*>(fn), S::kLds, "gemm_wq_wide")) return st;
     const int tm = (m + S::kBM - 1) / S::kBM, tn = (n + S::kBN - 1) / S::kBN;
     fn<<<dim3(tm * tn, splits), S::kNW * 64, S::kLds, s>>>(x, w, sc, b, y, m, n, k, tm, tn, gsh, planes, split_slabs);
@@ -763,6 +764,7 @@ nq_status launch_wq_wide(const XT* x, const uint8_t* w, const ST* sc, const floa
 // two 91.9, 256 x 128 in three 100).
 struct WqTile {
     int fm, fn, sk;
+    bool shallow = false;  // a two-slot ring (fm = 1, fn = 2 or 4): more workgroups per CU
 };
 constexpr WqTile kWqTiles[] = {{4, 9, 64}, {4, 8, 64}, {2, 9, 128}, {4, 4, 64}, {2, 8, 128},
                                {2, 4, 128}, {1, 8, 128}, {1, 4, 128}, {1, 2, 128}};
@@ -805,33 +807,48 @@ nq_status wq_wide_tiles(const XT* x, const uint8_t* w, const ST* sc, const float
     // waves, as in the W8A8 wide kernel (m = 2048: 74.3 -> 71.7 us); Q4G keeps 8
     // waves (its group-scaled partial sums do not fit 170 registers: 106.9 vs
     // 128.9 us).
-    auto with_g = [&](auto skt, auto fmt, auto fnt) -> nq_status {
-        constexpr int SK = decltype(skt)::value, FM = decltype(fmt)::value, FN2 = decltype(fnt)::value;
-        constexpr int WN = Q4 ? 2 : FN2 % 3 == 0 ? 3 : FN2 % 4 == 0 ? 4 : 2, FN = FN2 * 2 / WN;
+    using std::integral_constant;
+    // One wave layout and fragment shape: the group-size dispatch of Q4G.
+    auto launch_g = [&](auto skt, auto fmt, auto fnt, auto wnt, auto wmt, auto dt) -> nq_status {
+        constexpr int SK = decltype(skt)::value, FM = decltype(fmt)::value, FN = decltype(fnt)::value;
+        constexpr int WN = decltype(wnt)::value, WM = decltype(wmt)::value, DM = decltype(dt)::value;
         constexpr int BIG = SK == 128 ? 2 : 1;  // one scale per slab from this shift on
-        if constexpr (!Q4 && !F32X && FM == 4 && FN2 % 3 == 0) {
-            // 256-row Q8 tiles as 2 x 6 waves of (128 x 16 * FN2 / 3): each
-            // weight fragment is converted to fp16 by two waves instead of four
-            // (the conversion is a third of the MFMA time; m = 2048: 66.1 -> 63.7 us).
-            return launch_wq_wide<false, SK, 8, FN2 / 3, 0, YT, ST, XT, 6, 2>(x, w, sc, b, y, m, n, k, 0, planes, splits, split_slabs, s);
-        }
         if constexpr (!Q4) {
-            return launch_wq_wide<false, SK, FM, FN, 0, YT, ST, XT, WN>(x, w, sc, b, y, m, n, k, 0, planes, splits, split_slabs, s);
+            return launch_wq_wide<false, SK, FM, FN, 0, YT, ST, XT, WN, WM, DM>(x, w, sc, b, y, m, n, k, 0, planes, splits, split_slabs, s);
         } else {
-            if (gsh == 0) return launch_wq_wide<true, SK, FM, FN, 0, YT, ST, XT, WN>(x, w, sc, b, y, m, n, k, 0, planes, splits, split_slabs, s);
+            if (gsh == 0) return launch_wq_wide<true, SK, FM, FN, 0, YT, ST, XT, WN, WM, DM>(x, w, sc, b, y, m, n, k, 0, planes, splits, split_slabs, s);
             if constexpr (SK == 64) {  // excluded by wq_sk64_ok
                 return fail(NQ_BAD_ARG, "gemm_wq_wide: 64-column slabs take groups of 32 only (got %d)", group);
             } else {
-                if (gsh == 1) return launch_wq_wide<true, SK, FM, FN, 1, YT, ST, XT, WN>(x, w, sc, b, y, m, n, k, 1, planes, splits, split_slabs, s);
+                if (gsh == 1) return launch_wq_wide<true, SK, FM, FN, 1, YT, ST, XT, WN, WM, DM>(x, w, sc, b, y, m, n, k, 1, planes, splits, split_slabs, s);
                 if constexpr (sizeof(ST) == 2) {  // excluded by wq_wide_ok
                     return fail(NQ_BAD_ARG, "gemm_wq_wide: fp16 scales in groups of %d are not supported", group);
                 } else {
-                    return launch_wq_wide<true, SK, FM, FN, BIG, YT, ST, XT, WN>(x, w, sc, b, y, m, n, k, gsh, planes, splits, split_slabs, s);
+                    return launch_wq_wide<true, SK, FM, FN, BIG, YT, ST, XT, WN, WM, DM>(x, w, sc, b, y, m, n, k, gsh, planes, splits, split_slabs, s);
                 }
             }
         }
     };
-    using std::integral_constant;
+    auto with_g = [&](auto skt, auto fmt, auto fnt) -> nq_status {
+        constexpr int SK = decltype(skt)::value, FM = decltype(fmt)::value, FN2 = decltype(fnt)::value;
+        constexpr int WN = Q4 ? 2 : FN2 % 3 == 0 ? 3 : FN2 % 4 == 0 ? 4 : 2, FN = FN2 * 2 / WN;
+        using D8 = integral_constant<int, 8>;
+        if constexpr (FM == 1 && (FN2 == 2 || FN2 == 4)) {
+            if (pick.shallow)  // two ring slots: two or three workgroups per CU
+                return launch_g(skt, fmt, integral_constant<int, FN>{}, integral_constant<int, WN>{},
+                                integral_constant<int, 4>{}, integral_constant<int, 2>{});
+        }
+        if constexpr (!Q4 && !F32X && FM == 4 && FN2 % 3 == 0) {
+            // 256-row Q8 tiles as 2 x 6 waves of (128 x 16 * FN2 / 3): each
+            // weight fragment is converted to fp16 by two waves instead of four
+            // (the conversion is a third of the MFMA time; m = 2048: 66.1 -> 63.7 us).
+            return launch_g(skt, integral_constant<int, 8>{}, integral_constant<int, FN2 / 3>{},
+                            integral_constant<int, 6>{}, integral_constant<int, 2>{}, D8{});
+        } else {
+            return launch_g(skt, fmt, integral_constant<int, FN>{}, integral_constant<int, WN>{},
+                            integral_constant<int, 4>{}, D8{});
+        }
+    };
     using I64 = integral_constant<int, 64>;
     using I128 = integral_constant<int, 128>;
     if constexpr (F32X) {
@@ -900,19 +917,24 @@ bool wq_wide_ok(int64_t m, int64_t n, int64_t k, int64_t group) {
 // Split-K, when the caller gives a workspace for the fp32 partial planes. A
 // weight with few rows leaves most CUs idle, each workgroup walking all of K,
 // so long K splits into up to kWqMaxSplits ranges summed by wq_reduce_kernel
-// (about 3 us more: a second launch and the planes' traffic). Measured with
-// fp16 x (us, unsplit -> split): n = 1536, k = 8960: m = 16 20.6 -> 14.9
-// (16-row kernel), m = 64 43.5 -> 17.3 (wide 64 x 64 tiles, 8 ranges), m = 128
-// 42.7 -> 21.3 (64 x 128 tiles); n = 896, k = 4864, m = 64: 25.1 -> 13.7; n =
-// 256, k = 1536, m = 64: 10.5 -> 9.3. Short K with a hundred or more
-// workgroups lost (n = 1536, k = 1536, m = 64: 10.7 -> 11.6), and so did a
-// 16-row grid that already fills the CUs (n = 4096, k = 4096, m = 16: 11.8 ->
-// 16.0): those stay whole. Wide split: m > 32, k >= 4096, at most 256
-// workgroups (one per CU, as their LDS ring takes) of at least kWqMinSlabs
-// slabs each. 16-row split: under 256 workgroups unsplit, k >= 4096 (or at
-// most 32 workgroups and m > 32 or fp32 x), about kWqRowSplitWgs workgroups,
-// each wave with at least two chunks of its range.
-constexpr int kWqRowSplitWgs = 1024, kWqWideSplitWgs = 256, kWqMinSlabs = 4;
+// (a second launch and the planes' traffic). Wide split (k >= 4096, 16 <= m <=
+// 128, fp32 x from m = 32): 64 x 64 tiles (64 x 128 above m = 64) with a
+// two-slot LDS ring, so two or three workgroups share a CU (with the deep ring
+// of the unsplit tiles, one workgroup of 8 waves per CU left the SIMDs waiting:
+// n = 1536, k = 8960, m = 64 18.5 -> 15.5 us), about kWqWideSplitWgs workgroups
+// of at least kWqMinSlabs slabs. It runs ahead of the unsplit wide tiles
+// whenever it splits. Measured (us, unsplit -> split, fp16 / fp32 x): n = 1536,
+// k = 8960: m = 16 20.6 -> 13.2, m = 64 43.4 -> 15.6 / 80.3 -> 25.0, m = 128
+// 42.9 -> 21.1; n = 896, k = 4864, m = 64 25.1 -> 10.2; n = 8960, k = 4096, m =
+// 16 27.3 -> 19.0, m = 64 28.5 -> 22.4; n = 4096, k = 4096, m = 128 28.4 ->
+// 26.1 (m = 16 11.8 -> 12.7: the one loss kept; fp32 x at m = 16 lost 16.5 ->
+// 23.1, the split kernel converting all 64 tile rows, hence m >= 32 there).
+// Otherwise the 16-row kernel splits when its unsplit grid is under 256
+// workgroups and k >= 4096 (or at most 32 workgroups at m > 32 or fp32 x), to
+// about kWqRowSplitWgs workgroups with at least two chunks per wave (n = 256,
+// k = 1536, m = 64: 10.6 -> 8.7). Short K with a hundred or more workgroups
+// stays whole (n = 1536, k = 1536, m = 64 split: 10.7 -> 11.6).
+constexpr int kWqRowSplitWgs = 1024, kWqWideSplitWgs = 768, kWqMinSlabs = 4;
 struct WqRoute {
     bool wide;
     WqTile tile;         // wide
@@ -922,17 +944,11 @@ struct WqRoute {
 WqRoute plan_wq_route(int64_t m, int64_t n, int64_t k, bool wide_ok, bool wide_contract, bool sk64_ok, bool f32x,
                       bool allow_split) {
     WqRoute r{};
-    if (wide_ok) {
-        r.wide = true;
-        r.tile = plan_wq_wide(m, n, sk64_ok, f32x).tile;
-        r.splits = 1;
-        r.per = static_cast<int>(k / r.tile.sk);
-        return r;
-    }
-    if (allow_split && wide_contract && m > 32 && m <= 128 && k >= 4096) {
-        const WqTile t{1, m <= 64 ? 2 : 4, f32x ? 64 : 128};
+    if (allow_split && wide_contract && m >= (f32x ? 32 : 16) && m <= 128 && k >= 4096) {
+        WqTile t{1, m <= 64 ? 2 : 4, f32x ? 64 : 128};
+        t.shallow = true;
         const int64_t tiles = ((m + 63) / 64) * ((n + 32 * t.fn - 1) / (32 * t.fn)), nk = k / t.sk;
-        const int64_t sp = std::min<int64_t>({kWqMaxSplits, kWqWideSplitWgs / tiles, nk / kWqMinSlabs});
+        const int64_t sp = std::min<int64_t>({kWqMaxSplits, (kWqWideSplitWgs + tiles - 1) / tiles, nk / kWqMinSlabs});
         if (sp >= 2) {
             const int64_t per = (nk + sp - 1) / sp;
             r.wide = true;
@@ -941,6 +957,13 @@ WqRoute plan_wq_route(int64_t m, int64_t n, int64_t k, bool wide_ok, bool wide_c
             r.splits = static_cast<int>((nk + per - 1) / per);
             return r;
         }
+    }
+    if (wide_ok) {
+        r.wide = true;
+        r.tile = plan_wq_wide(m, n, sk64_ok, f32x).tile;
+        r.splits = 1;
+        r.per = static_cast<int>(k / r.tile.sk);
+        return r;
     }
     WqRowPlan& p = r.row;
     p.tm = m > 64 ? 4 : static_cast<int>((m + 15) / 16);

@@ -285,11 +285,12 @@ def test_weight_only_q8_wide_2x6(dev, nq, orc, m, n, k, bias):
 
 # Split K over a workspace (nq_linear_q8_ws / nq_linear_q4g_ws, which the
 # Python linears call): weights with few rows at batched m run K in ranges whose
-# fp32 planes a reduce kernel sums in order. 16-row kernel splits (m <= 32, or
-# short K with a tiny grid), wide 64-row tile splits (32 < m <= 128, k >= 4096;
-# fp32 x takes 64-column slabs), ragged m and n (n % 4 != 0: the scalar reduce),
-# fp16 / fp32 scales, group 128 (one scale per slab). Against the oracle, and
-# against the unsplit entry point on the same inputs.
+# fp32 planes a reduce kernel sums in order. 16-row kernel splits (fp32 x below
+# m = 32, or short K with a tiny grid), wide 64-row tile splits with the
+# two-slot ring (16 <= m <= 128, k >= 4096; fp32 x takes 64-column slabs),
+# ragged m and n (n % 4 != 0: the scalar reduce), fp16 / fp32 scales, groups 32,
+# 64 and 128. Against the oracle, and against the unsplit entry point on the
+# same inputs.
 WQ_SPLIT_CASES = [
     ("q8", 16, 896, 4864, 0, False, F16, F32, F16),
     ("q4g", 24, 1536, 8960, 32, True, F32, F16, F32),
@@ -300,6 +301,8 @@ WQ_SPLIT_CASES = [
     ("q8", 40, 256, 1536, 0, True, F32, F32, F32),
     ("q4g", 72, 202, 1536, 64, False, F16, F16, F16),
     ("q8", 97, 1001, 4096, 0, True, F16, F32, F16),
+    ("q4g", 32, 1000, 4096, 64, False, F16, F16, F32),
+    ("q4g", 17, 4100, 4224, 32, True, F16, F32, F16),
 ]
 
 
