@@ -185,7 +185,8 @@ nq_status nq_nit_load_q4g(const char* path, uint8_t* q, void* scale, nq_dtype sc
  * kernel and row grouping); larger m runs the GEMV in slices of 8 rows (as
  * nq_linear_q8 does where its MFMA GEMM does not apply). Shapes outside the GEMV's fast path (k %
  * 16 != 0, k > 16384, misaligned operands) compute the logits into the
- * workspace first. ids: int64 [m], 8-byte aligned. workspace: >=
+ * workspace first. ids: int64 [m], 8-byte aligned. workspace (its first 256 bytes hold
+ * the final reduction's per-row key and ticket): >=
  * nq_lm_head_argmax_q8_workspace_size(m, n, k) bytes, 256-byte aligned. */
 size_t nq_lm_head_argmax_q8_workspace_size(int64_t m, int64_t n, int64_t k);
 nq_status nq_lm_head_argmax_q8(const void* x, nq_dtype x_dtype, const int8_t* q, const float* w_scale,

@@ -112,6 +112,16 @@ struct ArgPart {
     int i;
 };
 constexpr int kArgNone = 0x7FFFFFFF;
+// Per activation row of the fused LM head: the running best as one 64-bit key
+// (order-preserving bits of the value above, 0xFFFFFFFF - index below, so the
+// larger key is the larger value and, on ties, the smaller index; all ones:
+// logit 0 is NaN; 0: no candidate) and the count of final workgroups done. The
+// GEMV zeroes both; the final kernel's device-scope atomics update them.
+struct ArgCtl {
+    unsigned long long key;
+    unsigned ticket, pad;
+};
+constexpr int kArgCtlBytes = 256;  // 8 rows, at the start of the fused path's workspace
 __device__ __forceinline__ bool arg_better(float v, int i, float bv, int bi) {
     return v > bv || (v == bv && i < bi);
 }
@@ -134,7 +144,8 @@ __device__ __forceinline__ int xcd_row_group() {
 template <int R, int M, typename XT, typename YT, bool AM = false>
 __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q8_kernel(
     const XT* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ ws,
-    const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, ArgPart* __restrict__ part) {
+    const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, ArgPart* __restrict__ part,
+    ArgCtl* __restrict__ ctl) {
     __shared__ float red[kMaxGemvWaves * R * M];
     const int tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6;
     const int chunks = k >> 4;
@@ -198,6 +209,7 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q8_kernel(
                 }
             }
             part[static_cast<size_t>(tid) * gridDim.x + blockIdx.x] = ArgPart{bv, bi};
+            if (blockIdx.x == 0) ctl[tid] = ArgCtl{0, 0, 0};  // read by the next launch only
         }
         return;
     }
@@ -824,6 +836,57 @@ __global__ __launch_bounds__(1024) void argmax_final_kernel(const ArgPart* __res
     if (tid == 0) ids[i] = (p[0].i == -1 || bi == kArgNone) ? 0 : bi;
 }
 
+// Fused path's final reduction: gridDim.x workgroups per activation row
+// (blockIdx.y), each reducing T * U partials with all its loads in flight, then
+// one 64-bit device-scope atomic max of its key and a ticket; the workgroup
+// that takes the last ticket reads the key and writes the id. Device-scope
+// atomics are performed past the per-XCD L2s, in issue order for one thread
+// (the max has returned before the ticket is taken), so the last ticket sees
+// every key. Same result as argmax_final_kernel: the reference scan's first
+// maximal index, 0 when logit 0 is NaN or nothing qualifies.
+__device__ __forceinline__ unsigned arg_order_bits(float v) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+template <int T, int U>
+__global__ __launch_bounds__(T) void argmax_final_multi_kernel(const ArgPart* __restrict__ part, int nparts,
+                                                                ArgCtl* __restrict__ ctl, int64_t* __restrict__ ids) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const int i = blockIdx.y, tid = threadIdx.x;
+    const ArgPart* p = part + static_cast<size_t>(i) * nparts;
+    const int base = blockIdx.x * T * U + tid;
+    ArgPart q[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int j = base + u * T;
+        q[u] = p[min(j, nparts - 1)];
+        if (j >= nparts) q[u].i = kArgNone;
+    }
+    float bv = -__builtin_inff();
+    int bi = kArgNone;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        if (q[u].i >= 0 && arg_better(q[u].v, q[u].i, bv, bi)) {
+            bv = q[u].v;
+            bi = q[u].i;
+        }
+    arg_reduce_block<T>(bv, bi, sv, si);
+    if (tid == 0) {
+        unsigned long long key = 0;
+        if (blockIdx.x == 0 && p[0].i == -1) key = ~0ull;
+        else if (bi != kArgNone) key = (static_cast<unsigned long long>(arg_order_bits(bv)) << 32) | (0xFFFFFFFFu - static_cast<unsigned>(bi));
+        __hip_atomic_fetch_max(&ctl[i].key, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const unsigned t = __hip_atomic_fetch_add(&ctl[i].ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (t == gridDim.x - 1) {
+            const unsigned long long f = __hip_atomic_load(&ctl[i].key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ids[i] = (f == ~0ull || f == 0) ? 0 : static_cast<int64_t>(0xFFFFFFFFu - static_cast<unsigned>(f & 0xFFFFFFFFu));
+        }
+    }
+}
+constexpr int kArgFinalT = 256, kArgFinalU = 8;
+
 // ---- host dispatch ----------------------------------------------------------------------
 inline int m_bucket(int64_t m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8; }
 
@@ -853,24 +916,24 @@ int q8_rows(int n, int k) {
 
 template <int M, bool AM = false, typename XT, typename YT>
 void launch_q8(const XT* x, const int8_t* w, const float* ws, const float* b, YT* y, int m, int n,
-               int k, hipStream_t s, ArgPart* part = nullptr) {
+               int k, hipStream_t s, ArgPart* part = nullptr, ArgCtl* ctl = nullptr) {
     const int chunks = k >> 4;
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
     constexpr int R = rows_for<M>();
     const int rows = q8_rows<M, XT>(n, k);
     if constexpr (M <= 2 || (M == 8 && sizeof(XT) == 4)) {  // the other row counts q8_rows picks
         if (rows == 8 && R != 8) {
-            gemv_q8_kernel<8, M, XT, YT, AM><<<(n + 7) / 8, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part);
+            gemv_q8_kernel<8, M, XT, YT, AM><<<(n + 7) / 8, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part, ctl);
             return;
         }
     }
     if constexpr (M >= 4 && sizeof(XT) == 4) {
         if (rows == 4) {
-            gemv_q8_kernel<4, M, XT, YT, AM><<<(n + 3) / 4, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part);
+            gemv_q8_kernel<4, M, XT, YT, AM><<<(n + 3) / 4, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part, ctl);
             return;
         }
     }
-    gemv_q8_kernel<R, M, XT, YT, AM><<<(n + R - 1) / R, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part);
+    gemv_q8_kernel<R, M, XT, YT, AM><<<(n + R - 1) / R, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part, ctl);
 }
 
 template <typename XT, typename YT>
@@ -1235,7 +1298,7 @@ bool lm_head_fused_ok(const void* x, const int8_t* q, int64_t k) {
 }
 size_t lm_head_ws(int64_t m, int64_t n, int64_t k, bool fused) {
     // one partial per workgroup of at least 2 rows (rows_for), per activation row of a slice
-    if (fused) return round_up(static_cast<size_t>(std::min<int64_t>(m, 8)) * ((n + 1) / 2) * sizeof(ArgPart), 256);
+    if (fused) return kArgCtlBytes + round_up(static_cast<size_t>(std::min<int64_t>(m, 8)) * ((n + 1) / 2) * sizeof(ArgPart), 256);
     return round_up(static_cast<size_t>(m) * n * 4, 256) +
            round_up(static_cast<size_t>(m) * ((n + kArgSeg - 1) / kArgSeg) * sizeof(ArgPart), 256);
 }
@@ -1275,7 +1338,8 @@ extern "C" nq_status nq_lm_head_argmax_q8(const void* x, nq_dtype x_dtype, const
         argmax_final_kernel<<<static_cast<unsigned>(m), 1024, 0, s>>>(part, nseg, ids);
         return launch_status("lm_head_argmax_q8");
     }
-    ArgPart* part = static_cast<ArgPart*>(workspace);
+    ArgCtl* ctl = static_cast<ArgCtl*>(workspace);
+    ArgPart* part = reinterpret_cast<ArgPart*>(static_cast<char*>(workspace) + kArgCtlBytes);
     // Activation rows in slices of 8 (the GEMV's batch), each with the kernel
     // and row grouping nq_linear_q8 uses for that slice, so the fused logits
     // equal nq_linear_q8's fp32 output bit for bit.
@@ -1287,15 +1351,17 @@ extern "C" nq_status nq_lm_head_argmax_q8(const void* x, nq_dtype x_dtype, const
             const XT* xs = xp + static_cast<size_t>(r0) * k;
             float* none = nullptr;
             switch (m_bucket(mi)) {
-                case 1: nwg = (ni + q8_rows<1, XT>(ni, ki) - 1) / q8_rows<1, XT>(ni, ki); launch_q8<1, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part); break;
-                case 2: nwg = (ni + q8_rows<2, XT>(ni, ki) - 1) / q8_rows<2, XT>(ni, ki); launch_q8<2, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part); break;
-                case 4: nwg = (ni + q8_rows<4, XT>(ni, ki) - 1) / q8_rows<4, XT>(ni, ki); launch_q8<4, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part); break;
-                default: nwg = (ni + q8_rows<8, XT>(ni, ki) - 1) / q8_rows<8, XT>(ni, ki); launch_q8<8, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part); break;
+                case 1: nwg = (ni + q8_rows<1, XT>(ni, ki) - 1) / q8_rows<1, XT>(ni, ki); launch_q8<1, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part, ctl); break;
+                case 2: nwg = (ni + q8_rows<2, XT>(ni, ki) - 1) / q8_rows<2, XT>(ni, ki); launch_q8<2, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part, ctl); break;
+                case 4: nwg = (ni + q8_rows<4, XT>(ni, ki) - 1) / q8_rows<4, XT>(ni, ki); launch_q8<4, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part, ctl); break;
+                default: nwg = (ni + q8_rows<8, XT>(ni, ki) - 1) / q8_rows<8, XT>(ni, ki); launch_q8<8, true>(xs, q, w_scale, bias, none, mi, ni, ki, s, part, ctl); break;
             }
         };
         if (x_dtype == NQ_F32) go(static_cast<const float*>(x));
         else go(static_cast<const _Float16*>(x));
-        argmax_final_kernel<<<static_cast<unsigned>(mi), 1024, 0, s>>>(part, nwg, ids + r0);
+        const unsigned nfin = static_cast<unsigned>((nwg + kArgFinalT * kArgFinalU - 1) / (kArgFinalT * kArgFinalU));
+        argmax_final_multi_kernel<kArgFinalT, kArgFinalU><<<dim3(nfin, static_cast<unsigned>(mi)), kArgFinalT, 0, s>>>(
+            part, nwg, ctl, ids + r0);
         if (nq_status st = launch_status("lm_head_argmax_q8")) return st;
     }
     return NQ_OK;

@@ -99,6 +99,22 @@ def test_lm_head_argmax(dev, nq, orc, m, n, k, bias, xdt):
             assert int(host(ids)[i]) == int(np.argmax(ref[i])), i
 
 
+def test_lm_head_argmax_many_inputs(dev, nq):
+    """The fused LM head's final reduction combines workgroup keys with
+    device-scope atomics across the XCDs: 24 inputs on one vocabulary-sized
+    weight, each id equal to the argmax of the GEMV's own logits."""
+    rng = np.random.default_rng(5)
+    n, k = 151936, 1536
+    w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    t = nq.quantize_q8(to_dev(w, dev))
+    for it in range(24):
+        m = 1 + it % 3
+        xd = to_dev(rng.normal(0, 1, (m, k)).astype(np.float32), dev, F16 if it % 2 else F32)
+        ids = host(nq.lm_head_argmax(xd, t, None)).tolist()
+        logits = host(gemv_logits(nq, xd, t, None))
+        assert ids == [ref_argmax(r) for r in logits], it
+
+
 def test_lm_head_argmax_ties_nan_inf(dev, nq):
     """Ties go to the first index (within and across workgroups); a NaN logit 0
     gives 0; other NaN logits are skipped; all -inf gives 0. Each case is also
