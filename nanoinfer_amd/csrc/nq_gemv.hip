@@ -271,8 +271,8 @@ __device__ __forceinline__ float dot32_q4_f32(v4i wv, const float (&xf)[32]) {
     return p;
 }
 
-template <int R, int M, typename XT, typename YT, typename ST>
-__global__ __launch_bounds__(kMaxGemvThreads) void gemv_q4g_kernel(
+template <int R, int M, typename XT, typename YT, typename ST, int LB = kMaxGemvThreads>
+__global__ __launch_bounds__(LB) void gemv_q4g_kernel(
     const XT* __restrict__ x, const uint8_t* __restrict__ w, const ST* __restrict__ scale,
     const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int group) {
     __shared__ float red[kMaxGemvWaves * R * M];
@@ -954,9 +954,21 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
     // the unpack math over many SIMDs, and each activation chunk serves two rows
     // (measured at k = 8960, n = 1536: 1 row 4.83 us, 2 rows 4.46, 3 rows (512
     // workgroups, two per CU) 4.51, 4 rows 4.82, 6 rows 5.21, 8 rows 4.98).
+    // fp32 activations at m = 3..8: 4 rows, so each 128-byte activation chunk
+    // serves twice the codes (with 2 rows the x re-reads bound the kernel); the
+    // 320-thread launch bound (k <= 10240) leaves 256 VGPRs per lane, where the
+    // 576-thread bound spilled 7-22 of them (m = 8, n = 1536, k = 8960: 30.2 ->
+    // 23.2 us; n = 8960, k = 1536 33.3 -> 20.1; m = 4, n = 1536, k = 8960 19.0 ->
+    // 15.0). fp16 activations measured slower with 4 rows (12.5 -> 19.6).
     constexpr int R = 2;
     const int chunks = k >> 5;
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
+    if constexpr (M >= 4 && sizeof(XT) == 4) {
+        if (threads <= 320) {
+            gemv_q4g_kernel<4, M, XT, YT, ST, 320><<<(n + 3) / 4, threads, 0, s>>>(x, w, sc, b, y, m, n, k, g);
+            return;
+        }
+    }
     gemv_q4g_kernel<R, M, XT, YT, ST><<<(n + R - 1) / R, threads, 0, s>>>(x, w, sc, b, y, m, n, k, g);
 }
 

@@ -174,6 +174,10 @@ Q4_CASES = [
     (16, 64, 40, 8, False, F32, F32, F32),      # test_quant.cpp:265-280 shapes
     (2, 33, 137, 5, True, F32, F32, F32),       # odd k, odd group
     (9, 7, 40, 16, True, F32, F32, F32),
+    (8, 1536, 8960, 32, False, F32, F16, F32),  # fp32 x, m = 5..8: 4 rows, 320-thread bound
+    (6, 1001, 4096, 64, True, F32, F32, F16),   # fp32 x, 4 rows, ragged n
+    (4, 4864, 896, 128, False, F32, F32, F32),  # fp32 x, m = 3..4: 4 rows
+    (7, 300, 12288, 32, True, F32, F16, F32),   # fp32 x, k > 10240: 2 rows, 576 threads
 ]
 
 
