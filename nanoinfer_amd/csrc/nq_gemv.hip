@@ -22,7 +22,7 @@
 
 namespace nq {
 bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m, int64_t n, int64_t k,
-                int64_t group);
+                int64_t group, bool ws);
 template <bool Q4, typename XT, typename YT, typename ST>
 nq_status wq_gemm(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int64_t m, int64_t n,
                   int64_t k, int64_t group, void* workspace, size_t workspace_bytes, hipStream_t s);
@@ -1164,7 +1164,7 @@ nq_status linear_q8_impl(const void* x, nq_dtype x_dtype, const int8_t* q, const
     const int ni = static_cast<int>(n), ki = static_cast<int>(k);
     // Batched activations: the fp16 MFMA GEMM when the shape rule in wq_gemm_ok
     // picks it, else GEMV slices of 8 rows.
-    if (wq_gemm_ok(false, x, dtype_size(x_dtype), q, m, n, k, 32)) {
+    if (wq_gemm_ok(false, x, dtype_size(x_dtype), q, m, n, k, 32, ws != nullptr)) {
         const uint8_t* w = reinterpret_cast<const uint8_t*>(q);
         if (x_dtype == NQ_F32 && y_dtype == NQ_F32)
             return wq_gemm<false>(static_cast<const float*>(x), w, w_scale, bias, static_cast<float*>(y), m, n, k, 32, ws, ws_bytes, s);
@@ -1219,7 +1219,7 @@ nq_status linear_q4g_impl(const void* x, nq_dtype x_dtype, const uint8_t* q, con
     const int ni = static_cast<int>(n), ki = static_cast<int>(k), gi = static_cast<int>(group);
     // Batched activations: the fp16 MFMA GEMM when the shape rule in wq_gemm_ok
     // picks it, else GEMV slices of 8 rows.
-    if (wq_gemm_ok(true, x, dtype_size(x_dtype), q, m, n, k, group)) {
+    if (wq_gemm_ok(true, x, dtype_size(x_dtype), q, m, n, k, group, ws != nullptr)) {
         auto go = [&](auto* xp, auto* yp) {
             if (scale_dtype == NQ_F32)
                 return wq_gemm<true>(xp, q, static_cast<const float*>(scale), bias, yp, m, n, k, group, ws, ws_bytes, s);

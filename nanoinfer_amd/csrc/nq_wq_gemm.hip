@@ -944,7 +944,7 @@ struct WqRoute {
 WqRoute plan_wq_route(int64_t m, int64_t n, int64_t k, bool wide_ok, bool wide_contract, bool sk64_ok, bool f32x,
                       bool allow_split) {
     WqRoute r{};
-    if (allow_split && wide_contract && m >= (f32x ? 32 : 16) && m <= 128 && k >= 4096) {
+    if (allow_split && wide_contract && m >= (f32x ? 32 : 9) && m <= 128 && k >= 4096) {
         WqTile t{1, m <= 64 ? 2 : 4, f32x ? 64 : 128};
         t.shallow = true;
         const int64_t tiles = ((m + 63) / 64) * ((n + 32 * t.fn - 1) / (32 * t.fn)), nk = k / t.sk;
@@ -984,18 +984,26 @@ size_t wq_route_bytes(const WqRoute& r, int64_t m, int64_t n) {
 }
 }  // namespace
 
-bool wq_gemm_shape_ok(int64_t m, int64_t n) { return m > 8 && (m >= 16 || n >= 4096); }
+// m = 9..15 with a short weight runs GEMV slices, unless a workspace lets fp16
+// activations take the split wide tiles: k >= 4096 and at least 6 Mi codes
+// (us, slices -> split, m = 9 / 12 / 15: n = 1536, k = 8960 16.0 / 18.7 / 22.0 ->
+// 13.3 / 13.1 / 13.2; n = 2048, k = 8192 18.5 / 20.5 / 24.4 -> 12.3 / 12.3 /
+// 12.5; the smaller n = 896, k = 4864 lost at m = 9: 8.7 -> 10.4).
+bool wq_gemm_shape_ok(int64_t m, int64_t n, int64_t k, size_t x_elem, bool ws) {
+    return m > 8 && (m >= 16 || n >= 4096 ||
+                     (ws && x_elem == 2 && k >= 4096 && k % 128 == 0 && n * k >= (int64_t(6) << 20)));
+}
 
 // Whether the MFMA path takes this call (the caller runs GEMV slices otherwise):
 // whole 32-column chunks, groups of a power-of-two number of chunks, 16-byte aligned operands and
 // 32-bit buffer offsets.
 bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m, int64_t n, int64_t k,
-                int64_t group) {
+                int64_t group, bool ws) {
     const int64_t rowb = q4 ? k / 2 : k;
     // Shape rule (measured): the GEMM runs one workgroup per 16 (or 32) weight
     // rows, each reading all of x, so below 4096 rows it fills under 256 CUs; a
     // GEMV slice of 8 rows plus a remainder slice is then faster up to m = 15.
-    if (!wq_gemm_shape_ok(m, n)) return false;
+    if (!wq_gemm_shape_ok(m, n, k, x_elem, ws)) return false;
     return k > 0 && k % 32 == 0 && (!q4 || (group % 32 == 0 && ((group / 32) & (group / 32 - 1)) == 0)) && aligned(x, 16) && aligned(w, 16) &&
            m <= (int64_t(65535) * 64) && std::min<int64_t>(m, 64) * k * static_cast<int64_t>(x_elem) < (int64_t(1) << 31) - 64 &&
            n * rowb < (int64_t(1) << 31) - 64;
@@ -1020,7 +1028,7 @@ nq_status wq_gemm(const XT* x, const uint8_t* w, const ST* sc, const float* b, Y
 // Workspace the split-K planes take at this shape (0: no split): the most any
 // activation dtype or group size can plan, so one size serves every call.
 size_t wq_workspace_bytes(int64_t m, int64_t n, int64_t k) {
-    if (m <= 0 || n <= 0 || k <= 0 || !wq_gemm_shape_ok(m, n)) return 0;
+    if (m <= 0 || n <= 0 || k <= 0 || !wq_gemm_shape_ok(m, n, k, 2, true)) return 0;
     size_t most = 0;
     for (int f32x = 0; f32x < 2; ++f32x)
         for (int contract = 0; contract < 2; ++contract)

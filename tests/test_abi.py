@@ -99,6 +99,8 @@ def test_weight_only_split_workspace_rules(lib):
     # decode-sized m and short K with a full grid: no planes
     assert lib.nq_linear_wq_workspace_size(1, 1536, 8960) == 0
     assert lib.nq_linear_wq_workspace_size(8, 1536, 8960) == 0
+    assert lib.nq_linear_wq_workspace_size(12, 1536, 8960) > 0     # m = 9..15: split wide tiles
+    assert lib.nq_linear_wq_workspace_size(12, 896, 4864) == 0     # small weight: GEMV slices
     assert lib.nq_linear_wq_workspace_size(64, 1536, 1536) == 0
     assert lib.nq_linear_wq_workspace_size(0, 1536, 8960) == 0
     assert lib.nq_linear_q8_ws(fake, 1, fake, fake, None, fake, 1, 0, 1536, 8960, None, 0, None) == L.NQ_OK

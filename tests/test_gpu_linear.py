@@ -323,6 +323,8 @@ WQ_SPLIT_CASES = [
     ("q8", 97, 1001, 4096, 0, True, F16, F32, F16),
     ("q4g", 32, 1000, 4096, 64, False, F16, F16, F32),
     ("q4g", 17, 4100, 4224, 32, True, F16, F32, F16),
+    ("q8", 12, 1536, 8960, 0, True, F16, F32, F16),     # m = 9..15 with a workspace
+    ("q4g", 9, 2000, 4096, 32, False, F16, F16, F32),
 ]
 
 
