@@ -278,18 +278,24 @@ __global__ __launch_bounds__(LB) void gemv_q4g_kernel(
     __shared__ float red[kMaxGemvWaves * R * M];
     const int tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6;
     const int chunks = k >> 5;  // 32 codes per 16-byte chunk
-    const int rb = k >> 1, blocks = k / group;
+    const int rb = k >> 1;
     const bool act = tid < chunks;
     const int row0 = xcd_row_group() * R;
 
     const int c = act ? tid : 0;
-    const int blk = group == 32 ? c : (c * 32) / group;
     v4i wv[R];
     ST sraw[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int row = min(row0 + r, n - 1);
         wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * rb + c * 16));
+    }
+    const unsigned ug = static_cast<unsigned>(group);
+    const unsigned blocks = ug == 32 ? static_cast<unsigned>(chunks) : static_cast<unsigned>(k) / ug;
+    const unsigned blk = ug == 32 ? static_cast<unsigned>(c) : static_cast<unsigned>(c * 32) / ug;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = min(row0 + r, n - 1);
         sraw[r] = scale[static_cast<size_t>(row) * blocks + blk];
     }
     // Activation chunks of all M rows are loaded up front while they fit in 64
@@ -954,16 +960,17 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
     // the unpack math over many SIMDs, and each activation chunk serves two rows
     // (measured at k = 8960, n = 1536: 1 row 4.83 us, 2 rows 4.46, 3 rows (512
     // workgroups, two per CU) 4.51, 4 rows 4.82, 6 rows 5.21, 8 rows 4.98).
-    // fp32 activations at m = 3..8: 4 rows, so each 128-byte activation chunk
+    // fp32 activations at m = 2..8: 4 rows, so each 128-byte activation chunk
     // serves twice the codes (with 2 rows the x re-reads bound the kernel); the
     // 320-thread launch bound (k <= 10240) leaves 256 VGPRs per lane, where the
     // 576-thread bound spilled 7-22 of them (m = 8, n = 1536, k = 8960: 30.2 ->
     // 23.2 us; n = 8960, k = 1536 33.3 -> 20.1; m = 4, n = 1536, k = 8960 19.0 ->
-    // 15.0). fp16 activations measured slower with 4 rows (12.5 -> 19.6).
+    // 15.0; m = 2: 11.7 -> 10.6, n = 8960, k = 1536 10.4 -> 8.0). fp16
+    // activations measured slower with 4 rows (12.5 -> 19.6), m = 1 about even.
     constexpr int R = 2;
     const int chunks = k >> 5;
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
-    if constexpr (M >= 4 && sizeof(XT) == 4) {
+    if constexpr (M >= 2 && sizeof(XT) == 4) {
         if (threads <= 320) {
             gemv_q4g_kernel<4, M, XT, YT, ST, 320><<<(n + 3) / 4, threads, 0, s>>>(x, w, sc, b, y, m, n, k, g);
             return;

@@ -178,6 +178,8 @@ Q4_CASES = [
     (6, 1001, 4096, 64, True, F32, F32, F16),   # fp32 x, 4 rows, ragged n
     (4, 4864, 896, 128, False, F32, F32, F32),  # fp32 x, m = 3..4: 4 rows
     (7, 300, 12288, 32, True, F32, F16, F32),   # fp32 x, k > 10240: 2 rows, 576 threads
+    (2, 8960, 1536, 32, False, F32, F16, F16),  # fp32 x, m = 2: 4 rows
+    (1, 1536, 8960, 32, True, F32, F32, F32),   # fp32 x, m = 1: 2 rows, unsigned group math
 ]
 
 
