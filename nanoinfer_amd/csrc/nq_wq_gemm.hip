@@ -982,8 +982,6 @@ WqRoute plan_wq_route(int64_t m, int64_t n, int64_t k, bool wide_ok, bool wide_c
 size_t wq_route_bytes(const WqRoute& r, int64_t m, int64_t n) {
     return r.splits > 1 ? round_up(static_cast<size_t>(r.splits) * static_cast<size_t>(m) * static_cast<size_t>(n) * 4, 256) : 0;
 }
-}  // namespace
-
 // m = 9..15 with a short weight runs GEMV slices, unless a workspace lets fp16
 // activations take the split wide tiles: k >= 4096 and at least 6 Mi codes
 // (us, slices -> split, m = 9 / 12 / 15: n = 1536, k = 8960 16.0 / 18.7 / 22.0 ->
@@ -993,6 +991,7 @@ bool wq_gemm_shape_ok(int64_t m, int64_t n, int64_t k, size_t x_elem, bool ws) {
     return m > 8 && (m >= 16 || n >= 4096 ||
                      (ws && x_elem == 2 && k >= 4096 && k % 128 == 0 && n * k >= (int64_t(6) << 20)));
 }
+}  // namespace
 
 // Whether the MFMA path takes this call (the caller runs GEMV slices otherwise):
 // whole 32-column chunks, groups of a power-of-two number of chunks, 16-byte aligned operands and
