@@ -717,8 +717,16 @@ __global__ void w8a8_reduce_kernel(const int32_t* __restrict__ parts, int splits
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const int64_t mn = static_cast<int64_t>(m) * n;
     if (i >= mn) return;
+    // Eight plane loads in flight per step rather than one per add (int32 sums
+    // are exact in any order).
     int sum = 0;
-    for (int sp = 0; sp < splits; ++sp) sum += parts[sp * mn + i];
+    for (int s0 = 0; s0 < splits; s0 += 8) {
+        int v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = s0 + u < splits ? parts[(s0 + u) * mn + i] : 0;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) sum += v[u];
+    }
     if constexpr (TO_ACC) {
         acc[i] = sum;
     } else {
