@@ -347,15 +347,15 @@ struct WideShape {
     static constexpr int kBM = kWM * FM * 16, kBN = kWN * FN * 16;
     static constexpr int kXB = kBM / 8, kNB = kXB + kBN / 8, kQ = (kNB + kWaves - 1) / kWaves;
     static constexpr int kSlab = (kBM + kBN) * kRow;
-    // Ring slots: when four or more fit in half the LDS, as many as let two
-    // workgroups share a CU (64 x 64 tiles: 4; with 8 slots one workgroup per CU
-    // left its 8 waves waiting on memory: config 4 q|k|v 8.09 -> 7.23 us, o 7.93
-    // -> 7.13, m = 64 gate/up 11.5 -> 10.8; 3 slots (three workgroups) lost:
-    // down 23.5 -> 28.0); otherwise as many as 160 KB holds beside the sink (at
-    // most 8).
+    // Ring slots: when three or more fit in half the LDS, as many as let two
+    // workgroups share a CU (64 x 64 tiles: 4, 64 x 128: 3; with 8 or 6 slots one
+    // workgroup per CU left its 8 waves waiting on memory: config 4 q|k|v 8.09 ->
+    // 7.23 us, o 7.93 -> 7.13, m = 64 gate/up 11.5 -> 10.8, m = 128 n = 8960 13.0
+    // -> 12.6; 3 slots of 64 x 64 (three workgroups) lost: down 23.5 -> 28.0);
+    // otherwise as many as 160 KB holds beside the sink (at most 8).
     static constexpr int kEpsBytes = (kBM + 2 * ((kBN + 63) / 64) * 64) * 4;
     static constexpr int kDTwo = (80 * 1024 - 1024 - kEpsBytes) / kSlab;
-    static constexpr int kD = kDTwo >= 4 ? std::min(8, kDTwo) : std::min(8, (160 * 1024 - 1024 - kEpsBytes) / kSlab);
+    static constexpr int kD = kDTwo >= 3 ? std::min(8, kDTwo) : std::min(8, (160 * 1024 - 1024 - kEpsBytes) / kSlab);
     static_assert(kD >= 2, "two slabs must fit");
     static constexpr int kSink = kD * kSlab;  // 1 KB
     // fp16 staging rows of the epilogue: 16 bytes of padding make the stride an
