@@ -453,7 +453,13 @@ struct WqWideShape {
     // start, after the ring and the staging rows.
     static constexpr int kEpsN = (kBN + 63) / 64 * 64;
     static constexpr int kEpsBytes = sizeof(YT) == 2 ? 2 * kEpsN * 4 : 0;
-    static constexpr int kD = std::min(DMAX, (160 * 1024 - 1024 - kEpsBytes) / kSlab);
+    // Ring slots: with the default depth, where three or more fit in half the
+    // LDS, as many as let two workgroups share a CU (n = 8960, k = 1536, m = 64:
+    // Q4G 17.1 -> 15.5 us; n = 4864, k = 896, m = 128 Q8 10.6 -> 9.5); otherwise
+    // as many as 160 KB holds beside the sink, at most DMAX.
+    static constexpr int kDTwo = (80 * 1024 - 1024 - kEpsBytes) / kSlab;
+    static constexpr int kD = DMAX == 8 && kDTwo >= 3 ? std::min(8, kDTwo)
+                                                      : std::min(DMAX, (160 * 1024 - 1024 - kEpsBytes) / kSlab);
     static constexpr int kSink = kD * kSlab;
     // fp16 staging rows padded by 16 bytes (an odd multiple of 16: the rows a
     // store instruction touches fall on distinct banks).
