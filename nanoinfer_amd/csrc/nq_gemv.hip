@@ -429,15 +429,20 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_fused_kernel(
     const int row0 = xcd_row_group() * R;
 
     const int c = act ? tid : 0;
+    // The activation loads go out first: the absmax below waits on them, and the
+    // in-order load counter would otherwise make it wait for the weight rows too,
+    // putting the absmax, the barrier and the quantize after the weights' HBM
+    // latency instead of under it.
+    XChunk<XT> xc[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) xc[i].load(x + static_cast<size_t>(min(i, m - 1)) * k + c * 16);
+    __builtin_amdgcn_sched_barrier(0);
     v4i wv[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int row = min(row0 + r, n - 1);
         wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * k + c * 16));
     }
-    XChunk<XT> xc[M];
-#pragma unroll
-    for (int i = 0; i < M; ++i) xc[i].load(x + static_cast<size_t>(min(i, m - 1)) * k + c * 16);
     float am[M];
 #pragma unroll
     for (int i = 0; i < M; ++i) {
@@ -569,17 +574,29 @@ __global__ __launch_bounds__(kDecThreads) void w8a8_decode_kernel(const XT* __re
                 buf[t][r] = __builtin_nontemporal_load(wv + static_cast<size_t>(min(r0 + r, n - 1)) * cpr + c);
         }
     };
-    // (Long K: not held across phase 1, whose activation vectors need the registers.)
-    if constexpr (DB)
-        if (g < groups) load(g, cur);
-
+    // The activations are requested before that first group: phase 1 waits on
+    // them, and the in-order load counter would otherwise hold it until the
+    // weights had arrived too (long K: the weights are not held across phase 1,
+    // whose activation vectors need the registers).
     if constexpr (PRE) {
         // Phase 1 for pre-quantized codes: 16-byte copies into LDS (rows past m zero).
         const int8_t* xc = reinterpret_cast<const int8_t*>(x);
-        for (int v = tid; v < M * cpr; v += kDecThreads) {
-            const int i = v / cpr;
-            reinterpret_cast<v4i*>(xq)[v] =
-                i < m ? *reinterpret_cast<const v4i*>(xc + static_cast<size_t>(i) * k + 16 * (v - i * cpr)) : v4i{0, 0, 0, 0};
+        constexpr int UC = (M * T * 64 + kDecThreads - 1) / kDecThreads;  // M * cpr <= M * 64 T chunks
+        v4i cv[UC];
+#pragma unroll
+        for (int u = 0; u < UC; ++u) {
+            const int v = tid + kDecThreads * u, i = v / cpr;
+            cv[u] = v < M * cpr && i < m ? *reinterpret_cast<const v4i*>(xc + static_cast<size_t>(i) * k + 16 * (v - i * cpr))
+                                         : v4i{0, 0, 0, 0};
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (DB)
+            if (g < groups) load(g, cur);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < UC; ++u) {
+            const int v = tid + kDecThreads * u;
+            if (v < M * cpr) reinterpret_cast<v4i*>(xq)[v] = cv[u];
         }
         if (tid < M) a_scale[tid] = tid < m ? pre_scale[tid] : 0.0f;
         __syncthreads();
@@ -594,10 +611,18 @@ __global__ __launch_bounds__(kDecThreads) void w8a8_decode_kernel(const XT* __re
     for (int i = 0; i < M; ++i) am[i] = 0.0f;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+        const int v = min(tid + kDecThreads * u, nv - 1), i = v / vpr;
+        xv[u].load(x + static_cast<size_t>(min(i, m - 1)) * k + 8 * (v - i * vpr));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (DB)
+        if (g < groups) load(g, cur);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
         const int v = tid + kDecThreads * u;
         if (v < nv) {
             const int i = v / vpr;
-            xv[u].load(x + static_cast<size_t>(min(i, m - 1)) * k + 8 * (v - i * vpr));
             float a = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) a = absmax_step(a, xv[u].at(j));
