@@ -360,6 +360,42 @@ def test_weight_only_split_k(dev, nq, orc, mode, m, n, k, g, bias, xdt, sdt, ydt
     assert_close_rms(host(y.float()), host(y0.float()), f"{mode} split vs whole {m}x{n}x{k}", fp16_out=(ydt == F16))
 
 
+def _split_random_cases():
+    rng = np.random.default_rng(11)
+    cases = []
+    for i in range(14):
+        mode = "q8" if i % 2 else "q4g"
+        m = int(rng.integers(9, 129))
+        n = int(rng.integers(64, 3000))
+        k = 128 * int(rng.integers(32, 80))          # k >= 4096: the split routes
+        sdt = F16 if i % 3 else F32
+        g = 32 if sdt == F16 or i % 4 else 128
+        xdt = F32 if i % 5 == 0 else F16
+        cases.append((mode, m, n, k, g, bool(i % 3 == 1), xdt, sdt, F16 if i % 2 else F32))
+    return cases
+
+
+@pytest.mark.parametrize("mode,m,n,k,g,bias,xdt,sdt,ydt", _split_random_cases())
+def test_weight_only_split_random_shapes(dev, nq, mode, m, n, k, g, bias, xdt, sdt, ydt):
+    """Random batched shapes with long K through the workspace entries (split
+    wide tiles, split 16-row kernel or unsplit, as planned) against a torch fp32
+    reference on the dequantized weight."""
+    gen = torch.Generator(device=dev).manual_seed(m * 7 + n * 3 + k)
+    x = torch.randn((m, k), generator=gen, device=dev).to(xdt)
+    w = torch.randn((n, k), generator=gen, device=dev) * 0.05
+    b = torch.randn(n, generator=gen, device=dev) if bias else None
+    if mode == "q8":
+        t = nq.quantize_q8(w)
+        deq = t.q.float() * t.scale[:, None]
+        y = nq.linear_q8(x, t, b, out_dtype=ydt)
+    else:
+        t = nq.quantize_q4g(w, g, scale_dtype=sdt)
+        deq = _dequant_q4g(t, g)
+        y = nq.linear_q4g(x, t, b, out_dtype=ydt)
+    ref = x.float() @ deq.t() + (b if b is not None else 0.0)
+    assert_close_rms(host(y.float()), host(ref), f"{mode} split random {m}x{n}x{k} g{g}", fp16_out=(ydt == F16))
+
+
 # fp32 activations far outside fp16's range and deep in its subnormals, on both
 # weight-only MFMA kernels (16-row tiles: k % 128 != 0 or small m; wide tiles:
 # m > 128, k % 128 == 0): the exact bf16 split keeps every row at the accuracy of
