@@ -476,14 +476,11 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_fused_kernel(
             const RowQuantizer rq(as[i]);
             int qd[4];
 #pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                int packed = 0;
+            for (int h = 0; h < 2; ++h) {
+                float v[8];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int code = static_cast<int>(rq.code(xc[i].at(4 * d + e), 127.0f));
-                    packed |= (code & 0xFF) << (8 * e);
-                }
-                qd[d] = packed;
+                for (int e = 0; e < 8; ++e) v[e] = xc[i].at(8 * h + e);
+                rq.pack8(v, qd[2 * h], qd[2 * h + 1]);
             }
 #pragma unroll
             for (int r = 0; r < R; ++r)
@@ -650,11 +647,10 @@ __global__ __launch_bounds__(kDecThreads) void w8a8_decode_kernel(const XT* __re
             int lo = 0, hi = 0;
             if (i < m) {
                 const RowQuantizer rq(a_scale[i]);
+                float vv[8];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    lo |= (static_cast<int>(rq.code(xv[u].at(j), 127.0f)) & 0xFF) << (8 * j);
-                    hi |= (static_cast<int>(rq.code(xv[u].at(4 + j), 127.0f)) & 0xFF) << (8 * j);
-                }
+                for (int j = 0; j < 8; ++j) vv[j] = xv[u].at(j);
+                rq.pack8(vv, lo, hi);
             }
             typedef int v2i __attribute__((ext_vector_type(2)));
             reinterpret_cast<v2i*>(xq)[v] = v2i{lo, hi};  // rows past m hold zero codes
