@@ -1256,15 +1256,19 @@ extern "C" nq_status nq_linear_w8a8(const void* x, nq_dtype x_dtype, const int8_
     // kernel while the rows are short (every workgroup quantizes all m rows, a
     // VALU cost that grows with m * k); else, up to m = 16, one act-quant launch
     // and the decode kernel on its codes where the weight is small.
+    // One activation row takes the fused-quant GEMV first, whatever k: its
+    // workgroups stream their rows once and quantize one short row (m = 1: n = k =
+    // 1536 5.29 -> 3.41 us, n = 256 4.30 -> 3.11, n = 4864, k = 896 5.44 -> 4.72
+    // against the decode kernel; m = 2..4 measured even and keep it).
     const bool decode = path == NQ_PATH_AUTO && m <= 8;
     const bool decode16 = path == NQ_PATH_AUTO && m <= 16;
-    if (decode && m * k <= kDecodeFuseMax) {
-        nq_status st = NQ_OK;
-        if (w8a8_decode_launch(x, x_dtype, wq, w_scale, bias, y, y_dtype, m, n, k, s, &st, nullptr)) return st;
-    }
     if (p == NQ_PATH_GEMV) {
         nq_status st = NQ_OK;
         if (gemv_w8a8_fused_launch(x, x_dtype, wq, w_scale, bias, y, y_dtype, m, n, k, s, &st)) return st;
+    }
+    if (decode && m * k <= kDecodeFuseMax) {
+        nq_status st = NQ_OK;
+        if (w8a8_decode_launch(x, x_dtype, wq, w_scale, bias, y, y_dtype, m, n, k, s, &st, nullptr)) return st;
     }
     char* base = static_cast<char*>(workspace);
     int8_t* xq = reinterpret_cast<int8_t*>(base);
