@@ -44,7 +44,7 @@ typedef enum nq_dtype { NQ_F32 = 0, NQ_F16 = 1 } nq_dtype;
 /* Kernel selection for the W8A8 linears. AUTO: m <= 4 (m <= 8 when k >= 4096 or n >= 8192)
  * -> workgroup-per-rows GEMV (v_dot4_i32_i8), larger m -> int8 MFMA GEMM; nq_linear_w8a8 runs
  * m = 1 as one GEMV launch with the act quant fused in, and with AUTO tries the one-launch
- * decode kernel (m <= 8, m * k <= 4096) and the decode kernel over the act quant's codes
+ * decode kernel (m * k <= 4096, or m <= 4 and m * k <= 8192) and the decode kernel over the act quant's codes
  * (m <= 16, n and k <= 2048) before the rest. The forced values exist for A/B
  * tests, like the reference's CudaPolicy::force_tiled_w8a8
  * (cuda_backend.hpp:43-89). GENERIC is the scalar bounds-checked kernel. */
