@@ -1268,8 +1268,10 @@ extern "C" nq_status nq_linear_w8a8(const void* x, nq_dtype x_dtype, const int8_
     }
     // Up to 4 rows the in-kernel quant stays cheap to 8192 codes (m = 4, n = k =
     // 1536: 6.75 -> 6.06 us; m = 3: 6.65 -> 5.69; n = 256: 6.23 -> 5.17); at 8
-    // rows and k = 1536 it lost (7.0 -> 8.1), which the 4096 limit keeps out.
-    if (decode && (m * k <= kDecodeFuseMax || (m <= 4 && m * k <= 2 * kDecodeFuseMax))) {
+    // rows and k = 1536 it lost (7.0 -> 8.1), which the 4096 limit keeps out, and
+    // so did fp32 activations on a tall weight (m = 4, n = 8960: 7.84 -> 8.45).
+    if (decode && (m * k <= kDecodeFuseMax ||
+                   (m <= 4 && m * k <= 2 * kDecodeFuseMax && (x_dtype == NQ_F16 || n <= 4096)))) {
         nq_status st = NQ_OK;
         if (w8a8_decode_launch(x, x_dtype, wq, w_scale, bias, y, y_dtype, m, n, k, s, &st, nullptr)) return st;
     }
