@@ -992,7 +992,7 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
     const int chunks = k >> 5;
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
     if constexpr (M >= 2 && sizeof(XT) == 4) {
-        if (threads <= 320) {
+        if (threads <= 320 && n >= 1024) {  // 256+ workgroups (n = 256, m = 5: 5.66 -> 6.76 us with 4 rows)
             gemv_q4g_kernel<4, M, XT, YT, ST, 320><<<(n + 3) / 4, threads, 0, s>>>(x, w, sc, b, y, m, n, k, g);
             return;
         }

@@ -177,7 +177,7 @@ struct WFrag<false> {  // 8 int8 codes = two dwords, byte t of dword d = column 
     }
 };
 
-template <bool Q4, int TM, int TN, typename XT, typename YT, typename ST>
+template <bool Q4, int TM, int TN, typename XT, typename YT, typename ST, bool SPLIT = false>
 __global__ __launch_bounds__(wq_waves<TM>() * 64) void gemm_wq_kernel(
     const XT* __restrict__ x, const uint8_t* __restrict__ wq, const ST* __restrict__ scale,
     const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int group, float* __restrict__ planes,
@@ -194,9 +194,10 @@ __global__ __launch_bounds__(wq_waves<TM>() * 64) void gemm_wq_kernel(
     x += static_cast<size_t>(blockIdx.y) * 64 * k;
     y += static_cast<size_t>(blockIdx.y) * 64 * n;
     m = min(64, m - static_cast<int>(blockIdx.y) * 64);
-    // gridDim.z ranges of split_chunks chunks of K (one range without a split)
-    const int c_begin = blockIdx.z * split_chunks;
-    const int chunks = min(k >> 5, c_begin + split_chunks) - c_begin;
+    // SPLIT: gridDim.z ranges of split_chunks chunks of K (the unsplit kernel is
+    // compiled without the range arithmetic)
+    const int c_begin = SPLIT ? static_cast<int>(blockIdx.z) * split_chunks : 0;
+    const int chunks = SPLIT ? min(k >> 5, c_begin + split_chunks) - c_begin : k >> 5;
     const int rowb = Q4 ? (k >> 1) : k;  // weight bytes per row
     const int groups = Q4 ? k / group : 1;
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<XT*>(x), 0, m * k * static_cast<int>(sizeof(XT)), 0x00020000);
@@ -321,7 +322,7 @@ __global__ __launch_bounds__(wq_waves<TM>() * 64) void gemm_wq_kernel(
         if (mm >= m || nn >= n) continue;
         float s = 0.0f;
         for (int w = 0; w < kWqWaves; ++w) s += part[w][i][j][l][v];
-        if (planes) {  // split K: this range's raw sum (Q8 before its row scale)
+        if constexpr (SPLIT) {  // this range's raw sum (Q8 before its row scale)
             planes[(static_cast<size_t>(blockIdx.z) * m_all + blockIdx.y * 64 + mm) * n + nn] = s;
             continue;
         }
@@ -386,8 +387,12 @@ nq_status launch_wq(const XT* x, const uint8_t* w, const ST* sc, const float* b,
     auto go = [&](auto tmtag, auto tntag) {
         constexpr int TM = decltype(tmtag)::value, TN = decltype(tntag)::value;
         const dim3 grid(static_cast<unsigned>((n + 16 * TN - 1) / (16 * TN)), mblocks, static_cast<unsigned>(p.splits));
-        gemm_wq_kernel<Q4, TM, TN, XT, YT, ST><<<grid, wq_waves<TM>() * 64, 0, s>>>(x, w, sc, b, y, m, n, k, g, planes,
-                                                                                   p.per);
+        if (planes)
+            gemm_wq_kernel<Q4, TM, TN, XT, YT, ST, true><<<grid, wq_waves<TM>() * 64, 0, s>>>(x, w, sc, b, y, m, n, k,
+                                                                                             g, planes, p.per);
+        else
+            gemm_wq_kernel<Q4, TM, TN, XT, YT, ST><<<grid, wq_waves<TM>() * 64, 0, s>>>(x, w, sc, b, y, m, n, k, g,
+                                                                                       nullptr, p.per);
     };
     auto with_tn = [&](auto tmtag) {
         if constexpr (decltype(tmtag)::value <= 2) {
