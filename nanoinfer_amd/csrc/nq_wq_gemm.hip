@@ -534,8 +534,11 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_wq_wide_kernel(
         sloff[q] = b < S::kNS ? S::kSOff + b * 256 : S::kSink;
     }
     // gridDim.y ranges of split_slabs slabs of K (one range without a split)
-    const int kb = blockIdx.y * split_slabs;
-    const int nk = min(k / SK, kb + split_slabs) - kb;
+    // Only the two-slot ring (DMAX < 8) runs split K; the other instantiations
+    // are compiled without the range arithmetic.
+    constexpr bool kSplit = DMAX < 8;
+    const int kb = kSplit ? static_cast<int>(blockIdx.y) * split_slabs : 0;
+    const int nk = kSplit ? min(k / SK, kb + split_slabs) - kb : k / SK;
     const unsigned lds_base = static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds));
     auto issue = [&](int sl) {
         const unsigned slot = static_cast<unsigned>(sl % D) * S::kSlab;
@@ -680,7 +683,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_wq_wide_kernel(
 
     // Lane l holds, for fragment (i, j), rows m0 + wm*16*FM + j*16 + 4*(l/16) + v
     // of column n0 + wn*16*FN + i*16 + l%16.
-    if (planes) {  // split K: this range's raw sums (Q8 before its row scale) into plane blockIdx.y
+    if constexpr (kSplit) {  // this range's raw sums (Q8 before its row scale) into plane blockIdx.y
         float* pl = planes + static_cast<size_t>(blockIdx.y) * m * n;
 #pragma unroll
         for (int i = 0; i < FN; ++i) {
@@ -880,10 +883,11 @@ nq_status wq_wide_tiles(const XT* x, const uint8_t* w, const ST* sc, const float
 template <bool Q4, typename XT, typename YT, typename ST>
 nq_status wq_wide(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n, int k,
                   int group, WqTile pick, float* planes, int splits, int split_slabs, hipStream_t s) {
-    if (!planes || splits <= 1) {  // no planes: one range over all of K
+    if (!planes || splits <= 1 || !pick.shallow) {  // one range over all of K (split K runs shallow tiles)
         planes = nullptr;
         splits = 1;
         split_slabs = k / pick.sk;
+        pick.shallow = false;
     }
     if (nq_status st = wq_wide_tiles<Q4>(x, w, sc, b, y, m, n, k, group, pick, splits > 1 ? planes : nullptr, splits,
                                          split_slabs, s))
