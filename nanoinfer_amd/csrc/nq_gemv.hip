@@ -52,13 +52,11 @@ constexpr int w8a8_rows_for() {
 // BPERM: exchanges through ds_bpermute instead of DPP / row swaps (see
 // wave_reduce_stage_bperm), for the kernels whose all-VALU reduction spilled.
 template <int R, int M, bool BPERM = false, typename T>
-__device__ __forceinline__ void reduce_to_lds(T (&acc)[R][M], T* red, int wave, int lane) {
+__device__ __forceinline__ T wave_reduce_rows(T (&acc)[R][M], int lane) {
     constexpr int NV = R * M;
     if constexpr (NV == 1) {
-        T v;
-        if constexpr (std::is_floating_point_v<T>) v = wave_sum_f32(acc[0][0]);
-        else v = wave_sum_i32(acc[0][0]);
-        if (lane == 0) red[wave] = v;
+        if constexpr (std::is_floating_point_v<T>) return wave_sum_f32(acc[0][0]);
+        else return wave_sum_i32(acc[0][0]);
     } else {
         T v[NV];
 #pragma unroll
@@ -67,9 +65,15 @@ __device__ __forceinline__ void reduce_to_lds(T (&acc)[R][M], T* red, int wave, 
             for (int i = 0; i < M; ++i) v[r * M + i] = acc[r][i];
         if constexpr (BPERM) wave_reduce_stage_bperm<NV, 32>(v, lane);
         else wave_reduce_multi<NV>(v, lane);
-        constexpr int G = 64 / NV;
-        if (lane % G == 0) red[wave * NV + lane / G] = v[0];
+        return v[0];
     }
+}
+// The wave's total of value j = r * M + i is in lane j * (64 / (R * M)).
+template <int R, int M, bool BPERM = false, typename T>
+__device__ __forceinline__ void reduce_to_lds(T (&acc)[R][M], T* red, int wave, int lane) {
+    constexpr int NV = R * M, G = 64 / NV;
+    const T v = wave_reduce_rows<R, M, BPERM>(acc, lane);
+    if (lane % G == 0) red[wave * NV + lane / G] = v;
 }
 
 // ---- activation chunk loaders ------------------------------------------------------
@@ -179,6 +183,20 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q8_kernel(
             }
             acc[r][i] = act ? p : 0.0f;
         }
+    }
+    if (!AM && nw == 1) {
+        // One wave (k <= 1024): its lanes hold the row totals after the exchange;
+        // no LDS round trip and no barrier.
+        constexpr int G = 64 / (R * M);
+        const float v = wave_reduce_rows<R, M>(acc, tid);
+        if (tid % G == 0) {
+            const int j = tid / G, r = j / M, i = j % M, row = row0 + r;
+            if (row < n && i < m) {
+                const float b = bias ? bias[row] : 0.0f;
+                y[static_cast<size_t>(i) * n + row] = from_f32<YT>(__builtin_fmaf(v, ws[row], b));
+            }
+        }
+        return;
     }
     reduce_to_lds<R, M>(acc, red, wave, tid & 63);
     __syncthreads();
@@ -347,6 +365,18 @@ __global__ __launch_bounds__(LB) void gemv_q4g_kernel(
     // int4 batches of 8 rows (and 4 fp16 rows) spilled with the all-VALU
     // exchanges (m = 8, k = 8960, n = 1536: 96 -> 12 us with ds_bpermute)
     constexpr bool kBperm = R * M >= 16 || (M == 4 && sizeof(XT) == 2);
+    // One wave (k <= 2048): write from the lanes holding the totals. Not for
+    // 2 rows x 4 fp32 activation rows, where it raised the spills from 4 to 6.
+    constexpr bool kLaneOut = !(R == 2 && M == 4 && sizeof(XT) == 4);
+    if (kLaneOut && nw == 1) {
+        constexpr int G = 64 / (R * M);
+        const float v = wave_reduce_rows<R, M, kBperm>(acc, tid);
+        if (tid % G == 0) {
+            const int j = tid / G, r = j / M, i = j % M, row = row0 + r;
+            if (row < n && i < m) y[static_cast<size_t>(i) * n + row] = from_f32<YT>(v + (bias ? bias[row] : 0.0f));
+        }
+        return;
+    }
     reduce_to_lds<R, M, kBperm>(acc, red, wave, tid & 63);
     __syncthreads();
     if (tid < R * M) {
