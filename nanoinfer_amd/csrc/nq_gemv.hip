@@ -691,7 +691,11 @@ __global__ __launch_bounds__(kDecThreads) void w8a8_decode_kernel(const XT* __re
 
     // Phase 2: groups of R weight rows; T passes of 64 chunk positions.
     for (; g < groups; g += wstride) {
-        if constexpr (DB) load(g + wstride, nxt);
+        // The next group only where there is one: a clamped re-load of the last
+        // group by every wave without a second group hammered one L2 channel.
+        if constexpr (DB) {
+            if (g + wstride < groups) load(g + wstride, nxt);
+        }
         else load(g, cur);
         int acc[R * M];
 #pragma unroll
