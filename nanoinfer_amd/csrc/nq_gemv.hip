@@ -1136,9 +1136,11 @@ bool w8a8_decode_launch(const void* x, nq_dtype xdt, const int8_t* w, const floa
     };
     // Passes padded up to 2, 4 or 9 (a masked extra pass re-loads the last
     // chunk). R rows per group: the m code chunks read from LDS per pass serve R
-    // rows; long K keeps R <= 2 for registers, and weights with fewer rows than
-    // about four groups per CU take single-row groups so that every CU streams.
-    const bool few = n < 4 * static_cast<int64_t>(cus);
+    // rows; long K keeps R <= 2 for registers, and short-K weights with fewer
+    // rows than 16 per CU take single-row groups, so that most of a CU's 16 waves
+    // stream (m = 8, n = k = 1536 with codes: 7.06 -> 6.49 us; n = 2048: 7.22 ->
+    // 6.61; from 4 per CU; 48 per CU lost at n = 4864 and 8960).
+    const bool few = n < 16 * static_cast<int64_t>(cus);
     auto with_t = [&](auto mtag, auto* xp, auto* yp) {
         constexpr int M = decltype(mtag)::value;
         constexpr int RS = M == 16 ? 2 : M == 8 ? 4 : M == 4 ? 2 : M;  // short K
