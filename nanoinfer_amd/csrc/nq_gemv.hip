@@ -1100,15 +1100,18 @@ nq_status gemv_w8a8_launch(const int8_t* xq, const float* as, const int8_t* w, c
 
 // The decode kernel for m <= 8 (see w8a8_decode_kernel): with pre_scale ==
 // nullptr it quantizes x itself (one launch), else x is the int8 codes of
-// nq_act_quant_i8 and pre_scale their row scales (then also m <= 16, as one
-// batch of 16). Returns false (nothing launched) outside its contract:
+// nq_act_quant_i8 and pre_scale their row scales (then also m <= 32, as one
+// batch of 16 or 32). Returns false (nothing launched) outside its contract:
 // k % 16 == 0, k <= 9216, the padded m * k codes within 128 KB of LDS, 16-byte
 // aligned x and w.
 bool w8a8_decode_launch(const void* x, nq_dtype xdt, const int8_t* w, const float* ws, const float* bias,
                         void* y, nq_dtype ydt, int64_t m, int64_t n, int64_t k, hipStream_t s, nq_status* st,
                         const float* pre_scale) {
-    const int mb = m > 8 ? 16 : m_bucket(m);  // 9..16 rows: pre-quantized codes only
-    if (!(m >= 1 && m <= (pre_scale ? 16 : 8) && k > 0 && k % 16 == 0 && (k + 1023) / 1024 <= 9 &&
+    // 9..32 rows: pre-quantized codes only, as one batch of 16 or 32 (32 for k <=
+    // 2048)
+    const int mb = m > 16 ? 32 : m > 8 ? 16 : m_bucket(m);
+    if (!(m >= 1 && m <= (pre_scale ? 32 : 8) && k > 0 && k % 16 == 0 && (k + 1023) / 1024 <= 9 &&
+          (mb <= 16 || k <= 2048) &&
           static_cast<int64_t>(mb) * k <= kDecMaxCodes &&
           aligned(w, 16) && aligned(x, 16) && n <= kMaxIndex))
         return false;
@@ -1145,10 +1148,12 @@ bool w8a8_decode_launch(const void* x, nq_dtype xdt, const int8_t* w, const floa
         constexpr int M = decltype(mtag)::value;
         // short K: 2 rows from m = 2 (m = 8 over codes, n = 4864, k = 896: 7.59
         // -> 7.19 us with 2 rows against 4; 1 row at m = 2..4 lost 0.2-0.5 us)
-        constexpr int RS = M == 1 ? 1 : 2;
+        constexpr int RS = M == 1 || M == 32 ? 1 : 2;
         constexpr int RL = M == 16 ? 1 : RS < 2 ? RS : 2;                // long K
         using One = std::integral_constant<int, 1>;
-        if (T <= 2) {
+        if constexpr (M == 32) {
+            go(mtag, One{}, std::integral_constant<int, 2>{}, xp, yp);
+        } else if (T <= 2) {
             if (few) go(mtag, One{}, std::integral_constant<int, 2>{}, xp, yp);
             else go(mtag, std::integral_constant<int, RS>{}, std::integral_constant<int, 2>{}, xp, yp);
         } else if (T <= 4) {
@@ -1163,7 +1168,8 @@ bool w8a8_decode_launch(const void* x, nq_dtype xdt, const int8_t* w, const floa
             case 2: with_t(std::integral_constant<int, 2>{}, xp, yp); break;
             case 4: with_t(std::integral_constant<int, 4>{}, xp, yp); break;
             case 8: with_t(std::integral_constant<int, 8>{}, xp, yp); break;
-            default: with_t(std::integral_constant<int, 16>{}, xp, yp); break;
+            case 16: with_t(std::integral_constant<int, 16>{}, xp, yp); break;
+            default: with_t(std::integral_constant<int, 32>{}, xp, yp); break;
         }
     };
     auto with_y = [&](auto* xp) {
