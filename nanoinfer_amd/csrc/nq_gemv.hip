@@ -570,7 +570,10 @@ struct Vec8x<float> {
 
 // PRE: x holds codes already (int8 [m, k] from nq_act_quant_i8, scales in
 // pre_scale); phase 1 then only copies them into LDS.
-template <int M, int R, int T, typename XT, typename YT, bool PRE = false>
+// S > 1 (codes only): the waves of a workgroup form groups of S, and the S
+// waves of a group share its weight rows, each taking M / S activation rows
+// (narrow weights with many rows: more waves stream, each with a short chain).
+template <int M, int R, int T, typename XT, typename YT, bool PRE = false, int S = 1>
 __global__ __launch_bounds__(kDecThreads) void w8a8_decode_kernel(const XT* __restrict__ x,
                                                                   const int8_t* __restrict__ w,
                                                                   const float* __restrict__ ws,
@@ -584,10 +587,14 @@ __global__ __launch_bounds__(kDecThreads) void w8a8_decode_kernel(const XT* __re
     const int cpr = k >> 4;  // 16-byte code chunks per row
     const int vpr = k >> 3;  // 8-element activation vectors per row
 
+    static_assert(S == 1 || (PRE && M % S == 0 && (kDecThreads / 64) % S == 0), "row slices");
+    constexpr int MS = M / S;  // activation rows per wave
+    const int i0 = (wave % S) * MS;
+
     // This wave's first group of weights, requested before anything else.
     const int groups = (n + R - 1) / R;
-    const int wstride = gridDim.x * (kDecThreads / 64);
-    int g = blockIdx.x + gridDim.x * wave;
+    const int wstride = gridDim.x * (kDecThreads / 64 / S);
+    int g = blockIdx.x + gridDim.x * (wave / S);
     const v4i* wv = reinterpret_cast<const v4i*>(w);
     constexpr bool DB = T <= 2;
     v4i cur[T][R], nxt[DB ? T : 1][DB ? R : 1];
@@ -697,26 +704,27 @@ __global__ __launch_bounds__(kDecThreads) void w8a8_decode_kernel(const XT* __re
             if (g + wstride < groups) load(g + wstride, nxt);
         }
         else load(g, cur);
-        int acc[R * M];
+        int acc[R * MS];
 #pragma unroll
-        for (int j = 0; j < R * M; ++j) acc[j] = 0;
+        for (int j = 0; j < R * MS; ++j) acc[j] = 0;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int c = lane + 64 * t;
             if (c < cpr) {
 #pragma unroll
-                for (int i = 0; i < M; ++i) {
-                    const v4i a = reinterpret_cast<const v4i*>(xq)[i * cpr + c];
+                for (int i = 0; i < MS; ++i) {
+                    const v4i a = reinterpret_cast<const v4i*>(xq)[(i0 + i) * cpr + c];
 #pragma unroll
                     for (int r = 0; r < R; ++r)
 #pragma unroll
-                        for (int d = 0; d < 4; ++d) acc[r * M + i] = __builtin_amdgcn_sdot4(a[d], cur[t][r][d], acc[r * M + i], false);
+                        for (int d = 0; d < 4; ++d)
+                            acc[r * MS + i] = __builtin_amdgcn_sdot4(a[d], cur[t][r][d], acc[r * MS + i], false);
                 }
             }
         }
-        wave_reduce_multi<R * M>(acc, lane);
-        constexpr int G = 64 / (R * M);
-        const int idx = lane / G, r = idx / M, i = idx % M, row = g * R + r;
+        wave_reduce_multi<R * MS>(acc, lane);
+        constexpr int G = 64 / (R * MS);
+        const int idx = lane / G, r = idx / MS, i = i0 + idx % MS, row = g * R + r;
         if (lane % G == 0 && row < n && i < m) {
             const float b = bias ? bias[row] : 0.0f;
             y[static_cast<size_t>(i) * n + row] = from_f32<YT>(w8a8_epilogue(acc[0], a_scale[i], ws[row], b));
@@ -1107,10 +1115,10 @@ nq_status gemv_w8a8_launch(const int8_t* xq, const float* as, const int8_t* w, c
 bool w8a8_decode_launch(const void* x, nq_dtype xdt, const int8_t* w, const float* ws, const float* bias,
                         void* y, nq_dtype ydt, int64_t m, int64_t n, int64_t k, hipStream_t s, nq_status* st,
                         const float* pre_scale) {
-    // 9..32 rows: pre-quantized codes only, as one batch of 16 or 32 (32 for k <=
-    // 2048)
-    const int mb = m > 16 ? 32 : m > 8 ? 16 : m_bucket(m);
-    if (!(m >= 1 && m <= (pre_scale ? 32 : 8) && k > 0 && k % 16 == 0 && (k + 1023) / 1024 <= 9 &&
+    // 9..64 rows: pre-quantized codes only, as one batch of 16, 32 or 64 (32 and
+    // 64 for k <= 2048)
+    const int mb = m > 32 ? 64 : m > 16 ? 32 : m > 8 ? 16 : m_bucket(m);
+    if (!(m >= 1 && m <= (pre_scale ? 64 : 8) && k > 0 && k % 16 == 0 && (k + 1023) / 1024 <= 9 &&
           (mb <= 16 || k <= 2048) &&
           static_cast<int64_t>(mb) * k <= kDecMaxCodes &&
           aligned(w, 16) && aligned(x, 16) && n <= kMaxIndex))
@@ -1123,12 +1131,17 @@ bool w8a8_decode_launch(const void* x, nq_dtype xdt, const int8_t* w, const floa
     *st = NQ_OK;
     auto go = [&](auto mtag, auto rtag, auto ttag, auto* xp, auto* yp) {
         constexpr int M = decltype(mtag)::value, R = decltype(rtag)::value, TT = decltype(ttag)::value;
+        // Waves that share a row group, each with M / S activation rows: 8 rows per
+        // wave from 16 (n = 256, k = 1536: m = 16 6.64 -> 6.25 us, m = 64 10.76 ->
+        // 7.46); 4 at m = 8 with single-row groups (k/v 6.07 -> 5.91; with 2-row
+        // groups, n = 4864, k = 896, it lost 7.07 -> 7.24).
+        constexpr int S = M >= 16 ? M / 8 : M == 8 && R == 1 && TT == 2 ? 2 : 1;
         using XT = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
         using YT = std::remove_pointer_t<decltype(yp)>;
         const int groups = (ni + R - 1) / R;
         const unsigned grid = static_cast<unsigned>(std::max(1, std::min(cus, groups)));
         if (pre_scale) {
-            auto* fn = w8a8_decode_kernel<M, R, TT, int8_t, YT, true>;
+            auto* fn = w8a8_decode_kernel<M, R, TT, int8_t, YT, true, S>;
             if ((*st = set_dynamic_lds(reinterpret_cast<const void*>(fn), lds, "w8a8_decode"))) return;
             fn<<<grid, kDecThreads, lds, s>>>(static_cast<const int8_t*>(x), w, ws, bias, yp, mi, ni, ki, pre_scale);
         } else if constexpr (M <= 8) {
@@ -1148,10 +1161,10 @@ bool w8a8_decode_launch(const void* x, nq_dtype xdt, const int8_t* w, const floa
         constexpr int M = decltype(mtag)::value;
         // short K: 2 rows from m = 2 (m = 8 over codes, n = 4864, k = 896: 7.59
         // -> 7.19 us with 2 rows against 4; 1 row at m = 2..4 lost 0.2-0.5 us)
-        constexpr int RS = M == 1 || M == 32 ? 1 : 2;
+        constexpr int RS = M == 1 || M >= 32 ? 1 : 2;
         constexpr int RL = M == 16 ? 1 : RS < 2 ? RS : 2;                // long K
         using One = std::integral_constant<int, 1>;
-        if constexpr (M == 32) {
+        if constexpr (M >= 32) {
             go(mtag, One{}, std::integral_constant<int, 2>{}, xp, yp);
         } else if (T <= 2) {
             if (few) go(mtag, One{}, std::integral_constant<int, 2>{}, xp, yp);
@@ -1169,7 +1182,8 @@ bool w8a8_decode_launch(const void* x, nq_dtype xdt, const int8_t* w, const floa
             case 4: with_t(std::integral_constant<int, 4>{}, xp, yp); break;
             case 8: with_t(std::integral_constant<int, 8>{}, xp, yp); break;
             case 16: with_t(std::integral_constant<int, 16>{}, xp, yp); break;
-            default: with_t(std::integral_constant<int, 32>{}, xp, yp); break;
+            case 32: with_t(std::integral_constant<int, 32>{}, xp, yp); break;
+            default: with_t(std::integral_constant<int, 64>{}, xp, yp); break;
         }
     };
     auto with_y = [&](auto* xp) {

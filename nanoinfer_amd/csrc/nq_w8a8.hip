@@ -1190,9 +1190,10 @@ constexpr int64_t kDecodePreMaxN = 2048, kDecodePreMaxK = 2048;
 // Up to 8 rows, a weight of short rows (k <= 1024) also takes it to 5120 rows
 // (m = 8, n = 4864, k = 896: 8.23 -> 7.54 us; n = 8960 stays: 9.82 vs 10.29).
 constexpr int64_t kDecodePreShortK = 1024, kDecodePreShortMaxN = 5120;
-// 17 to 32 rows as one batch of 32 on narrow weights (n = 256, k = 1536: m = 24
-// 8.41 -> 7.71 us, m = 32 8.81 -> 7.71; n = 1536 even or slower, 64 rows slower).
-constexpr int64_t kDecodePre32MaxN = 512;
+// 17 to 64 rows as one batch of 32 or 64, 8 rows per wave, on narrow weights
+// (k = 1536: n = 256, m = 32 8.75 -> 6.68 us, m = 64 10.76 -> 7.46; n = 512, m =
+// 64 10.50 -> 8.29; n = 1536, m = 32 8.86 -> 8.35, m = 64 10.76 vs 11.49 stays).
+constexpr int64_t kDecodePre32MaxN = 1536, kDecodePre64MaxN = 512;
 nq_status act_quant(const void* x, nq_dtype xdt, int64_t m, int64_t k, int8_t* xq, float* as, hipStream_t s);
 bool gemv_w8a8_fused_launch(const void* x, nq_dtype xdt, const int8_t* w, const float* ws,
                             const float* bias, void* y, nq_dtype ydt, int64_t m, int64_t n,
@@ -1289,7 +1290,8 @@ extern "C" nq_status nq_linear_w8a8(const void* x, nq_dtype x_dtype, const int8_
     if (nq_status st = act_quant(x, x_dtype, m, k, xq, as, s)) return st;
     if (decode16 && ((n <= kDecodePreMaxN && k <= kDecodePreMaxK) ||
                      (m <= 8 && k <= kDecodePreShortK && n <= kDecodePreShortMaxN)) ||
-        (path == NQ_PATH_AUTO && m > 16 && m <= 32 && n <= kDecodePre32MaxN && k <= kDecodePreMaxK)) {
+        (path == NQ_PATH_AUTO && m > 16 && k <= kDecodePreMaxK &&
+         ((m <= 32 && n <= kDecodePre32MaxN) || (m <= 64 && n <= kDecodePre64MaxN)))) {
         nq_status st = NQ_OK;
         if (w8a8_decode_launch(xq, NQ_F16, wq, w_scale, bias, y, y_dtype, m, n, k, s, &st, as)) return st;
     }
