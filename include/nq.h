@@ -45,8 +45,9 @@ typedef enum nq_dtype { NQ_F32 = 0, NQ_F16 = 1 } nq_dtype;
  * -> workgroup-per-rows GEMV (v_dot4_i32_i8), larger m -> int8 MFMA GEMM; nq_linear_w8a8 runs
  * m = 1 as one GEMV launch with the act quant fused in, and with AUTO tries the one-launch
  * decode kernel (m * k <= 4096, or m <= 4 and m * k <= 8192) and the decode kernel over the act quant's codes
- * (m <= 16 with n and k <= 2048; m <= 8 with k <= 1024 and n <= 5120; m <= 32 with n <= 512
- * and k <= 2048) before the rest. The forced values exist for A/B
+ * (m <= 16 with n and k <= 2048; m <= 8 with k <= 1024 and n <= 5120; m = 5..8 with k >= 8192 and
+ * n <= 2048; m <= 32 with n <= 1536 and m <= 64 with n <= 512, both with k <= 2048) before
+ * the rest. The forced values exist for A/B
  * tests, like the reference's CudaPolicy::force_tiled_w8a8
  * (cuda_backend.hpp:43-89). GENERIC is the scalar bounds-checked kernel. */
 typedef enum nq_path { NQ_PATH_AUTO = 0, NQ_PATH_GEMV = 1, NQ_PATH_MFMA = 2, NQ_PATH_GENERIC = 3 } nq_path;

@@ -1134,8 +1134,9 @@ bool w8a8_decode_launch(const void* x, nq_dtype xdt, const int8_t* w, const floa
         // Waves that share a row group, each with M / S activation rows: 8 rows per
         // wave from 16 (n = 256, k = 1536: m = 16 6.64 -> 6.25 us, m = 64 10.76 ->
         // 7.46); 4 at m = 8 with single-row groups (k/v 6.07 -> 5.91; with 2-row
-        // groups, n = 4864, k = 896, it lost 7.07 -> 7.24).
-        constexpr int S = M >= 16 ? M / 8 : M == 8 && R == 1 && TT == 2 ? 2 : 1;
+        // groups, n = 4864, k = 896, it lost 7.07 -> 7.24) and on long K (n = 1536,
+        // k = 8960: 11.25 -> 11.07 with the act quant; 2 rows per wave 11.85).
+        constexpr int S = M >= 16 ? M / 8 : M == 8 && (R == 1 || TT > 2) ? 2 : 1;
         using XT = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
         using YT = std::remove_pointer_t<decltype(yp)>;
         const int groups = (ni + R - 1) / R;

@@ -1184,12 +1184,16 @@ namespace nq {
 constexpr int64_t kDecodeFuseMax = 4096;
 // Shapes on which the decode kernel over pre-quantized codes beat the GEMV /
 // MFMA paths (m = 8: k/v 7.45 -> 6.37 us, q/o 7.46 -> 7.07; m = 16: k/v 7.77 ->
-// 6.86, q/o 7.81 -> 7.49); wide (n = 8960) and long-K (k = 8960) weights stay
-// on those (m = 8: 10.3 vs 10.3, 12.5 vs 11.2; m = 16: 12.4 vs 10.3, 15.9 vs 14.6).
+// 6.86, q/o 7.81 -> 7.49); wide weights (n = 8960) stay on those (m = 8: 10.3 vs
+// 10.3; m = 16: 12.4 vs 10.3), and so do long-K ones (k = 8960) at m = 9..16
+// (15.9 vs 14.6).
 constexpr int64_t kDecodePreMaxN = 2048, kDecodePreMaxK = 2048;
 // Up to 8 rows, a weight of short rows (k <= 1024) also takes it to 5120 rows
 // (m = 8, n = 4864, k = 896: 8.23 -> 7.54 us; n = 8960 stays: 9.82 vs 10.29).
 constexpr int64_t kDecodePreShortK = 1024, kDecodePreShortMaxN = 5120;
+// 5 to 8 rows on long K up to 2048 rows (n = 1536, k = 8960: m = 8 11.25 -> 11.07
+// us, m = 6 11.09 -> 10.89; k = 4096, n = 2048 lost 8.19 -> 8.31).
+constexpr int64_t kDecodePreLongK = 8192;
 // 17 to 64 rows as one batch of 32 or 64, 8 rows per wave, on narrow weights
 // (k = 1536: n = 256, m = 32 8.75 -> 6.68 us, m = 64 10.76 -> 7.46; n = 512, m =
 // 64 10.50 -> 8.29; n = 1536, m = 32 8.86 -> 8.35, m = 64 10.76 vs 11.49 stays).
@@ -1289,7 +1293,8 @@ extern "C" nq_status nq_linear_w8a8(const void* x, nq_dtype x_dtype, const int8_
     const size_t rest_bytes = workspace_bytes - static_cast<size_t>(rest - base);
     if (nq_status st = act_quant(x, x_dtype, m, k, xq, as, s)) return st;
     if (decode16 && ((n <= kDecodePreMaxN && k <= kDecodePreMaxK) ||
-                     (m <= 8 && k <= kDecodePreShortK && n <= kDecodePreShortMaxN)) ||
+                     (m <= 8 && k <= kDecodePreShortK && n <= kDecodePreShortMaxN) ||
+                     (m > 4 && m <= 8 && k >= kDecodePreLongK && n <= kDecodePreMaxN)) ||
         (path == NQ_PATH_AUTO && m > 16 && k <= kDecodePreMaxK &&
          ((m <= 32 && n <= kDecodePre32MaxN) || (m <= 64 && n <= kDecodePre64MaxN)))) {
         nq_status st = NQ_OK;

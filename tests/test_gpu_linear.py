@@ -730,7 +730,8 @@ def test_w8a8_plans_random_shapes(dev, nq, m, n, k):
 
 # The decode-batch routes of nq_linear_w8a8 (AUTO, m <= 64): the act quant fused
 # into the decode kernel (m <= 8, m * k <= 4096), the decode kernel over
-# pre-quantized codes (n, k <= 2048; m <= 8 with k <= 1024 to n = 5120; m = 17..32
+# pre-quantized codes (n, k <= 2048; m <= 8 with k <= 1024 to n = 5120; m = 5..8
+# with k >= 8192 to n = 2048; m = 17..32
 # as one 32-row batch to n = 1536, m = 33..64 as one of 64 to n = 512; waves
 # sharing a row group over slices of the activation rows), and the GEMV / MFMA
 # paths otherwise. All share the act
@@ -744,7 +745,8 @@ def test_w8a8_plans_random_shapes(dev, nq, m, n, k):
                                    (8, 4864, 896), (6, 5120, 1024), (17, 256, 1536), (24, 256, 1536),
                                    (32, 512, 2048), (31, 100, 528), (20, 33, 16), (32, 513, 2048),
                                    (48, 256, 1536), (64, 512, 2048), (33, 300, 1040), (64, 1, 16),
-                                   (30, 1536, 1536), (40, 512, 528), (5, 256, 1536)])
+                                   (30, 1536, 1536), (40, 512, 528), (5, 256, 1536), (6, 1536, 8960),
+                                   (8, 2000, 8192), (7, 33, 9216)])
 @pytest.mark.parametrize("xdt,ydt", [(torch.float16, torch.float16), (torch.float32, torch.float32),
                                      (torch.float16, torch.float32)])
 def test_w8a8_decode_routes_equal_mfma(dev, nq, m, n, k, xdt, ydt):
