@@ -145,16 +145,28 @@ __device__ __forceinline__ int xcd_row_group() {
 // AM: instead of storing y, reduce this workgroup's R logits of each activation
 // row to an ArgPart (part[i * gridDim.x + blockIdx.x]); the logits are the same
 // fp32 values the plain kernel would store, so argmax(fused) == argmax(y).
-template <int R, int M, typename XT, typename YT, bool AM = false>
+// XS > 1: XS workgroups per row group, each taking M of the activation rows
+// (neighbouring indices of xcd_row_group, so the XS readers of a weight row
+// group run together on one XCD and share its L2).
+template <int R, int M, typename XT, typename YT, bool AM = false, int XS = 1>
 __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q8_kernel(
     const XT* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ ws,
     const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, ArgPart* __restrict__ part,
     ArgCtl* __restrict__ ctl) {
+    static_assert(XS == 1 || !AM, "activation slices write y");
     __shared__ float red[kMaxGemvWaves * R * M];
     const int tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6;
     const int chunks = k >> 4;
     const bool act = tid < chunks;
-    const int row0 = xcd_row_group() * R;
+    int rg = xcd_row_group();
+    if constexpr (XS > 1) {
+        const int sl = rg % XS;  // rows [sl * M, sl * M + M) of x and y; m > (XS - 1) * M
+        rg /= XS;
+        x += static_cast<size_t>(sl) * M * k;
+        y += static_cast<size_t>(sl) * M * n;
+        m -= sl * M;
+    }
+    const int row0 = rg * R;
 
     const int c = act ? tid : 0;
     v4i wv[R];
@@ -990,6 +1002,39 @@ void launch_q8(const XT* x, const int8_t* w, const float* ws, const float* b, YT
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
     constexpr int R = rows_for<M>();
     const int rows = q8_rows<M, XT>(n, k);
+    // fp32 activations at m = 5..8: two workgroups per row group, 4 activation
+    // rows each (half the x registers and twice the workgroups; the pair shares
+    // the weight rows through its XCD's L2), 8 weight rows where q8_rows picks 8
+    // on short K, else 4; long K with at least 256 groups of 8 keeps the single
+    // 8 x 8 workgroup (us, m = 8, old -> new: n = 1536, k = 8960 15.41 -> 14.05;
+    // n = 8960, k = 1536 13.75 -> 12.20; n = 4864, k = 896 6.20 -> 5.41; n = k =
+    // 1536 5.55 -> 4.49; n = 256, k = 1536 3.99 -> 3.64; n = 2048, k = 8192 stays
+    // 13.74, against 14.55 / 16.35 with the pairs).
+    // fp16 activations the same way on short K (m = 8: n = 8960, k = 1536 11.28 ->
+    // 10.83; n = 4864, k = 896, m = 6 5.23 -> 5.05; n = 1536, k = 8960 lost 11.40 ->
+    // 12.50).
+    if constexpr (M == 8 && !AM && sizeof(XT) == 2) {
+        if (k < 4096) {
+            gemv_q8_kernel<4, 4, XT, YT, false, 2><<<(n + 3) / 4 * 2, threads, 0, s>>>(x, w, ws, b, y, m, n, k,
+                                                                                       part, ctl);
+            return;
+        }
+    }
+    if constexpr (M == 8 && !AM && sizeof(XT) == 4) {
+        if (m > 4) {
+            const bool long_k = k >= 4096;
+            if (long_k && rows == 8 && n >= 8 * 256) {
+                gemv_q8_kernel<8, 8, XT, YT><<<(n + 7) / 8, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part, ctl);
+            } else if (!long_k && rows == 8) {
+                gemv_q8_kernel<8, 4, XT, YT, false, 2><<<(n + 7) / 8 * 2, threads, 0, s>>>(x, w, ws, b, y, m, n, k,
+                                                                                           part, ctl);
+            } else {
+                gemv_q8_kernel<4, 4, XT, YT, false, 2><<<(n + 3) / 4 * 2, threads, 0, s>>>(x, w, ws, b, y, m, n, k,
+                                                                                           part, ctl);
+            }
+            return;
+        }
+    }
     if constexpr (M <= 2 || (M == 8 && sizeof(XT) == 4)) {  // the other row counts q8_rows picks
         if (rows == 8 && R != 8) {
             gemv_q8_kernel<8, M, XT, YT, AM><<<(n + 7) / 8, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part, ctl);

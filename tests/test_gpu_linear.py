@@ -35,9 +35,14 @@ Q8_CASES = [
     (16, 896, 896, True, F32, F16),       # m > 8: slices of 8 rows
     (100, 896, 4864, False, F32, F32),    # :440 ragged m, wide k
     (5, 64, 16384, False, F32, F32),      # k beyond one workgroup (generic)
-    (8, 1536, 8960, True, F32, F32),      # fp32 x, m = 5..8: 8 rows per workgroup
-    (6, 4864, 896, False, F32, F16),      # fp32 x, m = 5..8: 4 rows per workgroup
-    (7, 1001, 2048, True, F32, F32),      # fp32 x, m = 5..8, small: 2 rows, ragged n
+    (8, 1536, 8960, True, F32, F32),      # fp32 x, m = 5..8, long K: 4 weight x 4 activation rows, pairs
+    (6, 4864, 896, False, F32, F16),      # fp32 x, m = 5..8: 4 x 4 rows per workgroup, pairs
+    (7, 1001, 2048, True, F32, F32),      # fp32 x, m = 5..8, small: pairs, ragged n
+    (5, 8960, 1536, True, F32, F32),      # fp32 x, short K, tall: 8 x 4 rows, pairs, 1 row in the second
+    (8, 2048, 8192, False, F32, F16),     # fp32 x, long K, 256 groups of 8: one 8 x 8 workgroup
+    (7, 2051, 8192, True, F32, F32),      # ragged n on the 8 x 8 route
+    (8, 8963, 1536, True, F16, F16),      # fp16 x, short K: pairs, ragged n
+    (5, 1536, 8960, False, F16, F32),     # fp16 x, long K: no pairs
     (4, 4864, 896, True, F32, F32),       # fp32 x, m = 3..4: 4 rows per workgroup
     (3, 1537, 2048, False, F32, F16),     # fp32 x, m = 3..4: 4 rows, ragged n
 ]
