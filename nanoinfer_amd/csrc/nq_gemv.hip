@@ -301,7 +301,8 @@ __device__ __forceinline__ float dot32_q4_f32(v4i wv, const float (&xf)[32]) {
     return p;
 }
 
-template <int R, int M, typename XT, typename YT, typename ST, int LB = kMaxGemvThreads>
+// XS: workgroups per row group over slices of M activation rows (as gemv_q8_kernel).
+template <int R, int M, typename XT, typename YT, typename ST, int LB = kMaxGemvThreads, int XS = 1>
 __global__ __launch_bounds__(LB) void gemv_q4g_kernel(
     const XT* __restrict__ x, const uint8_t* __restrict__ w, const ST* __restrict__ scale,
     const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int group) {
@@ -310,7 +311,15 @@ __global__ __launch_bounds__(LB) void gemv_q4g_kernel(
     const int chunks = k >> 5;  // 32 codes per 16-byte chunk
     const int rb = k >> 1;
     const bool act = tid < chunks;
-    const int row0 = xcd_row_group() * R;
+    int rg = xcd_row_group();
+    if constexpr (XS > 1) {
+        const int sl = rg % XS;  // rows [sl * M, sl * M + M) of x and y; m > (XS - 1) * M
+        rg /= XS;
+        x += static_cast<size_t>(sl) * M * k;
+        y += static_cast<size_t>(sl) * M * n;
+        m -= sl * M;
+    }
+    const int row0 = rg * R;
 
     const int c = act ? tid : 0;
     v4i wv[R];
@@ -1078,6 +1087,30 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
     constexpr int R = 2;
     const int chunks = k >> 5;
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
+    // Pairs of workgroups per row group over halves of the activation rows (as
+    // the q8 GEMV; us, m = 8 / 4, old -> pairs): m = 3..4 always (n = 1536, k =
+    // 8960 fp16 10.48 -> 9.31, fp32 15.17 -> 14.96; n = 4864, k = 896 fp16 m = 3
+    // 6.59 -> 5.42); m = 5..8 fp32 x from k = 1024 (k = 8960 23.6 -> 21.6, n =
+    // 8960, k = 1536 20.1 -> 19.0; n = 4864, k = 896 lost 9.74 -> 10.56), fp16 x
+    // on short K (n = 8960, k = 1536 13.0 -> 12.5; k = 8960 lost 12.0 -> 17.9).
+    constexpr bool kPairs = M == 4 || M == 8;
+    if constexpr (kPairs) {
+        constexpr int MH = M / 2;
+        const bool pairs = M == 4 ? m > 2 : m > 4 && (sizeof(XT) == 4 ? k >= 1024 : k < 4096);
+        if (pairs) {
+            if constexpr (sizeof(XT) == 4) {
+                if (threads <= 320 && n >= 1024) {
+                    gemv_q4g_kernel<4, MH, XT, YT, ST, 320, 2><<<(n + 3) / 4 * 2, threads, 0, s>>>(x, w, sc, b, y, m, n,
+                                                                                                 k, g);
+                    return;
+                }
+            } else {
+                gemv_q4g_kernel<R, MH, XT, YT, ST, kMaxGemvThreads, 2><<<(n + R - 1) / R * 2, threads, 0, s>>>(
+                    x, w, sc, b, y, m, n, k, g);
+                return;
+            }
+        }
+    }
     if constexpr (M >= 2 && sizeof(XT) == 4) {
         if (threads <= 320 && n >= 1024) {  // 256+ workgroups (n = 256, m = 5: 5.66 -> 6.76 us with 4 rows)
             gemv_q4g_kernel<4, M, XT, YT, ST, 320><<<(n + 3) / 4, threads, 0, s>>>(x, w, sc, b, y, m, n, k, g);

@@ -185,6 +185,12 @@ Q4_CASES = [
     (7, 300, 12288, 32, True, F32, F16, F32),   # fp32 x, k > 10240: 2 rows, 576 threads
     (2, 8960, 1536, 32, False, F32, F16, F16),  # fp32 x, m = 2: 4 rows
     (1, 1536, 8960, 32, True, F32, F32, F32),   # fp32 x, m = 1: 2 rows, unsigned group math
+    (3, 1536, 8960, 32, True, F16, F16, F16),   # m = 3..4: workgroup pairs over activation rows
+    (4, 4867, 896, 32, False, F16, F32, F32),   # pairs, ragged n
+    (3, 2048, 1536, 64, True, F32, F32, F16),   # fp32 x pairs, 4 rows, 320-thread bound
+    (5, 8960, 1536, 32, True, F16, F16, F16),   # m = 5..8 fp16 short K: pairs, 1 row in the second
+    (8, 1027, 2048, 32, False, F32, F16, F32),  # m = 5..8 fp32 pairs, ragged n
+    (7, 1536, 8960, 32, True, F16, F16, F32),   # fp16 long K: no pairs
 ]
 
 
