@@ -1011,6 +1011,17 @@ void launch_q8(const XT* x, const int8_t* w, const float* ws, const float* b, YT
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
     constexpr int R = rows_for<M>();
     const int rows = q8_rows<M, XT>(n, k);
+    // m = 2: a workgroup per activation row, the pair on one XCD (n = 1536, k =
+    // 8960 fp16 x 7.47 -> 5.88 us, fp32 x 7.71 -> 6.71; n = 4864, k = 896 fp16
+    // 3.96 -> 3.58; n = k = 1536 3.87 -> 3.41), except tall short-K weights (n =
+    // 8960, k = 1536 lost 6.04 -> 6.48).
+    if constexpr (M == 2 && !AM) {
+        if (m > 1 && rows == R && (n < 8192 || k >= 4096)) {
+            gemv_q8_kernel<R, 1, XT, YT, false, 2><<<(n + R - 1) / R * 2, threads, 0, s>>>(x, w, ws, b, y, m, n, k,
+                                                                                           part, ctl);
+            return;
+        }
+    }
     // fp32 activations at m = 5..8: two workgroups per row group, 4 activation
     // rows each (half the x registers and twice the workgroups; the pair shares
     // the weight rows through its XCD's L2), 8 weight rows where q8_rows picks 8
@@ -1093,10 +1104,14 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
     // 6.59 -> 5.42); m = 5..8 fp32 x from k = 1024 (k = 8960 23.6 -> 21.6, n =
     // 8960, k = 1536 20.1 -> 19.0; n = 4864, k = 896 lost 9.74 -> 10.56), fp16 x
     // on short K (n = 8960, k = 1536 13.0 -> 12.5; k = 8960 lost 12.0 -> 17.9).
-    constexpr bool kPairs = M == 4 || M == 8;
+    // m = 2: fp32 x on long K (n = 1536, k = 8960: 10.83 -> 8.30; fp16 x and
+    // short K lost 2-4%).
+    constexpr bool kPairs = M == 2 || M == 4 || M == 8;
     if constexpr (kPairs) {
         constexpr int MH = M / 2;
-        const bool pairs = M == 4 ? m > 2 : m > 4 && (sizeof(XT) == 4 ? k >= 1024 : k < 4096);
+        const bool pairs = M == 2   ? m > 1 && sizeof(XT) == 4 && k >= 4096
+                           : M == 4 ? m > 2
+                                    : m > 4 && (sizeof(XT) == 4 ? k >= 1024 : k < 4096);
         if (pairs) {
             if constexpr (sizeof(XT) == 4) {
                 if (threads <= 320 && n >= 1024) {

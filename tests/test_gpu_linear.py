@@ -45,6 +45,9 @@ Q8_CASES = [
     (5, 1536, 8960, False, F16, F32),     # fp16 x, long K: no pairs
     (4, 4864, 896, True, F32, F32),       # fp32 x, m = 3..4: 4 rows per workgroup
     (3, 1537, 2048, False, F32, F16),     # fp32 x, m = 3..4: 4 rows, ragged n
+    (2, 1537, 8960, True, F16, F16),      # m = 2: a workgroup per activation row, ragged n
+    (2, 4864, 896, False, F32, F32),      # m = 2 pairs, fp32 x
+    (2, 40000, 1536, False, F16, F16),    # m = 2, very tall: 8 rows, no pairs
 ]
 
 
@@ -191,6 +194,7 @@ Q4_CASES = [
     (5, 8960, 1536, 32, True, F16, F16, F16),   # m = 5..8 fp16 short K: pairs, 1 row in the second
     (8, 1027, 2048, 32, False, F32, F16, F32),  # m = 5..8 fp32 pairs, ragged n
     (7, 1536, 8960, 32, True, F16, F16, F32),   # fp16 long K: no pairs
+    (2, 1539, 8960, 32, True, F32, F16, F16),   # m = 2 fp32 long K: pairs, ragged n
 ]
 
 
