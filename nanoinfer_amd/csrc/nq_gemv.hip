@@ -387,8 +387,10 @@ __global__ __launch_bounds__(LB) void gemv_q4g_kernel(
     // exchanges (m = 8, k = 8960, n = 1536: 96 -> 12 us with ds_bpermute)
     constexpr bool kBperm = R * M >= 16 || (M == 4 && sizeof(XT) == 2);
     // One wave (k <= 2048): write from the lanes holding the totals. Not for
-    // 2 rows x 4 fp32 activation rows, where it raised the spills from 4 to 6.
-    constexpr bool kLaneOut = !(R == 2 && M == 4 && sizeof(XT) == 4);
+    // 2 rows x 4 fp32 activation rows, where it raised the spills from 4 to 6, nor
+    // for one fp16 activation row: the untaken branch cost the k = 8960 kernel
+    // 4.61 -> 4.76 us in code generation, against 3.14 -> 3.09 at k = 1536.
+    constexpr bool kLaneOut = !(R == 2 && M == 4 && sizeof(XT) == 4) && !(M == 1 && sizeof(XT) == 2);
     if (kLaneOut && nw == 1) {
         constexpr int G = 64 / (R * M);
         const float v = wave_reduce_rows<R, M, kBperm>(acc, tid);
