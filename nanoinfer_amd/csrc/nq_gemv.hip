@@ -470,7 +470,10 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_kernel(
 // waves, derives a_scale = absmax / 127 exactly as the activation-quant kernel
 // does, quantizes its own 16-element chunk in registers and runs the same
 // v_dot4_i32_i8 core. Identical int32 accumulators and epilogue, one launch.
-template <int R, int M, typename XT, typename YT>
+// W1: one wave (k <= 1024): the wave's butterfly absmax is the row's in every
+// lane (no LDS round trip or barrier), and the lanes holding the row totals
+// store them.
+template <int R, int M, typename XT, typename YT, bool W1 = false>
 __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_fused_kernel(
     const XT* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ ws,
     const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k) {
@@ -504,18 +507,23 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_fused_kernel(
         for (int e = 0; e < 16; ++e) a = absmax_step(a, xc[i].at(e));
         am[i] = act ? a : 0.0f;
     }
-#pragma unroll
-    for (int i = 0; i < M; ++i) {
-        const float a = wave_absmax(am[i]);
-        if ((tid & 63) == 0) amax_red[wave * M + i] = a;
-    }
-    __syncthreads();
     float as[M];
+    if constexpr (W1) {
 #pragma unroll
-    for (int i = 0; i < M; ++i) {
-        float a = 0.0f;
-        for (int v = 0; v < nw; ++v) a = absmax_step(a, amax_red[v * M + i]);
-        as[i] = a / 127.0f;
+        for (int i = 0; i < M; ++i) as[i] = wave_absmax(am[i]) / 127.0f;  // am >= 0: as the fold below
+    } else {
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            const float a = wave_absmax(am[i]);
+            if ((tid & 63) == 0) amax_red[wave * M + i] = a;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            float a = 0.0f;
+            for (int v = 0; v < nw; ++v) a = absmax_step(a, amax_red[v * M + i]);
+            as[i] = a / 127.0f;
+        }
     }
 
     int acc[R][M];
@@ -542,6 +550,18 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_fused_kernel(
 #pragma unroll
             for (int r = 0; r < R; ++r) acc[r][i] = act ? acc[r][i] : 0;
         }
+    }
+    if constexpr (W1) {
+        constexpr int G = 64 / (R * M);
+        const int v = wave_reduce_rows<R, M>(acc, tid);
+        if (tid % G == 0) {
+            const int j = tid / G, r = j / M, i = j % M, row = row0 + r;
+            if (row < n && i < m) {
+                const float b = bias ? bias[row] : 0.0f;
+                y[static_cast<size_t>(i) * n + row] = from_f32<YT>(w8a8_epilogue(v, as[i], ws[row], b));
+            }
+        }
+        return;
     }
     reduce_to_lds<R, M>(acc, red, wave, tid & 63);
     __syncthreads();
@@ -1310,8 +1330,12 @@ bool gemv_w8a8_fused_launch(const void* x, nq_dtype xdt, const int8_t* w, const 
         constexpr int R = rows_for<M>();
         using XT = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
         using YT = std::remove_pointer_t<decltype(yp)>;
-        gemv_w8a8_fused_kernel<R, M, XT, YT><<<static_cast<unsigned>((n + R - 1) / R), threads, 0, s>>>(
-            xp, w, ws, bias, yp, mi, ni, ki);
+        if (threads == kWave)
+            gemv_w8a8_fused_kernel<R, M, XT, YT, true><<<static_cast<unsigned>((n + R - 1) / R), threads, 0, s>>>(
+                xp, w, ws, bias, yp, mi, ni, ki);
+        else
+            gemv_w8a8_fused_kernel<R, M, XT, YT><<<static_cast<unsigned>((n + R - 1) / R), threads, 0, s>>>(
+                xp, w, ws, bias, yp, mi, ni, ki);
     };
     auto with_y = [&](auto* xp) {
         if (ydt == NQ_F32) go(std::integral_constant<int, 1>{}, xp, static_cast<float*>(y));

@@ -761,7 +761,8 @@ def test_w8a8_plans_random_shapes(dev, nq, m, n, k):
                                    (32, 512, 2048), (31, 100, 528), (20, 33, 16), (32, 513, 2048),
                                    (48, 256, 1536), (64, 512, 2048), (33, 300, 1040), (64, 1, 16),
                                    (30, 1536, 1536), (40, 512, 528), (5, 256, 1536), (6, 1536, 8960),
-                                   (8, 2000, 8192), (7, 33, 9216)])
+                                   (8, 2000, 8192), (7, 33, 9216), (1, 4864, 896), (1, 1001, 1024),
+                                   (1, 3, 16)])
 @pytest.mark.parametrize("xdt,ydt", [(torch.float16, torch.float16), (torch.float32, torch.float32),
                                      (torch.float16, torch.float32)])
 def test_w8a8_decode_routes_equal_mfma(dev, nq, m, n, k, xdt, ydt):
