@@ -88,6 +88,7 @@ def gemv_logits(nq, xd, t, b):
     (4, 9000, 1024, False, F32),      # fp32 x, m = 3..4: 4 rows per workgroup
     (13, 20000, 512, True, F32),      # a slice of 8 and one of 5, 8 rows per workgroup
     (3, 700, 90, True, F32),          # ragged k: logits in the workspace, then argmax
+    (2, 200000, 64, False, F16),      # 25000 partials per row: 13 final workgroups
 ])
 def test_lm_head_argmax(dev, nq, orc, m, n, k, bias, xdt):
     x, w, b = data(m, n, k, m * 13 + n + k, bias=bias)
@@ -121,6 +122,21 @@ def test_lm_head_argmax_many_inputs(dev, nq):
         ids = host(nq.lm_head_argmax(xd, t, None)).tolist()
         logits = host(gemv_logits(nq, xd, t, None))
         assert ids == [ref_argmax(r) for r in logits], it
+
+
+def test_lm_head_argmax_tie_far_apart(dev, nq):
+    """A tie between rows far apart in a 200000-row head (25000 workgroup
+    partials, reduced by 13 final workgroups) goes to the first of them."""
+    n, k = 200000, 64                                   # 8 rows per workgroup, 25000 partials
+    rng = np.random.default_rng(9)
+    w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    x = rng.normal(0, 1, (1, k)).astype(np.float32)
+    for r in (170001, 199999):
+        w[r] = np.sign(x[0]) * 0.05
+    t = nq.quantize_q8(to_dev(w, dev))
+    xd = to_dev(x, dev, F16)
+    got = int(nq.lm_head_argmax(xd, t, None)[0])
+    assert got == ref_argmax(host(gemv_logits(nq, xd, t, None))[0]) == 170001
 
 
 def test_lm_head_argmax_ties_nan_inf(dev, nq):
