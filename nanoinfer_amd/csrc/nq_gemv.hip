@@ -330,7 +330,7 @@ __global__ __launch_bounds__(LB) void gemv_q4g_kernel(
         wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * rb + c * 16));
     }
     const unsigned ug = static_cast<unsigned>(group);
-    const unsigned blocks = ug == 32 ? static_cast<unsigned>(chunks) : static_cast<unsigned>(k) / ug;
+    const unsigned blocks = ug == 32 ? static_cast<unsigned>(chunks) : (static_cast<unsigned>(k) + ug - 1) / ug;  // ceil: a short last group
     const unsigned blk = ug == 32 ? static_cast<unsigned>(c) : static_cast<unsigned>(c * 32) / ug;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -409,6 +409,72 @@ __global__ __launch_bounds__(LB) void gemv_q4g_kernel(
             for (int wv_i = 0; wv_i < nw; ++wv_i) s += red[(wv_i * R + r) * M + i];
             const float b = bias ? bias[row] : 0.0f;
             y[static_cast<size_t>(i) * n + row] = from_f32<YT>(s + b);
+        }
+    }
+}
+
+// Exact int4 x fp16 dot over half a chunk (8 bytes, 16 codes), as dot32_q4_f16.
+__device__ __forceinline__ float dot16_q4_f16(unsigned w0, unsigned w1, const h2 (&xp)[8]) {
+    const h2 off1 = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
+    const h2 off16 = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
+    float p1 = 0.0f, p16 = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+        const unsigned w = d ? w1 : w0;
+        const unsigned u = w >> 8;
+        p1 = __builtin_amdgcn_fdot2(q4_pair(w, 0x000F000Fu) + off1, xp[4 * d + 0], p1, false);
+        p16 = __builtin_amdgcn_fdot2(q4_pair(w, 0x00F000F0u) + off16, xp[4 * d + 1], p16, false);
+        p1 = __builtin_amdgcn_fdot2(q4_pair(u, 0x000F000Fu) + off1, xp[4 * d + 2], p1, false);
+        p16 = __builtin_amdgcn_fdot2(q4_pair(u, 0x00F000F0u) + off16, xp[4 * d + 3], p16, false);
+    }
+    return __builtin_fmaf(p16, 0.0625f, p1);
+}
+// One fp16 activation row, half a chunk per lane: lane t takes K columns
+// 16t .. 16t + 15 (8 bytes of codes, 32 bytes of x) of each of the R rows, so a
+// workgroup has twice the waves of gemv_q4g_kernel, each lane one 8-byte load
+// per row. group is a multiple of 32, so a half chunk has one scale.
+template <int R, typename YT, typename ST>
+__global__ __launch_bounds__(kMaxGemvThreads) void gemv_q4g_x1h_half_kernel(
+    const _Float16* __restrict__ x, const uint8_t* __restrict__ w, const ST* __restrict__ scale,
+    const float* __restrict__ bias, YT* __restrict__ y, int n, int k, int group) {
+    __shared__ float red[kMaxGemvWaves * R];
+    const int tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6;
+    const int halves = k >> 4, rb = k >> 1;
+    const int row0 = xcd_row_group() * R;
+    const bool act = tid < halves;
+    const int hc = act ? tid : 0;  // half chunk: K columns 16 hc .. 16 hc + 15
+    typedef int v2i_t __attribute__((ext_vector_type(2)));
+    v2i_t wv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v2i_t*>(w + static_cast<size_t>(min(row0 + r, n - 1)) * rb + hc * 8));
+    const unsigned ug = static_cast<unsigned>(group);
+    const unsigned blocks = (static_cast<unsigned>(k) + ug - 1) / ug;  // ceil: a short last group
+    const unsigned blk = static_cast<unsigned>(hc * 16) / ug;
+    ST sraw[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) sraw[r] = scale[static_cast<size_t>(min(row0 + r, n - 1)) * blocks + blk];
+    XChunk<_Float16> xc;
+    xc.load(x + hc * 16);
+    h2 pairs[8];
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pairs[4 * d + j] = h2{xc.v[d][j], xc.v[d][j + 4]};
+    float acc[R][1];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float p = dot16_q4_f16(static_cast<unsigned>(wv[r][0]), static_cast<unsigned>(wv[r][1]), pairs) * to_f32(sraw[r]);
+        acc[r][0] = act ? p : 0.0f;
+    }
+    reduce_to_lds<R, 1>(acc, red, wave, tid & 63);
+    __syncthreads();
+    if (tid < R) {
+        const int row = row0 + tid;
+        if (row < n) {
+            float s = 0.0f;
+            for (int v = 0; v < nw; ++v) s += red[v * R + tid];
+            y[row] = from_f32<YT>(s + (bias ? bias[row] : 0.0f));
         }
     }
 }
@@ -1120,6 +1186,16 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
     constexpr int R = 2;
     const int chunks = k >> 5;
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
+    // One fp16 activation row on long K: half a chunk per lane, twice the waves
+    // (k = 8960, n = 1536: 4.67-4.69 -> 4.52-4.55 us; 3 or 4 rows per workgroup
+    // 4.67-4.72, one row 5.85, 2 or 3 whole chunks per lane 5.6-5.8).
+    if constexpr (M == 1 && sizeof(XT) == 2) {
+        const int th = ((2 * chunks + kWave - 1) / kWave) * kWave;
+        if (chunks >= 160 && th <= kMaxGemvThreads) {
+            gemv_q4g_x1h_half_kernel<R, YT, ST><<<(n + R - 1) / R, th, 0, s>>>(x, w, sc, b, y, n, k, g);
+            return;
+        }
+    }
     // Pairs of workgroups per row group over halves of the activation rows (as
     // the q8 GEMV; us, m = 8 / 4, old -> pairs): m = 3..4 always (n = 1536, k =
     // 8960 fp16 10.48 -> 9.31, fp32 15.17 -> 14.96; n = 4864, k = 896 fp16 m = 3

@@ -199,7 +199,7 @@ __global__ __launch_bounds__(wq_waves<TM>() * 64) void gemm_wq_kernel(
     const int c_begin = SPLIT ? static_cast<int>(blockIdx.z) * split_chunks : 0;
     const int chunks = SPLIT ? min(k >> 5, c_begin + split_chunks) - c_begin : k >> 5;
     const int rowb = Q4 ? (k >> 1) : k;  // weight bytes per row
-    const int groups = Q4 ? k / group : 1;
+    const int groups = Q4 ? (k + group - 1) / group : 1;  // scales per row: ceil, a short last group
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<XT*>(x), 0, m * k * static_cast<int>(sizeof(XT)), 0x00020000);
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(wq), 0, n * rowb, 0x00020000);
 
@@ -502,7 +502,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_wq_wide_kernel(
     const int m0 = (lin % tiles_m) * BM, n0 = (lin / tiles_m) * BN;
 
     const int wrow_bytes = Q4 ? k / 2 : k;
-    const int groups = Q4 ? k >> (5 + gsh) : 1;
+    const int groups = Q4 ? (k + (32 << gsh) - 1) >> (5 + gsh) : 1;  // ceil: a short last group
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<XT*>(x), 0, m * k * static_cast<int>(sizeof(XT)), 0x00020000);
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(wq), 0, n * wrow_bytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<ST*>(scale), 0, Q4 ? n * groups * static_cast<int>(sizeof(ST)) : 0, 0x00020000);
@@ -912,7 +912,7 @@ bool wq_wide_contract(int64_t m, int64_t n, int64_t k, int64_t group) {
     if (k % 128 != 0 || m * k * static_cast<int64_t>(sizeof(XT)) >= (int64_t(1) << 31) - 64) return false;
     if (!Q4) return n * k < (int64_t(1) << 31) - 64;
     if (sizeof(ST) == 2 && group != 32 && group != 64) return false;
-    return n * (k / 2) < (int64_t(1) << 31) - 64 && n * (k / group) * int64_t(sizeof(ST)) < (int64_t(1) << 31) - 64;
+    return n * (k / 2) < (int64_t(1) << 31) - 64 && n * ((k + group - 1) / group) * int64_t(sizeof(ST)) < (int64_t(1) << 31) - 64;
 }
 template <bool Q4, typename XT, typename ST>
 bool wq_wide_ok(int64_t m, int64_t n, int64_t k, int64_t group) {

@@ -211,6 +211,12 @@ Q4_CASES = [
     (8, 1027, 2048, 32, False, F32, F16, F32),  # m = 5..8 fp32 pairs, ragged n
     (7, 1536, 8960, 32, True, F16, F16, F32),   # fp16 long K: no pairs
     (2, 1539, 8960, 32, True, F32, F16, F16),   # m = 2 fp32 long K: pairs, ragged n
+    # one fp16 row, 5120 <= k <= 9216: half a chunk per lane
+    (1, 1537, 8960, 32, True, F16, F16, F32),   # ragged n: the last workgroup has one row
+    (1, 7, 5120, 64, False, F16, F32, F16),     # group 64, fewer rows than a workgroup pair
+    (1, 999, 9216, 128, True, F16, F16, F16),   # 576 threads, group 128
+    (1, 640, 7168, 96, False, F16, F32, F32),   # group 96, k % group = 64: a short last group
+    (3, 500, 1568, 64, True, F32, F32, F32),    # k % group = 32: scale rows of ceil(k / group)
 ]
 
 
@@ -243,6 +249,8 @@ WQ_GEMM_CASES = [  # m > 8: the fp16 MFMA GEMM (m >= 16 or n >= 4096) or GEMV sl
     ("q4g", 200, 2000, 1024, 64, False, F16, F16, F32),  # fp32 y: direct stores
     ("q4g", 130, 1000, 2048, 128, True, F16, F32, F16),  # fp32 scales, one group per slab
     ("q4g", 96, 700, 1536, 256, False, F16, F32, F16),   # a group spans two slabs
+    ("q4g", 16, 1536, 1568, 64, False, F16, F16, F16),   # k % group = 32: a short last group
+    ("q4g", 130, 1000, 1664, 256, True, F16, F32, F16),  # wide kernel, k % group = 128
     ("q8", 257, 2900, 1024, 0, True, F16, F32, F32),
     ("q4g", 1100, 640, 512, 32, True, F16, F16, F16),
     ("q4g", 40, 8960, 1536, 64, True, F16, F16, F16),    # m >= 32 with >= 128 tiles
