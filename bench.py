@@ -325,6 +325,17 @@ def main():
             sweep.append(entry("q8_lmhead_argmax_cfg5b M=1 K=1536 N=151936 fp16 (greedy id, no logits)",
                                *q8_lmhead_argmax(1, 151936, 1536, torch.float16), "hbm"))
         torch.cuda.empty_cache()
+        if want("lmhead_prefill"):
+            # the LM head over prefill rows: weight-only int8 (fp16 MFMA) against
+            # the opt-in W8A8 route on the same codes (use_w8a8_lmhead,
+            # cuda_quant.cu:362-372), incl. the activation quant
+            for m in (128, 512):
+                sweep.append(entry(f"q8_lmhead_prefill M={m} K=1536 N=151936 fp16 (weight-only)",
+                                   *q8_gemv(m, 151936, 1536, torch.float16), "mfma_f16"))
+                torch.cuda.empty_cache()
+                sweep.append(entry(f"w8a8_lmhead_prefill M={m} K=1536 N=151936 fp16 (use_w8a8_lmhead, incl. act quant)",
+                                   *w8a8_linear(m, 151936, 1536), "mfma"))
+                torch.cuda.empty_cache()
         if want("w8a8_cfg3"):
             for m in (8, 16, 32, 64):
                 for nm, (n, k) in (("qo", (1536, 1536)), ("kv", (256, 1536)), ("gateup", (8960, 1536)),

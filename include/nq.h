@@ -206,6 +206,22 @@ nq_status nq_linear_q4g_ws(const void* x, nq_dtype x_dtype, const uint8_t* q, co
                            nq_dtype scale_dtype, int64_t group, const float* bias, void* y,
                            nq_dtype y_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
                            size_t workspace_bytes, void* stream);
+/* The weight-only linears with a kernel choice per call (the nq_path values), the
+ * per-call form of the reference's global CudaPolicy::force_tiled_q8
+ * (cuda_backend.hpp:57-59, read at cuda_quant.cu:308), which forces the tiled
+ * int8 GEMM at decode m for A/B runs. AUTO is nq_linear_q8_ws / nq_linear_q4g_ws;
+ * GEMV runs the decode GEMV in slices of 8 activation rows at any m; MFMA runs the
+ * fp16 MFMA GEMM at any m (NQ_BAD_ARG when k % 32 != 0, a Q4G group is not 32 *
+ * 2^j, or x / q are not 16-byte aligned); GENERIC the bounds-checked scalar
+ * kernel. Every path computes the same sums in fp32; they agree to rounding.
+ * Same workspace rule as nq_linear_q8_ws. */
+nq_status nq_linear_q8_ex(const void* x, nq_dtype x_dtype, const int8_t* q, const float* w_scale,
+                          const float* bias, void* y, nq_dtype y_dtype, int64_t m, int64_t n, int64_t k,
+                          void* workspace, size_t workspace_bytes, int path, void* stream);
+nq_status nq_linear_q4g_ex(const void* x, nq_dtype x_dtype, const uint8_t* q, const void* scale,
+                           nq_dtype scale_dtype, int64_t group, const float* bias, void* y,
+                           nq_dtype y_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
+                           size_t workspace_bytes, int path, void* stream);
 
 /* ---- W8A8 ------------------------------------------------------------------------
  * Replaces cuda_linear_w8a8 (cuda/cuda.hpp:41, cuda_quant.cu:250-284) and the CPU

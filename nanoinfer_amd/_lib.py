@@ -39,6 +39,8 @@ SIGNATURES = {
     "nq_linear_wq_workspace_size": (_Z, [_I, _I, _I]),
     "nq_linear_q8_ws": (_D, [_P, _D, _P, _P, _P, _P, _D, _I, _I, _I, _P, _Z, _P]),
     "nq_linear_q4g_ws": (_D, [_P, _D, _P, _P, _D, _I, _P, _P, _D, _I, _I, _I, _P, _Z, _P]),
+    "nq_linear_q8_ex": (_D, [_P, _D, _P, _P, _P, _P, _D, _I, _I, _I, _P, _Z, _D, _P]),
+    "nq_linear_q4g_ex": (_D, [_P, _D, _P, _P, _D, _I, _P, _P, _D, _I, _I, _I, _P, _Z, _D, _P]),
     "nq_lm_head_argmax_q8_workspace_size": (_Z, [_I, _I, _I]),
     "nq_lm_head_argmax_q8": (_D, [_P, _D, _P, _P, _P, _P, _I, _I, _I, _P, _Z, _P]),
     "nq_linear_w8a8_workspace_size": (_Z, [_I, _I, _I]),

@@ -112,20 +112,6 @@ struct PyBackend {
     }
 };
 
-// The greedy pick over one row of logits: the reference's left-to-right scan
-// with a strict > from element 0 (sampling.cpp:13-19; a NaN element 0 is
-// never beaten, later NaNs never win).
-int64_t greedy_pick(const float* row, int64_t n) {
-    int64_t best = 0;
-    float bv = row[0];
-    for (int64_t i = 1; i < n; ++i)
-        if (row[i] > bv) {
-            bv = row[i];
-            best = i;
-        }
-    return best;
-}
-
 }  // namespace
 
 PYBIND11_MODULE(nicpp, m) {
@@ -165,6 +151,20 @@ PYBIND11_MODULE(nicpp, m) {
         .def("load_quant_weight", &PyBackend::load_quant_weight, py::arg("path"), py::arg("mode"));
 
     m.def("make_backend", [](const std::string& device) { return PyBackend(device); }, py::arg("device") = "hip");
+
+    // The process-wide kernel-selection policy of the int8 embedding / LM head
+    // (the reference's cuda_policy() fields use_w8a8_lmhead and force_tiled_q8,
+    // cuda_backend.hpp:43-89).
+    m.def("set_policy", [](bool use_w8a8_lmhead, bool force_tiled_q8) {
+              hip_policy().use_w8a8_lmhead = use_w8a8_lmhead;
+              hip_policy().force_tiled_q8 = force_tiled_q8;
+          }, py::arg("use_w8a8_lmhead") = false, py::arg("force_tiled_q8") = false);
+    m.def("policy", []() {
+        py::dict d;
+        d["use_w8a8_lmhead"] = hip_policy().use_w8a8_lmhead;
+        d["force_tiled_q8"] = hip_policy().force_tiled_q8;
+        return d;
+    });
 
     py::class_<Config>(m, "Config", "Model dimensions read from config.txt.")
         .def_readonly("vocab_size", &Config::vocab_size)
@@ -221,9 +221,8 @@ PYBIND11_MODULE(nicpp, m) {
                 {
                     py::gil_scoped_release release;
                     for (int t = 0; t < max_tokens; ++t) {
-                        const Tensor lg = self.forward(ids);
-                        const int64_t v = lg.size(1);
-                        const int64_t nxt = greedy_pick(lg.data() + (lg.size(0) - 1) * v, v);
+                        // the argmax fused into the last position's LM-head GEMV
+                        const int64_t nxt = self.next_token(ids);
                         out.push_back(nxt);
                         if (nxt == eos_id) break;
                         ids.push_back(nxt);
@@ -232,6 +231,11 @@ PYBIND11_MODULE(nicpp, m) {
                 return out;
             },
             py::arg("prompt"), py::arg("max_tokens") = 20, py::arg("eos_id") = -1,
-            "Greedy continuation of prompt by full recompute; returns the new ids.")
+            "Greedy continuation of prompt by full recompute; returns the new ids. Each pick is the "
+            "LM-head GEMV with the argmax fused in (no logits leave the GPU).")
+        .def("next_token", [](const Model& self, const std::vector<int64_t>& ids) {
+                 py::gil_scoped_release release;
+                 return self.next_token(ids);
+             }, py::arg("ids"), "The greedy next token after ids (argmax of forward(ids)[-1]).")
         .def("weight_bytes", &Model::weight_bytes, "(actual_bytes, fp32_bytes) of the weights.");
 }

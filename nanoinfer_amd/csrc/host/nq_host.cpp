@@ -136,6 +136,25 @@ Tensor::Tensor(std::vector<int64_t> shape, DType dtype, Device device)
     }
 }
 
+Tensor Tensor::rows(int64_t begin, int64_t count) const {
+    require(on_device() && ndim() >= 1 && begin >= 0 && count >= 0 && begin + count <= size(0),
+            "Tensor::rows: a row range of a device tensor");
+    Tensor t;
+    t.shape_ = shape_;
+    t.shape_[0] = count;
+    t.numel_ = product(t.shape_);
+    t.dtype_ = dtype_;
+    t.device_ = device_;
+    const size_t row_bytes = size(0) ? nbytes() / static_cast<size_t>(size(0)) : 0;
+    t.dev_ = std::shared_ptr<void>(dev_, static_cast<char*>(dev_.get()) + static_cast<size_t>(begin) * row_bytes);
+    return t;
+}
+
+HipPolicy& hip_policy() {
+    static HipPolicy p;
+    return p;
+}
+
 Tensor to_device(const Tensor& host, DType dtype) {
     require(!host.on_device(), "to_device expects a host tensor");
     Tensor d(host.shape(), dtype, Device::HIP);
@@ -246,17 +265,23 @@ static const float* bias_ptr(const Tensor* bias, int64_t out, const char* who) {
     return static_cast<const float*>(bias->device_ptr());
 }
 
-Tensor linear_q8(const Tensor& x, const QTensor& w, const Tensor* bias, DType out_dtype) {
+namespace {
+Tensor linear_q8_path(const Tensor& x, const QTensor& w, const Tensor* bias, DType out_dtype, int path) {
     check_device_2d(x, "linear_q8 expects 2-D device x");
     require(x.size(1) == w.in, "linear_q8: x cols must match weight in-features");
     const float* b = bias_ptr(bias, w.out, "linear_q8: bias must be a device fp32 tensor");
     Tensor y({x.size(0), w.out}, out_dtype, Device::HIP);
     const size_t need = nq_linear_wq_workspace_size(x.size(0), w.out, w.in);
     void* ws = need ? workspace(need) : nullptr;
-    nq_check(nq_linear_q8_ws(x.device_ptr(), abi_dtype(x.dtype()), static_cast<const int8_t*>(w.q.device_ptr()),
+    nq_check(nq_linear_q8_ex(x.device_ptr(), abi_dtype(x.dtype()), static_cast<const int8_t*>(w.q.device_ptr()),
                              static_cast<const float*>(w.scale.device_ptr()), b, y.device_ptr(),
-                             abi_dtype(out_dtype), x.size(0), w.out, w.in, ws, need, g_stream));
+                             abi_dtype(out_dtype), x.size(0), w.out, w.in, ws, need, path, g_stream));
     return y;
+}
+}  // namespace
+
+Tensor linear_q8(const Tensor& x, const QTensor& w, const Tensor* bias, DType out_dtype) {
+    return linear_q8_path(x, w, bias, out_dtype, NQ_PATH_AUTO);
 }
 
 Tensor linear_w8a8(const Tensor& x, const QTensor& w, const Tensor* bias, DType out_dtype) {
@@ -326,10 +351,18 @@ public:
     Format format() const override { return Format::W8A8; }
 };
 
+// The int8 embedding / LM head (CudaEmbedQ8Weight, cuda_quant.cu:350-379):
+// linear() follows hip_policy() as the reference's follows cuda_policy().
 class HipEmbedQ8Weight : public HipQ8Weight {
 public:
     using HipQ8Weight::HipQ8Weight;
+    Tensor linear(const Tensor& x, const Tensor* bias) const override {
+        const HipPolicy& pol = hip_policy();
+        if (pol.use_w8a8_lmhead && x.ndim() == 2 && x.size(0) > kGemvMaxM) return linear_w8a8(x, t_, bias);
+        return linear_q8_path(x, t_, bias, x.dtype(), pol.force_tiled_q8 ? NQ_PATH_MFMA : NQ_PATH_AUTO);
+    }
     Tensor gather(const std::vector<int64_t>& ids) const override { return embedding_q8(t_, ids); }
+    const QTensor& codes() const { return t_; }
 };
 
 class HipQ4GWeight : public Weight {
@@ -417,6 +450,12 @@ std::vector<int64_t> lm_head_argmax(const Tensor& x, const QTensor& head, const 
               "hipMemcpyAsync");
     hip_check(hipStreamSynchronize(static_cast<hipStream_t>(g_stream)), "hipStreamSynchronize");
     return out;
+}
+
+std::vector<int64_t> lm_head_argmax(const Tensor& x, const Weight& head, const Tensor* bias) {
+    const auto* e = dynamic_cast<const HipEmbedQ8Weight*>(&head);
+    require(e != nullptr, "lm_head_argmax: the head must be an int8 embedding weight (make_q8_embed)");
+    return lm_head_argmax(x, e->codes(), bias);
 }
 
 std::unique_ptr<Weight> HipBackend::make_quant_weight(const Tensor& host, QuantMode mode) const {

@@ -65,6 +65,9 @@ public:
     float operator[](int64_t i) const { return host_[static_cast<size_t>(i)]; }
 
     void* device_ptr() const { return dev_.get(); }     // device only
+    // Rows [begin, begin + count) of a device tensor as a tensor sharing its
+    // buffer (the first dimension narrowed).
+    Tensor rows(int64_t begin, int64_t count) const;
     size_t nbytes() const { return static_cast<size_t>(numel_) * dtype_bytes(dtype_); }
 
 private:
@@ -108,6 +111,20 @@ Tensor linear_w8a8(const Tensor& x, const QTensor& w, const Tensor* bias, DType 
 Tensor linear_q4g(const Tensor& x, const Q4GTensor& w, const Tensor* bias, DType out_dtype);
 Tensor embedding_q8(const QTensor& table, const std::vector<int64_t>& ids);
 
+// Kernel selection of the int8 embedding / LM-head weight: the two fields of the
+// reference's CudaPolicy (cuda_backend.hpp:43-89) that reach the quantized path.
+// use_w8a8_lmhead: its linear at m > kGemvMaxM (prefill) runs as W8A8 on the same
+// int8 codes (cuda_quant.cu:362-372); opt-in, since the activation quant can flip
+// a close greedy token. force_tiled_q8: its weight-only linear runs the MFMA GEMM
+// at any m (cuda_quant.cu:308), for A/B runs. Process-wide and mutable, as
+// cuda_policy(); not to be flipped while another thread runs a linear.
+struct HipPolicy {
+    bool use_w8a8_lmhead = false;
+    bool force_tiled_q8 = false;
+};
+HipPolicy& hip_policy();
+constexpr int64_t kGemvMaxM = 8;  // the decode GEMVs' activation batch
+
 // Polymorphic device weight (quant.hpp:120-133).
 class Weight {
 public:
@@ -133,6 +150,9 @@ std::unique_ptr<Weight> load_quantized(const std::string& path, QuantMode mode);
 // with the reference's first-index / NaN rules (sampling.cpp:14-20), computed
 // without writing the logits. Synchronizes the stream.
 std::vector<int64_t> lm_head_argmax(const Tensor& x, const QTensor& head, const Tensor* bias = nullptr);
+// The same for an int8 embedding Weight (make_q8_embed);
+// std::invalid_argument for any other weight.
+std::vector<int64_t> lm_head_argmax(const Tensor& x, const Weight& head, const Tensor* bias = nullptr);
 
 // The backend factory seam (backend.hpp:109-114): host fp32 weights in,
 // device-resident quantized weights out.
@@ -177,12 +197,18 @@ class Model {
 public:
     explicit Model(const std::string& weights_dir, QuantMode mode = QuantMode::W8A8, Device device = Device::HIP);
     Tensor forward(const std::vector<int64_t>& ids) const;
+    // The greedy next token after ids (sampling.cpp:95 on forward's last row),
+    // with the argmax fused into the LM-head GEMV of the last position: no
+    // logits are written or copied to the host.
+    int64_t next_token(const std::vector<int64_t>& ids) const;
     const Config& config() const { return cfg_; }
     Device device() const { return Device::HIP; }
     // {actual weight bytes, bytes if everything were fp32} (model.cpp:298-322).
     std::pair<int64_t, int64_t> weight_bytes() const;
 
 private:
+    Tensor hidden(const std::vector<int64_t>& ids) const;  // final-normed [seq, hidden], device fp32
+    const Weight& head() const { return lm_head_ ? *lm_head_ : *embed_; }  // model.cpp:290-296
     struct Layer {
         std::unique_ptr<Weight> qkv, o, gate_up, down;  // q|k|v and gate|up fused by output rows
         Tensor qkv_bias, in_norm, post_norm;             // device fp32

@@ -186,12 +186,15 @@ Model::Model(const std::string& weights_dir, QuantMode mode, Device device) {
     Tensor emb = take("embed_tokens.weight");
     check2d(emb, cfg_.vocab_size, H, "embed_tokens");
     embed_ = make_q8_embed(emb);
+    // An untied checkpoint's own head; without lm_head.weight the head stays the
+    // embedding, as the reference's Model leaves lm_head_ null (model.cpp:187, 290-296).
     if (!cfg_.tie_word_embeddings) {
         auto it = w.find("lm_head.weight");
-        if (it == w.end()) throw std::runtime_error("Model: untied config without lm_head.weight");
-        check2d(it->second, cfg_.vocab_size, H, "lm_head");
-        lm_head_ = make_q8_embed(it->second);
-        w.erase(it);
+        if (it != w.end()) {
+            check2d(it->second, cfg_.vocab_size, H, "lm_head");
+            lm_head_ = make_q8_embed(it->second);
+            w.erase(it);
+        }
     }
     // RoPE tables (ops.cpp:120-142): inv_freq and angles in double, rounded to float.
     const int64_t P = cfg_.max_position_embeddings, half = d / 2;
@@ -208,7 +211,7 @@ Model::Model(const std::string& weights_dir, QuantMode mode, Device device) {
     hip_ok(hipStreamSynchronize(stream()), "hipStreamSynchronize");
 }
 
-Tensor Model::forward(const std::vector<int64_t>& ids) const {
+Tensor Model::hidden(const std::vector<int64_t>& ids) const {
     const int64_t s = static_cast<int64_t>(ids.size());
     if (s == 0) throw std::invalid_argument("Model::forward: empty ids");
     if (s > cfg_.max_position_embeddings)
@@ -239,8 +242,14 @@ Tensor Model::forward(const std::vector<int64_t>& ids) const {
         pending = ly.down->linear(act, nullptr);
     }
     nq_ok(nq_rmsnorm_f32(fp(x), fp(pending), fp(x), fp(final_norm_), eps, s, H, fp(h), st));
-    const Weight& head = lm_head_ ? *lm_head_ : *embed_;  // model.cpp:290-296
-    return to_host(head.linear(h, nullptr));
+    return h;
+}
+
+Tensor Model::forward(const std::vector<int64_t>& ids) const { return to_host(head().linear(hidden(ids), nullptr)); }
+
+int64_t Model::next_token(const std::vector<int64_t>& ids) const {
+    const Tensor h = hidden(ids);
+    return lm_head_argmax(h.rows(h.size(0) - 1, 1), head())[0];
 }
 
 std::pair<int64_t, int64_t> Model::weight_bytes() const {

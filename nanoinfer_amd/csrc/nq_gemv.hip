@@ -22,7 +22,7 @@
 
 namespace nq {
 bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m, int64_t n, int64_t k,
-                int64_t group, bool ws);
+                int64_t group, bool ws, bool forced = false);
 template <bool Q4, typename XT, typename YT, typename ST>
 nq_status wq_gemm(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int64_t m, int64_t n,
                   int64_t k, int64_t group, void* workspace, size_t workspace_bytes, hipStream_t s);
@@ -1433,10 +1433,15 @@ nq_status check_wq_workspace(const void* ws, size_t bytes, int64_t m, int64_t n,
     return NQ_OK;
 }
 
+// path: NQ_PATH_AUTO (the shape rules below), NQ_PATH_GEMV (GEMV slices of 8
+// rows at any m), NQ_PATH_MFMA (the fp16 MFMA GEMM at any m; NQ_BAD_ARG where
+// its operand contract does not hold), NQ_PATH_GENERIC (the bounds-checked
+// wave-per-row kernel).
 nq_status linear_q8_impl(const void* x, nq_dtype x_dtype, const int8_t* q, const float* w_scale, const float* bias,
                          void* y, nq_dtype y_dtype, int64_t m, int64_t n, int64_t k, void* ws, size_t ws_bytes,
-                         void* stream) {
+                         void* stream, int path = NQ_PATH_AUTO) {
     NQ_REQUIRE(dtype_ok(x_dtype) && dtype_ok(y_dtype), NQ_BAD_ARG, "linear_q8: unknown dtype");
+    NQ_REQUIRE(path >= NQ_PATH_AUTO && path <= NQ_PATH_GENERIC, NQ_BAD_ARG, "linear_q8: unknown path %d", path);
     if (m == 0 || n == 0) return NQ_OK;
     NQ_REQUIRE(w_scale, NQ_BAD_ARG, "linear_q8: null w_scale");
     NQ_REQUIRE(aligned(x, dtype_size(x_dtype)) && aligned(y, dtype_size(y_dtype)) &&
@@ -1446,7 +1451,11 @@ nq_status linear_q8_impl(const void* x, nq_dtype x_dtype, const int8_t* q, const
     const int ni = static_cast<int>(n), ki = static_cast<int>(k);
     // Batched activations: the fp16 MFMA GEMM when the shape rule in wq_gemm_ok
     // picks it, else GEMV slices of 8 rows.
-    if (wq_gemm_ok(false, x, dtype_size(x_dtype), q, m, n, k, 32, ws != nullptr)) {
+    const bool mfma = path == NQ_PATH_MFMA;
+    NQ_REQUIRE(!mfma || wq_gemm_ok(false, x, dtype_size(x_dtype), q, m, n, k, 32, ws != nullptr, true), NQ_BAD_ARG,
+               "linear_q8: the MFMA path needs k %% 32 == 0 and 16-byte aligned x and q (m=%lld n=%lld k=%lld)",
+               (long long)m, (long long)n, (long long)k);
+    if (mfma || (path == NQ_PATH_AUTO && wq_gemm_ok(false, x, dtype_size(x_dtype), q, m, n, k, 32, ws != nullptr))) {
         const uint8_t* w = reinterpret_cast<const uint8_t*>(q);
         if (x_dtype == NQ_F32 && y_dtype == NQ_F32)
             return wq_gemm<false>(static_cast<const float*>(x), w, w_scale, bias, static_cast<float*>(y), m, n, k, 32, ws, ws_bytes, s);
@@ -1456,7 +1465,8 @@ nq_status linear_q8_impl(const void* x, nq_dtype x_dtype, const int8_t* q, const
             return wq_gemm<false>(static_cast<const _Float16*>(x), w, w_scale, bias, static_cast<float*>(y), m, n, k, 32, ws, ws_bytes, s);
         return wq_gemm<false>(static_cast<const _Float16*>(x), w, w_scale, bias, static_cast<_Float16*>(y), m, n, k, 32, ws, ws_bytes, s);
     }
-    const bool fast = k % 16 == 0 && k > 0 && k / 16 <= kMaxGemvThreads && aligned(q, 16) && aligned(x, 16);
+    const bool fast = path != NQ_PATH_GENERIC && k % 16 == 0 && k > 0 && k / 16 <= kMaxGemvThreads &&
+                      aligned(q, 16) && aligned(x, 16);
     // Otherwise x rows beyond 8 run in slices of 8 (each slice re-streams the weight).
     for (int64_t r0 = 0; r0 < m; r0 += 8) {
         const int mi = static_cast<int>(m - r0 < 8 ? m - r0 : 8);
@@ -1488,8 +1498,10 @@ nq_status linear_q8_impl(const void* x, nq_dtype x_dtype, const int8_t* q, const
 
 nq_status linear_q4g_impl(const void* x, nq_dtype x_dtype, const uint8_t* q, const void* scale,
                           nq_dtype scale_dtype, int64_t group, const float* bias, void* y, nq_dtype y_dtype,
-                          int64_t m, int64_t n, int64_t k, void* ws, size_t ws_bytes, void* stream) {
+                          int64_t m, int64_t n, int64_t k, void* ws, size_t ws_bytes, void* stream,
+                          int path = NQ_PATH_AUTO) {
     NQ_REQUIRE(group > 0 && group <= kMaxIndex, NQ_BAD_SHAPE, "linear_q4g: group must be positive");
+    NQ_REQUIRE(path >= NQ_PATH_AUTO && path <= NQ_PATH_GENERIC, NQ_BAD_ARG, "linear_q4g: unknown path %d", path);
     NQ_REQUIRE(dtype_ok(x_dtype) && dtype_ok(y_dtype) && dtype_ok(scale_dtype), NQ_BAD_ARG,
                "linear_q4g: unknown dtype");
     if (m == 0 || n == 0) return NQ_OK;
@@ -1501,7 +1513,11 @@ nq_status linear_q4g_impl(const void* x, nq_dtype x_dtype, const uint8_t* q, con
     const int ni = static_cast<int>(n), ki = static_cast<int>(k), gi = static_cast<int>(group);
     // Batched activations: the fp16 MFMA GEMM when the shape rule in wq_gemm_ok
     // picks it, else GEMV slices of 8 rows.
-    if (wq_gemm_ok(true, x, dtype_size(x_dtype), q, m, n, k, group, ws != nullptr)) {
+    const bool mfma = path == NQ_PATH_MFMA;
+    NQ_REQUIRE(!mfma || wq_gemm_ok(true, x, dtype_size(x_dtype), q, m, n, k, group, ws != nullptr, true), NQ_BAD_ARG,
+               "linear_q4g: the MFMA path needs k %% 32 == 0, group = 32 * 2^j and 16-byte aligned x and q "
+               "(m=%lld n=%lld k=%lld group=%lld)", (long long)m, (long long)n, (long long)k, (long long)group);
+    if (mfma || (path == NQ_PATH_AUTO && wq_gemm_ok(true, x, dtype_size(x_dtype), q, m, n, k, group, ws != nullptr))) {
         auto go = [&](auto* xp, auto* yp) {
             if (scale_dtype == NQ_F32)
                 return wq_gemm<true>(xp, q, static_cast<const float*>(scale), bias, yp, m, n, k, group, ws, ws_bytes, s);
@@ -1514,8 +1530,8 @@ nq_status linear_q4g_impl(const void* x, nq_dtype x_dtype, const uint8_t* q, con
         if (x_dtype == NQ_F32) return with_y(static_cast<const float*>(x));
         return with_y(static_cast<const _Float16*>(x));
     }
-    const bool fast = k % 32 == 0 && k > 0 && group % 32 == 0 && k / 32 <= kMaxGemvThreads &&
-                      aligned(q, 16) && aligned(x, 16);
+    const bool fast = path != NQ_PATH_GENERIC && k % 32 == 0 && k > 0 && group % 32 == 0 &&
+                      k / 32 <= kMaxGemvThreads && aligned(q, 16) && aligned(x, 16);
     for (int64_t r0 = 0; r0 < m; r0 += 8) {
         const int mi = static_cast<int>(m - r0 < 8 ? m - r0 : 8);
         const size_t xo = static_cast<size_t>(r0) * k, yo = static_cast<size_t>(r0) * n;
@@ -1579,6 +1595,25 @@ extern "C" nq_status nq_linear_q4g_ws(const void* x, nq_dtype x_dtype, const uin
     if (nq_status st = check_wq_workspace(workspace, workspace_bytes, m, n, k, "linear_q4g_ws")) return st;
     return linear_q4g_impl(x, x_dtype, q, scale, scale_dtype, group, bias, y, y_dtype, m, n, k, workspace,
                            workspace_bytes, stream);
+}
+
+extern "C" nq_status nq_linear_q8_ex(const void* x, nq_dtype x_dtype, const int8_t* q, const float* w_scale,
+                                     const float* bias, void* y, nq_dtype y_dtype, int64_t m, int64_t n, int64_t k,
+                                     void* workspace, size_t workspace_bytes, int path, void* stream) {
+    if (nq_status st = check_linear(x, q, y, m, n, k, "linear_q8_ex")) return st;
+    if (nq_status st = check_wq_workspace(workspace, workspace_bytes, m, n, k, "linear_q8_ex")) return st;
+    return linear_q8_impl(x, x_dtype, q, w_scale, bias, y, y_dtype, m, n, k, workspace, workspace_bytes, stream,
+                          path);
+}
+
+extern "C" nq_status nq_linear_q4g_ex(const void* x, nq_dtype x_dtype, const uint8_t* q, const void* scale,
+                                      nq_dtype scale_dtype, int64_t group, const float* bias, void* y,
+                                      nq_dtype y_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
+                                      size_t workspace_bytes, int path, void* stream) {
+    if (nq_status st = check_linear(x, q, y, m, n, k, "linear_q4g_ex")) return st;
+    if (nq_status st = check_wq_workspace(workspace, workspace_bytes, m, n, k, "linear_q4g_ex")) return st;
+    return linear_q4g_impl(x, x_dtype, q, scale, scale_dtype, group, bias, y, y_dtype, m, n, k, workspace,
+                           workspace_bytes, stream, path);
 }
 
 // ---- LM head with fused greedy argmax ----------------------------------------------------

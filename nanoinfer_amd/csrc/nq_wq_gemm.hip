@@ -1002,14 +1002,15 @@ bool wq_gemm_shape_ok(int64_t m, int64_t n, int64_t k, size_t x_elem, bool ws) {
 // Whether the MFMA path takes this call (the caller runs GEMV slices otherwise):
 // whole 32-column chunks, groups of a power-of-two number of chunks, 16-byte aligned operands and
 // 32-bit buffer offsets.
+// forced: the caller asked for this path (NQ_PATH_MFMA); only the operand contract applies.
 bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m, int64_t n, int64_t k,
-                int64_t group, bool ws) {
+                int64_t group, bool ws, bool forced) {
     const int64_t rowb = q4 ? k / 2 : k;
     // Shape rule (measured): the GEMM runs one workgroup per 16 (or 32) weight
     // rows, each reading all of x, so below 4096 rows it fills under 256 CUs; a
     // GEMV slice of 8 rows plus a remainder slice is then faster up to m = 15.
-    if (!wq_gemm_shape_ok(m, n, k, x_elem, ws)) return false;
-    return k > 0 && k % 32 == 0 && (!q4 || (group % 32 == 0 && ((group / 32) & (group / 32 - 1)) == 0)) && aligned(x, 16) && aligned(w, 16) &&
+    if (!forced && !wq_gemm_shape_ok(m, n, k, x_elem, ws)) return false;
+    return m > 0 && k > 0 && k % 32 == 0 && (!q4 || (group % 32 == 0 && ((group / 32) & (group / 32 - 1)) == 0)) && aligned(x, 16) && aligned(w, 16) &&
            m <= (int64_t(65535) * 64) && std::min<int64_t>(m, 64) * k * static_cast<int64_t>(x_elem) < (int64_t(1) << 31) - 64 &&
            n * rowb < (int64_t(1) << 31) - 64;
 }

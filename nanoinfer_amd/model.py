@@ -226,7 +226,7 @@ class Model:
         model has its own lm_head), fp32 logits."""
         if isinstance(self.head, torch.Tensor):
             return torch.nn.functional.linear(x.float(), self.head)
-        return quant.linear_q8(x, self.head.t, None, out_dtype=torch.float32)
+        return quant.lm_head_linear(x, self.head.t, None, out_dtype=torch.float32)
 
     def gemm(self, xq_as, name: str) -> torch.Tensor:
         """W8A8 projection of activations quantized by a fused producer."""

@@ -246,10 +246,12 @@ def _x2d(x, w_in, who):
     return x
 
 
-def linear_q8(x: torch.Tensor, w: QTensor, bias=None, out_dtype=None) -> torch.Tensor:
+def linear_q8(x: torch.Tensor, w: QTensor, bias=None, out_dtype=None, path: int = NQ_PATH_AUTO) -> torch.Tensor:
     """quant.cpp:136-163 / cuda_quant.cu:300-322. Batched shapes whose weight
     has too few rows to fill the GPU split K over a workspace from torch's
-    allocator (nq_linear_q8_ws)."""
+    allocator. path forces a kernel family (the per-call form of the
+    reference's CudaPolicy::force_tiled_q8, cuda_backend.hpp:57-59):
+    NQ_PATH_GEMV, NQ_PATH_MFMA or NQ_PATH_GENERIC (nq_linear_q8_ex)."""
     w.check()
     x = _x2d(x, w.in_, "linear_q8")
     b = _bias(bias, w.out)
@@ -257,14 +259,15 @@ def linear_q8(x: torch.Tensor, w: QTensor, bias=None, out_dtype=None) -> torch.T
     lib = _lib.load()
     nbytes = lib.nq_linear_wq_workspace_size(x.shape[0], w.out, w.in_)
     ws = _workspace(nbytes, x.device) if nbytes else None
-    check(lib.nq_linear_q8_ws(_ptr(x), _dtype_code(x, "x"), _ptr(w.q), _ptr(w.scale), _ptr(b), _ptr(y),
-                              _dtype_code(y, "y"), x.shape[0], w.out, w.in_, _ptr(ws), nbytes, _stream()))
+    check(lib.nq_linear_q8_ex(_ptr(x), _dtype_code(x, "x"), _ptr(w.q), _ptr(w.scale), _ptr(b), _ptr(y),
+                              _dtype_code(y, "y"), x.shape[0], w.out, w.in_, _ptr(ws), nbytes, int(path),
+                              _stream()))
     return y
 
 
-def linear_q4g(x: torch.Tensor, w: Q4GTensor, bias=None, out_dtype=None) -> torch.Tensor:
-    """quant.cpp:337-389 (no GPU counterpart in the reference); split K as
-    linear_q8 does (nq_linear_q4g_ws)."""
+def linear_q4g(x: torch.Tensor, w: Q4GTensor, bias=None, out_dtype=None, path: int = NQ_PATH_AUTO) -> torch.Tensor:
+    """quant.cpp:337-389 (no GPU counterpart in the reference); split K and
+    the per-call path as linear_q8 (nq_linear_q4g_ex)."""
     w.check()
     x = _x2d(x, w.in_, "linear_q4g")
     b = _bias(bias, w.out)
@@ -272,9 +275,9 @@ def linear_q4g(x: torch.Tensor, w: Q4GTensor, bias=None, out_dtype=None) -> torc
     lib = _lib.load()
     nbytes = lib.nq_linear_wq_workspace_size(x.shape[0], w.out, w.in_)
     ws = _workspace(nbytes, x.device) if nbytes else None
-    check(lib.nq_linear_q4g_ws(_ptr(x), _dtype_code(x, "x"), _ptr(w.q), _ptr(w.scale),
+    check(lib.nq_linear_q4g_ex(_ptr(x), _dtype_code(x, "x"), _ptr(w.q), _ptr(w.scale),
                                _dtype_code(w.scale, "scale"), w.group, _ptr(b), _ptr(y), _dtype_code(y, "y"),
-                               x.shape[0], w.out, w.in_, _ptr(ws), nbytes, _stream()))
+                               x.shape[0], w.out, w.in_, _ptr(ws), nbytes, int(path), _stream()))
     return y
 
 
@@ -478,7 +481,42 @@ class _W8A8Weight(_Q8Weight):
         return linear_w8a8(x, self.t, bias)
 
 
+@dataclass
+class Policy:
+    """Kernel-selection knobs of the int8 embedding / LM-head weight, the two
+    CudaPolicy fields (cuda_backend.hpp:43-89) that reach the quantized path:
+    use_w8a8_lmhead runs the LM head's prefill linear (m > 8, the decode GEMV's
+    batch) as W8A8 on the same int8 codes (cuda_quant.cu:362-372; opt-in: the
+    activation quant can flip a close greedy token); force_tiled_q8 runs its
+    weight-only linear on the MFMA GEMM at any m (cuda_quant.cu:308, A/B only)."""
+    use_w8a8_lmhead: bool = False
+    force_tiled_q8: bool = False
+
+
+_POLICY = Policy()
+
+
+def policy() -> Policy:
+    """The process-wide policy (mutable, as the reference's cuda_policy())."""
+    return _POLICY
+
+
+GEMV_MAX_M = 8  # decode GEMV batch: rows beyond it are prefill (the reference's kGemvMaxM)
+
+
+def lm_head_linear(x: torch.Tensor, t: QTensor, bias=None, out_dtype=None) -> torch.Tensor:
+    """The int8 embedding's linear under policy() (CudaEmbedQ8Weight::linear,
+    cuda_quant.cu:362-372)."""
+    pol = policy()
+    if pol.use_w8a8_lmhead and x.shape[0] > GEMV_MAX_M:
+        return linear_w8a8(x, t, bias, out_dtype)
+    return linear_q8(x, t, bias, out_dtype, _lib.NQ_PATH_MFMA if pol.force_tiled_q8 else NQ_PATH_AUTO)
+
+
 class _EmbedQ8Weight(_Q8Weight):
+    def linear(self, x, bias=None):
+        return lm_head_linear(x, self.t, bias)
+
     def gather(self, ids):
         return embedding_q8(self.t, ids)
 

@@ -135,3 +135,27 @@ def test_workspace_sizes_all_shapes():
                 g = lib.nq_gemm_w8a8_workspace_size(m, n, k)
                 lw = lib.nq_linear_w8a8_workspace_size(m, n, k)
                 assert g % 256 == 0 and lw >= g
+
+
+def test_weight_only_path_validation(lib):
+    """nq_linear_q8_ex / nq_linear_q4g_ex: an unknown path, and a forced MFMA
+    path whose operand contract fails (k % 32 != 0, a Q4G group that is not
+    32 * 2^j, x not 16-byte aligned), are refused before any launch."""
+    from nanoinfer_amd import _lib as L
+    fake = ctypes.c_void_p(0x1000)
+    assert lib.nq_linear_q8_ex(fake, 1, fake, fake, None, fake, 1, 1, 64, 64, None, 0, 7, None) == L.NQ_BAD_ARG
+    assert b"unknown path" in lib.nq_last_error()
+    assert lib.nq_linear_q8_ex(fake, 1, fake, fake, None, fake, 1, 1, 64, 48, None, 0, L.NQ_PATH_MFMA,
+                               None) == L.NQ_BAD_ARG
+    assert b"MFMA path" in lib.nq_last_error()
+    x16 = ctypes.c_void_p(0x1008)                     # fp16-aligned, not 16-byte aligned
+    assert lib.nq_linear_q8_ex(x16, 1, fake, fake, None, fake, 1, 1, 64, 64, None, 0, L.NQ_PATH_MFMA,
+                               None) == L.NQ_BAD_ARG
+    assert lib.nq_linear_q4g_ex(fake, 1, fake, fake, 1, 96, None, fake, 1, 1, 64, 192, None, 0, L.NQ_PATH_MFMA,
+                                None) == L.NQ_BAD_ARG
+    assert lib.nq_linear_q4g_ex(fake, 1, fake, fake, 1, 32, None, fake, 1, 1, 64, 64, None, 0, -1,
+                                None) == L.NQ_BAD_ARG
+    # the split-K workspace rule holds on every path
+    need = lib.nq_linear_wq_workspace_size(64, 1536, 8960)
+    assert lib.nq_linear_q8_ex(fake, 1, fake, fake, None, fake, 1, 64, 1536, 8960, fake, need - 256,
+                               L.NQ_PATH_GEMV, None) == L.NQ_BAD_ARG
