@@ -274,13 +274,6 @@ nq_status nq_embedding_q8(const int8_t* codes, const float* scale, int64_t vocab
                           const int64_t* ids, int64_t n, void* out, nq_dtype out_dtype,
                           void* stream);
 
-/* ---- measurement helper ---------------------------------------------------------
- * No reference counterpart: one streaming read of `bytes` (16-byte aligned, a
- * multiple of 16) with the 16-byte non-temporal loads the decode GEMVs use,
- * for the benchmark's read-floor context. sink: >= 64 ints, written only in a
- * case the data never produces. */
-nq_status nq_probe_read(const void* p, size_t bytes, int* sink, void* stream);
-
 #ifdef __cplusplus
 }
 #endif

@@ -52,7 +52,6 @@ SIGNATURES = {
     "nq_w8a8_acc_i32": (_D, [_P, _P, _P, _I, _I, _I, _P, _Z, ctypes.c_int, _P]),
     "nq_embedding_q8": (_D, [_P, _P, _I, _I, _P, _I, _P, _D, _P]),
     "nq_rope_qkv": (_D, [_P, _D, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
-    "nq_probe_read": (_D, [_P, _Z, _P, _P]),
     "nq_rmsnorm_f32": (_D, [_P, _P, _P, _P, ctypes.c_float, _I, _I, _P, _P]),
     "nq_silu_mul_f32": (_D, [_P, _P, _I, _I, _I, _P, _P]),
     "nq_attention_causal_f32": (_D, [_P, _P, _P, _I, _I, _I, _I, _P, _P]),

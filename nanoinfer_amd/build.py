@@ -23,7 +23,9 @@ HOST_TEST = os.path.join(ROOT, "tests", "cpp", "test_host.bin")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["nq_abi.cpp", "nq_quantize.hip", "nq_gemv.hip", "nq_w8a8.hip", "nq_embed.hip", "nq_fused.hip", "nq_wq_gemm.hip", "nq_nit.hip", "nq_rope.hip", "nq_dequant.hip", "nq_probe.hip", "nq_ops.hip"]
+SOURCES = ["nq_abi.cpp", "nq_quantize.hip", "nq_gemv.hip", "nq_w8a8.hip", "nq_embed.hip", "nq_fused.hip", "nq_wq_gemm.hip", "nq_nit.hip", "nq_rope.hip", "nq_dequant.hip", "nq_ops.hip"]
+BENCH_SRC = os.path.join("bench", "nq_probe.hip")  # libnq_bench.so: bench.py's read probe
+BENCH_LIB = os.path.join(PKG, "libnq_bench.so")
 
 # -packed-fp32-ops: keep hipcc from forming v_pk_{add,mul,fma}_f32 (the host
 # pass prints that it does not know the feature; that is harmless).
@@ -82,12 +84,16 @@ def _host_artifacts():
 
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(SOURCES) + 1)) as ex:
+        objs = list(ex.map(_compile, SOURCES + [BENCH_SRC]))
+    bench_obj = objs.pop()
     tmp = LIB + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], "libnq_hip link")
     os.replace(tmp, LIB)
-    extra = _host_artifacts()
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", BENCH_LIB + ".tmp", bench_obj],
+         "libnq_bench link")
+    os.replace(BENCH_LIB + ".tmp", BENCH_LIB)
+    extra = [BENCH_LIB, *_host_artifacts()]
     if verbose:
         for p in [LIB, *extra]:
             print("built", p)

@@ -433,47 +433,64 @@ __device__ __forceinline__ float dot16_q4_f16(unsigned w0, unsigned w1, const h2
 // 16t .. 16t + 15 (8 bytes of codes, 32 bytes of x) of each of the R rows, so a
 // workgroup has twice the waves of gemv_q4g_kernel, each lane one 8-byte load
 // per row. group is a multiple of 32, so a half chunk has one scale.
+// The activation chunk is requested first and each row's scale and codes after
+// it, so a row's dot starts when its own load lands (the in-order load counter
+// would otherwise hold every row until the last load); R = 3 or 6 rows per
+// workgroup cut the activation re-reads, which every workgroup takes from L2
+// (n = 1536, k = 8960: 2 rows with x last 4.49-4.64 us, 3 rows x first
+// 4.32-4.35; n = 8960, k = 5120: 9.03 -> 7.26 with 6 rows).
 template <int R, typename YT, typename ST>
 __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q4g_x1h_half_kernel(
     const _Float16* __restrict__ x, const uint8_t* __restrict__ w, const ST* __restrict__ scale,
     const float* __restrict__ bias, YT* __restrict__ y, int n, int k, int group) {
+    constexpr int RP = R <= 1 ? 1 : R <= 2 ? 2 : R <= 4 ? 4 : 8;  // reduced values, a power of two
     __shared__ float red[kMaxGemvWaves * R];
     const int tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6;
     const int halves = k >> 4, rb = k >> 1;
     const int row0 = xcd_row_group() * R;
     const bool act = tid < halves;
     const int hc = act ? tid : 0;  // half chunk: K columns 16 hc .. 16 hc + 15
+    XChunk<_Float16> xc;
+    xc.load(x + hc * 16);
+    __builtin_amdgcn_sched_barrier(0);  // the activation request goes out first
     typedef int v2i_t __attribute__((ext_vector_type(2)));
-    v2i_t wv[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-        wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v2i_t*>(w + static_cast<size_t>(min(row0 + r, n - 1)) * rb + hc * 8));
     const unsigned ug = static_cast<unsigned>(group);
     const unsigned blocks = (static_cast<unsigned>(k) + ug - 1) / ug;  // ceil: a short last group
     const unsigned blk = static_cast<unsigned>(hc * 16) / ug;
+    v2i_t wv[R];
     ST sraw[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) sraw[r] = scale[static_cast<size_t>(min(row0 + r, n - 1)) * blocks + blk];
-    XChunk<_Float16> xc;
-    xc.load(x + hc * 16);
+    for (int r = 0; r < R; ++r) {
+        const size_t row = static_cast<size_t>(min(row0 + r, n - 1));
+        sraw[r] = scale[row * blocks + blk];
+        wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v2i_t*>(w + row * rb + hc * 8));
+        __builtin_amdgcn_sched_barrier(0);  // rows in order: row r's dot waits only for rows <= r
+    }
     h2 pairs[8];
 #pragma unroll
     for (int d = 0; d < 2; ++d)
 #pragma unroll
         for (int j = 0; j < 4; ++j) pairs[4 * d + j] = h2{xc.v[d][j], xc.v[d][j + 4]};
-    float acc[R][1];
+    float acc[RP][1];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const float p = dot16_q4_f16(static_cast<unsigned>(wv[r][0]), static_cast<unsigned>(wv[r][1]), pairs) * to_f32(sraw[r]);
-        acc[r][0] = act ? p : 0.0f;
+    for (int r = 0; r < RP; ++r) {
+        if (r < R) {
+            const float p = dot16_q4_f16(static_cast<unsigned>(wv[r][0]), static_cast<unsigned>(wv[r][1]), pairs) *
+                            to_f32(sraw[r]);
+            acc[r][0] = act ? p : 0.0f;
+        } else {
+            acc[r][0] = 0.0f;
+        }
     }
-    reduce_to_lds<R, 1>(acc, red, wave, tid & 63);
+    constexpr int G = 64 / RP;
+    const float v = wave_reduce_rows<RP, 1>(acc, tid & 63);
+    if ((tid & 63) % G == 0 && (tid & 63) / G < R) red[wave * R + (tid & 63) / G] = v;
     __syncthreads();
     if (tid < R) {
         const int row = row0 + tid;
         if (row < n) {
             float s = 0.0f;
-            for (int v = 0; v < nw; ++v) s += red[v * R + tid];
+            for (int q = 0; q < nw; ++q) s += red[q * R + tid];
             y[row] = from_f32<YT>(s + (bias ? bias[row] : 0.0f));
         }
     }
@@ -1016,12 +1033,13 @@ __global__ __launch_bounds__(1024) void argmax_final_kernel(const ArgPart* __res
 
 // Fused path's final reduction: gridDim.x workgroups per activation row
 // (blockIdx.y), each reducing T * U partials with all its loads in flight, then
-// one 64-bit device-scope atomic max of its key and a ticket; the workgroup
-// that takes the last ticket reads the key and writes the id. Device-scope
-// atomics are performed past the per-XCD L2s, in issue order for one thread
-// (the max has returned before the ticket is taken), so the last ticket sees
-// every key. Same result as argmax_final_kernel: the reference scan's first
-// maximal index, 0 when logit 0 is NaN or nothing qualifies.
+// one 64-bit agent-scope atomic max of its key and a ticket; the workgroup
+// that takes the last ticket reads the key and writes the id. Ordering: each
+// workgroup's key max is sequenced before its ticket increment, which is a
+// release; the last ticket's increment is also an acquire, so every key max
+// happens before its load of the key (release sequence on the ticket). Same
+// result as argmax_final_kernel: the reference scan's first maximal index, 0
+// when logit 0 is NaN or nothing qualifies.
 __device__ __forceinline__ unsigned arg_order_bits(float v) {
     const unsigned u = __builtin_bit_cast(unsigned, v);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -1055,8 +1073,7 @@ __global__ __launch_bounds__(T) void argmax_final_multi_kernel(const ArgPart* __
         if (blockIdx.x == 0 && p[0].i == -1) key = ~0ull;
         else if (bi != kArgNone) key = (static_cast<unsigned long long>(arg_order_bits(bv)) << 32) | (0xFFFFFFFFu - static_cast<unsigned>(bi));
         __hip_atomic_fetch_max(&ctl[i].key, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        const unsigned t = __hip_atomic_fetch_add(&ctl[i].ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned t = __hip_atomic_fetch_add(&ctl[i].ticket, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         if (t == gridDim.x - 1) {
             const unsigned long long f = __hip_atomic_load(&ctl[i].key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             ids[i] = (f == ~0ull || f == 0) ? 0 : static_cast<int64_t>(0xFFFFFFFFu - static_cast<unsigned>(f & 0xFFFFFFFFu));
@@ -1187,12 +1204,17 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
     const int chunks = k >> 5;
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
     // One fp16 activation row on long K: half a chunk per lane, twice the waves
-    // (k = 8960, n = 1536: 4.67-4.69 -> 4.52-4.55 us; 3 or 4 rows per workgroup
-    // 4.67-4.72, one row 5.85, 2 or 3 whole chunks per lane 5.6-5.8).
+    // (k = 8960, n = 1536: 4.67-4.69 -> 4.52-4.55 us with 2 rows; one row 5.85,
+    // 2 or 3 whole chunks per lane 5.6-5.8), 3 rows per workgroup with the
+    // activation loaded first, 6 for tall weights (n = 8960, k = 5120: whole
+    // chunks with 2 / 4 / 6 rows 8.0 / 7.6 / 8.3 us, half chunks with 6 rows 7.3).
     if constexpr (M == 1 && sizeof(XT) == 2) {
         const int th = ((2 * chunks + kWave - 1) / kWave) * kWave;
         if (chunks >= 160 && th <= kMaxGemvThreads) {
-            gemv_q4g_x1h_half_kernel<R, YT, ST><<<(n + R - 1) / R, th, 0, s>>>(x, w, sc, b, y, n, k, g);
+            if (n >= 4096)
+                gemv_q4g_x1h_half_kernel<6, YT, ST><<<(n + 5) / 6, th, 0, s>>>(x, w, sc, b, y, n, k, g);
+            else
+                gemv_q4g_x1h_half_kernel<3, YT, ST><<<(n + 2) / 3, th, 0, s>>>(x, w, sc, b, y, n, k, g);
             return;
         }
     }

@@ -40,3 +40,25 @@ def dev():
 def nq():
     from nanoinfer_amd import quant
     return quant
+
+
+# NQ_TEST_TIMES=<path>: append "<start_ns> <end_ns> <test id>" per test (CLOCK_MONOTONIC
+# and CLOCK_BOOTTIME both, as "mono"/"boot" lines), so that a kernel trace of the
+# same run (rocprofv3 --kernel-trace) can name the test that launched each kernel.
+_TIMES = os.environ.get("NQ_TEST_TIMES")
+if _TIMES:
+    import time
+
+    @pytest.hookimpl(hookwrapper=True)
+    def pytest_runtest_call(item):
+        t0m, t0b = time.clock_gettime_ns(time.CLOCK_MONOTONIC), time.clock_gettime_ns(time.CLOCK_BOOTTIME)
+        yield
+        try:
+            import torch
+            if torch.cuda.is_initialized():
+                torch.cuda.synchronize()
+        except Exception:
+            pass
+        t1m, t1b = time.clock_gettime_ns(time.CLOCK_MONOTONIC), time.clock_gettime_ns(time.CLOCK_BOOTTIME)
+        with open(_TIMES, "a") as f:
+            f.write(f"mono {t0m} {t1m} {item.nodeid}\nboot {t0b} {t1b} {item.nodeid}\n")

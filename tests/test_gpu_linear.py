@@ -251,6 +251,9 @@ WQ_GEMM_CASES = [  # m > 8: the fp16 MFMA GEMM (m >= 16 or n >= 4096) or GEMV sl
     ("q4g", 96, 700, 1536, 256, False, F16, F32, F16),   # a group spans two slabs
     ("q4g", 16, 1536, 1568, 64, False, F16, F16, F16),   # k % group = 32: a short last group
     ("q4g", 130, 1000, 1664, 256, True, F16, F32, F16),  # wide kernel, k % group = 128
+    ("q4g", 64, 1536, 4224, 256, False, F16, F16, F16),  # wide split K over the workspace, k % group = 128
+    ("q4g", 16, 1536, 4128, 64, True, F16, F32, F16),    # 16-row split K, k % group = 32
+    ("q8", 12, 1536, 4224, 0, False, F16, F16, F16),     # m = 9..15, wide split K
     ("q8", 257, 2900, 1024, 0, True, F16, F32, F32),
     ("q4g", 1100, 640, 512, 32, True, F16, F16, F16),
     ("q4g", 40, 8960, 1536, 64, True, F16, F16, F16),    # m >= 32 with >= 128 tiles

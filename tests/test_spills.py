@@ -26,7 +26,7 @@ ALLOWED = {
     "gemv_q8_kernelILi8ELi8Ef": 4,
 }
 SOURCES = ["nq_gemv.hip", "nq_w8a8.hip", "nq_wq_gemm.hip", "nq_fused.hip", "nq_quantize.hip", "nq_dequant.hip",
-           "nq_ops.hip", "nq_rope.hip", "nq_embed.hip", "nq_nit.hip", "nq_probe.hip"]
+           "nq_ops.hip", "nq_rope.hip", "nq_embed.hip", "nq_nit.hip", "bench/nq_probe.hip"]
 
 
 def _spills(src):

@@ -73,3 +73,43 @@ def test_noalloc_refuses_beyond_scratch(dev):
     torch.cuda.synchronize()
     assert bool((y == 7.0).all())              # nothing was enqueued
     np.testing.assert_equal(lib.nq_linear_w8a8_noalloc(None, 0, None, None, None, None, 0, 0, n, k, 0, None), 0)
+
+
+def test_noalloc_allocates_nothing_and_replays_in_a_graph(dev):
+    """The property the entry exists for: a warm call changes no device
+    allocation (free bytes before == after), and the call records into a HIP
+    graph (capture refuses hipMalloc) whose replays, with eager work on y in
+    between, each equal the eager call."""
+    from nanoinfer_amd import _lib
+    lib = _lib.load()
+    m, n, k = 64, 8960, 1536
+    g = torch.Generator(device=dev).manual_seed(3)
+    x = torch.randn((m, k), generator=g, device=dev).half()
+    wq = torch.randint(-127, 128, (n, k), generator=g, device=dev, dtype=torch.int8)
+    ws = torch.rand(n, generator=g, device=dev) * 1e-3
+    y = torch.empty((m, n), dtype=torch.float16, device=dev)
+    s = torch.cuda.Stream()
+
+    def call():
+        st = lib.nq_linear_w8a8_noalloc(_ptr(x), _lib.NQ_F16, _ptr(wq), _ptr(ws), None, _ptr(y), _lib.NQ_F16,
+                                        m, n, k, 0, torch.cuda.current_stream().cuda_stream)
+        assert st == _lib.NQ_OK, lib.nq_last_error()
+    with torch.cuda.stream(s):
+        call()                                          # first call on the device: set-up
+    torch.cuda.synchronize()
+    ref = y.clone()
+    free0 = torch.cuda.mem_get_info()[0]
+    with torch.cuda.stream(s):
+        call()
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+    assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr, stream=s):
+        call()
+    for i in range(3):
+        y.fill_(float(i + 1))                           # eager work between replays
+        torch.cuda.synchronize()
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), i
