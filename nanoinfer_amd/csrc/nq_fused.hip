@@ -254,11 +254,7 @@ void by_shape(int64_t m, int64_t k, Fn&& fn) {
         case 1: return fn(std::integral_constant<int, 1>{}, I{});
         case 2: return fn(std::integral_constant<int, 2>{}, I{});
         case 3: return fn(std::integral_constant<int, 3>{}, I{});
-        case 4: return fn(std::integral_constant<int, 4>{}, I{});
-        case 5: return fn(std::integral_constant<int, 5>{}, I{});
-        case 6: return fn(std::integral_constant<int, 6>{}, I{});
-        case 7: return fn(std::integral_constant<int, 7>{}, I{});
-        case 8: return fn(std::integral_constant<int, 8>{}, I{});
+        case 4: return fn(std::integral_constant<int, 4>{}, I{});  // 5..8 took the 512-thread rows above
         default: break;
     }
     switch ((steps + 1023) / 1024) {

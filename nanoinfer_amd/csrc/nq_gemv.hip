@@ -169,15 +169,27 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q8_kernel(
     const int row0 = rg * R;
 
     const int c = act ? tid : 0;
+    // One or two activation rows: their chunks are requested first and the
+    // weight rows after them in order, so each row's dot starts when its own
+    // load lands (as the int4 GEMV).
+    constexpr bool kXFirst = M <= 2;
+    XChunk<XT> xc[M];
+    if constexpr (kXFirst) {
+#pragma unroll
+        for (int i = 0; i < M; ++i) xc[i].load(x + static_cast<size_t>(min(i, m - 1)) * k + c * 16);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     v4i wv[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int row = min(row0 + r, n - 1);
         wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * k + c * 16));
+        if constexpr (kXFirst) __builtin_amdgcn_sched_barrier(0);
     }
-    XChunk<XT> xc[M];
+    if constexpr (!kXFirst) {
 #pragma unroll
-    for (int i = 0; i < M; ++i) xc[i].load(x + static_cast<size_t>(min(i, m - 1)) * k + c * 16);
+        for (int i = 0; i < M; ++i) xc[i].load(x + static_cast<size_t>(min(i, m - 1)) * k + c * 16);
+    }
 
     float acc[R][M];
 #pragma unroll
@@ -1145,34 +1157,34 @@ void launch_q8(const XT* x, const int8_t* w, const float* ws, const float* b, YT
             return;
         }
     }
-    if constexpr (M == 8 && !AM && sizeof(XT) == 4) {
-        if (m > 4) {
-            const bool long_k = k >= 4096;
-            if (long_k && rows == 8 && n >= 8 * 256) {
-                gemv_q8_kernel<8, 8, XT, YT><<<(n + 7) / 8, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part, ctl);
-            } else if (!long_k && rows == 8) {
-                gemv_q8_kernel<8, 4, XT, YT, false, 2><<<(n + 7) / 8 * 2, threads, 0, s>>>(x, w, ws, b, y, m, n, k,
-                                                                                           part, ctl);
-            } else {
-                gemv_q8_kernel<4, 4, XT, YT, false, 2><<<(n + 3) / 4 * 2, threads, 0, s>>>(x, w, ws, b, y, m, n, k,
-                                                                                           part, ctl);
+    if constexpr (M == 8 && !AM && sizeof(XT) == 4) {  // m = 5..8 (the M = 8 bucket)
+        const bool long_k = k >= 4096;
+        if (long_k && rows == 8 && n >= 8 * 256) {
+            gemv_q8_kernel<8, 8, XT, YT><<<(n + 7) / 8, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part, ctl);
+        } else if (!long_k && rows == 8) {
+            gemv_q8_kernel<8, 4, XT, YT, false, 2><<<(n + 7) / 8 * 2, threads, 0, s>>>(x, w, ws, b, y, m, n, k,
+                                                                                       part, ctl);
+        } else {
+            gemv_q8_kernel<4, 4, XT, YT, false, 2><<<(n + 3) / 4 * 2, threads, 0, s>>>(x, w, ws, b, y, m, n, k,
+                                                                                       part, ctl);
+        }
+        return;
+    }
+    if constexpr (!(M == 8 && !AM && sizeof(XT) == 4)) {
+        if constexpr (M <= 2 || (M == 8 && sizeof(XT) == 4)) {  // the other row counts q8_rows picks
+            if (rows == 8 && R != 8) {
+                gemv_q8_kernel<8, M, XT, YT, AM><<<(n + 7) / 8, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part, ctl);
+                return;
             }
-            return;
         }
-    }
-    if constexpr (M <= 2 || (M == 8 && sizeof(XT) == 4)) {  // the other row counts q8_rows picks
-        if (rows == 8 && R != 8) {
-            gemv_q8_kernel<8, M, XT, YT, AM><<<(n + 7) / 8, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part, ctl);
-            return;
+        if constexpr (M >= 4 && sizeof(XT) == 4) {
+            if (rows == 4) {
+                gemv_q8_kernel<4, M, XT, YT, AM><<<(n + 3) / 4, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part, ctl);
+                return;
+            }
         }
+        gemv_q8_kernel<R, M, XT, YT, AM><<<(n + R - 1) / R, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part, ctl);
     }
-    if constexpr (M >= 4 && sizeof(XT) == 4) {
-        if (rows == 4) {
-            gemv_q8_kernel<4, M, XT, YT, AM><<<(n + 3) / 4, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part, ctl);
-            return;
-        }
-    }
-    gemv_q8_kernel<R, M, XT, YT, AM><<<(n + R - 1) / R, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part, ctl);
 }
 
 template <typename XT, typename YT>
@@ -1226,12 +1238,13 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
     // on short K (n = 8960, k = 1536 13.0 -> 12.5; k = 8960 lost 12.0 -> 17.9).
     // m = 2: fp32 x on long K (n = 1536, k = 8960: 10.83 -> 8.30; fp16 x and
     // short K lost 2-4%).
-    constexpr bool kPairs = M == 2 || M == 4 || M == 8;
+    // (m = 2 with fp16 x never pairs; the M = 4 bucket, m = 3..4, always does)
+    constexpr bool kPairs = (M == 2 && sizeof(XT) == 4) || M == 4 || M == 8;
     if constexpr (kPairs) {
         constexpr int MH = M / 2;
-        const bool pairs = M == 2   ? m > 1 && sizeof(XT) == 4 && k >= 4096
-                           : M == 4 ? m > 2
-                                    : m > 4 && (sizeof(XT) == 4 ? k >= 1024 : k < 4096);
+        const bool pairs = M == 2   ? k >= 4096
+                           : M == 4 ? true
+                                    : sizeof(XT) == 4 ? k >= 1024 : k < 4096;
         if (pairs) {
             if constexpr (sizeof(XT) == 4) {
                 if (threads <= 320 && n >= 1024) {
@@ -1246,13 +1259,17 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
             }
         }
     }
-    if constexpr (M >= 2 && sizeof(XT) == 4) {
-        if (threads <= 320 && n >= 1024) {  // 256+ workgroups (n = 256, m = 5: 5.66 -> 6.76 us with 4 rows)
-            gemv_q4g_kernel<4, M, XT, YT, ST, 320><<<(n + 3) / 4, threads, 0, s>>>(x, w, sc, b, y, m, n, k, g);
-            return;
+    if constexpr (M == 4 && sizeof(XT) == 2) {
+        return;  // the pairs above took every m = 3..4 launch
+    } else {
+        if constexpr (M >= 2 && M != 4 && sizeof(XT) == 4) {  // (M = 4 pairs on this condition above)
+            if (threads <= 320 && n >= 1024) {  // 256+ workgroups (n = 256, m = 5: 5.66 -> 6.76 us with 4 rows)
+                gemv_q4g_kernel<4, M, XT, YT, ST, 320><<<(n + 3) / 4, threads, 0, s>>>(x, w, sc, b, y, m, n, k, g);
+                return;
+            }
         }
+        gemv_q4g_kernel<R, M, XT, YT, ST><<<(n + R - 1) / R, threads, 0, s>>>(x, w, sc, b, y, m, n, k, g);
     }
-    gemv_q4g_kernel<R, M, XT, YT, ST><<<(n + R - 1) / R, threads, 0, s>>>(x, w, sc, b, y, m, n, k, g);
 }
 
 template <typename XT, typename YT, typename ST>
@@ -1338,6 +1355,13 @@ bool w8a8_decode_launch(const void* x, nq_dtype xdt, const int8_t* w, const floa
         return false;
     const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
     const int T = (ki / 16 + 63) / 64;
+    // The forms nq_linear_w8a8 reaches (the others are not compiled): in-kernel
+    // quant at m = 2..4 with k <= 4096 and m = 5..8 with k <= 1024 (m = 1 takes
+    // the fused-quant GEMV); over codes at m = 5..8 with k <= 2048 or k >= 8192,
+    // and m = 9..64 with k <= 2048.
+    const int tb = T <= 2 ? 2 : T <= 4 ? 4 : 9;
+    if (!(pre_scale ? (mb == 8 ? tb != 4 : mb >= 16 && tb == 2) : (mb == 2 || mb == 4) ? tb <= 4 : mb == 8 && tb == 2))
+        return false;
     const size_t lds = static_cast<size_t>(mb) * ki;
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
@@ -1354,11 +1378,15 @@ bool w8a8_decode_launch(const void* x, nq_dtype xdt, const int8_t* w, const floa
         using YT = std::remove_pointer_t<decltype(yp)>;
         const int groups = (ni + R - 1) / R;
         const unsigned grid = static_cast<unsigned>(std::max(1, std::min(cus, groups)));
+        constexpr bool kPre = M == 8 ? TT != 4 : M >= 16 && TT == 2;
+        constexpr bool kFused = (M == 2 || M == 4) ? TT <= 4 : M == 8 && TT == 2;
         if (pre_scale) {
-            auto* fn = w8a8_decode_kernel<M, R, TT, int8_t, YT, true, S>;
-            if ((*st = set_dynamic_lds(reinterpret_cast<const void*>(fn), lds, "w8a8_decode"))) return;
-            fn<<<grid, kDecThreads, lds, s>>>(static_cast<const int8_t*>(x), w, ws, bias, yp, mi, ni, ki, pre_scale);
-        } else if constexpr (M <= 8) {
+            if constexpr (kPre) {
+                auto* fn = w8a8_decode_kernel<M, R, TT, int8_t, YT, true, S>;
+                if ((*st = set_dynamic_lds(reinterpret_cast<const void*>(fn), lds, "w8a8_decode"))) return;
+                fn<<<grid, kDecThreads, lds, s>>>(static_cast<const int8_t*>(x), w, ws, bias, yp, mi, ni, ki, pre_scale);
+            }
+        } else if constexpr (kFused) {
             auto* fn = w8a8_decode_kernel<M, R, TT, XT, YT>;
             if ((*st = set_dynamic_lds(reinterpret_cast<const void*>(fn), lds, "w8a8_decode"))) return;
             fn<<<grid, kDecThreads, lds, s>>>(xp, w, ws, bias, yp, mi, ni, ki, nullptr);
@@ -1378,7 +1406,7 @@ bool w8a8_decode_launch(const void* x, nq_dtype xdt, const int8_t* w, const floa
         constexpr int RS = M == 1 || M >= 32 ? 1 : 2;
         constexpr int RL = M == 16 ? 1 : RS < 2 ? RS : 2;                // long K
         using One = std::integral_constant<int, 1>;
-        if constexpr (M >= 32) {
+        if constexpr (M >= 16) {  // k <= 2048 (T = 2); one row per group (n <= 2048 is "few" at m <= 16)
             go(mtag, One{}, std::integral_constant<int, 2>{}, xp, yp);
         } else if (T <= 2) {
             if (few) go(mtag, One{}, std::integral_constant<int, 2>{}, xp, yp);
@@ -1391,7 +1419,6 @@ bool w8a8_decode_launch(const void* x, nq_dtype xdt, const int8_t* w, const floa
     };
     auto with_m = [&](auto* xp, auto* yp) {
         switch (mb) {
-            case 1: with_t(std::integral_constant<int, 1>{}, xp, yp); break;
             case 2: with_t(std::integral_constant<int, 2>{}, xp, yp); break;
             case 4: with_t(std::integral_constant<int, 4>{}, xp, yp); break;
             case 8: with_t(std::integral_constant<int, 8>{}, xp, yp); break;

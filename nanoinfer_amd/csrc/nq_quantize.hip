@@ -242,11 +242,7 @@ nq_status act_quant(const void* x, nq_dtype xdt, int64_t m, int64_t k, int8_t* x
                 case 2: act_quant_vec_kernel<XT, 2, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki); return;
                 case 3: act_quant_vec_kernel<XT, 3, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki); return;
                 case 4: act_quant_vec_kernel<XT, 4, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki); return;
-                case 5: act_quant_vec_kernel<XT, 5, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki); return;
-                case 6: act_quant_vec_kernel<XT, 6, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki); return;
-                case 7: act_quant_vec_kernel<XT, 7, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki); return;
-                case 8: act_quant_vec_kernel<XT, 8, 256><<<grid, 256, 0, s>>>(xp, xq, as, mi, ki); return;
-                default: break;
+                default: break;  // 5..8 took the 512-thread rows above; more: 1024 threads
             }
             switch ((steps + 1023) / 1024) {
                 case 1: act_quant_vec_kernel<XT, 1, 1024><<<grid, 1024, 0, s>>>(xp, xq, as, mi, ki); break;

@@ -844,9 +844,9 @@ struct WideTile {
 constexpr WideTile kWideTiles[] = {{4, 10}, {4, 9}, {4, 8}, {2, 10}, {2, 9}, {4, 4}, {2, 8},
                                    {2, 4}, {2, 2}, {1, 4}, {1, 3}, {1, 2}};
 struct PrefillPlan {
-    bool narrow;  // 64 x 128 tiles
     int wide_fn;  // 0: not wide
     int wide_fm;  // wide tile rows / 64
+    int best_fm, best_fn;  // the cheapest wide tile (also when the plan splits K instead)
     int sw;       // K slab bytes of the prefill kernel (64 or 128)
     int tiles, splits, k_slabs;
     size_t acc_bytes;
@@ -862,8 +862,8 @@ PrefillPlan plan_prefill(int64_t m, int64_t n, int64_t k) {
         if (best_cost == 0 || cost < best_cost) {
             best_cost = cost;
             best_tiles = c;
-            p.wide_fm = t.fm;
-            p.wide_fn = t.fn;
+            p.wide_fm = p.best_fm = t.fm;
+            p.wide_fn = p.best_fn = t.fn;
         }
     }
     if (best_tiles >= 128 || nk < 64) {
@@ -878,22 +878,17 @@ PrefillPlan plan_prefill(int64_t m, int64_t n, int64_t k) {
     // Fewer than 256 tiles: K splits into ranges of at least 32 slabs (the
     // partial planes and the reduction launch cost more than a short K loop
     // saves: m = 512, n = 1536, k = 1536 ran 13.0 us unsplit vs 15.4 in three
-    // ranges; k = 8960 ran best in four ranges, 25.3 us vs 29.5 in six). Short-K
-    // shapes left with fewer than 128 tiles use 64 x 128 tiles instead.
-    if (p.tiles < 256) {
-        splits = std::max(1, nk / 32);
-        if (splits == 1 && p.tiles < 128) {
-            p.narrow = true;
-            p.tiles = static_cast<int>(((m + 63) / 64) * ((n + 127) / 128));
-        }
-    }
+    // ranges; k = 8960 ran best in four ranges, 25.3 us vs 29.5 in six). With
+    // k >= 64 slabs here that is always two or more ranges; a plan left with one
+    // range (the planes' cap below) runs the cheapest wide tile instead.
+    if (p.tiles < 256) splits = std::max(1, nk / 32);
     // at most 64 MiB of partial planes
     splits = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(splits, (int64_t(64) << 20) / std::max<int64_t>(1, m * n * 4))));
     // 128 x 128 tiles that fit one round (split ranges included) take 128-byte
     // slabs in a 3-slot ring (m = 512, n = 1536, k = 8960 in four ranges: 25.4
     // -> 23.2 us); where a second workgroup per CU matters, the 64-byte ring
     // keeps its smaller LDS footprint.
-    p.sw = !p.narrow && int64_t(p.tiles) * splits <= 256 ? 128 : 64;
+    p.sw = int64_t(p.tiles) * splits <= 256 ? 128 : 64;
     const int ns = p.sw == 128 ? static_cast<int>((k + 127) / 128) : nk;
     p.k_slabs = (ns + splits - 1) / splits;
     p.splits = (ns + p.k_slabs - 1) / p.k_slabs;
@@ -942,10 +937,18 @@ nq_status launch_wide_tile(int fm, int fn, const int8_t* xq, const float* as, co
         constexpr int FM = decltype(fmtag)::value, FN2 = decltype(fntag)::value;
         constexpr int WN = FN2 % 3 == 0 ? 3 : FN2 % 4 == 0 ? 4 : 2, FN = FN2 * 2 / WN;  // 16-column fragments per wave
         if (splits > 1) {
-            const nq_status st = launch_wide<4, FN, FM, Out::PARTIAL, float, WN>(xq, as, wq, ws, bias, nullptr, parts,
-                                                                                 mi, ni, ki, s, splits, k_slabs);
-            if (st != NQ_OK) return st;
-            return reduce_partials(parts, splits, as, ws, bias, y, ydt, acc_out, mi, ni, s);
+            // Split K runs only the 64 x 32 tiles: plan_small_wide splits when the
+            // 32-column tiles number at most 128 (wider tiles are chosen only past
+            // 256 of them, which leaves no room to split).
+            if constexpr (FM == 1 && FN2 == 1) {
+                const nq_status st = launch_wide<4, FN, FM, Out::PARTIAL, float, WN>(xq, as, wq, ws, bias, nullptr,
+                                                                                     parts, mi, ni, ki, s, splits,
+                                                                                     k_slabs);
+                if (st != NQ_OK) return st;
+                return reduce_partials(parts, splits, as, ws, bias, y, ydt, acc_out, mi, ni, s);
+            } else {
+                return fail(NQ_BAD_ARG, "w8a8 gemm: split K on a %d x %d tile", 64 * FM, 32 * FN2);
+            }
         }
         if (acc_out)
             return launch_wide<4, FN, FM, Out::ACC, float, WN>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki, s);
@@ -980,6 +983,7 @@ nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const fl
     const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
     const PrefillPlan p = plan_prefill(m, n, k);
     if (p.wide_fn) return launch_wide_tile(p.wide_fm, p.wide_fn, xq, as, wq, ws, bias, y, ydt, acc_out, mi, ni, ki, s);
+    if (p.splits == 1) return launch_wide_tile(p.best_fm, p.best_fn, xq, as, wq, ws, bias, y, ydt, acc_out, mi, ni, ki, s);
     int32_t* parts = nullptr;
     if (p.splits > 1) {
         NQ_REQUIRE(workspace && ws_bytes >= p.acc_bytes, NQ_BAD_ARG,
@@ -990,28 +994,16 @@ nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const fl
     auto go = [&](auto wmtag, auto wntag, auto dtag, auto swtag) -> nq_status {
         constexpr int WM = decltype(wmtag)::value, WN = decltype(wntag)::value, D = decltype(dtag)::value;
         constexpr int SW = decltype(swtag)::value;
-        if (p.splits > 1)
-            return launch_prefill<WM, WN, D, SW, Out::PARTIAL, float>(xq, as, wq, ws, bias, nullptr, parts, mi, ni,
-                                                                     ki, p.splits, p.k_slabs, s);
-        if (acc_out)
-            return launch_prefill<WM, WN, D, SW, Out::ACC, float>(xq, as, wq, ws, bias, nullptr, acc_out, mi, ni, ki,
-                                                                 1, p.k_slabs, s);
-        if (ydt == NQ_F32)
-            return launch_prefill<WM, WN, D, SW, Out::Y, float>(xq, as, wq, ws, bias, static_cast<float*>(y), nullptr,
-                                                               mi, ni, ki, 1, p.k_slabs, s);
-        return launch_prefill<WM, WN, D, SW, Out::Y, _Float16>(xq, as, wq, ws, bias, static_cast<_Float16*>(y),
-                                                              nullptr, mi, ni, ki, 1, p.k_slabs, s);
+        return launch_prefill<WM, WN, D, SW, Out::PARTIAL, float>(xq, as, wq, ws, bias, nullptr, parts, mi, ni, ki,
+                                                                 p.splits, p.k_slabs, s);
     };
-    using I = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
     using I3 = std::integral_constant<int, 3>;
     using I4 = std::integral_constant<int, 4>;
     using I64 = std::integral_constant<int, 64>;
     using I128 = std::integral_constant<int, 128>;
-    const nq_status st = p.narrow    ? go(I{}, I2{}, I4{}, I64{})
-                         : p.sw == 128 ? go(I2{}, I2{}, I3{}, I128{})
-                                       : go(I2{}, I2{}, I4{}, I64{});
-    if (st != NQ_OK || p.splits == 1) return st;
+    const nq_status st = p.sw == 128 ? go(I2{}, I2{}, I3{}, I128{}) : go(I2{}, I2{}, I4{}, I64{});
+    if (st != NQ_OK) return st;
     return reduce_partials(parts, p.splits, as, ws, bias, y, ydt, acc_out, mi, ni, s);
 }
 

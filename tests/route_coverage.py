@@ -32,7 +32,10 @@ SUMMARY = os.path.join(ROOT, "profiles", "gpu_test_kernel_coverage.txt")
 
 
 def demangle(names):
-    names = list(names)
+    """Itanium demangling with binutils' c++filt, which does not know the
+    _Float16 code DF16_: it is rewritten to Dh (a builtin type as well, so the
+    substitution numbering is unchanged) and shows as `half`."""
+    names = [n.replace("DF16_", "Dh") if n.startswith("_Z") else n for n in names]
     if not names:
         return []
     r = subprocess.run(["c++filt"], input="\n".join(names), capture_output=True, text=True, check=True)
@@ -45,7 +48,7 @@ def key(demangled: str) -> str | None:
     m = re.search(r"nq::\(anonymous namespace\)::(\w+(?:<.*>)?)\(", demangled)
     if not m:
         return None
-    return m.group(1).replace("nq::(anonymous namespace)::", "")
+    return m.group(1).replace("nq::(anonymous namespace)::", "").replace("_Float16", "half")
 
 
 def library_kernels(lib: str = LIB) -> set[str]:
