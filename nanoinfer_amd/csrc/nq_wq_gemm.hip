@@ -69,8 +69,11 @@ struct XFrag<_Float16> {
     __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, int off) {
         raw = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
     }
-    // The 8 halves as pairs (c, c+4), the order the int4 nibble trick gives the codes.
+    // The 8 halves in the order WFrag<Q4>::codes() gives the weight codes:
+    // column order for int8, pairs (c, c+4) for int4 (the nibble trick's order).
+    template <bool Q4>
     __device__ __forceinline__ h8 operands() const {
+        if constexpr (!Q4) return __builtin_bit_cast(h8, raw);
         const h8 v = __builtin_bit_cast(h8, raw);
         h8 hi;
 #pragma unroll
@@ -110,7 +113,8 @@ struct XFrag<float> {
     }
 };
 
-// Weight fragment of one chunk: 8 codes of one row as fp16 pairs (c, c+4).
+// Weight fragment of one chunk: 8 codes of one row as fp16 (int4: pairs
+// (c, c+4); int8: column order).
 template <bool Q4>
 struct WFrag;
 template <>
@@ -125,7 +129,10 @@ struct WFrag<true> {  // 8 nibbles = one dword, nibble e = column e
         h8 r;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const h2 p = __builtin_bit_cast(h2, ((u >> (4 * j)) & 0x000F000Fu) | 0x64006400u) + off;
+            // one v_and_or_b32 (mask in an SGPR, magic in a VGPR) per pair
+            unsigned b;
+            asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(b) : "v"(u >> (4 * j)), "s"(0x000F000Fu), "v"(0x64006400u));
+            const h2 p = __builtin_bit_cast(h2, b) + off;
             r[2 * j] = p[0];
             r[2 * j + 1] = p[1];
         }
@@ -150,13 +157,15 @@ struct WFrag<false> {  // 8 int8 codes = two dwords, byte t of dword d = column 
         w1 = v[1];
     }
     __device__ __forceinline__ h8 codes() const {
-        // (byte t of w0, byte t of w1) into the low bytes of two halves; XOR with
-        // 0x6480 gives the fp16 value 1024 + (code + 128) exactly; -1152 -> code.
+        // Columns (2t, 2t + 1) into the low bytes of two halves (bytes 2t, 2t + 1
+        // of the pair w1:w0); XOR with 0x6480 gives the fp16 value 1024 + (code +
+        // 128) exactly; -1152 -> code. Column order, so the activation fragment
+        // needs no permutation.
         const h2 off = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
         h8 r;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            const unsigned sel = 0x0C000C00u | static_cast<unsigned>(t) | (static_cast<unsigned>(4 + t) << 16);
+            const unsigned sel = 0x0C000C00u | static_cast<unsigned>(2 * t) | (static_cast<unsigned>(2 * t + 1) << 16);
             const unsigned b = __builtin_amdgcn_perm(static_cast<unsigned>(w1), static_cast<unsigned>(w0), sel);
             const h2 p = __builtin_bit_cast(h2, b ^ 0x64806480u) + off;
             r[2 * t] = p[0];
@@ -276,7 +285,7 @@ __global__ __launch_bounds__(wq_waves<TM>() * 64) void gemm_wq_kernel(
             for (int j = 0; j < TN; ++j) b[j] = st.wf[j].codes();
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
-                const h8 hi = st.xf[i].operands();
+                const h8 hi = st.xf[i].template operands<Q4>();
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
                     if constexpr (Q4) {
@@ -596,47 +605,64 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_wq_wide_kernel(
                 asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(dst), "v"(vo), "s"(brs) : "memory");
         }
     }
+    // Fragment addresses: a 16-row step moves a row's chunk swizzle by a
+    // multiple of its chunk count (16 / C rows share one XOR value and C <= 16),
+    // so every fragment of a wave shares the swizzle of its first row and the
+    // fragments differ by constant offsets (immediate LDS offsets).
+    static_assert(XC <= 16 && WC <= 16, "swizzle shared by the fragments");
+    const int xr0 = fxo[0], wr0 = fwr[0];
+    const int xsw = wq_swz<XC>(xr0), wsw = wq_swz<WC>(wr0);
+    const int xlane = S::kXOff + xr0 * XROW, wlane = S::kWOff + wr0 * WROW, slane = S::kSOff + wr0 * S::kSRow;
 #pragma unroll
     for (int sl = 0; sl < D - 1; ++sl) issue(sl);
+    unsigned slot_off = 0;  // (kt % D) * kSlab, kept as a plain rotating offset
     for (int kt = 0; kt < nk; ++kt) {
         wait_vmcnt<(Q + (Q4 ? QS : 0)) * (D - 2)>();
         __builtin_amdgcn_s_barrier();
         issue(kt + D - 1);
-        const int8_t* base = lds + (kt % D) * S::kSlab;
+        const int8_t* base = lds + slot_off;
+        slot_off = slot_off + S::kSlab == static_cast<unsigned>(D * S::kSlab) ? 0u : slot_off + S::kSlab;
         f4 part[FN][FM];
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             // fp16 x: one fp16 MFMA per fragment pair; fp32 x: three bf16 ones.
             using XOp = std::conditional_t<F32X, b8, h8>;
             XOp xa[FM], xm[FM], xl[FM], wb[FN];
+            if constexpr (F32X) {  // 8 floats = chunks 8t + 2 fq and the next
+                const int c = t * 8 + fq * 2;
+                const int8_t* pa = base + xlane + ((c ^ xsw) << 4);
+                const int8_t* pb = base + xlane + (((c + 1) ^ xsw) << 4);
 #pragma unroll
-            for (int j = 0; j < FM; ++j) {
-                const int r = fxo[j];
-                if constexpr (F32X) {  // 8 floats = chunks 8t + 2 fq and the next
-                    const int c = t * 8 + fq * 2;
+                for (int j = 0; j < FM; ++j) {
                     XFrag<float> f;
-                    f.a = *reinterpret_cast<const v4i*>(base + S::kXOff + r * XROW + ((c ^ wq_swz<XC>(r)) << 4));
-                    f.b = *reinterpret_cast<const v4i*>(base + S::kXOff + r * XROW + (((c + 1) ^ wq_swz<XC>(r)) << 4));
+                    f.a = *reinterpret_cast<const v4i*>(pa + j * 16 * XROW);
+                    f.b = *reinterpret_cast<const v4i*>(pb + j * 16 * XROW);
                     f.split3(xa[j], xm[j], xl[j]);
-                } else {  // 8 halves = chunk 4t + fq
-                    const int c = t * 4 + fq;
+                }
+            } else {  // 8 halves = chunk 4t + fq
+                const int8_t* pa = base + xlane + (((t * 4 + fq) ^ xsw) << 4);
+#pragma unroll
+                for (int j = 0; j < FM; ++j) {
                     XFrag<_Float16> f;
-                    f.raw = *reinterpret_cast<const v4i*>(base + S::kXOff + r * XROW + ((c ^ wq_swz<XC>(r)) << 4));
-                    xa[j] = f.operands();
+                    f.raw = *reinterpret_cast<const v4i*>(pa + j * 16 * XROW);
+                    xa[j] = f.template operands<Q4>();
                 }
             }
+            if constexpr (Q4) {  // 8 codes = one dword: chunk t, dword fq
+                const int8_t* pw = base + wlane + ((t ^ wsw) << 4) + fq * 4;
 #pragma unroll
-            for (int i = 0; i < FN; ++i) {
-                const int r = fwr[i];
-                if constexpr (Q4) {  // 8 codes = one dword: chunk t, dword fq
+                for (int i = 0; i < FN; ++i) {
                     WFrag<true> f;
-                    f.w = *reinterpret_cast<const int*>(base + S::kWOff + r * WROW + ((t ^ wq_swz<WC>(r)) << 4) + fq * 4);
+                    f.w = *reinterpret_cast<const int*>(pw + i * 16 * WROW);
                     if constexpr (F32X) wb[i] = f.codes_bf16();
                     else wb[i] = f.codes();
-                } else {  // 8 codes = two dwords: chunk 2t + fq / 2, half fq % 2
-                    typedef int v2i __attribute__((ext_vector_type(2)));
-                    const int c = t * 2 + (fq >> 1);
-                    const v2i v = *reinterpret_cast<const v2i*>(base + S::kWOff + r * WROW + ((c ^ wq_swz<WC>(r)) << 4) + (fq & 1) * 8);
+                }
+            } else {  // 8 codes = two dwords: chunk 2t + fq / 2, half fq % 2
+                typedef int v2i __attribute__((ext_vector_type(2)));
+                const int8_t* pw = base + wlane + (((t * 2 + (fq >> 1)) ^ wsw) << 4) + (fq & 1) * 8;
+#pragma unroll
+                for (int i = 0; i < FN; ++i) {
+                    const v2i v = *reinterpret_cast<const v2i*>(pw + i * 16 * WROW);
                     WFrag<false> f;
                     f.w0 = v[0];
                     f.w1 = v[1];
@@ -647,6 +673,26 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_wq_wide_kernel(
             auto mma = [&](const XOp& a, const XOp& b, const f4& c) {
                 if constexpr (F32X) return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
                 else return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+            };
+            // Q4G: the group's last step scales each fragment's partial into the
+            // accumulator, one fragment behind its MFMAs so the adds do not wait
+            // on the MFMA they follow.
+            const bool scale_now = Q4 && t % S::kCPG == S::kCPG - 1;
+            float sc[Q4 ? FN : 1];
+            if constexpr (Q4) {
+                if (scale_now) {
+                    const int gi = GSH >= S::kGBig ? 0 : t >> GSH;  // group within the slab
+                    const int8_t* ps = base + slane + gi * static_cast<int>(sizeof(ST));
+#pragma unroll
+                    for (int i = 0; i < FN; ++i) {
+                        if constexpr (sizeof(ST) == 4) sc[i] = *reinterpret_cast<const float*>(ps + i * 16 * S::kSRow);
+                        else sc[i] = static_cast<float>(*reinterpret_cast<const _Float16*>(ps + i * 16 * S::kSRow));
+                    }
+                }
+            }
+            auto scale_into = [&](int i, int j) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(part[i][j][v], sc[i], acc[i][j][v]);
             };
 #pragma unroll
             for (int i = 0; i < FN; ++i)
@@ -659,22 +705,13 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_wq_wide_kernel(
                         d = mma(xm[j], wb[i], d);
                         d = mma(xl[j], wb[i], d);
                     }
-                }
-            if constexpr (Q4) {
-                if (t % S::kCPG == S::kCPG - 1) {
-                    const int gi = GSH >= S::kGBig ? 0 : t >> GSH;  // group within the slab
-#pragma unroll
-                    for (int i = 0; i < FN; ++i) {
-                        const int8_t* sp = base + S::kSOff + fwr[i] * S::kSRow + gi * static_cast<int>(sizeof(ST));
-                        float sc;
-                        if constexpr (sizeof(ST) == 4) sc = *reinterpret_cast<const float*>(sp);
-                        else sc = static_cast<float>(*reinterpret_cast<const _Float16*>(sp));
-#pragma unroll
-                        for (int j = 0; j < FM; ++j)
-#pragma unroll
-                            for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(part[i][j][v], sc, acc[i][j][v]);
+                    if constexpr (Q4) {
+                        if (scale_now && (i > 0 || j > 0)) scale_into(j > 0 ? i : i - 1, j > 0 ? j - 1 : FM - 1);
                     }
                 }
+            if constexpr (Q4) {
+                if (scale_now) scale_into(FN - 1, FM - 1);
+                __builtin_amdgcn_sched_barrier(0);  // keep the next step's reads below (registers)
             }
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this slab's reads are done
