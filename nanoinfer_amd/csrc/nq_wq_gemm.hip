@@ -848,7 +848,8 @@ nq_status wq_wide_tiles(const XT* x, const uint8_t* w, const ST* sc, const float
     // Q8 tile widths that split in three (four) 16-column multiples run 12 (16)
     // waves, as in the W8A8 wide kernel (m = 2048: 74.3 -> 71.7 us); Q4G keeps 8
     // waves (its group-scaled partial sums do not fit 170 registers: 106.9 vs
-    // 128.9 us).
+    // 128.9 us; with the scaling one fragment behind its MFMAs 12 waves fit but
+    // ran 99.5 vs 91.1).
     using std::integral_constant;
     // One wave layout and fragment shape: the group-size dispatch of Q4G.
     auto launch_g = [&](auto skt, auto fmt, auto fnt, auto wnt, auto wmt, auto dt) -> nq_status {
