@@ -47,6 +47,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--only", default="", help="comma list of sweep entries to run (debug)")
+    p.add_argument("--shape-sweep", action="store_true",
+                   help="only time the dispatch over a grid of common model shapes (one JSON line)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a device-to-device copy of MIB MiB (FETCH_SIZE/WRITE_SIZE calibration)")
     return p.parse_args()
@@ -284,6 +286,11 @@ def main():
              "warmup": sweep_warmup}
         return e
 
+    if args.shape_sweep:
+        print(json.dumps({"shape_sweep": shape_sweep(args, time_graph, q4g_gemv, q8_gemv, w8a8_linear, entry,
+                                                     copies_for, stream_ptr)}), flush=True)
+        return
+
     # ---------------- headline: configs[1] int4 GEMV ------------------------------------------
     M, N, K, G = 1, 1536, 8960, 32
     launches, nbytes, ops = q4g_gemv(M, N, K, G)
@@ -439,6 +446,70 @@ def main():
     if sweep:
         out["sweep"] = sweep
     print(json.dumps(out), flush=True)
+
+
+# (model, projection, n, k): the projections of Llama-3-8B, Qwen2.5-7B and
+# Qwen2.5-1.5B (q|k|v and gate|up fused by rows as this library runs them) and
+# two LM heads, none of which the dispatch thresholds were tuned on except
+# Qwen2.5-1.5B's.
+SWEEP_SHAPES = [
+    ("llama3-8b", "qkv", 6144, 4096), ("llama3-8b", "o", 4096, 4096), ("llama3-8b", "gate|up", 28672, 4096),
+    ("llama3-8b", "down", 4096, 14336), ("llama3-8b", "lm_head", 128256, 4096),
+    ("qwen2.5-7b", "qkv", 4608, 3584), ("qwen2.5-7b", "o", 3584, 3584), ("qwen2.5-7b", "gate|up", 37888, 3584),
+    ("qwen2.5-7b", "down", 3584, 18944),
+    ("qwen2.5-1.5b", "qkv", 2048, 1536), ("qwen2.5-1.5b", "o", 1536, 1536), ("qwen2.5-1.5b", "gate|up", 17920, 1536),
+    ("qwen2.5-1.5b", "down", 1536, 8960),
+]
+
+
+def shape_sweep(args, time_graph, q4g_gemv, q8_gemv, w8a8_linear, entry, copies_for, stream_ptr):
+    """Decode (m = 1) GEMVs in the three quant modes over SWEEP_SHAPES, each
+    beside a streaming read of the same weight bytes (the single-launch floor
+    at that size), and the prefill GEMMs at m = 512: evidence that the
+    dispatch holds up away from the shapes it was tuned on."""
+    import ctypes
+
+    import torch
+    dev = torch.device("cuda:0")
+    blib = ctypes.CDLL(os.path.join(ROOT, "nanoinfer_amd", "libnq_bench.so"))
+    blib.nq_probe_read_cfg.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
+    sink = torch.zeros(64, dtype=torch.int32, device=dev)
+
+    def read_us(nbytes):
+        rb = (nbytes + 15) // 16 * 16
+        src = [torch.empty(rb, dtype=torch.uint8, device=dev) for _ in range(copies_for(rb))]
+        best = None
+        for th, u in ((256, 4), (512, 2), (1024, 1)):
+            ms = time_graph([lambda i=i: blib.nq_probe_read_cfg(src[i].data_ptr(), rb, th, u, None, 0,
+                                                                sink.data_ptr(), stream_ptr())
+                             for i in range(len(src))], args.steps, 10)
+            best = ms if best is None else min(best, ms)
+        del src
+        torch.cuda.empty_cache()
+        return round(best * 1e3, 3)
+
+    out = []
+    for model, proj, n, k in SWEEP_SHAPES:
+        row = {"model": model, "proj": proj, "n": n, "k": k}
+        for kind, mk in (("q4g_g32_m1", lambda: q4g_gemv(1, n, k, 32)),
+                         ("q8_m1", lambda: q8_gemv(1, n, k, torch.float16)),
+                         ("w8a8_m1", lambda: w8a8_linear(1, n, k))):
+            e = entry(kind, *mk(), "hbm")
+            torch.cuda.empty_cache()
+            wbytes = n * k // 2 + n * (k // 32) * 2 if kind.startswith("q4g") else n * k + n * 4
+            e["read_floor_us"] = read_us(wbytes)
+            e["floor_ratio"] = round(e["read_floor_us"] / e["us"], 3)
+            row[kind] = {key: e[key] for key in ("us", "GB/s", "frac", "read_floor_us", "floor_ratio")}
+        for kind, mk, bound in (("w8a8_m512", lambda: w8a8_linear(512, n, k, gemm_only=True), "mfma"),
+                                ("q8_m512", lambda: q8_gemv(512, n, k, torch.float16), "mfma_f16"),
+                                ("q4g_g32_m512", lambda: q4g_gemv(512, n, k, 32), "mfma_f16")):
+            e = entry(kind, *mk(), bound)
+            torch.cuda.empty_cache()
+            row[kind] = {key: e[key] for key in ("us", "TOPS", "frac")}
+        print(json.dumps(row), file=sys.stderr, flush=True)  # progress
+        out.append(row)
+    return out
 
 
 def decoder_layer_cfg4(rnd, time_graph, args, w8a8_linear, entry):

@@ -300,6 +300,29 @@ __device__ __forceinline__ float dot32_q4_f16(v4i wv, const h2 (&xp)[16]) {
     return __builtin_fmaf(p16, 0.0625f, p1);
 }
 
+// dot32_q4_f16 with the 0x64006400 magic in a caller-held VGPR: in a loop the
+// asm operand would otherwise be rematerialized, and hoisted, once per use.
+__device__ __forceinline__ float dot32_q4_f16m(v4i wv, const h2 (&xp)[16], unsigned magic) {
+    const h2 off1 = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
+    const h2 off16 = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
+    auto pair = [&](unsigned w, unsigned mask) {
+        unsigned b;
+        asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(b) : "v"(w), "s"(mask), "v"(magic));
+        return __builtin_bit_cast(h2, b);
+    };
+    float p1 = 0.0f, p16 = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const unsigned w = static_cast<unsigned>(wv[d]);
+        const unsigned u = w >> 8;
+        p1 = __builtin_amdgcn_fdot2(pair(w, 0x000F000Fu) + off1, xp[4 * d + 0], p1, false);
+        p16 = __builtin_amdgcn_fdot2(pair(w, 0x00F000F0u) + off16, xp[4 * d + 1], p16, false);
+        p1 = __builtin_amdgcn_fdot2(pair(u, 0x000F000Fu) + off1, xp[4 * d + 2], p1, false);
+        p16 = __builtin_amdgcn_fdot2(pair(u, 0x00F000F0u) + off16, xp[4 * d + 3], p16, false);
+    }
+    return __builtin_fmaf(p16, 0.0625f, p1);
+}
+
 // The same chunk dot in fp32 for fp32 activations.
 __device__ __forceinline__ float dot32_q4_f32(v4i wv, const float (&xf)[32]) {
     float p = 0.0f;
@@ -876,6 +899,195 @@ __global__ __launch_bounds__(kDecThreads) void w8a8_decode_kernel(const XT* __re
     }
 }
 
+// ---- long K: several 16-byte chunks per lane --------------------------------------------
+// The kernels above give each lane one 16-byte weight chunk of a row, so a
+// 576-lane workgroup covers int8 k <= 9216 and int4 k <= 18432. Longer rows
+// (Llama-3-8B's down projection, k = 14336; Qwen2.5-7B's, k = 18944) take these:
+// 256 lanes stride K one chunk at a time, R weight rows per workgroup (their R
+// loads in flight per lane, several workgroups per CU), the same per-chunk dot
+// products as the one-chunk kernels and the same cross-wave reduction.
+constexpr int kLongKThreads = 256;
+
+template <int R, int M, typename XT, typename YT>
+__global__ __launch_bounds__(kLongKThreads) void gemv_q8_longk_kernel(
+    const XT* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ ws,
+    const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k) {
+    __shared__ float red[(kLongKThreads / kWave) * R * M];
+    const int tid = threadIdx.x, wave = tid >> 6;
+    const int chunks = k >> 4, row0 = xcd_row_group() * R;
+    float acc[R][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < M; ++i) acc[r][i] = 0.0f;
+#pragma unroll 1
+    for (int c = tid; c < chunks; c += kLongKThreads) {
+        v4i wv[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            wv[r] = __builtin_nontemporal_load(
+                reinterpret_cast<const v4i*>(w + static_cast<size_t>(min(row0 + r, n - 1)) * k + c * 16));
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            XChunk<XT> xc;
+            xc.load(x + static_cast<size_t>(min(i, m - 1)) * k + c * 16);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float p = acc[r][i];
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const int wd = wv[r][d];
+                    p = __builtin_fmaf(xc.at(4 * d + 0), sbyte_f32<0>(wd), p);
+                    p = __builtin_fmaf(xc.at(4 * d + 1), sbyte_f32<1>(wd), p);
+                    p = __builtin_fmaf(xc.at(4 * d + 2), sbyte_f32<2>(wd), p);
+                    p = __builtin_fmaf(xc.at(4 * d + 3), sbyte_f32<3>(wd), p);
+                }
+                acc[r][i] = p;
+            }
+        }
+    }
+    reduce_to_lds<R, M, (R * M >= 16)>(acc, red, wave, tid & 63);
+    __syncthreads();
+    if (tid < R * M) {
+        const int r = tid / M, i = tid % M, row = row0 + r;
+        if (row < n && i < m) {
+            float s = 0.0f;
+#pragma unroll
+            for (int q = 0; q < kLongKThreads / kWave; ++q) s += red[(q * R + r) * M + i];
+            const float b = bias ? bias[row] : 0.0f;
+            y[static_cast<size_t>(i) * n + row] = from_f32<YT>(__builtin_fmaf(s, ws[row], b));
+        }
+    }
+}
+
+// group: a multiple of 32 (each chunk's 32 codes share one scale).
+template <int R, int M, typename XT, typename YT, typename ST>
+__global__ __launch_bounds__(kLongKThreads) void gemv_q4g_longk_kernel(
+    const XT* __restrict__ x, const uint8_t* __restrict__ w, const ST* __restrict__ scale,
+    const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int group) {
+    __shared__ float red[(kLongKThreads / kWave) * R * M];
+    const int tid = threadIdx.x, wave = tid >> 6;
+    const int chunks = k >> 5, rb = k >> 1, row0 = xcd_row_group() * R;
+    const int blocks = (k + group - 1) / group;
+    unsigned magic = 0x64006400u;
+    asm volatile("" : "+v"(magic));  // one VGPR for every nibble pair below
+    float acc[R][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < M; ++i) acc[r][i] = 0.0f;
+#pragma unroll 1
+    for (int c = tid; c < chunks; c += kLongKThreads) {
+        v4i wv[R];
+        float sc[R];
+        const int blk = (c * 32) / group;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const size_t row = static_cast<size_t>(min(row0 + r, n - 1));
+            wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + row * rb + c * 16));
+            sc[r] = to_f32(scale[row * blocks + blk]);
+        }
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            const XT* xp = x + static_cast<size_t>(min(i, m - 1)) * k + c * 32;
+            XChunk<XT> lo, hi;
+            lo.load(xp);
+            hi.load(xp + 16);
+            // the codes as seen by this activation row: without the opaque copy
+            // the compiler converts every code once for all M rows and keeps the
+            // converted values live
+            v4i wq[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                wq[r] = wv[r];
+                if constexpr (M > 1) asm volatile("" : "+v"(wq[r]));
+            }
+            if constexpr (sizeof(XT) == 2) {
+                const typename XChunk<XT>::h8 q[4] = {lo.v[0], lo.v[1], hi.v[0], hi.v[1]};
+                h2 pairs[16];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) pairs[4 * e + j] = h2{q[e][j], q[e][j + 4]};
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[r][i] = __builtin_fmaf(dot32_q4_f16m(wq[r], pairs, magic), sc[r], acc[r][i]);
+            } else {
+                float xf[32];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    xf[e] = lo.at(e);
+                    xf[16 + e] = hi.at(e);
+                }
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[r][i] = __builtin_fmaf(dot32_q4_f32(wq[r], xf), sc[r], acc[r][i]);
+            }
+        }
+    }
+    reduce_to_lds<R, M, (R * M >= 16)>(acc, red, wave, tid & 63);
+    __syncthreads();
+    if (tid < R * M) {
+        const int r = tid / M, i = tid % M, row = row0 + r;
+        if (row < n && i < m) {
+            float s = 0.0f;
+#pragma unroll
+            for (int q = 0; q < kLongKThreads / kWave; ++q) s += red[(q * R + r) * M + i];
+            y[static_cast<size_t>(i) * n + row] = from_f32<YT>(s + (bias ? bias[row] : 0.0f));
+        }
+    }
+}
+
+// int8 activation codes: exact int32 sums (equal to every other W8A8 path).
+template <int R, int M, typename YT, bool ACC_OUT>
+__global__ __launch_bounds__(kLongKThreads) void gemv_w8a8_longk_kernel(
+    const int8_t* __restrict__ xq, const float* __restrict__ as, const int8_t* __restrict__ w,
+    const float* __restrict__ ws, const float* __restrict__ bias, YT* __restrict__ y,
+    int32_t* __restrict__ acc_out, int m, int n, int k) {
+    __shared__ int red[(kLongKThreads / kWave) * R * M];
+    const int tid = threadIdx.x, wave = tid >> 6;
+    const int chunks = k >> 4, row0 = xcd_row_group() * R;
+    int acc[R][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < M; ++i) acc[r][i] = 0;
+#pragma unroll 1
+    for (int c = tid; c < chunks; c += kLongKThreads) {
+        v4i wv[R], xv[M];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            wv[r] = __builtin_nontemporal_load(
+                reinterpret_cast<const v4i*>(w + static_cast<size_t>(min(row0 + r, n - 1)) * k + c * 16));
+#pragma unroll
+        for (int i = 0; i < M; ++i)
+            xv[i] = *reinterpret_cast<const v4i*>(xq + static_cast<size_t>(min(i, m - 1)) * k + c * 16);
+#pragma unroll
+        for (int i = 0; i < M; ++i)
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                int p = acc[r][i];
+#pragma unroll
+                for (int d = 0; d < 4; ++d) p = __builtin_amdgcn_sdot4(xv[i][d], wv[r][d], p, false);
+                acc[r][i] = p;
+            }
+    }
+    reduce_to_lds<R, M, (R * M >= 16)>(acc, red, wave, tid & 63);
+    __syncthreads();
+    if (tid < R * M) {
+        const int r = tid / M, i = tid % M, row = row0 + r;
+        if (row < n && i < m) {
+            int s = 0;
+#pragma unroll
+            for (int q = 0; q < kLongKThreads / kWave; ++q) s += red[(q * R + r) * M + i];
+            if constexpr (ACC_OUT) {
+                acc_out[static_cast<size_t>(i) * n + row] = s;
+            } else {
+                const float b = bias ? bias[row] : 0.0f;
+                y[static_cast<size_t>(i) * n + row] = from_f32<YT>(w8a8_epilogue(s, as[i], ws[row], b));
+            }
+        }
+    }
+}
+
 // ---- generic bounds-checked kernels (any k, any alignment) -----------------------------
 // One wave per output row; lanes stride K one element at a time; rows of x loop.
 template <typename XT, typename YT>
@@ -1283,6 +1495,38 @@ void dispatch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, Y
     }
 }
 
+// Long-K launches (one m bucket of up to 8 activation rows each): 4 weight rows
+// per workgroup for one or two activation rows, 2 for more.
+template <typename XT, typename YT>
+void dispatch_q8_longk(const XT* x, const int8_t* w, const float* ws, const float* b, YT* y, int m, int n, int k,
+                       hipStream_t s) {
+    auto go = [&](auto mt) {
+        constexpr int M = decltype(mt)::value, R = M <= 2 ? 4 : 2;
+        gemv_q8_longk_kernel<R, M, XT, YT><<<(n + R - 1) / R, kLongKThreads, 0, s>>>(x, w, ws, b, y, m, n, k);
+    };
+    switch (m_bucket(m)) {
+        case 1: go(std::integral_constant<int, 1>{}); break;
+        case 2: go(std::integral_constant<int, 2>{}); break;
+        case 4: go(std::integral_constant<int, 4>{}); break;
+        default: go(std::integral_constant<int, 8>{}); break;
+    }
+}
+template <typename XT, typename YT, typename ST>
+void dispatch_q4g_longk(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n, int k,
+                        int group, hipStream_t s) {
+    auto go = [&](auto mt) {
+        constexpr int M = decltype(mt)::value, R = M <= 2 ? 4 : 2;
+        gemv_q4g_longk_kernel<R, M, XT, YT, ST><<<(n + R - 1) / R, kLongKThreads, 0, s>>>(x, w, sc, b, y, m, n, k,
+                                                                                          group);
+    };
+    switch (m_bucket(m)) {
+        case 1: go(std::integral_constant<int, 1>{}); break;
+        case 2: go(std::integral_constant<int, 2>{}); break;
+        case 4: go(std::integral_constant<int, 4>{}); break;
+        default: go(std::integral_constant<int, 8>{}); break;
+    }
+}
+
 nq_status check_linear(const void* x, const void* w, const void* y, int64_t m, int64_t n,
                        int64_t k, const char* who) {
     NQ_REQUIRE(m >= 0 && n >= 0 && k >= 0, NQ_BAD_SHAPE, "%s: negative shape", who);
@@ -1304,6 +1548,30 @@ nq_status gemv_w8a8_launch(const int8_t* xq, const float* as, const int8_t* w, c
     const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
     const bool fast = !generic && k > 0 && k % 16 == 0 && k / 16 <= kMaxGemvThreads && m <= 8 &&
                       aligned(xq, 16) && aligned(w, 16);
+    const bool long_k = !generic && k % 16 == 0 && k / 16 > kMaxGemvThreads && m <= 8 && aligned(xq, 16) &&
+                        aligned(w, 16);
+    if (long_k) {
+        auto go = [&](auto mt) {
+            constexpr int M = decltype(mt)::value, R = M <= 2 ? 4 : 2;
+            const unsigned grid = static_cast<unsigned>((n + R - 1) / R);
+            if (acc_out)
+                gemv_w8a8_longk_kernel<R, M, float, true><<<grid, kLongKThreads, 0, s>>>(xq, as, w, ws, bias, nullptr,
+                                                                                         acc_out, mi, ni, ki);
+            else if (ydt == NQ_F32)
+                gemv_w8a8_longk_kernel<R, M, float, false><<<grid, kLongKThreads, 0, s>>>(
+                    xq, as, w, ws, bias, static_cast<float*>(y), nullptr, mi, ni, ki);
+            else
+                gemv_w8a8_longk_kernel<R, M, _Float16, false><<<grid, kLongKThreads, 0, s>>>(
+                    xq, as, w, ws, bias, static_cast<_Float16*>(y), nullptr, mi, ni, ki);
+        };
+        switch (m_bucket(m)) {
+            case 1: go(std::integral_constant<int, 1>{}); break;
+            case 2: go(std::integral_constant<int, 2>{}); break;
+            case 4: go(std::integral_constant<int, 4>{}); break;
+            default: go(std::integral_constant<int, 8>{}); break;
+        }
+        return launch_status("gemv_w8a8_longk_kernel");
+    }
     if (!fast) {
         const int wpb = 4;
         const unsigned grid = static_cast<unsigned>((n + wpb - 1) / wpb);
@@ -1516,11 +1784,22 @@ nq_status linear_q8_impl(const void* x, nq_dtype x_dtype, const int8_t* q, const
     }
     const bool fast = path != NQ_PATH_GENERIC && k % 16 == 0 && k > 0 && k / 16 <= kMaxGemvThreads &&
                       aligned(q, 16) && aligned(x, 16);
+    const bool long_k = path != NQ_PATH_GENERIC && k % 16 == 0 && k / 16 > kMaxGemvThreads && aligned(q, 16) &&
+                        aligned(x, 16);
     // Otherwise x rows beyond 8 run in slices of 8 (each slice re-streams the weight).
     for (int64_t r0 = 0; r0 < m; r0 += 8) {
         const int mi = static_cast<int>(m - r0 < 8 ? m - r0 : 8);
         const size_t xo = static_cast<size_t>(r0) * k, yo = static_cast<size_t>(r0) * n;
-        if (fast) {
+        if (long_k) {
+            if (x_dtype == NQ_F32 && y_dtype == NQ_F32)
+                dispatch_q8_longk(static_cast<const float*>(x) + xo, q, w_scale, bias, static_cast<float*>(y) + yo, mi, ni, ki, s);
+            else if (x_dtype == NQ_F32)
+                dispatch_q8_longk(static_cast<const float*>(x) + xo, q, w_scale, bias, static_cast<_Float16*>(y) + yo, mi, ni, ki, s);
+            else if (y_dtype == NQ_F32)
+                dispatch_q8_longk(static_cast<const _Float16*>(x) + xo, q, w_scale, bias, static_cast<float*>(y) + yo, mi, ni, ki, s);
+            else
+                dispatch_q8_longk(static_cast<const _Float16*>(x) + xo, q, w_scale, bias, static_cast<_Float16*>(y) + yo, mi, ni, ki, s);
+        } else if (fast) {
             if (x_dtype == NQ_F32 && y_dtype == NQ_F32)
                 dispatch_q8(static_cast<const float*>(x) + xo, q, w_scale, bias, static_cast<float*>(y) + yo, mi, ni, ki, s);
             else if (x_dtype == NQ_F32)
@@ -1581,11 +1860,15 @@ nq_status linear_q4g_impl(const void* x, nq_dtype x_dtype, const uint8_t* q, con
     }
     const bool fast = path != NQ_PATH_GENERIC && k % 32 == 0 && k > 0 && group % 32 == 0 &&
                       k / 32 <= kMaxGemvThreads && aligned(q, 16) && aligned(x, 16);
+    const bool long_k = path != NQ_PATH_GENERIC && k % 32 == 0 && group % 32 == 0 && k / 32 > kMaxGemvThreads &&
+                        aligned(q, 16) && aligned(x, 16);
     for (int64_t r0 = 0; r0 < m; r0 += 8) {
         const int mi = static_cast<int>(m - r0 < 8 ? m - r0 : 8);
         const size_t xo = static_cast<size_t>(r0) * k, yo = static_cast<size_t>(r0) * n;
         auto run = [&](auto* xp, auto* yp, auto* sp) {
-            if (fast)
+            if (long_k)
+                dispatch_q4g_longk(xp + xo, q, sp, bias, yp + yo, mi, ni, ki, gi, s);
+            else if (fast)
                 dispatch_q4g(xp + xo, q, sp, bias, yp + yo, mi, ni, ki, gi, s);
             else
                 gemv_q4g_generic_kernel<<<static_cast<unsigned>((n + 3) / 4), 256, 0, s>>>(

@@ -8,8 +8,8 @@ trace of this suite), each against an independent reference.
   producer (fused), over every vector width and workgroup size;
 * weight-only linears: against torch fp64 on the dequantized weight (whose
   dequant is bit-exact with the oracle), 1e-3 * RMS (+ half an fp16 ulp for
-  fp16 outputs), over m buckets, row groups, split-K plans, activation / output
-  / scale dtypes and group sizes;
+  fp16 outputs), over m buckets, row groups, split-K plans, long K (several
+  chunks per lane), activation / output / scale dtypes and group sizes;
 * W8A8: every AUTO route's output equals the bounds-checked generic kernel's
   bit for bit (one shared epilogue), its int32 accumulators equal the exact
   integer product, and the generic output is within 1e-3 * RMS of fp64.
@@ -148,6 +148,9 @@ WQ_SHAPES = [  # (m, n, k): GEMV buckets, row-group rules, GEMM tile plans, spli
     (16, 1536, 4096), (40, 1536, 4096), (100, 1536, 4096),
     (16, 1536, 4128), (24, 1536, 4128), (24, 6000, 4128), (40, 1536, 4128), (56, 1536, 4128), (100, 1536, 4128), (16, 6000, 4128),
     (24, 1536, 1536), (40, 6000, 1024),
+    # long K (several chunks per lane): int8 past k = 9216, int4 past k = 18432, each m bucket
+    (1, 100, 9232), (2, 37, 14336), (4, 70, 9744), (7, 50, 10240),
+    (1, 60, 18944), (2, 37, 18464), (3, 50, 20480), (8, 45, 18944),
     # outside the fast paths (k % 32 != 0: the bounds-checked kernels)
     (3, 300, 100), (1, 129, 90),
 ]
@@ -192,6 +195,8 @@ W8A8_SHAPES = [
     (128, 256, 8960), (128, 1536, 8960), (128, 8960, 1536), (200, 1003, 192), (256, 1536, 1536),
     (300, 640, 4096), (512, 1536, 8960), (512, 2048, 1536), (512, 17920, 1536), (1024, 8960, 1536),
     (2048, 8960, 1536), (2048, 1536, 1536),
+    # long K on the GEMV (several chunks per lane past k = 9216), each m bucket
+    (1, 100, 9232), (2, 37, 14336), (3, 70, 9744), (7, 2100, 9232),
 ]
 
 
