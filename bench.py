@@ -501,6 +501,14 @@ def shape_sweep(args, time_graph, q4g_gemv, q8_gemv, w8a8_linear, entry, copies_
             e["read_floor_us"] = read_us(wbytes)
             e["floor_ratio"] = round(e["read_floor_us"] / e["us"], 3)
             row[kind] = {key: e[key] for key in ("us", "GB/s", "frac", "read_floor_us", "floor_ratio")}
+        for mb in (8, 64):  # batched decode: HBM-bound, beside the same read floor
+            for kind, mk in ((f"q4g_g32_m{mb}", lambda: q4g_gemv(mb, n, k, 32)),
+                             (f"q8_m{mb}", lambda: q8_gemv(mb, n, k, torch.float16)),
+                             (f"w8a8_m{mb}", lambda: w8a8_linear(mb, n, k))):
+                e = entry(kind, *mk(), "hbm")
+                torch.cuda.empty_cache()
+                floor = row[kind.replace(f"_m{mb}", "_m1")]["read_floor_us"]
+                row[kind] = {"us": e["us"], "GB/s": e["GB/s"], "floor_ratio": round(floor / e["us"], 3)}
         for kind, mk, bound in (("w8a8_m512", lambda: w8a8_linear(512, n, k, gemm_only=True), "mfma"),
                                 ("q8_m512", lambda: q8_gemv(512, n, k, torch.float16), "mfma_f16"),
                                 ("q4g_g32_m512", lambda: q4g_gemv(512, n, k, 32), "mfma_f16")):

@@ -1025,7 +1025,7 @@ struct SmallWidePlan {
     int fn, splits, k_slabs;
     size_t acc_bytes;
 };
-SmallWidePlan plan_small_wide(int64_t m, int64_t n, int64_t k) {
+SmallWidePlan plan_small_wide(int64_t m, int64_t n, int64_t k, bool rounds = true) {
     SmallWidePlan p{};
     if (m > kSkinnyMaxM || m <= 0 || n <= 0 || k <= 0 || !prefill_ok(m, n, k)) return p;
     int64_t best = 0;
@@ -1036,6 +1036,15 @@ SmallWidePlan plan_small_wide(int64_t m, int64_t n, int64_t k) {
             best = c;
             fn = f;
         }
+    }
+    // Tall weights: 64 x 128 tiles in more than one round, against the skinny
+    // kernel's 16- or 32-column workgroups (m = 64, k = 3584, n = 37888: 84.3 ->
+    // 42.9 us; n = 128256, k = 4096: 273.9 -> 119.5; m = 24: 174.2 -> 113.9;
+    // m = 20, n = 60000, k = 2048: 54.5 -> 29.0). The GEMV / MFMA choice at m <= 8
+    // keeps the one-round test (m = 5, n = 40000, k = 3072 lost 32.0 -> 35.2).
+    if (best == 0 && rounds && k <= 4096) {
+        fn = 4;
+        best = (n + 127) / 128;
     }
     if (best == 0) return p;
     const int nslab = static_cast<int>((k + 127) / 128);
@@ -1103,7 +1112,7 @@ bool skinny_ok(int64_t m, int64_t n, int64_t k) {
 // shapes k = 1536 / 8960, n = 256 .. 8960.
 int resolve_path(int path, int64_t m, int64_t n, int64_t k) {
     if (path != NQ_PATH_AUTO) return path;
-    return (m <= 4 || (m <= 8 && (k >= 4096 || (n >= 8192 && !plan_small_wide(m, n, k).fn)))) ? NQ_PATH_GEMV
+    return (m <= 4 || (m <= 8 && (k >= 4096 || (n >= 8192 && !plan_small_wide(m, n, k, false).fn)))) ? NQ_PATH_GEMV
                                                                                           : NQ_PATH_MFMA;
 }
 

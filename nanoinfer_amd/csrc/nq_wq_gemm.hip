@@ -961,7 +961,7 @@ bool wq_wide_ok(int64_t m, int64_t n, int64_t k, int64_t group) {
 // Split-K, when the caller gives a workspace for the fp32 partial planes. A
 // weight with few rows leaves most CUs idle, each workgroup walking all of K,
 // so long K splits into up to kWqMaxSplits ranges summed by wq_reduce_kernel
-// (a second launch and the planes' traffic). Wide split (k >= 4096, 16 <= m <=
+// (a second launch and the planes' traffic). Wide split (k >= 2048, 16 <= m <=
 // 128, fp32 x from m = 32): 64 x 64 tiles (64 x 128 above m = 64) with a
 // two-slot LDS ring, so two or three workgroups share a CU (with the deep ring
 // of the unsplit tiles, one workgroup of 8 waves per CU left the SIMDs waiting:
@@ -973,6 +973,11 @@ bool wq_wide_ok(int64_t m, int64_t n, int64_t k, int64_t group) {
 // 16 27.3 -> 19.0, m = 64 28.5 -> 22.4; n = 4096, k = 4096, m = 128 28.4 ->
 // 26.1 (m = 16 11.8 -> 12.7: the one loss kept; fp32 x at m = 16 lost 16.5 ->
 // 23.1, the split kernel converting all 64 tile rows, hence m >= 32 there).
+// From k = 2048 (was 4096), found on Qwen2.5-7B shapes (k = 3584, fp16 x, q4g /
+// q8): m = 64, n = 4608 42.4 -> 16.6 / 36.0 -> 15.1; m = 64, n = 3584 23.0 ->
+// 15.4; m = 32 22.5 -> 14.1; m = 16 19.0 -> 12.9; m = 128 30.0 -> 25.2; m = 64,
+// n = 1536, k = 2048 14.7 -> 10.2. From k = 1024 lost at m = 16..32 and n = 8960
+// (k = 1536, m = 16: 7.2 -> 9.3; m = 64, n = 8960: 15.4 -> 16.5).
 // Otherwise the 16-row kernel splits when its unsplit grid is under 256
 // workgroups and k >= 4096 (or at most 32 workgroups at m > 32 or fp32 x), to
 // about kWqRowSplitWgs workgroups with at least two chunks per wave (n = 256,
@@ -988,7 +993,7 @@ struct WqRoute {
 WqRoute plan_wq_route(int64_t m, int64_t n, int64_t k, bool wide_ok, bool wide_contract, bool sk64_ok, bool f32x,
                       bool allow_split) {
     WqRoute r{};
-    if (allow_split && wide_contract && m >= (f32x ? 32 : 9) && m <= 128 && k >= 4096) {
+    if (allow_split && wide_contract && m >= (f32x ? 32 : 9) && m <= 128 && k >= 2048) {
         WqTile t{1, m <= 64 ? 2 : 4, f32x ? 64 : 128};
         t.shallow = true;
         const int64_t tiles = ((m + 63) / 64) * ((n + 32 * t.fn - 1) / (32 * t.fn)), nk = k / t.sk;
@@ -1047,7 +1052,14 @@ bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m,
     // Shape rule (measured): the GEMM runs one workgroup per 16 (or 32) weight
     // rows, each reading all of x, so below 4096 rows it fills under 256 CUs; a
     // GEMV slice of 8 rows plus a remainder slice is then faster up to m = 15.
-    if (!forced && !wq_gemm_shape_ok(m, n, k, x_elem, ws)) return false;
+    // int8 codes with fp16 x at m = 5..8 on large weights: the GEMV's per-row
+    // FMAs make it VALU-bound there (m = 8, fp16 x, us, GEMV -> GEMM: n = 28672,
+    // k = 4096 69.3 -> 46.0; n = 128256, k = 4096 279.5 -> 174.2; n = 4096, k =
+    // 14336 37.8 -> 25.8; n = 17920, k = 1536 19.0 -> 14.8; n = 4096, k = 4096
+    // 13.3 -> 10.4; m = 5, n = 28672 60.2 -> 43.6; smaller weights keep the GEMV:
+    // n = 1536, k = 8960 11.7 -> 16.8). int4 codes gain nothing there.
+    const bool q8_batch = !q4 && x_elem == 2 && m >= 5 && m <= 8 && n >= 4096 && n * k >= (int64_t(16) << 20);
+    if (!forced && !q8_batch && !wq_gemm_shape_ok(m, n, k, x_elem, ws)) return false;
     return m > 0 && k > 0 && k % 32 == 0 && (!q4 || (group % 32 == 0 && ((group / 32) & (group / 32 - 1)) == 0)) && aligned(x, 16) && aligned(w, 16) &&
            m <= (int64_t(65535) * 64) && std::min<int64_t>(m, 64) * k * static_cast<int64_t>(x_elem) < (int64_t(1) << 31) - 64 &&
            n * rowb < (int64_t(1) << 31) - 64;

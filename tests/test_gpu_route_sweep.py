@@ -148,6 +148,10 @@ WQ_SHAPES = [  # (m, n, k): GEMV buckets, row-group rules, GEMM tile plans, spli
     (16, 1536, 4096), (40, 1536, 4096), (100, 1536, 4096),
     (16, 1536, 4128), (24, 1536, 4128), (24, 6000, 4128), (40, 1536, 4128), (56, 1536, 4128), (100, 1536, 4128), (16, 6000, 4128),
     (24, 1536, 1536), (40, 6000, 1024),
+    # int8 codes, fp16 x, m = 5..8 on large weights: the MFMA GEMM
+    (6, 4160, 4096), (8, 17920, 1024),
+    # split wide tiles from k = 2048 (k % 128 == 0)
+    (40, 4608, 3584), (16, 1536, 2048),
     # long K (several chunks per lane): int8 past k = 9216, int4 past k = 18432, each m bucket
     (1, 100, 9232), (2, 37, 14336), (4, 70, 9744), (7, 50, 10240),
     (1, 60, 18944), (2, 37, 18464), (3, 50, 20480), (8, 45, 18944),
@@ -195,6 +199,8 @@ W8A8_SHAPES = [
     (128, 256, 8960), (128, 1536, 8960), (128, 8960, 1536), (200, 1003, 192), (256, 1536, 1536),
     (300, 640, 4096), (512, 1536, 8960), (512, 2048, 1536), (512, 17920, 1536), (1024, 8960, 1536),
     (2048, 8960, 1536), (2048, 1536, 1536),
+    # 64 x 128 tiles over more than one round (more than 256 of them, k <= 4096)
+    (17, 33000, 256), (40, 33000, 512),
     # long K on the GEMV (several chunks per lane past k = 9216), each m bucket
     (1, 100, 9232), (2, 37, 14336), (3, 70, 9744), (7, 2100, 9232),
 ]
