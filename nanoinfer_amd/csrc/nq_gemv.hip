@@ -1480,6 +1480,22 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
                 return;
             }
         }
+        if constexpr (M == 1) {
+            // Tall weights: more rows per workgroup, fewer re-reads of the
+            // activation chunk (every workgroup reads all of x, as many bytes as
+            // two rows of codes at k = 4096): fp16 x, us, 2 / 4 / 8 rows: n =
+            // 128256, k = 4096 64.5 / 54.5 / 52.7; n = 152064, k = 3584 66.2 /
+            // 58.2 / 54.7; n = 37888, k = 3584 18.1 / 16.0 / 16.6; n = 28672 14.8 /
+            // 13.7 / 14.4; n = 6144 5.7 / 6.0 / 6.6 (fewer workgroups lose below).
+            if (n >= 65536) {
+                gemv_q4g_kernel<8, 1, XT, YT, ST><<<(n + 7) / 8, threads, 0, s>>>(x, w, sc, b, y, m, n, k, g);
+                return;
+            }
+            if (n >= 24576) {
+                gemv_q4g_kernel<4, 1, XT, YT, ST><<<(n + 3) / 4, threads, 0, s>>>(x, w, sc, b, y, m, n, k, g);
+                return;
+            }
+        }
         gemv_q4g_kernel<R, M, XT, YT, ST><<<(n + R - 1) / R, threads, 0, s>>>(x, w, sc, b, y, m, n, k, g);
     }
 }

@@ -148,6 +148,8 @@ WQ_SHAPES = [  # (m, n, k): GEMV buckets, row-group rules, GEMM tile plans, spli
     (16, 1536, 4096), (40, 1536, 4096), (100, 1536, 4096),
     (16, 1536, 4128), (24, 1536, 4128), (24, 6000, 4128), (40, 1536, 4128), (56, 1536, 4128), (100, 1536, 4128), (16, 6000, 4128),
     (24, 1536, 1536), (40, 6000, 1024),
+    # one activation row on tall weights: 4 and 8 weight rows per workgroup
+    (1, 24600, 512), (1, 65600, 256),
     # int8 codes, fp16 x, m = 5..8 on large weights: the MFMA GEMM
     (6, 4160, 4096), (8, 17920, 1024),
     # split wide tiles from k = 2048 (k % 128 == 0)
