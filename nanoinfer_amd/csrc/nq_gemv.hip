@@ -32,6 +32,7 @@ namespace {
 
 constexpr int kMaxGemvWaves = 9;          // 576 lanes: int8 k <= 9216, int4 k <= 18432
 constexpr int kMaxGemvThreads = kMaxGemvWaves * kWave;
+constexpr int kLongKThreads = 256;     // the long-K kernels' workgroup (several chunks per lane)
 
 // Rows per workgroup as a function of the activation-row count: more rows =
 // more reuse of each loaded activation chunk, fewer = more workgroups.
@@ -906,7 +907,6 @@ __global__ __launch_bounds__(kDecThreads) void w8a8_decode_kernel(const XT* __re
 // 256 lanes stride K one chunk at a time, R weight rows per workgroup (their R
 // loads in flight per lane, several workgroups per CU), the same per-chunk dot
 // products as the one-chunk kernels and the same cross-wave reduction.
-constexpr int kLongKThreads = 256;
 
 template <int R, int M, typename XT, typename YT>
 __global__ __launch_bounds__(kLongKThreads) void gemv_q8_longk_kernel(
@@ -1512,7 +1512,10 @@ void dispatch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, Y
 }
 
 // Long-K launches (one m bucket of up to 8 activation rows each): 4 weight rows
-// per workgroup for one or two activation rows, 2 for more.
+// per workgroup for one or two activation rows, 2 for more; one activation row
+// on 8192 weight rows or more takes 8 (half the activation re-reads: n = 8192,
+// k = 28672 int8 42.8 -> 39.9 us, int4 27.5 -> 26.2; n = 14336, k = 10240 27.5 ->
+// 26.1; n = 1536, k = 20480 lost 10.5 -> 11.3).
 template <typename XT, typename YT>
 void dispatch_q8_longk(const XT* x, const int8_t* w, const float* ws, const float* b, YT* y, int m, int n, int k,
                        hipStream_t s) {
@@ -1520,6 +1523,10 @@ void dispatch_q8_longk(const XT* x, const int8_t* w, const float* ws, const floa
         constexpr int M = decltype(mt)::value, R = M <= 2 ? 4 : 2;
         gemv_q8_longk_kernel<R, M, XT, YT><<<(n + R - 1) / R, kLongKThreads, 0, s>>>(x, w, ws, b, y, m, n, k);
     };
+    if (m == 1 && n >= 8192) {
+        gemv_q8_longk_kernel<8, 1, XT, YT><<<(n + 7) / 8, kLongKThreads, 0, s>>>(x, w, ws, b, y, m, n, k);
+        return;
+    }
     switch (m_bucket(m)) {
         case 1: go(std::integral_constant<int, 1>{}); break;
         case 2: go(std::integral_constant<int, 2>{}); break;
@@ -1535,6 +1542,10 @@ void dispatch_q4g_longk(const XT* x, const uint8_t* w, const ST* sc, const float
         gemv_q4g_longk_kernel<R, M, XT, YT, ST><<<(n + R - 1) / R, kLongKThreads, 0, s>>>(x, w, sc, b, y, m, n, k,
                                                                                           group);
     };
+    if (m == 1 && n >= 8192) {
+        gemv_q4g_longk_kernel<8, 1, XT, YT, ST><<<(n + 7) / 8, kLongKThreads, 0, s>>>(x, w, sc, b, y, m, n, k, group);
+        return;
+    }
     switch (m_bucket(m)) {
         case 1: go(std::integral_constant<int, 1>{}); break;
         case 2: go(std::integral_constant<int, 2>{}); break;

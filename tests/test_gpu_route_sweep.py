@@ -156,7 +156,7 @@ WQ_SHAPES = [  # (m, n, k): GEMV buckets, row-group rules, GEMM tile plans, spli
     (40, 4608, 3584), (16, 1536, 2048),
     # long K (several chunks per lane): int8 past k = 9216, int4 past k = 18432, each m bucket
     (1, 100, 9232), (2, 37, 14336), (4, 70, 9744), (7, 50, 10240),
-    (1, 60, 18944), (2, 37, 18464), (3, 50, 20480), (8, 45, 18944),
+    (1, 60, 18944), (2, 37, 18464), (3, 50, 20480), (8, 45, 18944), (1, 8200, 9232), (1, 8200, 18464),
     # outside the fast paths (k % 32 != 0: the bounds-checked kernels)
     (3, 300, 100), (1, 129, 90),
 ]
@@ -204,7 +204,7 @@ W8A8_SHAPES = [
     # 64 x 128 tiles over more than one round (more than 256 of them, k <= 4096)
     (17, 33000, 256), (40, 33000, 512),
     # long K on the GEMV (several chunks per lane past k = 9216), each m bucket
-    (1, 100, 9232), (2, 37, 14336), (3, 70, 9744), (7, 2100, 9232),
+    (1, 100, 9232), (2, 37, 14336), (3, 70, 9744), (7, 2100, 9232), (1, 64, 32768),
 ]
 
 
