@@ -1058,8 +1058,19 @@ bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m,
     // 14336 37.8 -> 25.8; n = 17920, k = 1536 19.0 -> 14.8; n = 4096, k = 4096
     // 13.3 -> 10.4; m = 5, n = 28672 60.2 -> 43.6; smaller weights keep the GEMV:
     // n = 1536, k = 8960 11.7 -> 16.8). int4 codes gain nothing there.
-    const bool q8_batch = !q4 && x_elem == 2 && m >= 5 && m <= 8 && n >= 4096 && n * k >= (int64_t(16) << 20);
-    if (!forced && !q8_batch && !wq_gemm_shape_ok(m, n, k, x_elem, ws)) return false;
+    // fp32 x at m = 5..8 (int8 and int4 codes): the GEMM from n, k >= 4096 and on
+    // the long K of the chunk-striding GEMVs (int8 k > 9216; int4 k > 18432 from
+    // n = 3072), whose slices re-read 8 fp32 activation rows per workgroup (m = 8,
+    // us, GEMV -> GEMM, int8 / int4: n = 4096, k = 14336 113.1 -> 35.5 / 119.6 ->
+    // 44.7; n = 3584, k = 18944 128.8 -> 44.9 / 126.3 -> 56.9; n = 6144, k = 4096
+    // 19.5 -> 17.4 / 29.4 -> 24.2; int8 n = 2048, k = 10240 37.0 -> 26.8; n = 1536,
+    // k = 8960 keeps the GEMV: 14.6 against 22.9; int4 n = 1536, k = 9728 22.8
+    // against 30.7).
+    const bool batch5 = m >= 5 && m <= 8 &&
+                        ((!q4 && x_elem == 2 && n >= 4096 && n * k >= (int64_t(16) << 20)) ||
+                         (x_elem == 4 && ((n >= 4096 && k >= 4096) || (!q4 && k > 9216) ||
+                                          (q4 && k > 18432 && n >= 3072))));
+    if (!forced && !batch5 && !wq_gemm_shape_ok(m, n, k, x_elem, ws)) return false;
     return m > 0 && k > 0 && k % 32 == 0 && (!q4 || (group % 32 == 0 && ((group / 32) & (group / 32 - 1)) == 0)) && aligned(x, 16) && aligned(w, 16) &&
            m <= (int64_t(65535) * 64) && std::min<int64_t>(m, 64) * k * static_cast<int64_t>(x_elem) < (int64_t(1) << 31) - 64 &&
            n * rowb < (int64_t(1) << 31) - 64;

@@ -150,8 +150,8 @@ WQ_SHAPES = [  # (m, n, k): GEMV buckets, row-group rules, GEMM tile plans, spli
     (24, 1536, 1536), (40, 6000, 1024),
     # one activation row on tall weights: 4 and 8 weight rows per workgroup
     (1, 24600, 512), (1, 65600, 256),
-    # int8 codes, fp16 x, m = 5..8 on large weights: the MFMA GEMM
-    (6, 4160, 4096), (8, 17920, 1024),
+    # m = 5..8 on large weights (int8 with fp16 x; fp32 x from n, k >= 4096 or on long K): the MFMA GEMM
+    (6, 4160, 4096), (8, 17920, 1024), (7, 64, 9728), (5, 3100, 18464),
     # split wide tiles from k = 2048 (k % 128 == 0)
     (40, 4608, 3584), (16, 1536, 2048),
     # long K (several chunks per lane): int8 past k = 9216, int4 past k = 18432, each m bucket
@@ -177,6 +177,11 @@ def test_sweep_weight_only(dev, nq, mode, g, sdt, xdt, ydt):
         y = nq.linear_q8(x, t, b, out_dtype=ydt) if mode == "q8" else nq.linear_q4g(x, t, b, out_dtype=ydt)
         ref = _wq_ref(nq, mode, t, g, x, b)
         assert_close_rms(host(y.double()), host(ref), f"{mode} g{g} {m}x{n}x{k} {xdt}->{ydt}", fp16_out=ydt == F16)
+        if 5 <= m <= 8 and k > 9216:  # the GEMV slices AUTO leaves to the GEMM there (fp32 x): forced
+            from nanoinfer_amd import _lib as L
+            lin = nq.linear_q8 if mode == "q8" else nq.linear_q4g
+            y2 = lin(x, t, b, out_dtype=ydt, path=L.NQ_PATH_GEMV)
+            assert_close_rms(host(y2.double()), host(ref), f"GEMV {mode} {m}x{n}x{k}", fp16_out=ydt == F16)
 
 
 # ---- W8A8 ---------------------------------------------------------------------------------
