@@ -106,6 +106,19 @@ struct RowQuantizer {
     }
 };
 
+// Threads per workgroup, read at kernel start. blockDim.x comes from the second
+// 64-byte line of the kernel arguments; left to itself the compiler loads it where
+// it is first used, which in the GEMVs is after the workgroup barrier, so a cold
+// scalar miss sat on the critical path of every workgroup (int4 GEMV, n = 24,
+// k = 8960: 3.59 -> 3.42 us; within noise at the bench shapes, where other
+// workgroups have the line in L2 by then). The empty asm makes the value, and its
+// load, due at the point of the call, beside the other argument loads.
+__device__ __forceinline__ int block_threads() {
+    const int t = blockDim.x;
+    asm volatile("" ::"s"(t));
+    return t;
+}
+
 // std::max(absmax, |v|) exactly as quant.cpp:100 evaluates it: a NaN |v| leaves
 // absmax unchanged.
 __device__ __forceinline__ float absmax_step(float absmax, float v) {

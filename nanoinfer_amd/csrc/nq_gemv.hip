@@ -156,7 +156,7 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q8_kernel(
     ArgCtl* __restrict__ ctl) {
     static_assert(XS == 1 || !AM, "activation slices write y");
     __shared__ float red[kMaxGemvWaves * R * M];
-    const int tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6;
+    const int tid = threadIdx.x, wave = tid >> 6, nw = block_threads() >> 6;
     const int chunks = k >> 4;
     const bool act = tid < chunks;
     int rg = xcd_row_group();
@@ -343,7 +343,7 @@ __global__ __launch_bounds__(LB) void gemv_q4g_kernel(
     const XT* __restrict__ x, const uint8_t* __restrict__ w, const ST* __restrict__ scale,
     const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int group) {
     __shared__ float red[kMaxGemvWaves * R * M];
-    const int tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6;
+    const int tid = threadIdx.x, wave = tid >> 6, nw = block_threads() >> 6;
     const int chunks = k >> 5;  // 32 codes per 16-byte chunk
     const int rb = k >> 1;
     const bool act = tid < chunks;
@@ -481,7 +481,7 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_q4g_x1h_half_kernel(
     const float* __restrict__ bias, YT* __restrict__ y, int n, int k, int group) {
     constexpr int RP = R <= 1 ? 1 : R <= 2 ? 2 : R <= 4 ? 4 : 8;  // reduced values, a power of two
     __shared__ float red[kMaxGemvWaves * R];
-    const int tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6;
+    const int tid = threadIdx.x, wave = tid >> 6, nw = block_threads() >> 6;
     const int halves = k >> 4, rb = k >> 1;
     const int row0 = xcd_row_group() * R;
     const bool act = tid < halves;
@@ -540,7 +540,7 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_kernel(
     const float* __restrict__ ws, const float* __restrict__ bias, YT* __restrict__ y,
     int32_t* __restrict__ acc_out, int m, int n, int k) {
     __shared__ int red[kMaxGemvWaves * R * M];
-    const int tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6;
+    const int tid = threadIdx.x, wave = tid >> 6, nw = block_threads() >> 6;
     const int chunks = k >> 4;
     const bool act = tid < chunks;
     const int row0 = xcd_row_group() * R;
@@ -598,7 +598,7 @@ __global__ __launch_bounds__(kMaxGemvThreads) void gemv_w8a8_fused_kernel(
     const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k) {
     __shared__ float amax_red[kMaxGemvWaves * M];
     __shared__ int red[kMaxGemvWaves * R * M];
-    const int tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6;
+    const int tid = threadIdx.x, wave = tid >> 6, nw = block_threads() >> 6;
     const int chunks = k >> 4;
     const bool act = tid < chunks;
     const int row0 = xcd_row_group() * R;

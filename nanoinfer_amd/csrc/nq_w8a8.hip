@@ -612,7 +612,7 @@ __global__ __launch_bounds__(1024) void gemm_w8a8_skinny_kernel(
     xq += row_base * k;
     if (as) as += row_base;
     const size_t out_base = row_base * n;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nthr = blockDim.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nthr = block_threads();
     const int nw = nthr >> 6;
     const int n0 = blockIdx.x * (TN * 16);
     const bool split = gridDim.y > 1;
