@@ -872,6 +872,31 @@ PrefillPlan plan_prefill(int64_t m, int64_t n, int64_t k) {
         p.k_slabs = nk;
         return p;
     }
+    // Long K with fewer than 128 tiles: 64 x 64 wide tiles with K in S ranges,
+    // S = min(6, 256 / tiles), so that about one round of 170..256 workgroups
+    // shares the work (each range's int32 tile into its own plane, then the
+    // reduction launch). Measured against the 128 x 128 prefill kernel below
+    // (us, S in brackets): m = 128, n = 1536, k = 8960 21.1 -> 13.0 [4];
+    // n = 896, k = 4864 20.2 -> 9.6 [6]; n = 2048, k = 8192 18.8 -> 11.5 [4];
+    // n = 1536, k = 4096 18.7 -> 9.9 [4]; m = 192: 20.5 -> 14.5 [3], 20.0 ->
+    // 10.0 [6], 19.5 -> 15.1 [2], 18.9 -> 11.0 [3]; m = 256: 21.2 -> 17.0 [2],
+    // 20.4 -> 10.7 [4], 19.8 -> 12.2 [2]; m = 384, n = 896, k = 4864 21.0 -> 11.7
+    // [3].
+    {
+        const int64_t t64 = ((m + 63) / 64) * ((n + 63) / 64);
+        const int nsl = static_cast<int>((k + 127) / 128);
+        int sp = static_cast<int>(std::min<int64_t>(6, 256 / std::max<int64_t>(1, t64)));
+        sp = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(sp, (int64_t(64) << 20) / std::max<int64_t>(1, m * n * 4))));
+        if (sp >= 2) {
+            p.wide_fm = 1;
+            p.wide_fn = 2;
+            p.tiles = static_cast<int>(t64);
+            p.k_slabs = (nsl + sp - 1) / sp;
+            p.splits = (nsl + p.k_slabs - 1) / p.k_slabs;
+            p.acc_bytes = round_up(static_cast<size_t>(p.splits) * static_cast<size_t>(m * n) * 4, 256);
+            return p;
+        }
+    }
     p.wide_fm = p.wide_fn = 0;
     p.tiles = static_cast<int>(((m + 127) / 128) * ((n + 127) / 128));
     int splits = 1;
@@ -937,10 +962,10 @@ nq_status launch_wide_tile(int fm, int fn, const int8_t* xq, const float* as, co
         constexpr int FM = decltype(fmtag)::value, FN2 = decltype(fntag)::value;
         constexpr int WN = FN2 % 3 == 0 ? 3 : FN2 % 4 == 0 ? 4 : 2, FN = FN2 * 2 / WN;  // 16-column fragments per wave
         if (splits > 1) {
-            // Split K runs only the 64 x 32 tiles: plan_small_wide splits when the
-            // 32-column tiles number at most 128 (wider tiles are chosen only past
-            // 256 of them, which leaves no room to split).
-            if constexpr (FM == 1 && FN2 == 1) {
+            // Split K runs the 64 x 32 tiles (plan_small_wide: when they number at
+            // most 128; wider tiles are chosen only past 256 of them) and the 64 x 64
+            // tiles (plan_prefill: long K with fewer than 128 tiles).
+            if constexpr (FM == 1 && FN2 <= 2) {
                 const nq_status st = launch_wide<4, FN, FM, Out::PARTIAL, float, WN>(xq, as, wq, ws, bias, nullptr,
                                                                                      parts, mi, ni, ki, s, splits,
                                                                                      k_slabs);
@@ -982,8 +1007,6 @@ nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const fl
                    int64_t k, void* workspace, size_t ws_bytes, hipStream_t s) {
     const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
     const PrefillPlan p = plan_prefill(m, n, k);
-    if (p.wide_fn) return launch_wide_tile(p.wide_fm, p.wide_fn, xq, as, wq, ws, bias, y, ydt, acc_out, mi, ni, ki, s);
-    if (p.splits == 1) return launch_wide_tile(p.best_fm, p.best_fn, xq, as, wq, ws, bias, y, ydt, acc_out, mi, ni, ki, s);
     int32_t* parts = nullptr;
     if (p.splits > 1) {
         NQ_REQUIRE(workspace && ws_bytes >= p.acc_bytes, NQ_BAD_ARG,
@@ -991,6 +1014,10 @@ nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const fl
         NQ_REQUIRE(aligned(workspace, 256), NQ_BAD_ALIGN, "w8a8 gemm: workspace must be 256-byte aligned");
         parts = static_cast<int32_t*>(workspace);
     }
+    if (p.wide_fn)
+        return launch_wide_tile(p.wide_fm, p.wide_fn, xq, as, wq, ws, bias, y, ydt, acc_out, mi, ni, ki, s, p.splits,
+                                p.splits > 1 ? p.k_slabs : 1 << 30, parts);
+    if (p.splits == 1) return launch_wide_tile(p.best_fm, p.best_fn, xq, as, wq, ws, bias, y, ydt, acc_out, mi, ni, ki, s);
     auto go = [&](auto wmtag, auto wntag, auto dtag, auto swtag) -> nq_status {
         constexpr int WM = decltype(wmtag)::value, WN = decltype(wntag)::value, D = decltype(dtag)::value;
         constexpr int SW = decltype(swtag)::value;

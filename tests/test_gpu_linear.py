@@ -666,7 +666,10 @@ def test_w8a8_split_workspace_too_small(dev, nq, m, n, k):
                                    (512, 17920, 1536), (500, 17917, 1536),
                                    # k % 64 != 0: the skinny kernel over 64-row blocks in one launch,
                                    # with split K and its partial planes for the long k
-                                   (200, 1000, 528), (130, 512, 6160)])
+                                   (200, 1000, 528), (130, 512, 6160),
+                                   # long K, fewer than 128 tiles: 64 x 64 wide tiles with K in 5 / 4 / 4 / 6
+                                   # ranges (k % 128 == 64 puts the half slab in the last range; ragged m, n)
+                                   (128, 1536, 8960), (200, 896, 4864), (256, 1000, 4160), (100, 700, 4096)])
 def test_w8a8_prefill_plans_exact(dev, nq, orc, m, n, k):
     """Every prefill plan (wide 256 x 256..320 tiles, 256x128 / 128x128 tiles,
     split K with int32 partial planes) gives the GEMV path's accumulators bit for bit, and the linear's
