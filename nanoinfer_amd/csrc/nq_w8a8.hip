@@ -7,12 +7,11 @@
 // (l % 16) and of B column (l % 16) for K slice (l / 16); the 16x16 int32
 // result lands as rows 4*(l/16)+v, column l%16, v = 0..3.
 //
-// Three MFMA kernels: a skinny one for batched decode (m <= 64: operands
+// Two MFMA kernels: a skinny one for batched decode (m <= 64: operands
 // loaded straight into the MFMA lane layout, K steps interleaved over waves);
-// the wide-tile kernel (one round of up to 256 tiles of 64 x 32 .. 256 x 320,
-// LDS-DMA ring of 128-byte K slabs), which takes most shapes with m > 64 and
-// decode batches with tall weights; and the LDS-tiled prefill kernel for m > 64
-// shapes with few tiles and a long K. When a launch would have too few
+// and the wide-tile kernel (rounds of up to 256 tiles of 64 x 32 .. 256 x 320,
+// LDS-DMA ring of 128-byte K slabs), which takes the shapes with m > 64 and
+// decode batches with tall weights. When a launch would have too few
 // workgroups, they split K: each K range writes its int32 partial tile to its
 // own workspace plane and a reduction launch sums the planes in a fixed order
 // (integer addition is exact, so the result is bit-identical to a single pass)
@@ -35,287 +34,14 @@ nq_status gemv_w8a8_launch(const int8_t* xq, const float* as, const int8_t* w, c
 namespace {
 
 constexpr int kBK = 64;         // K bytes per MFMA step / LDS slab
-constexpr int kLdsRow = kBK + 16;  // padded LDS row stride (bytes)
 
 enum class Out { Y, ACC, PARTIAL };
-
-// ---- prefill W8A8 GEMM (m > 64, few tiles and long K) -------------------------------------
-// A workgroup of WM x WN waves owns a (WM*64) x (WN*64) output tile; each wave
-// owns 64 x 64 (4 x 4 MFMA 16x16x64 fragments). K advances in SW-byte slabs
-// (SW = 64 or 128) that the buffer unit writes straight into a D-deep LDS ring
-// (buffer_load ... lds: no VGPR staging, no ds_write); each lane picks the
-// global chunk that belongs at its LDS slot, which applies an XOR swizzle
-// (16-byte chunk c of row r lands in slot c ^ ((r >> 1) & (SW/16 - 1)); the
-// MFMA fragment reads are then bank-conflict free). One barrier per slab.
-// SW = 64: the MFMAs of slab kt run while slab kt + D - 1 is requested and the
-// fragments of slab kt + 1 are read. SW = 128 (two MFMA K steps per slab): a
-// 1 KB DMA request covers 8 rows x 128 bytes, whole cache lines, which loads a
-// tile faster than 16 rows x 64 bytes but takes twice the LDS per slab; the
-// fragments of the second K step are read during the first step's MFMAs.
-// The MFMA computes D = W_tile * xq_tile^T (weights as the A operand), so a lane
-// ends with four consecutive output columns of one row. fp16 outputs are staged
-// through LDS and written as whole 16-byte row chunks.
-// Workgroup ids are remapped so each XCD (ids are dealt round-robin over the 8
-// XCDs) covers a contiguous band of column tiles, walked row-tile fastest: the
-// XCD's band of the weight stays in its L2 while the row tiles stream past.
-// The LDS-DMA loads are issued from inline asm, so the compiler does not track
-// them: the kernel waits for them itself (s_waitcnt vmcnt) before each barrier
-// and before the epilogue.
-// Byte offset of 16-byte chunk c of row r in a swizzled SW-byte-row LDS tile.
-template <int SW>
-__device__ __forceinline__ int swz(int r, int c) { return r * SW + ((c ^ ((r >> 1) & (SW / 16 - 1))) << 4); }
-
-template <int WM, int WN, int D, int SW = 64>
-struct PrefillShape {
-    static constexpr int kWaves = WM * WN, kBM = WM * 64, kBN = WN * 64;
-    static constexpr int kRows = 1024 / SW;                // rows per 1 KB LDS-DMA block
-    static constexpr int kXB = kBM / kRows, kWB = kBN / kRows;  // blocks per slab
-    static constexpr int kQ = (kXB + kWB) / kWaves;        // LDS-DMA instructions per wave per slab
-    static constexpr int kSlab = (kBM + kBN) * SW;         // bytes per slab
-    static constexpr int kOutStride = kBN * 2 + 16;        // staged fp16 row stride (bytes)
-    static constexpr size_t kLds = std::max<size_t>(size_t(D) * kSlab, size_t(kBM) * kOutStride);
-    static_assert((kXB + kWB) % kWaves == 0, "whole LDS-DMA blocks per wave");
-};
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
-
-template <int WM, int WN, int D, int SW, Out OUT, typename YT>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_w8a8_prefill_kernel(
-    const int8_t* __restrict__ xq, const float* __restrict__ as, const int8_t* __restrict__ wq,
-    const float* __restrict__ ws, const float* __restrict__ bias, YT* __restrict__ y,
-    int32_t* __restrict__ acc_out, int m, int n, int k, int tiles_m, int tiles_n, int k_slabs) {
-    using S = PrefillShape<WM, WN, D, SW>;
-    constexpr int Q = S::kQ, XB = S::kXB, BM = S::kBM, BN = S::kBN, CPR = SW / 16;
-    extern __shared__ __attribute__((aligned(16))) int8_t lds[];
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / WN, wn = wave % WN;
-    const int total = tiles_m * tiles_n;
-    int lin = blockIdx.x;
-    if (total % 8 == 0) lin = (blockIdx.x % 8) * (total / 8) + blockIdx.x / 8;
-    const int mt = lin % tiles_m, nt = lin / tiles_m;
-    const int m0 = mt * BM, n0 = nt * BN;
-
-    // Raw buffers: rows past m / n and slabs past the end get an offset beyond
-    // the buffer, which reads zeros without touching memory.
-    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(xq), 0, m * k, 0x00020000);
-    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(wq), 0, n * k, 0x00020000);
-    constexpr int kOob = 0x7FFFFFF0;
-    // Wave w issues blocks w*Q .. w*Q+Q-1 of each slab: blocks [0, XB) are the
-    // activation tile, the rest the weight tile. Lane i of a block writes LDS
-    // bytes 16i..16i+15 of it (row i / CPR, slot i % CPR) and so loads the
-    // chunk that the swizzle puts in that slot. vtail: the same offsets with
-    // the upper half of a 128-byte row out of range (the last slab when
-    // k % 128 == 64).
-    int voff[Q], vtail[Q];
-#pragma unroll
-    for (int q = 0; q < Q; ++q) {
-        const int blk = wave * Q + q;
-        const bool isx = blk < XB;
-        const int r = (isx ? blk : blk - XB) * S::kRows + lane / CPR;
-        const int c = (lane % CPR) ^ ((r >> 1) & (CPR - 1));
-        const int grow = (isx ? m0 : n0) + r;
-        voff[q] = grow < (isx ? m : n) ? grow * k + c * 16 : kOob;
-        vtail[q] = c < 4 ? voff[q] : kOob;
-    }
-    // This workgroup's K range: slabs [s0, s1) (the whole K unless the launch
-    // splits K over gridDim.y; the prefill contract has k % 64 == 0).
-    const int nslab = (k + SW - 1) / SW;
-    const bool half_tail = SW == 128 && (k % SW) != 0;
-    const int s0 = blockIdx.y * k_slabs, s1 = min(nslab, s0 + k_slabs);
-    const unsigned lds_base = static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds));
-    auto issue = [&](int sl) {  // sl counts from s0
-        const unsigned slot = static_cast<unsigned>(sl % D) * S::kSlab;
-        const int g = s0 + sl;
-        const int soff = g < s1 ? g * SW : kOob;
-        const bool tail = half_tail && g == nslab - 1;
-#pragma unroll
-        for (int q = 0; q < Q; ++q) {
-            const int blk = wave * Q + q;
-            const unsigned dst = lds_base + slot + blk * 1024;
-            const int vo = tail ? vtail[q] : voff[q];
-            if (blk < XB)
-                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                             ::"s"(dst), "v"(vo), "s"(xrs), "s"(soff) : "memory");
-            else
-                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                             ::"s"(dst), "v"(vo), "s"(wrs), "s"(soff) : "memory");
-        }
-    };
-    // Own LDS-DMA of the oldest in-flight slab landed (D - 2 younger slabs may fly).
-    auto wait_slab = [&]() { wait_vmcnt<Q * (D - 2)>(); };
-
-    v4i acc[4][4];  // [n fragment][m fragment]
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
-    const int fr = lane & 15, fc = lane >> 4;
-    constexpr int T = SW / 64;  // MFMA K steps per slab
-    int fxo[T][4], fwo[T][4];
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) fxo[t][j] = swz<SW>(wm * 64 + j * 16 + fr, t * 4 + fc);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) fwo[t][i] = swz<SW>(BM + wn * 64 + i * 16 + fr, t * 4 + fc);
-    }
-    v4i fw[2][4], fx[2][4];
-    auto read = [&](int sl, int t, v4i (&w)[4], v4i (&x)[4]) {
-        const int8_t* base = lds + (sl % D) * S::kSlab;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = *reinterpret_cast<const v4i*>(base + fwo[t][i]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) x[j] = *reinterpret_cast<const v4i*>(base + fxo[t][j]);
-    };
-    auto mma = [&](const v4i (&w)[4], const v4i (&x)[4]) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[i], x[j], acc[i][j], 0, 0, 0);
-    };
-
-#pragma unroll
-    for (int sl = 0; sl < D - 1; ++sl) issue(sl);
-    wait_slab();
-    __builtin_amdgcn_s_barrier();
-    read(0, 0, fw[0], fx[0]);
-    const int nk = s1 - s0;
-    if constexpr (SW == 64) {
-        // The slot refilled at iteration kt held slab kt - 1, whose fragments every
-        // wave read before the previous iteration's barrier.
-        auto iter = [&](int kt, auto par) {
-            constexpr int P = decltype(par)::value;
-            mma(fw[P], fx[P]);
-            issue(kt + D - 1);
-            wait_slab();
-            __builtin_amdgcn_s_barrier();
-            read(kt + 1, 0, fw[P ^ 1], fx[P ^ 1]);
-        };
-        int kt = 0;
-        for (; kt + 2 <= nk; kt += 2) {
-            iter(kt, std::integral_constant<int, 0>{});
-            iter(kt + 1, std::integral_constant<int, 1>{});
-        }
-        if (kt < nk) iter(kt, std::integral_constant<int, 0>{});
-    } else {
-        for (int kt = 0; kt < nk; ++kt) {
-            // The slot refilled here held slab kt - 1, whose fragments every
-            // wave had in registers before the previous barrier.
-            issue(kt + D - 1);
-            read(kt, 1, fw[1], fx[1]);
-            mma(fw[0], fx[0]);
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // step-1 fragments of slab kt landed
-            wait_slab();
-            __builtin_amdgcn_s_barrier();
-            read(kt + 1, 0, fw[0], fx[0]);
-            mma(fw[1], fx[1]);
-        }
-    }
-    wait_vmcnt<0>();  // the ring's tail requests (zero reads) have retired
-
-    // Lane l holds, for fragment (i, j), output row m0 + wm*64 + j*16 + (l % 16)
-    // and columns n0 + wn*64 + i*16 + 4*(l / 16) + (0..3).
-    const int row_in = fr, col_in = fc * 4;
-    if constexpr (OUT == Out::PARTIAL) {
-        // Split K: this range's int32 partial tile goes to plane blockIdx.y of
-        // the workspace; a reduction launch sums the planes in a fixed order.
-        int32_t* plane = acc_out + static_cast<size_t>(blockIdx.y) * m * n;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int row = m0 + wm * 64 + j * 16 + row_in;
-            if (row >= m) continue;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int col = n0 + wn * 64 + i * 16 + col_in;
-                const size_t o = static_cast<size_t>(row) * n + col;
-                if (col + 3 < n && (n & 3) == 0) {
-                    *reinterpret_cast<v4i*>(plane + o) = acc[i][j];
-                } else {
-#pragma unroll
-                    for (int v = 0; v < 4; ++v)
-                        if (col + v < n) plane[o + v] = acc[i][j][v];
-                }
-            }
-        }
-        return;
-    }
-    if constexpr (OUT == Out::Y && sizeof(YT) == 2) {
-        if ((n & 7) == 0) {
-            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-            __builtin_amdgcn_s_barrier();  // every wave is done reading the ring
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int rl = wm * 64 + j * 16 + row_in;
-                const float a_s = m0 + rl < m ? as[m0 + rl] : 0.0f;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int cl = wn * 64 + i * 16 + col_in, col = n0 + cl;
-                    const bool cin = col < n;  // n % 8 == 0: a 4-column group is all in or all out
-                    const f4 w4 = cin ? *reinterpret_cast<const f4*>(ws + col) : f4{0, 0, 0, 0};
-                    const f4 b4 = cin && bias ? *reinterpret_cast<const f4*>(bias + col) : f4{0, 0, 0, 0};
-                    h4 r;
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) r[v] = from_f32<_Float16>(w8a8_epilogue(acc[i][j][v], a_s, w4[v], b4[v]));
-                    *reinterpret_cast<h4*>(lds + rl * S::kOutStride + cl * 2) = r;
-                }
-            }
-            __syncthreads();
-            constexpr int CPR = BN / 8;  // 16-byte chunks per tile row
-            for (int c = tid; c < BM * CPR; c += S::kWaves * 64) {
-                const int rl = c / CPR, cc = c % CPR;
-                const int row = m0 + rl, col = n0 + cc * 8;
-                if (row < m && col < n)
-                    *reinterpret_cast<v4i*>(y + static_cast<size_t>(row) * n + col) =
-                        *reinterpret_cast<const v4i*>(lds + rl * S::kOutStride + cc * 16);
-            }
-            return;
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int row = m0 + wm * 64 + j * 16 + row_in;
-        if (row >= m) continue;
-        const float a_s = OUT == Out::Y ? as[row] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int col = n0 + wn * 64 + i * 16 + col_in;
-            const size_t o = static_cast<size_t>(row) * n + col;
-            if (col + 3 < n && (n & 3) == 0) {
-                if constexpr (OUT == Out::ACC) {
-                    *reinterpret_cast<v4i*>(acc_out + o) = acc[i][j];
-                } else {
-                    const f4 w4 = *reinterpret_cast<const f4*>(ws + col);
-                    const f4 b4 = bias ? *reinterpret_cast<const f4*>(bias + col) : f4{0, 0, 0, 0};
-                    if constexpr (sizeof(YT) == 4) {
-                        f4 r;
-#pragma unroll
-                        for (int v = 0; v < 4; ++v) r[v] = w8a8_epilogue(acc[i][j][v], a_s, w4[v], b4[v]);
-                        *reinterpret_cast<f4*>(y + o) = r;
-                    } else {
-                        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-                        h4 r;
-#pragma unroll
-                        for (int v = 0; v < 4; ++v) r[v] = from_f32<YT>(w8a8_epilogue(acc[i][j][v], a_s, w4[v], b4[v]));
-                        *reinterpret_cast<h4*>(y + o) = r;
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    if (col + v >= n) break;
-                    if constexpr (OUT == Out::ACC) acc_out[o + v] = acc[i][j][v];
-                    else y[o + v] = from_f32<YT>(w8a8_epilogue(acc[i][j][v], a_s, ws[col + v], bias ? bias[col + v] : 0.0f));
-                }
-            }
-        }
-    }
-}
-
 
 // ---- wide-tile W8A8 GEMM: one (64*WM) x (32*FN) tile per CU ------------------------------
 // For shapes whose 256 x 256..320 (or 128 x 256..320) tiles number at most one
@@ -830,12 +556,10 @@ nq_status gemm_skinny(const int8_t* xq, const float* as, const int8_t* wq, const
 // m = 512, n = 2048: 64 x 64 7.7, 64 x 128 9.9, 128 x 128 12.4; m = 4096, n =
 // 8960: 256 x 288 in two rounds 77.1, 256 x 256 (560 tiles) 94.2; m = 8192, n =
 // 1536: 256 x 256 32.2 vs 256 x 288 34.9 (the same 192 tiles, less padding). When the chosen round has fewer than 128
-// tiles and K is long (>= 64 slabs of 64 bytes), the K-split prefill plan runs
-// instead: 128 x 128 tiles of 4 waves (64 x 128 with 2 waves when no split
-// applies and tiles are few), K in ranges of at least 32 slabs: each range
-// stores its int32 partial tile into its own workspace plane and a reduction
-// launch sums the planes and applies the epilogue (device-scope atomics into
-// one plane measured several times slower).
+// tiles and K is long, plan_prefill splits K over 64 x 64 tiles instead: each
+// range stores its int32 partial tile into its own workspace plane and a
+// reduction launch sums the planes and applies the epilogue (device-scope
+// atomics into one plane measured several times slower).
 struct WideTile {
     int fm, fn;  // tile = (64 * fm) x (32 * fn), 8 waves of (16 * fm) x (16 * fn)
 };
@@ -844,13 +568,21 @@ struct WideTile {
 constexpr WideTile kWideTiles[] = {{4, 10}, {4, 9}, {4, 8}, {2, 10}, {2, 9}, {4, 4}, {2, 8},
                                    {2, 4}, {2, 2}, {1, 4}, {1, 3}, {1, 2}};
 struct PrefillPlan {
-    int wide_fn;  // 0: not wide
-    int wide_fm;  // wide tile rows / 64
-    int best_fm, best_fn;  // the cheapest wide tile (also when the plan splits K instead)
-    int sw;       // K slab bytes of the prefill kernel (64 or 128)
-    int tiles, splits, k_slabs;
-    size_t acc_bytes;
+    int wide_fm, wide_fn;  // tile = (64 * wide_fm) x (32 * wide_fn)
+    int tiles, splits, k_slabs;  // k_slabs: 128-byte slabs per K range when split
+    size_t acc_bytes;            // partial planes of a split plan
 };
+// m > 64: the wide tile the cost model picks (one round of tiles, at most one per
+// CU, or several rounds of the largest tile); when it leaves fewer than 128
+// tiles and K is long (>= 64 slabs of 64 bytes), 64 x 64 tiles with K in S =
+// min(6, 256 / tiles) ranges, so that one round of about 170..256 workgroups
+// shares the work (each range's int32 tile into its own plane, then the
+// reduction launch). Measured against the 128 x 128-tile split-K kernel this
+// replaced (us, S in brackets): m = 128, n = 1536, k = 8960 21.1 -> 13.0 [4]; n =
+// 896, k = 4864 20.2 -> 9.6 [6]; n = 2048, k = 8192 18.8 -> 11.5 [4]; n = 1536,
+// k = 4096 18.7 -> 9.9 [4]; m = 192: 20.5 -> 14.5 [3], 20.0 -> 10.0 [6], 19.5 ->
+// 15.1 [2], 18.9 -> 11.0 [3]; m = 256: 21.2 -> 17.0 [2], 20.4 -> 10.7 [4], 19.8 ->
+// 12.2 [2]; m = 384, n = 896, k = 4864 21.0 -> 11.7 [3].
 PrefillPlan plan_prefill(int64_t m, int64_t n, int64_t k) {
     PrefillPlan p{};
     const int nk = std::max(1, static_cast<int>(k / kBK));  // also sized for shapes outside the contract
@@ -862,75 +594,25 @@ PrefillPlan plan_prefill(int64_t m, int64_t n, int64_t k) {
         if (best_cost == 0 || cost < best_cost) {
             best_cost = cost;
             best_tiles = c;
-            p.wide_fm = p.best_fm = t.fm;
-            p.wide_fn = p.best_fn = t.fn;
+            p.wide_fm = t.fm;
+            p.wide_fn = t.fn;
         }
     }
-    if (best_tiles >= 128 || nk < 64) {
-        p.tiles = static_cast<int>(best_tiles);
-        p.splits = 1;
-        p.k_slabs = nk;
-        return p;
-    }
-    // Long K with fewer than 128 tiles: 64 x 64 wide tiles with K in S ranges,
-    // S = min(6, 256 / tiles), so that about one round of 170..256 workgroups
-    // shares the work (each range's int32 tile into its own plane, then the
-    // reduction launch). Measured against the 128 x 128 prefill kernel below
-    // (us, S in brackets): m = 128, n = 1536, k = 8960 21.1 -> 13.0 [4];
-    // n = 896, k = 4864 20.2 -> 9.6 [6]; n = 2048, k = 8192 18.8 -> 11.5 [4];
-    // n = 1536, k = 4096 18.7 -> 9.9 [4]; m = 192: 20.5 -> 14.5 [3], 20.0 ->
-    // 10.0 [6], 19.5 -> 15.1 [2], 18.9 -> 11.0 [3]; m = 256: 21.2 -> 17.0 [2],
-    // 20.4 -> 10.7 [4], 19.8 -> 12.2 [2]; m = 384, n = 896, k = 4864 21.0 -> 11.7
-    // [3].
-    {
-        const int64_t t64 = ((m + 63) / 64) * ((n + 63) / 64);
-        const int nsl = static_cast<int>((k + 127) / 128);
-        int sp = static_cast<int>(std::min<int64_t>(6, 256 / std::max<int64_t>(1, t64)));
-        sp = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(sp, (int64_t(64) << 20) / std::max<int64_t>(1, m * n * 4))));
-        if (sp >= 2) {
-            p.wide_fm = 1;
-            p.wide_fn = 2;
-            p.tiles = static_cast<int>(t64);
-            p.k_slabs = (nsl + sp - 1) / sp;
-            p.splits = (nsl + p.k_slabs - 1) / p.k_slabs;
-            p.acc_bytes = round_up(static_cast<size_t>(p.splits) * static_cast<size_t>(m * n) * 4, 256);
-            return p;
-        }
-    }
-    p.wide_fm = p.wide_fn = 0;
-    p.tiles = static_cast<int>(((m + 127) / 128) * ((n + 127) / 128));
-    int splits = 1;
-    // Fewer than 256 tiles: K splits into ranges of at least 32 slabs (the
-    // partial planes and the reduction launch cost more than a short K loop
-    // saves: m = 512, n = 1536, k = 1536 ran 13.0 us unsplit vs 15.4 in three
-    // ranges; k = 8960 ran best in four ranges, 25.3 us vs 29.5 in six). With
-    // k >= 64 slabs here that is always two or more ranges; a plan left with one
-    // range (the planes' cap below) runs the cheapest wide tile instead.
-    if (p.tiles < 256) splits = std::max(1, nk / 32);
-    // at most 64 MiB of partial planes
-    splits = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(splits, (int64_t(64) << 20) / std::max<int64_t>(1, m * n * 4))));
-    // 128 x 128 tiles that fit one round (split ranges included) take 128-byte
-    // slabs in a 3-slot ring (m = 512, n = 1536, k = 8960 in four ranges: 25.4
-    // -> 23.2 us); where a second workgroup per CU matters, the 64-byte ring
-    // keeps its smaller LDS footprint.
-    p.sw = int64_t(p.tiles) * splits <= 256 ? 128 : 64;
-    const int ns = p.sw == 128 ? static_cast<int>((k + 127) / 128) : nk;
-    p.k_slabs = (ns + splits - 1) / splits;
-    p.splits = (ns + p.k_slabs - 1) / p.k_slabs;
+    p.tiles = static_cast<int>(best_tiles);
+    p.splits = 1;
+    if (best_tiles >= 128 || nk < 64) return p;
+    const int64_t t64 = ((m + 63) / 64) * ((n + 63) / 64);
+    const int nsl = static_cast<int>((k + 127) / 128);
+    const int64_t sp = std::min<int64_t>({6, 256 / std::max<int64_t>(1, t64),
+                                          (int64_t(64) << 20) / std::max<int64_t>(1, m * n * 4)});  // <= 64 MiB of planes
+    if (sp < 2) return p;
+    p.wide_fm = 1;
+    p.wide_fn = 2;
+    p.tiles = static_cast<int>(t64);
+    p.k_slabs = static_cast<int>((nsl + sp - 1) / sp);
+    p.splits = (nsl + p.k_slabs - 1) / p.k_slabs;
     if (p.splits > 1) p.acc_bytes = round_up(static_cast<size_t>(p.splits) * static_cast<size_t>(m * n) * 4, 256);
     return p;
-}
-
-template <int WM, int WN, int D, int SW, Out OUT, typename YT>
-nq_status launch_prefill(const int8_t* xq, const float* as, const int8_t* wq, const float* ws, const float* bias,
-                         YT* y, int32_t* acc_out, int m, int n, int k, int splits, int k_slabs, hipStream_t s) {
-    using S = PrefillShape<WM, WN, D, SW>;
-    auto* fn = gemm_w8a8_prefill_kernel<WM, WN, D, SW, OUT, YT>;
-    if (nq_status st = set_dynamic_lds(reinterpret_cast<const void*>(fn), S::kLds, "gemm_w8a8_prefill")) return st;
-    const int tm = (m + S::kBM - 1) / S::kBM, tn = (n + S::kBN - 1) / S::kBN;
-    const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(splits));
-    fn<<<grid, S::kWaves * 64, S::kLds, s>>>(xq, as, wq, ws, bias, y, acc_out, m, n, k, tm, tn, k_slabs);
-    return launch_status("gemm_w8a8_prefill_kernel");
 }
 
 template <int WM, int FN, int FM, Out OUT, typename YT, int WN = 2>
@@ -1007,34 +689,15 @@ nq_status gemm_big(const int8_t* xq, const float* as, const int8_t* wq, const fl
                    int64_t k, void* workspace, size_t ws_bytes, hipStream_t s) {
     const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
     const PrefillPlan p = plan_prefill(m, n, k);
-    int32_t* parts = nullptr;
-    if (p.splits > 1) {
-        NQ_REQUIRE(workspace && ws_bytes >= p.acc_bytes, NQ_BAD_ARG,
-                   "w8a8 gemm: workspace of %zu bytes required, %zu given", p.acc_bytes, ws_bytes);
-        NQ_REQUIRE(aligned(workspace, 256), NQ_BAD_ALIGN, "w8a8 gemm: workspace must be 256-byte aligned");
-        parts = static_cast<int32_t*>(workspace);
-    }
-    if (p.wide_fn)
-        return launch_wide_tile(p.wide_fm, p.wide_fn, xq, as, wq, ws, bias, y, ydt, acc_out, mi, ni, ki, s, p.splits,
-                                p.splits > 1 ? p.k_slabs : 1 << 30, parts);
-    if (p.splits == 1) return launch_wide_tile(p.best_fm, p.best_fn, xq, as, wq, ws, bias, y, ydt, acc_out, mi, ni, ki, s);
-    auto go = [&](auto wmtag, auto wntag, auto dtag, auto swtag) -> nq_status {
-        constexpr int WM = decltype(wmtag)::value, WN = decltype(wntag)::value, D = decltype(dtag)::value;
-        constexpr int SW = decltype(swtag)::value;
-        return launch_prefill<WM, WN, D, SW, Out::PARTIAL, float>(xq, as, wq, ws, bias, nullptr, parts, mi, ni, ki,
-                                                                 p.splits, p.k_slabs, s);
-    };
-    using I2 = std::integral_constant<int, 2>;
-    using I3 = std::integral_constant<int, 3>;
-    using I4 = std::integral_constant<int, 4>;
-    using I64 = std::integral_constant<int, 64>;
-    using I128 = std::integral_constant<int, 128>;
-    const nq_status st = p.sw == 128 ? go(I2{}, I2{}, I3{}, I128{}) : go(I2{}, I2{}, I4{}, I64{});
-    if (st != NQ_OK) return st;
-    return reduce_partials(parts, p.splits, as, ws, bias, y, ydt, acc_out, mi, ni, s);
+    if (p.splits == 1) return launch_wide_tile(p.wide_fm, p.wide_fn, xq, as, wq, ws, bias, y, ydt, acc_out, mi, ni, ki, s);
+    NQ_REQUIRE(workspace && ws_bytes >= p.acc_bytes, NQ_BAD_ARG,
+               "w8a8 gemm: workspace of %zu bytes required, %zu given", p.acc_bytes, ws_bytes);
+    NQ_REQUIRE(aligned(workspace, 256), NQ_BAD_ALIGN, "w8a8 gemm: workspace must be 256-byte aligned");
+    return launch_wide_tile(p.wide_fm, p.wide_fn, xq, as, wq, ws, bias, y, ydt, acc_out, mi, ni, ki, s, p.splits,
+                            p.k_slabs, static_cast<int32_t*>(workspace));
 }
 
-// The wide and prefill kernels' contract: whole 64-byte K slabs and 32-bit
+// The wide kernel's contract: whole 64-byte K slabs and 32-bit
 // buffer offsets.
 bool prefill_ok(int64_t m, int64_t n, int64_t k) {
     return k % kBK == 0 && m * k < (int64_t(1) << 31) - 64 && n * k < (int64_t(1) << 31) - 64;
@@ -1091,8 +754,8 @@ SmallWidePlan plan_small_wide(int64_t m, int64_t n, int64_t k, bool rounds = tru
 
 // Workspace of the MFMA GEMM for this shape: the int32 partial planes of the
 // plan run_gemm picks (the small-m wide tiles or the skinny plan for m <= 64,
-// the wide / prefill plan for m > 64, the skinny 64-row blocks for shapes
-// outside the prefill contract); zero when the plan does not split K.
+// the wide-tile plan for m > 64, the skinny 64-row blocks for shapes outside
+// the wide kernel's contract); zero when the plan does not split K.
 // One skinny launch covers all m rows (64-row blocks over gridDim.z) when its
 // split planes stay within 64 MiB.
 bool skinny_one_launch(int64_t m, int64_t n, int64_t k) {
@@ -1169,8 +832,7 @@ nq_status run_gemm(const int8_t* xq, const float* as, const int8_t* wq, const fl
             return gemm_skinny(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, workspace, ws_bytes, s);
         // (The skinny kernel over 64-row blocks in one launch was measured on the
         // m = 512 decoder shapes too: qkv 12.9 -> 20.7 us, down 29.6 -> 78 us
-        // against the split prefill plan, so it only takes what the prefill
-        // kernel cannot.)
+        // against the tiled plans, so it only takes what the wide kernel cannot.)
         if (prefill_ok(m, n, k))
             return gemm_big(xq, as, wq, ws, bias, y, ydt, acc_out, m, n, k, workspace, ws_bytes, s);
         if (skinny_one_launch(m, n, k))

@@ -195,7 +195,7 @@ W8A8_SHAPES = [
     # the skinny kernel: k % 64 != 0 (no wide tiles), one to four 16-row blocks, 64-row blocks past 64;
     # m <= 16 on long K
     (12, 8960, 1040), (24, 8960, 1040), (40, 8960, 1040), (64, 8960, 1040), (100, 8960, 1040), (12, 8960, 8192),
-    # each wide tile the cost model picks (k = 128), and the split-K prefill kernel's two slab widths
+    # each wide tile the cost model picks (k = 128), and long K on 64 x 64 tiles in K ranges
     (65, 64, 128), (65, 8960, 128), (192, 8960, 128), (768, 12288, 128), (384, 4096, 128), (65, 17920, 128),
     (384, 17920, 128), (512, 17920, 128), (1536, 12288, 128), (256, 17920, 128), (640, 17920, 128),
     (1024, 17920, 128), (65, 64, 4096), (512, 512, 65536),
