@@ -993,12 +993,23 @@ struct WqRoute {
 WqRoute plan_wq_route(int64_t m, int64_t n, int64_t k, bool wide_ok, bool wide_contract, bool sk64_ok, bool f32x,
                       bool allow_split) {
     WqRoute r{};
-    if (allow_split && wide_contract && m >= (f32x ? 32 : 9) && m <= 128 && k >= 2048) {
+    // Past m = 128 the split tiles take over where the unsplit plan leaves under
+    // 128 tiles (under 256 on K >= 8192) and the split tiles alone number under
+    // 256 (us, fp16 x, Q8 / Q4G, unsplit -> split: m = 192, n = 1536, k = 8960
+    // 51.1 -> 24.2 / 67.2 -> 24.5; m = 512, n = 896, k = 4864 29.9 -> 21.5 / 38.4
+    // -> 23.3; m = 256, n = 2048, k = 8192 48.2 -> 33.9 / 61.9 -> 34.6; m = 512,
+    // n = 1536, k = 8960 53.7 -> 44.8 / 67.5 -> 47.8; m = 1024 83.1 -> 76.6 /
+    // 104.6 -> 80.8; fp32 x, m = 256: 150.4 -> 58.9 / 169.3 -> 56.3; m = 192, n =
+    // 896, k = 4864 83.3 -> 25.8 / 93.5 -> 25.6). Not where the split tiles fill
+    // the part already (m = 2048, n = 1536, k = 8960: 101.2 against 128.4) nor on
+    // k = 4096 with 128 or more tiles (m = 192, n = 4096: no gain).
+    const bool big_split = m > 128 && plan_wq_wide(m, n, sk64_ok, f32x).tiles < (k >= 8192 ? 256 : 128);
+    if (allow_split && wide_contract && m >= (f32x ? 32 : 9) && (m <= 128 || big_split) && k >= 2048) {
         WqTile t{1, m <= 64 ? 2 : 4, f32x ? 64 : 128};
         t.shallow = true;
         const int64_t tiles = ((m + 63) / 64) * ((n + 32 * t.fn - 1) / (32 * t.fn)), nk = k / t.sk;
         const int64_t sp = std::min<int64_t>({kWqMaxSplits, (kWqWideSplitWgs + tiles - 1) / tiles, nk / kWqMinSlabs});
-        if (sp >= 2) {
+        if (sp >= 2 && (m <= 128 || tiles < 256)) {
             const int64_t per = (nk + sp - 1) / sp;
             r.wide = true;
             r.tile = t;

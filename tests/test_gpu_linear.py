@@ -273,6 +273,11 @@ WQ_GEMM_CASES = [  # m > 8: the fp16 MFMA GEMM (m >= 16 or n >= 4096) or GEMV sl
     ("q8", 300, 1536, 1536, 0, True, F32, F32, F32),
     ("q4g", 200, 2000, 1024, 32, False, F32, F16, F16),
     ("q4g", 130, 9000, 512, 32, True, F32, F32, F32),
+    # m > 128 with few unsplit tiles: the split wide tiles (64 x 128, K ranges)
+    ("q8", 200, 1536, 8960, 0, True, F16, F32, F16),
+    ("q4g", 300, 1000, 8192, 64, False, F16, F16, F16),  # ragged n, k >= 8192 rule
+    ("q8", 160, 896, 4864, 0, False, F32, F32, F32),     # fp32 x, 64-column slabs
+    ("q4g", 520, 896, 4864, 32, True, F16, F16, F32),
 ]
 
 
