@@ -465,8 +465,9 @@ SWEEP_SHAPES = [
 def shape_sweep(args, time_graph, q4g_gemv, q8_gemv, w8a8_linear, entry, copies_for, stream_ptr):
     """Decode (m = 1) GEMVs in the three quant modes over SWEEP_SHAPES, each
     beside a streaming read of the same weight bytes (the single-launch floor
-    at that size), and the prefill GEMMs at m = 512: evidence that the
-    dispatch holds up away from the shapes it was tuned on."""
+    at that size), batched decode at m = 8 and 64, and the prefill GEMMs at m =
+    128, 256 and 512: evidence that the dispatch holds up away from the shapes
+    it was tuned on."""
     import ctypes
 
     import torch
@@ -509,12 +510,13 @@ def shape_sweep(args, time_graph, q4g_gemv, q8_gemv, w8a8_linear, entry, copies_
                 torch.cuda.empty_cache()
                 floor = row[kind.replace(f"_m{mb}", "_m1")]["read_floor_us"]
                 row[kind] = {"us": e["us"], "GB/s": e["GB/s"], "floor_ratio": round(floor / e["us"], 3)}
-        for kind, mk, bound in (("w8a8_m512", lambda: w8a8_linear(512, n, k, gemm_only=True), "mfma"),
-                                ("q8_m512", lambda: q8_gemv(512, n, k, torch.float16), "mfma_f16"),
-                                ("q4g_g32_m512", lambda: q4g_gemv(512, n, k, 32), "mfma_f16")):
-            e = entry(kind, *mk(), bound)
-            torch.cuda.empty_cache()
-            row[kind] = {key: e[key] for key in ("us", "TOPS", "frac")}
+        for mp in (128, 256, 512):  # prefill chunks: the MFMA GEMMs' tile and split plans
+            for kind, mk, bound in ((f"w8a8_m{mp}", lambda: w8a8_linear(mp, n, k, gemm_only=True), "mfma"),
+                                    (f"q8_m{mp}", lambda: q8_gemv(mp, n, k, torch.float16), "mfma_f16"),
+                                    (f"q4g_g32_m{mp}", lambda: q4g_gemv(mp, n, k, 32), "mfma_f16")):
+                e = entry(kind, *mk(), bound)
+                torch.cuda.empty_cache()
+                row[kind] = {key: e[key] for key in ("us", "TOPS", "frac")}
         print(json.dumps(row), file=sys.stderr, flush=True)  # progress
         out.append(row)
     return out

@@ -582,7 +582,9 @@ struct PrefillPlan {
 // 896, k = 4864 20.2 -> 9.6 [6]; n = 2048, k = 8192 18.8 -> 11.5 [4]; n = 1536,
 // k = 4096 18.7 -> 9.9 [4]; m = 192: 20.5 -> 14.5 [3], 20.0 -> 10.0 [6], 19.5 ->
 // 15.1 [2], 18.9 -> 11.0 [3]; m = 256: 21.2 -> 17.0 [2], 20.4 -> 10.7 [4], 19.8 ->
-// 12.2 [2]; m = 384, n = 896, k = 4864 21.0 -> 11.7 [3].
+// 12.2 [2]; m = 384, n = 896, k = 4864 21.0 -> 11.7 [3]. On K >= 8192 128 tiles
+// split too (m = 128, n = 4096, k = 14336: 36.3 -> 26.4 us in two ranges; k =
+// 4096 lost, 12.8 -> 13.3).
 PrefillPlan plan_prefill(int64_t m, int64_t n, int64_t k) {
     PrefillPlan p{};
     const int nk = std::max(1, static_cast<int>(k / kBK));  // also sized for shapes outside the contract
@@ -600,7 +602,7 @@ PrefillPlan plan_prefill(int64_t m, int64_t n, int64_t k) {
     }
     p.tiles = static_cast<int>(best_tiles);
     p.splits = 1;
-    if (best_tiles >= 128 || nk < 64) return p;
+    if (best_tiles >= (k >= 8192 ? 256 : 128) || nk < 64) return p;
     const int64_t t64 = ((m + 63) / 64) * ((n + 63) / 64);
     const int nsl = static_cast<int>((k + 127) / 128);
     const int64_t sp = std::min<int64_t>({6, 256 / std::max<int64_t>(1, t64),

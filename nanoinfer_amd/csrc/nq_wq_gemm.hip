@@ -1002,14 +1002,19 @@ WqRoute plan_wq_route(int64_t m, int64_t n, int64_t k, bool wide_ok, bool wide_c
     // 104.6 -> 80.8; fp32 x, m = 256: 150.4 -> 58.9 / 169.3 -> 56.3; m = 192, n =
     // 896, k = 4864 83.3 -> 25.8 / 93.5 -> 25.6). Not where the split tiles fill
     // the part already (m = 2048, n = 1536, k = 8960: 101.2 against 128.4) nor on
-    // k = 4096 with 128 or more tiles (m = 192, n = 4096: no gain).
+    // k = 4096 with 128 or more tiles (m = 192, n = 4096: no gain). From m = 65 the
+    // split needs fewer than 256 split tiles: on wider weights the unsplit wide
+    // tiles win (Q8 / Q4G, m = 128, k = 4096: n = 28672 85.8 -> 54.6 / 91.7 ->
+    // 71.0; n = 17920, k = 2048 37.1 -> 25.1 / 39.3 -> 36.6; m = 100, n = 28672
+    // 84.8 -> 57.0 / 87.2 -> 67.0; n = 37888, k = 3584 95.6 -> 69.4 / 99.3 ->
+    // 101.7); at m <= 64 the split keeps them (m = 16, Q4G: 47.5 against 80.7).
     const bool big_split = m > 128 && plan_wq_wide(m, n, sk64_ok, f32x).tiles < (k >= 8192 ? 256 : 128);
     if (allow_split && wide_contract && m >= (f32x ? 32 : 9) && (m <= 128 || big_split) && k >= 2048) {
         WqTile t{1, m <= 64 ? 2 : 4, f32x ? 64 : 128};
         t.shallow = true;
         const int64_t tiles = ((m + 63) / 64) * ((n + 32 * t.fn - 1) / (32 * t.fn)), nk = k / t.sk;
         const int64_t sp = std::min<int64_t>({kWqMaxSplits, (kWqWideSplitWgs + tiles - 1) / tiles, nk / kWqMinSlabs});
-        if (sp >= 2 && (m <= 128 || tiles < 256)) {
+        if (sp >= 2 && (m <= 64 || tiles < 256)) {
             const int64_t per = (nk + sp - 1) / sp;
             r.wide = true;
             r.tile = t;

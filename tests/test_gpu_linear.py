@@ -278,6 +278,7 @@ WQ_GEMM_CASES = [  # m > 8: the fp16 MFMA GEMM (m >= 16 or n >= 4096) or GEMV sl
     ("q4g", 300, 1000, 8192, 64, False, F16, F16, F16),  # ragged n, k >= 8192 rule
     ("q8", 160, 896, 4864, 0, False, F32, F32, F32),     # fp32 x, 64-column slabs
     ("q4g", 520, 896, 4864, 32, True, F16, F16, F32),
+    ("q8", 100, 17000, 2048, 0, False, F16, F32, F16),   # m > 64 with >= 256 split tiles: unsplit wide
 ]
 
 
@@ -674,7 +675,9 @@ def test_w8a8_split_workspace_too_small(dev, nq, m, n, k):
                                    (200, 1000, 528), (130, 512, 6160),
                                    # long K, fewer than 128 tiles: 64 x 64 wide tiles with K in 5 / 4 / 4 / 6
                                    # ranges (k % 128 == 64 puts the half slab in the last range; ragged m, n)
-                                   (128, 1536, 8960), (200, 896, 4864), (256, 1000, 4160), (100, 700, 4096)])
+                                   (128, 1536, 8960), (200, 896, 4864), (256, 1000, 4160), (100, 700, 4096),
+                                   # 128 tiles on K >= 8192: two ranges (half slab at the end)
+                                   (100, 4096, 8256)])
 def test_w8a8_prefill_plans_exact(dev, nq, orc, m, n, k):
     """Every prefill plan (wide 256 x 256..320 tiles, 256x128 / 128x128 tiles,
     split K with int32 partial planes) gives the GEMV path's accumulators bit for bit, and the linear's
