@@ -1007,7 +1007,8 @@ WqRoute plan_wq_route(int64_t m, int64_t n, int64_t k, bool wide_ok, bool wide_c
     // tiles win (Q8 / Q4G, m = 128, k = 4096: n = 28672 85.8 -> 54.6 / 91.7 ->
     // 71.0; n = 17920, k = 2048 37.1 -> 25.1 / 39.3 -> 36.6; m = 100, n = 28672
     // 84.8 -> 57.0 / 87.2 -> 67.0; n = 37888, k = 3584 95.6 -> 69.4 / 99.3 ->
-    // 101.7); at m <= 64 the split keeps them (m = 16, Q4G: 47.5 against 80.7).
+    // 101.7); at m <= 64 the split keeps them (m = 16, n = 28672, k = 4096, Q4G:
+    // 47.5 against 80.7).
     const bool big_split = m > 128 && plan_wq_wide(m, n, sk64_ok, f32x).tiles < (k >= 8192 ? 256 : 128);
     if (allow_split && wide_contract && m >= (f32x ? 32 : 9) && (m <= 128 || big_split) && k >= 2048) {
         WqTile t{1, m <= 64 ? 2 : 4, f32x ? 64 : 128};
