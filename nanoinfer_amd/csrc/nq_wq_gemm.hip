@@ -991,7 +991,7 @@ struct WqRoute {
     WqRowPlan row;       // 16-row
 };
 WqRoute plan_wq_route(int64_t m, int64_t n, int64_t k, bool wide_ok, bool wide_contract, bool sk64_ok, bool f32x,
-                      bool allow_split) {
+                      bool allow_split, bool q4) {
     WqRoute r{};
     // Past m = 128 the split tiles take over where the unsplit plan leaves under
     // 128 tiles (under 256 on K >= 8192) and the split tiles alone number under
@@ -1010,7 +1010,7 @@ WqRoute plan_wq_route(int64_t m, int64_t n, int64_t k, bool wide_ok, bool wide_c
     // 101.7); at m <= 64 the split keeps them (m = 16, n = 28672, k = 4096, Q4G:
     // 47.5 against 80.7).
     const bool big_split = m > 128 && plan_wq_wide(m, n, sk64_ok, f32x).tiles < (k >= 8192 ? 256 : 128);
-    if (allow_split && wide_contract && m >= (f32x ? 32 : 9) && (m <= 128 || big_split) && k >= 2048) {
+    if (allow_split && wide_contract && m >= (f32x ? 32 : q4 ? 5 : 9) && (m <= 128 || big_split) && k >= 2048) {
         WqTile t{1, m <= 64 ? 2 : 4, f32x ? 64 : 128};
         t.shallow = true;
         const int64_t tiles = ((m + 63) / 64) * ((n + 32 * t.fn - 1) / (32 * t.fn)), nk = k / t.sk;
@@ -1053,6 +1053,17 @@ size_t wq_route_bytes(const WqRoute& r, int64_t m, int64_t n) {
 // (us, slices -> split, m = 9 / 12 / 15: n = 1536, k = 8960 16.0 / 18.7 / 22.0 ->
 // 13.3 / 13.1 / 13.2; n = 2048, k = 8192 18.5 / 20.5 / 24.4 -> 12.3 / 12.3 /
 // 12.5; the smaller n = 896, k = 4864 lost at m = 9: 8.7 -> 10.4).
+// int4 codes with fp16 x at m = 5..8 on a workspace: the split wide tiles (the
+// GEMV re-reads the activation rows per two weight rows, and the unsplit GEMM
+// converts and scales the codes per 64-row tile). us, GEMV -> split GEMM, m = 8:
+// n = 28672, k = 4096 75.2 -> 50.7; n = 37888, k = 3584 82.9 -> 49.9; n = 4096,
+// k = 14336 41.8 -> 27.0; n = 6144, k = 4096 19.9 -> 15.1; n = 4096, k = 4096
+// 13.0 -> 12.5. Kept on the GEMV: k < 4096 (n = 17920, k = 1536 22.9 against
+// 25.1), n < 4096 (n = 1536, k = 8960 12.6 against 13.5) and the 128256-row LM
+// head (280 against 296).
+bool wq_q4_batch5_shape(int64_t m, int64_t n, int64_t k) {
+    return m >= 5 && m <= 8 && k >= 4096 && k % 128 == 0 && n >= 4096 && n < 65536;
+}
 bool wq_gemm_shape_ok(int64_t m, int64_t n, int64_t k, size_t x_elem, bool ws) {
     return m > 8 && (m >= 16 || n >= 4096 ||
                      (ws && x_elem == 2 && k >= 4096 && k % 128 == 0 && n * k >= (int64_t(6) << 20)));
@@ -1074,7 +1085,9 @@ bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m,
     // k = 4096 69.3 -> 46.0; n = 128256, k = 4096 279.5 -> 174.2; n = 4096, k =
     // 14336 37.8 -> 25.8; n = 17920, k = 1536 19.0 -> 14.8; n = 4096, k = 4096
     // 13.3 -> 10.4; m = 5, n = 28672 60.2 -> 43.6; smaller weights keep the GEMV:
-    // n = 1536, k = 8960 11.7 -> 16.8). int4 codes gain nothing there.
+    // n = 1536, k = 8960 11.7 -> 16.8). int4 codes with fp16 x: the split wide
+    // tiles on wq_q4_batch5_shape when a workspace is given (the unsplit GEMM
+    // gains nothing there).
     // fp32 x at m = 5..8 (int8 and int4 codes): the GEMM from n, k >= 4096 and on
     // the long K of the chunk-striding GEMVs (int8 k > 9216; int4 k > 18432 from
     // n = 3072), whose slices re-read 8 fp32 activation rows per workgroup (m = 8,
@@ -1085,6 +1098,7 @@ bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m,
     // against 30.7).
     const bool batch5 = m >= 5 && m <= 8 &&
                         ((!q4 && x_elem == 2 && n >= 4096 && n * k >= (int64_t(16) << 20)) ||
+                         (q4 && x_elem == 2 && ws && group <= 64 && wq_q4_batch5_shape(m, n, k)) ||
                          (x_elem == 4 && ((n >= 4096 && k >= 4096) || (!q4 && k > 9216) ||
                                           (q4 && k > 18432 && n >= 3072))));
     if (!forced && !batch5 && !wq_gemm_shape_ok(m, n, k, x_elem, ws)) return false;
@@ -1100,9 +1114,9 @@ nq_status wq_gemm(const XT* x, const uint8_t* w, const ST* sc, const float* b, Y
                   int64_t k, int64_t group, void* workspace, size_t workspace_bytes, hipStream_t s) {
     const bool sk64 = wq_sk64_ok<Q4, ST>(group), f32x = sizeof(XT) == 4;
     const bool wide_ok = wq_wide_ok<Q4, XT, ST>(m, n, k, group), contract = wq_wide_contract<Q4, XT, ST>(m, n, k, group);
-    WqRoute r = plan_wq_route(m, n, k, wide_ok, contract, sk64, f32x, workspace != nullptr);
+    WqRoute r = plan_wq_route(m, n, k, wide_ok, contract, sk64, f32x, workspace != nullptr, Q4);
     if (r.splits > 1 && workspace_bytes < wq_route_bytes(r, m, n))
-        r = plan_wq_route(m, n, k, wide_ok, contract, sk64, f32x, false);
+        r = plan_wq_route(m, n, k, wide_ok, contract, sk64, f32x, false, Q4);
     float* planes = r.splits > 1 ? static_cast<float*>(workspace) : nullptr;
     const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k), gi = static_cast<int>(group);
     if (r.wide) return wq_wide<Q4>(x, w, sc, b, y, mi, ni, ki, gi, r.tile, planes, r.splits, r.per, s);
@@ -1112,11 +1126,12 @@ nq_status wq_gemm(const XT* x, const uint8_t* w, const ST* sc, const float* b, Y
 // Workspace the split-K planes take at this shape (0: no split): the most any
 // activation dtype or group size can plan, so one size serves every call.
 size_t wq_workspace_bytes(int64_t m, int64_t n, int64_t k) {
-    if (m <= 0 || n <= 0 || k <= 0 || !wq_gemm_shape_ok(m, n, k, 2, true)) return 0;
+    if (m <= 0 || n <= 0 || k <= 0 || !(wq_gemm_shape_ok(m, n, k, 2, true) || wq_q4_batch5_shape(m, n, k))) return 0;
     size_t most = 0;
     for (int f32x = 0; f32x < 2; ++f32x)
         for (int contract = 0; contract < 2; ++contract)
-            most = std::max(most, wq_route_bytes(plan_wq_route(m, n, k, false, contract, true, f32x, true), m, n));
+            for (int q4 = 0; q4 < 2; ++q4)
+                most = std::max(most, wq_route_bytes(plan_wq_route(m, n, k, false, contract, true, f32x, true, q4), m, n));
     return most;
 }
 

@@ -229,6 +229,9 @@ Q4_CASES = [
     (1, 999, 9216, 128, True, F16, F16, F16),   # 576 threads, group 128
     (1, 640, 7168, 96, False, F16, F32, F32),   # group 96, k % group = 64: a short last group
     (3, 500, 1568, 64, True, F32, F32, F32),    # k % group = 32: scale rows of ceil(k / group)
+    # fp16 x at m = 5..8 on n, k >= 4096: the split wide tiles (workspace) instead of the GEMV
+    (8, 4100, 4096, 64, True, F16, F32, F16),   # ragged n, fp32 scales, group 64
+    (5, 4096, 4224, 32, False, F16, F16, F32),  # 33 slabs of 128 codes
 ]
 
 
