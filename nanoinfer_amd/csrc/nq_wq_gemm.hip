@@ -1010,7 +1010,7 @@ WqRoute plan_wq_route(int64_t m, int64_t n, int64_t k, bool wide_ok, bool wide_c
     // 101.7); at m <= 64 the split keeps them (m = 16, n = 28672, k = 4096, Q4G:
     // 47.5 against 80.7).
     const bool big_split = m > 128 && plan_wq_wide(m, n, sk64_ok, f32x).tiles < (k >= 8192 ? 256 : 128);
-    if (allow_split && wide_contract && m >= (f32x ? 32 : q4 ? 5 : 9) && (m <= 128 || big_split) && k >= 2048) {
+    if (allow_split && wide_contract && m >= (f32x ? 32 : q4 || k >= 8192 ? 5 : 9) && (m <= 128 || big_split) && k >= 2048) {
         WqTile t{1, m <= 64 ? 2 : 4, f32x ? 64 : 128};
         t.shallow = true;
         const int64_t tiles = ((m + 63) / 64) * ((n + 32 * t.fn - 1) / (32 * t.fn)), nk = k / t.sk;
@@ -1056,13 +1056,23 @@ size_t wq_route_bytes(const WqRoute& r, int64_t m, int64_t n) {
 // int4 codes with fp16 x at m = 5..8 on a workspace: the split wide tiles (the
 // GEMV re-reads the activation rows per two weight rows, and the unsplit GEMM
 // converts and scales the codes per 64-row tile). us, GEMV -> split GEMM, m = 8:
-// n = 28672, k = 4096 75.2 -> 50.7; n = 37888, k = 3584 82.9 -> 49.9; n = 4096,
-// k = 14336 41.8 -> 27.0; n = 6144, k = 4096 19.9 -> 15.1; n = 4096, k = 4096
-// 13.0 -> 12.5. Kept on the GEMV: k < 4096 (n = 17920, k = 1536 22.9 against
-// 25.1), n < 4096 (n = 1536, k = 8960 12.6 against 13.5) and the 128256-row LM
-// head (280 against 296).
+// n = 28672, k = 4096 75.2 -> 50.7; n = 37888, k = 3584 86.5 -> 50.2; n = 4096,
+// k = 14336 41.8 -> 27.0; n = 3584, k = 18944 45.6 -> 29.1; n = 8960, k = 3072
+// 24.1 -> 18.6; n = 6144, k = 4096 19.9 -> 15.1; n = 4608, k = 3584 15.1 -> 12.7;
+// n = 2048, k = 8192 12.9 -> 12.0. Kept on the GEMV: weights under 14 Mi codes
+// (n = 1536, k = 8960 12.6 against 13.5; n = 2048, k = 4096 8.5 against 9.7;
+// n = 3072, k = 4096 even), k < 3072 (n = 6144, k = 2048 10.9 against 12.1) and
+// LM heads (n = 65536 even, n = 128256 280 against 296).
 bool wq_q4_batch5_shape(int64_t m, int64_t n, int64_t k) {
-    return m >= 5 && m <= 8 && k >= 4096 && k % 128 == 0 && n >= 4096 && n < 65536;
+    return m >= 5 && m <= 8 && k >= 3072 && k % 128 == 0 && n >= 2048 && n < 65536 && n * k >= (int64_t(14) << 20);
+}
+// int8 codes with fp16 x at m = 5..8 on long K (k >= 8192) from 2048 rows: the
+// split wide tiles too (us, m = 8, GEMV or unsplit GEMM -> split: n = 3584, k =
+// 18944 39.0 -> 28.6; n = 2048, k = 16384 23.0 -> 15.6; n = 2048, k = 8192 13.5
+// -> 10.8; n = 4096, k = 14336 25.0 -> 24.2; n = 1536, k = 8960 kept, 11.7
+// against 12.2; shorter K kept, n = 3584, k = 3584 9.8 against 11.0).
+bool wq_q8_batch5_shape(int64_t m, int64_t n, int64_t k) {
+    return m >= 5 && m <= 8 && k >= 8192 && k % 128 == 0 && n >= 2048;
 }
 bool wq_gemm_shape_ok(int64_t m, int64_t n, int64_t k, size_t x_elem, bool ws) {
     return m > 8 && (m >= 16 || n >= 4096 ||
@@ -1099,6 +1109,7 @@ bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m,
     const bool batch5 = m >= 5 && m <= 8 &&
                         ((!q4 && x_elem == 2 && n >= 4096 && n * k >= (int64_t(16) << 20)) ||
                          (q4 && x_elem == 2 && ws && group <= 64 && wq_q4_batch5_shape(m, n, k)) ||
+                         (!q4 && x_elem == 2 && ws && wq_q8_batch5_shape(m, n, k)) ||
                          (x_elem == 4 && ((n >= 4096 && k >= 4096) || (!q4 && k > 9216) ||
                                           (q4 && k > 18432 && n >= 3072))));
     if (!forced && !batch5 && !wq_gemm_shape_ok(m, n, k, x_elem, ws)) return false;
@@ -1126,7 +1137,8 @@ nq_status wq_gemm(const XT* x, const uint8_t* w, const ST* sc, const float* b, Y
 // Workspace the split-K planes take at this shape (0: no split): the most any
 // activation dtype or group size can plan, so one size serves every call.
 size_t wq_workspace_bytes(int64_t m, int64_t n, int64_t k) {
-    if (m <= 0 || n <= 0 || k <= 0 || !(wq_gemm_shape_ok(m, n, k, 2, true) || wq_q4_batch5_shape(m, n, k))) return 0;
+    if (m <= 0 || n <= 0 || k <= 0 || !(wq_gemm_shape_ok(m, n, k, 2, true) || wq_q4_batch5_shape(m, n, k) ||
+                                                   wq_q8_batch5_shape(m, n, k))) return 0;
     size_t most = 0;
     for (int f32x = 0; f32x < 2; ++f32x)
         for (int contract = 0; contract < 2; ++contract)

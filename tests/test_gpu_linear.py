@@ -48,6 +48,7 @@ Q8_CASES = [
     (2, 1537, 8960, True, F16, F16),      # m = 2: a workgroup per activation row, ragged n
     (2, 4864, 896, False, F32, F32),      # m = 2 pairs, fp32 x
     (2, 40000, 1536, False, F16, F16),    # m = 2, very tall: 8 rows, no pairs
+    (6, 2100, 8192, True, F16, F16),      # fp16 x, m = 5..8, long K: the split wide tiles
 ]
 
 
