@@ -475,12 +475,13 @@ __device__ __forceinline__ float dot16_q4_f16(unsigned w0, unsigned w1, const h2
 // workgroup cut the activation re-reads, which every workgroup takes from L2
 // (n = 1536, k = 8960: 2 rows with x last 4.49-4.64 us, 3 rows x first
 // 4.32-4.35; n = 8960, k = 5120: 9.03 -> 7.26 with 6 rows).
-template <int R, typename YT, typename ST>
-__global__ __launch_bounds__(kMaxGemvThreads) void gemv_q4g_x1h_half_kernel(
+// MAXT: the launch bound (576 threads, or 1024 for 9216 < k <= 16384).
+template <int R, typename YT, typename ST, int MAXT = kMaxGemvThreads>
+__global__ __launch_bounds__(MAXT) void gemv_q4g_x1h_half_kernel(
     const _Float16* __restrict__ x, const uint8_t* __restrict__ w, const ST* __restrict__ scale,
     const float* __restrict__ bias, YT* __restrict__ y, int n, int k, int group) {
     constexpr int RP = R <= 1 ? 1 : R <= 2 ? 2 : R <= 4 ? 4 : 8;  // reduced values, a power of two
-    __shared__ float red[kMaxGemvWaves * R];
+    __shared__ float red[(MAXT / kWave) * R];
     const int tid = threadIdx.x, wave = tid >> 6, nw = block_threads() >> 6;
     const int halves = k >> 4, rb = k >> 1;
     const int row0 = xcd_row_group() * R;
@@ -1439,6 +1440,21 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
                 gemv_q4g_x1h_half_kernel<6, YT, ST><<<(n + 5) / 6, th, 0, s>>>(x, w, sc, b, y, n, k, g);
             else
                 gemv_q4g_x1h_half_kernel<3, YT, ST><<<(n + 2) / 3, th, 0, s>>>(x, w, sc, b, y, n, k, g);
+            return;
+        }
+        // 9216 < k <= 16384: the same half chunks with up to 16 waves, against one
+        // whole chunk per lane over 2 rows (us: n = 4096, k = 14336 10.6 -> 9.6; n
+        // = 4096, k = 11008 9.1 -> 7.9; n = 5120, k = 13824 12.3 -> 11.5; n = 2048,
+        // k = 12288 6.2 -> 6.0; n = 8192, k = 14336 18.2 -> 16.4-16.8 with 6 rows;
+        // n = 14336, k = 12288 24.2 -> 20.3-22.9; 4 rows on n >= 8192 17.0 / 21.9-22.8,
+        // 2 rows lost everywhere).
+        if (th > kMaxGemvThreads && th <= 1024) {
+            if (n >= 8192)
+                gemv_q4g_x1h_half_kernel<6, YT, ST, 1024><<<(n + 5) / 6, th, 0, s>>>(x, w, sc, b, y, n, k, g);
+            else if (n >= 4096)
+                gemv_q4g_x1h_half_kernel<4, YT, ST, 1024><<<(n + 3) / 4, th, 0, s>>>(x, w, sc, b, y, n, k, g);
+            else
+                gemv_q4g_x1h_half_kernel<3, YT, ST, 1024><<<(n + 2) / 3, th, 0, s>>>(x, w, sc, b, y, n, k, g);
             return;
         }
     }
