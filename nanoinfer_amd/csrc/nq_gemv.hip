@@ -32,7 +32,11 @@ namespace {
 
 constexpr int kMaxGemvWaves = 9;          // 576 lanes: int8 k <= 9216, int4 k <= 18432
 constexpr int kMaxGemvThreads = kMaxGemvWaves * kWave;
-constexpr int kLongKThreads = 256;     // the long-K kernels' workgroup (several chunks per lane)
+// The long-K kernels' workgroups (several chunks per lane): int8 weight-only
+// 256 lanes; int4 and W8A8 512 (m = 1, us, 256 -> 512 lanes: int4 n = 3584, k =
+// 18944 11.5 -> 10.7, n = 4096, k = 28672 16.6 -> 15.8; W8A8 n = 3584, k = 18944
+// 18.6 -> 18.0; int8 lost: n = 4096, k = 14336 12.8 -> 13.1, m = 4 3-7%).
+constexpr int kLongKThreads = 256, kLongKThreadsWide = 512;
 
 // Rows per workgroup as a function of the activation-row count: more rows =
 // more reuse of each loaded activation chunk, fewer = more workgroups.
@@ -905,9 +909,10 @@ __global__ __launch_bounds__(kDecThreads) void w8a8_decode_kernel(const XT* __re
 // The kernels above give each lane one 16-byte weight chunk of a row, so a
 // 576-lane workgroup covers int8 k <= 9216 and int4 k <= 18432. Longer rows
 // (Llama-3-8B's down projection, k = 14336; Qwen2.5-7B's, k = 18944) take these:
-// 256 lanes stride K one chunk at a time, R weight rows per workgroup (their R
-// loads in flight per lane, several workgroups per CU), the same per-chunk dot
-// products as the one-chunk kernels and the same cross-wave reduction.
+// 256 (int8) or 512 (int4, W8A8) lanes stride K one chunk at a time, R weight
+// rows per workgroup (their R loads in flight per lane, several workgroups per
+// CU), the same per-chunk dot products as the one-chunk kernels and the same
+// cross-wave reduction.
 
 template <int R, int M, typename XT, typename YT>
 __global__ __launch_bounds__(kLongKThreads) void gemv_q8_longk_kernel(
@@ -963,10 +968,10 @@ __global__ __launch_bounds__(kLongKThreads) void gemv_q8_longk_kernel(
 
 // group: a multiple of 32 (each chunk's 32 codes share one scale).
 template <int R, int M, typename XT, typename YT, typename ST>
-__global__ __launch_bounds__(kLongKThreads) void gemv_q4g_longk_kernel(
+__global__ __launch_bounds__(kLongKThreadsWide) void gemv_q4g_longk_kernel(
     const XT* __restrict__ x, const uint8_t* __restrict__ w, const ST* __restrict__ scale,
     const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int group) {
-    __shared__ float red[(kLongKThreads / kWave) * R * M];
+    __shared__ float red[(kLongKThreadsWide / kWave) * R * M];
     const int tid = threadIdx.x, wave = tid >> 6;
     const int chunks = k >> 5, rb = k >> 1, row0 = xcd_row_group() * R;
     const int blocks = (k + group - 1) / group;
@@ -978,7 +983,7 @@ __global__ __launch_bounds__(kLongKThreads) void gemv_q4g_longk_kernel(
 #pragma unroll
         for (int i = 0; i < M; ++i) acc[r][i] = 0.0f;
 #pragma unroll 1
-    for (int c = tid; c < chunks; c += kLongKThreads) {
+    for (int c = tid; c < chunks; c += kLongKThreadsWide) {
         v4i wv[R];
         float sc[R];
         const int blk = (c * 32) / group;
@@ -1031,7 +1036,7 @@ __global__ __launch_bounds__(kLongKThreads) void gemv_q4g_longk_kernel(
         if (row < n && i < m) {
             float s = 0.0f;
 #pragma unroll
-            for (int q = 0; q < kLongKThreads / kWave; ++q) s += red[(q * R + r) * M + i];
+            for (int q = 0; q < kLongKThreadsWide / kWave; ++q) s += red[(q * R + r) * M + i];
             y[static_cast<size_t>(i) * n + row] = from_f32<YT>(s + (bias ? bias[row] : 0.0f));
         }
     }
@@ -1039,11 +1044,11 @@ __global__ __launch_bounds__(kLongKThreads) void gemv_q4g_longk_kernel(
 
 // int8 activation codes: exact int32 sums (equal to every other W8A8 path).
 template <int R, int M, typename YT, bool ACC_OUT>
-__global__ __launch_bounds__(kLongKThreads) void gemv_w8a8_longk_kernel(
+__global__ __launch_bounds__(kLongKThreadsWide) void gemv_w8a8_longk_kernel(
     const int8_t* __restrict__ xq, const float* __restrict__ as, const int8_t* __restrict__ w,
     const float* __restrict__ ws, const float* __restrict__ bias, YT* __restrict__ y,
     int32_t* __restrict__ acc_out, int m, int n, int k) {
-    __shared__ int red[(kLongKThreads / kWave) * R * M];
+    __shared__ int red[(kLongKThreadsWide / kWave) * R * M];
     const int tid = threadIdx.x, wave = tid >> 6;
     const int chunks = k >> 4, row0 = xcd_row_group() * R;
     int acc[R][M];
@@ -1052,7 +1057,7 @@ __global__ __launch_bounds__(kLongKThreads) void gemv_w8a8_longk_kernel(
 #pragma unroll
         for (int i = 0; i < M; ++i) acc[r][i] = 0;
 #pragma unroll 1
-    for (int c = tid; c < chunks; c += kLongKThreads) {
+    for (int c = tid; c < chunks; c += kLongKThreadsWide) {
         v4i wv[R], xv[M];
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -1078,7 +1083,7 @@ __global__ __launch_bounds__(kLongKThreads) void gemv_w8a8_longk_kernel(
         if (row < n && i < m) {
             int s = 0;
 #pragma unroll
-            for (int q = 0; q < kLongKThreads / kWave; ++q) s += red[(q * R + r) * M + i];
+            for (int q = 0; q < kLongKThreadsWide / kWave; ++q) s += red[(q * R + r) * M + i];
             if constexpr (ACC_OUT) {
                 acc_out[static_cast<size_t>(i) * n + row] = s;
             } else {
@@ -1555,11 +1560,11 @@ void dispatch_q4g_longk(const XT* x, const uint8_t* w, const ST* sc, const float
                         int group, hipStream_t s) {
     auto go = [&](auto mt) {
         constexpr int M = decltype(mt)::value, R = M <= 2 ? 4 : 2;
-        gemv_q4g_longk_kernel<R, M, XT, YT, ST><<<(n + R - 1) / R, kLongKThreads, 0, s>>>(x, w, sc, b, y, m, n, k,
+        gemv_q4g_longk_kernel<R, M, XT, YT, ST><<<(n + R - 1) / R, kLongKThreadsWide, 0, s>>>(x, w, sc, b, y, m, n, k,
                                                                                           group);
     };
     if (m == 1 && n >= 8192) {
-        gemv_q4g_longk_kernel<8, 1, XT, YT, ST><<<(n + 7) / 8, kLongKThreads, 0, s>>>(x, w, sc, b, y, m, n, k, group);
+        gemv_q4g_longk_kernel<8, 1, XT, YT, ST><<<(n + 7) / 8, kLongKThreadsWide, 0, s>>>(x, w, sc, b, y, m, n, k, group);
         return;
     }
     switch (m_bucket(m)) {
@@ -1598,13 +1603,13 @@ nq_status gemv_w8a8_launch(const int8_t* xq, const float* as, const int8_t* w, c
             constexpr int M = decltype(mt)::value, R = M <= 2 ? 4 : 2;
             const unsigned grid = static_cast<unsigned>((n + R - 1) / R);
             if (acc_out)
-                gemv_w8a8_longk_kernel<R, M, float, true><<<grid, kLongKThreads, 0, s>>>(xq, as, w, ws, bias, nullptr,
+                gemv_w8a8_longk_kernel<R, M, float, true><<<grid, kLongKThreadsWide, 0, s>>>(xq, as, w, ws, bias, nullptr,
                                                                                          acc_out, mi, ni, ki);
             else if (ydt == NQ_F32)
-                gemv_w8a8_longk_kernel<R, M, float, false><<<grid, kLongKThreads, 0, s>>>(
+                gemv_w8a8_longk_kernel<R, M, float, false><<<grid, kLongKThreadsWide, 0, s>>>(
                     xq, as, w, ws, bias, static_cast<float*>(y), nullptr, mi, ni, ki);
             else
-                gemv_w8a8_longk_kernel<R, M, _Float16, false><<<grid, kLongKThreads, 0, s>>>(
+                gemv_w8a8_longk_kernel<R, M, _Float16, false><<<grid, kLongKThreadsWide, 0, s>>>(
                     xq, as, w, ws, bias, static_cast<_Float16*>(y), nullptr, mi, ni, ki);
         };
         switch (m_bucket(m)) {
