@@ -1533,7 +1533,10 @@ void dispatch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, Y
 }
 
 // Long-K launches (one m bucket of up to 8 activation rows each): 4 weight rows
-// per workgroup for one or two activation rows, 2 for more; one activation row
+// per workgroup for up to four activation rows, 2 for more (m = 3..4 with 2 rows
+// re-read the activation twice as often: n = 8192, k = 28672 int8 86.5 -> 64.8
+// us with 4 rows; n = 4096, k = 14336 int8 22.9 -> 19.8, W8A8 20.6 -> 17.6; n =
+// 4096, k = 28672 int4 40.5 -> 37.8); one activation row
 // on 8192 weight rows or more takes 8 (half the activation re-reads: n = 8192,
 // k = 28672 int8 42.8 -> 39.9 us, int4 27.5 -> 26.2; n = 14336, k = 10240 27.5 ->
 // 26.1; n = 1536, k = 20480 lost 10.5 -> 11.3).
@@ -1541,7 +1544,7 @@ template <typename XT, typename YT>
 void dispatch_q8_longk(const XT* x, const int8_t* w, const float* ws, const float* b, YT* y, int m, int n, int k,
                        hipStream_t s) {
     auto go = [&](auto mt) {
-        constexpr int M = decltype(mt)::value, R = M <= 2 ? 4 : 2;
+        constexpr int M = decltype(mt)::value, R = M <= 4 ? 4 : 2;
         gemv_q8_longk_kernel<R, M, XT, YT><<<(n + R - 1) / R, kLongKThreads, 0, s>>>(x, w, ws, b, y, m, n, k);
     };
     if (m == 1 && n >= 8192) {
@@ -1559,7 +1562,7 @@ template <typename XT, typename YT, typename ST>
 void dispatch_q4g_longk(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT* y, int m, int n, int k,
                         int group, hipStream_t s) {
     auto go = [&](auto mt) {
-        constexpr int M = decltype(mt)::value, R = M <= 2 ? 4 : 2;
+        constexpr int M = decltype(mt)::value, R = M <= 4 ? 4 : 2;
         gemv_q4g_longk_kernel<R, M, XT, YT, ST><<<(n + R - 1) / R, kLongKThreadsWide, 0, s>>>(x, w, sc, b, y, m, n, k,
                                                                                           group);
     };
@@ -1600,7 +1603,7 @@ nq_status gemv_w8a8_launch(const int8_t* xq, const float* as, const int8_t* w, c
                         aligned(w, 16);
     if (long_k) {
         auto go = [&](auto mt) {
-            constexpr int M = decltype(mt)::value, R = M <= 2 ? 4 : 2;
+            constexpr int M = decltype(mt)::value, R = M <= 4 ? 4 : 2;
             const unsigned grid = static_cast<unsigned>((n + R - 1) / R);
             if (acc_out)
                 gemv_w8a8_longk_kernel<R, M, float, true><<<grid, kLongKThreadsWide, 0, s>>>(xq, as, w, ws, bias, nullptr,
