@@ -1368,6 +1368,17 @@ void launch_q8(const XT* x, const int8_t* w, const float* ws, const float* b, YT
     // fp16 activations the same way on short K (m = 8: n = 8960, k = 1536 11.28 ->
     // 10.83; n = 4864, k = 896, m = 6 5.23 -> 5.05; n = 1536, k = 8960 lost 11.40 ->
     // 12.50).
+    // fp16 activations at m = 3..4 on wide weights: 4 weight rows per workgroup
+    // (half the activation re-reads; us, 2 -> 4 rows, m = 4: n = 28672, k = 4096
+    // 40.0 -> 32.6; n = 6144, k = 4096 11.4 -> 10.6; n = 17920, k = 1536 even;
+    // narrower or longer-K weights lost: n = 1536, k = 8960 7.9 -> 9.7; n = 4608,
+    // k = 3584 8.6 -> 8.8).
+    if constexpr (M == 4 && !AM && sizeof(XT) == 2) {
+        if (n >= 6144 && k <= 8192) {
+            gemv_q8_kernel<4, 4, XT, YT><<<(n + 3) / 4, threads, 0, s>>>(x, w, ws, b, y, m, n, k, part, ctl);
+            return;
+        }
+    }
     if constexpr (M == 8 && !AM && sizeof(XT) == 2) {
         if (k < 4096) {
             gemv_q8_kernel<4, 4, XT, YT, false, 2><<<(n + 3) / 4 * 2, threads, 0, s>>>(x, w, ws, b, y, m, n, k,
@@ -1486,6 +1497,17 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
                     return;
                 }
             } else {
+                // m = 3..4 on wide, short-K weights: 4 weight rows per workgroup pair
+                // (us, m = 4: n = 28672, k = 4096 38.0 -> 35.0; n = 17920, k = 1536
+                // 13.5 -> 12.6; n = 3584, k = 3584 7.8 -> 7.5; lost on n = 1536, k =
+                // 8960 9.7 -> 11.3 and n = 4096, k = 14336 26.7 -> 29.1).
+                if constexpr (M == 4) {
+                    if (n >= 3584 && k <= 4096) {
+                        gemv_q4g_kernel<4, MH, XT, YT, ST, kMaxGemvThreads, 2><<<(n + 3) / 4 * 2, threads, 0, s>>>(
+                            x, w, sc, b, y, m, n, k, g);
+                        return;
+                    }
+                }
                 gemv_q4g_kernel<R, MH, XT, YT, ST, kMaxGemvThreads, 2><<<(n + R - 1) / R * 2, threads, 0, s>>>(
                     x, w, sc, b, y, m, n, k, g);
                 return;
