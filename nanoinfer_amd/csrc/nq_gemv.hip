@@ -1530,6 +1530,21 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
             // 128256, k = 4096 64.5 / 54.5 / 52.7; n = 152064, k = 3584 66.2 /
             // 58.2 / 54.7; n = 37888, k = 3584 18.1 / 16.0 / 16.6; n = 28672 14.8 /
             // 13.7 / 14.4; n = 6144 5.7 / 6.0 / 6.6 (fewer workgroups lose below).
+            // fp32 x (128 bytes of x per 16 bytes of codes): 4 rows from 4096 rows or
+            // k = 4096, 8 from 24576 rows (us, 2 -> 4 rows: n = 4096, k = 14336 22.8 ->
+            // 14.8; n = 17920, k = 1536 11.0 -> 8.6; n = 6144, k = 4096 9.5 -> 8.4; n =
+            // 1536, k = 8960 7.5 -> 7.3; n = 28672, k = 4096 23.3 -> 20.6 with 8 rows;
+            // n = k = 1536 lost 3.5 -> 3.8).
+            if constexpr (sizeof(XT) == 4) {
+                if (n >= 24576) {
+                    gemv_q4g_kernel<8, 1, XT, YT, ST><<<(n + 7) / 8, threads, 0, s>>>(x, w, sc, b, y, m, n, k, g);
+                    return;
+                }
+                if (n >= 4096 || k >= 4096) {
+                    gemv_q4g_kernel<4, 1, XT, YT, ST><<<(n + 3) / 4, threads, 0, s>>>(x, w, sc, b, y, m, n, k, g);
+                    return;
+                }
+            }
             if (n >= 65536) {
                 gemv_q4g_kernel<8, 1, XT, YT, ST><<<(n + 7) / 8, threads, 0, s>>>(x, w, sc, b, y, m, n, k, g);
                 return;
