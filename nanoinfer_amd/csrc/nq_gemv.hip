@@ -1496,6 +1496,17 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
                                                                                                  k, g);
                     return;
                 }
+                // Past k = 10240 the same 4 rows on the 576-thread bound for up to two
+                // activation rows per workgroup (143 VGPRs, no spills; us, 2 -> 4 rows:
+                // m = 2, n = 4096, k = 14336 36.4 -> 26.1; m = 4 64.2 -> 44.6; n = 8192,
+                // k = 11008 103.7 -> 75.4; n = 1536, k = 12288 23.3 -> 16.9).
+                if constexpr (MH <= 2) {
+                    if (threads > 320 && n >= 1024) {
+                        gemv_q4g_kernel<4, MH, XT, YT, ST, kMaxGemvThreads, 2><<<(n + 3) / 4 * 2, threads, 0, s>>>(
+                            x, w, sc, b, y, m, n, k, g);
+                        return;
+                    }
+                }
             } else {
                 // m = 3..4 on wide, short-K weights: 4 weight rows per workgroup pair
                 // (us, m = 4: n = 28672, k = 4096 38.0 -> 35.0; n = 17920, k = 1536

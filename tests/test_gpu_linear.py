@@ -219,6 +219,8 @@ Q4_CASES = [
     (1, 1536, 8960, 32, True, F32, F32, F32),   # fp32 x, m = 1, k >= 4096: 4 rows, unsigned group math
     (1, 1000, 2048, 64, False, F32, F16, F16),  # fp32 x, m = 1, small: 2 rows
     (1, 24600, 1024, 32, True, F32, F16, F32),  # fp32 x, m = 1, tall: 8 rows
+    (4, 1100, 12288, 32, True, F32, F16, F32),  # fp32 x, m = 3..4, k > 10240: pairs of 4-row workgroups
+    (2, 1030, 14336, 64, False, F32, F32, F16), # fp32 x, m = 2, k > 10240: the same
     (3, 1536, 8960, 32, True, F16, F16, F16),   # m = 3..4: workgroup pairs over activation rows
     (4, 4867, 896, 32, False, F16, F32, F32),   # pairs, ragged n
     (3, 2048, 1536, 64, True, F32, F32, F16),   # fp32 x pairs, 4 rows, 320-thread bound

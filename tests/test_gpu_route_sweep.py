@@ -136,6 +136,8 @@ WQ_SHAPES = [  # (m, n, k): GEMV buckets, row-group rules, GEMM tile plans, spli
     (1, 1000, 11008), (1, 4100, 12288), (1, 8200, 10240),
     # m = 3..4 fp16 on wide weights: 4 weight rows per workgroup (int8 n >= 6144, int4 n >= 3584, k <= 4096)
     (3, 6200, 2048), (4, 3600, 1536),
+    # fp32 x at m = 2..4 past k = 10240: pairs of 4-row workgroups on the 576-thread bound
+    (2, 1100, 12288), (4, 1100, 12288),
     (1, 1536, 1536), (1, 4864, 896), (1, 1536, 8960), (1, 8960, 5120), (1, 40000, 1536), (1, 1024, 4096),
     (2, 1536, 8960), (2, 4864, 896), (2, 40000, 1536), (2, 256, 1536), (2, 8960, 1536),
     (3, 1536, 2048), (4, 4864, 896), (4, 1536, 8960), (4, 256, 1536),
