@@ -153,13 +153,14 @@ __device__ __forceinline__ int xcd_row_group() {
 // XS > 1: XS workgroups per row group, each taking M of the activation rows
 // (neighbouring indices of xcd_row_group, so the XS readers of a weight row
 // group run together on one XCD and share its L2).
-template <int R, int M, typename XT, typename YT, bool AM = false, int XS = 1>
-__global__ __launch_bounds__(kMaxGemvThreads) void gemv_q8_kernel(
+// MAXT: the launch bound (576 threads, or 1024 for one fp16 row on 9216 < k <= 12288).
+template <int R, int M, typename XT, typename YT, bool AM = false, int XS = 1, int MAXT = kMaxGemvThreads>
+__global__ __launch_bounds__(MAXT) void gemv_q8_kernel(
     const XT* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ ws,
     const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, ArgPart* __restrict__ part,
     ArgCtl* __restrict__ ctl) {
     static_assert(XS == 1 || !AM, "activation slices write y");
-    __shared__ float red[kMaxGemvWaves * R * M];
+    __shared__ float red[(MAXT / kWave) * R * M];
     const int tid = threadIdx.x, wave = tid >> 6, nw = block_threads() >> 6;
     const int chunks = k >> 4;
     const bool act = tid < chunks;
@@ -1595,6 +1596,19 @@ void dispatch_q8_longk(const XT* x, const int8_t* w, const float* ws, const floa
         constexpr int M = decltype(mt)::value, R = M <= 4 ? 4 : 2;
         gemv_q8_longk_kernel<R, M, XT, YT><<<(n + R - 1) / R, kLongKThreads, 0, s>>>(x, w, ws, b, y, m, n, k);
     };
+    // One fp16 row up to k = 12288: one 16-byte chunk per lane over up to 16 waves,
+    // 4 rows per workgroup (us, long-K kernel -> this: n = 4096, k = 11008 11.9 ->
+    // 10.0; n = 2048, k = 12288 8.0 -> 6.8; n = 1536, k = 10240 6.8 -> 5.9; n =
+    // 14336, k = 12288 29.8 -> 28.2; k = 14336 and fp32 x lost: 12.2 -> 12.6, 14.1 ->
+    // 14.7).
+    if constexpr (sizeof(XT) == 2) {
+        if (m == 1 && k <= 12288) {
+            const int th = ((k / 16 + kWave - 1) / kWave) * kWave;
+            gemv_q8_kernel<4, 1, XT, YT, false, 1, 1024><<<(n + 3) / 4, th, 0, s>>>(x, w, ws, b, y, m, n, k, nullptr,
+                                                                                    nullptr);
+            return;
+        }
+    }
     if (m == 1 && n >= 8192) {
         gemv_q8_longk_kernel<8, 1, XT, YT><<<(n + 7) / 8, kLongKThreads, 0, s>>>(x, w, ws, b, y, m, n, k);
         return;

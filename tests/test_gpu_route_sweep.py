@@ -138,6 +138,8 @@ WQ_SHAPES = [  # (m, n, k): GEMV buckets, row-group rules, GEMM tile plans, spli
     (3, 6200, 2048), (4, 3600, 1536),
     # fp32 x at m = 2..4 past k = 10240: pairs of 4-row workgroups on the 576-thread bound
     (2, 1100, 12288), (4, 1100, 12288),
+    # one fp16 row, int8, 9216 < k <= 12288: one chunk per lane over up to 16 waves, 4 rows
+    (1, 1030, 11008),
     (1, 1536, 1536), (1, 4864, 896), (1, 1536, 8960), (1, 8960, 5120), (1, 40000, 1536), (1, 1024, 4096),
     (2, 1536, 8960), (2, 4864, 896), (2, 40000, 1536), (2, 256, 1536), (2, 8960, 1536),
     (3, 1536, 2048), (4, 4864, 896), (4, 1536, 8960), (4, 256, 1536),
