@@ -1048,11 +1048,14 @@ WqRoute plan_wq_route(int64_t m, int64_t n, int64_t k, bool wide_ok, bool wide_c
 size_t wq_route_bytes(const WqRoute& r, int64_t m, int64_t n) {
     return r.splits > 1 ? round_up(static_cast<size_t>(r.splits) * static_cast<size_t>(m) * static_cast<size_t>(n) * 4, 256) : 0;
 }
-// m = 9..15 with a short weight runs GEMV slices, unless a workspace lets fp16
-// activations take the split wide tiles: k >= 4096 and at least 6 Mi codes
-// (us, slices -> split, m = 9 / 12 / 15: n = 1536, k = 8960 16.0 / 18.7 / 22.0 ->
-// 13.3 / 13.1 / 13.2; n = 2048, k = 8192 18.5 / 20.5 / 24.4 -> 12.3 / 12.3 /
-// 12.5; the smaller n = 896, k = 4864 lost at m = 9: 8.7 -> 10.4).
+// m = 9..15 runs the GEMM from 1536 weight rows or on k <= 1024 (us, GEMV slices
+// -> GEMM, m = 9 / 15, fp16 x: n = 3584, k = 3584 Q8 14.2 / 19.2 -> 8.9 / 10.0,
+// Q4G 16.5 / 24.8 -> 11.6 / 12.4; n = k = 1536 Q8 7.2 / 8.5 -> 5.4 / 5.9; n = k =
+// 896 Q4G 6.7 / 8.1 -> 4.9 / 5.1; fp32 x, n = 1536, k = 8960 Q8 19.5 / 28.2 -> 15.9
+// / 17.7, Q4G 29.0 / 43.6 -> 18.7 / 20.6), and on narrower weights when a
+// workspace lets fp16 activations take the split wide tiles: k >= 4096 and at
+// least 6 Mi codes. GEMV slices stay on the rest (n = 896, k = 4864, fp16 x Q8
+// 9.1 against 10.6, fp32 x 9.2 against 14.6; n = 256, k = 1536 5.7 against 6.5).
 // int4 codes with fp16 x at m = 5..8 on a workspace: the split wide tiles (the
 // GEMV re-reads the activation rows per two weight rows, and the unsplit GEMM
 // converts and scales the codes per 64-row tile). us, GEMV -> split GEMM, m = 8:
@@ -1075,7 +1078,7 @@ bool wq_q8_batch5_shape(int64_t m, int64_t n, int64_t k) {
     return m >= 5 && m <= 8 && k >= 8192 && k % 128 == 0 && n >= 2048;
 }
 bool wq_gemm_shape_ok(int64_t m, int64_t n, int64_t k, size_t x_elem, bool ws) {
-    return m > 8 && (m >= 16 || n >= 4096 ||
+    return m > 8 && (m >= 16 || n >= 1536 || k <= 1024 ||
                      (ws && x_elem == 2 && k >= 4096 && k % 128 == 0 && n * k >= (int64_t(6) << 20)));
 }
 }  // namespace
@@ -1087,9 +1090,8 @@ bool wq_gemm_shape_ok(int64_t m, int64_t n, int64_t k, size_t x_elem, bool ws) {
 bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m, int64_t n, int64_t k,
                 int64_t group, bool ws, bool forced) {
     const int64_t rowb = q4 ? k / 2 : k;
-    // Shape rule (measured): the GEMM runs one workgroup per 16 (or 32) weight
-    // rows, each reading all of x, so below 4096 rows it fills under 256 CUs; a
-    // GEMV slice of 8 rows plus a remainder slice is then faster up to m = 15.
+    // Shape rule (measured, wq_gemm_shape_ok): up to m = 15 a narrow weight with
+    // long rows keeps GEMV slices of 8 rows plus a remainder slice.
     // int8 codes with fp16 x at m = 5..8 on large weights: the GEMV's per-row
     // FMAs make it VALU-bound there (m = 8, fp16 x, us, GEMV -> GEMM: n = 28672,
     // k = 4096 69.3 -> 46.0; n = 128256, k = 4096 279.5 -> 174.2; n = 4096, k =

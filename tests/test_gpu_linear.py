@@ -253,7 +253,9 @@ def test_linear_q4g(dev, nq, orc, m, n, k, g, bias, xdt, sdt, ydt):
 
 
 WQ_GEMM_CASES = [  # m > 8: the fp16 MFMA GEMM (m >= 16 or n >= 4096) or GEMV slices
-    ("q8", 9, 896, 896, 0, True, F16, F16, F16),       # GEMV slices 8 + 1
+    ("q8", 9, 896, 896, 0, True, F16, F16, F16),       # k <= 1024: the GEMM
+    ("q8", 9, 896, 4864, 0, True, F16, F16, F16),      # narrow, long rows: GEMV slices 8 + 1
+    ("q4g", 13, 1600, 2048, 32, False, F32, F32, F16),  # m = 9..15 from 1536 rows: the GEMM
     ("q8", 9, 4608, 896, 0, True, F16, F16, F16),      # GEMM, tall weight
     ("q4g", 12, 4104, 512, 32, False, F32, F16, F32),  # GEMM, ragged last tile
     ("q8", 64, 4864, 896, 0, False, F32, F32, F32),    # fp32 x: exact three-part bf16 split
