@@ -545,6 +545,80 @@ __global__ __launch_bounds__(MAXT) void gemv_q4g_x1h_half_kernel(
     }
 }
 
+// Exact int4 x fp32 dot over half a chunk (16 codes), as dot32_q4_f32.
+__device__ __forceinline__ float dot16_q4_f32(unsigned w0, unsigned w1, const XChunk<float>& xc) {
+    float p = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+        const unsigned wd = d ? w1 : w0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            p = __builtin_fmaf(xc.at(8 * d + e), static_cast<float>(static_cast<int>((wd >> (4 * e)) & 15u) - 8), p);
+    }
+    return p;
+}
+// Short rows (k <= 1024), one wave per workgroup: half a chunk per lane (8
+// bytes of codes, 16 codes) as the one-row kernel above, so a row of k = 896
+// occupies 56 lanes instead of 28 and each lane's activation vectors (16
+// elements per activation row) serve R rows of 16 codes, the int8 GEMV's ratio
+// at half its code bytes. The lanes holding the row totals after the exchange
+// store them (no LDS, no barrier).
+template <int R, int M, typename XT, typename YT, typename ST>
+__global__ __launch_bounds__(kWave) void gemv_q4g_short_kernel(
+    const XT* __restrict__ x, const uint8_t* __restrict__ w, const ST* __restrict__ scale,
+    const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int group) {
+    const int lane = threadIdx.x;
+    const int halves = k >> 4, rb = k >> 1;
+    const int row0 = xcd_row_group() * R;
+    const bool act = lane < halves;
+    const int hc = act ? lane : 0;  // K columns 16 hc .. 16 hc + 15
+    XChunk<XT> xc[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) xc[i].load(x + static_cast<size_t>(min(i, m - 1)) * k + hc * 16);
+    __builtin_amdgcn_sched_barrier(0);  // the activation requests go out first
+    typedef int v2i_t __attribute__((ext_vector_type(2)));
+    const unsigned ug = static_cast<unsigned>(group);
+    const unsigned blocks = (static_cast<unsigned>(k) + ug - 1) / ug;
+    const unsigned blk = static_cast<unsigned>(hc * 16) / ug;
+    v2i_t wv[R];
+    ST sraw[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const size_t row = static_cast<size_t>(min(row0 + r, n - 1));
+        sraw[r] = scale[row * blocks + blk];
+        wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v2i_t*>(w + row * rb + hc * 8));
+        __builtin_amdgcn_sched_barrier(0);  // rows in order: row r's dot waits only for rows <= r
+    }
+    float acc[R][M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        if constexpr (sizeof(XT) == 2) {
+            h2 pairs[8];
+#pragma unroll
+            for (int d = 0; d < 2; ++d)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) pairs[4 * d + j] = h2{xc[i].v[d][j], xc[i].v[d][j + 4]};
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                acc[r][i] = dot16_q4_f16(static_cast<unsigned>(wv[r][0]), static_cast<unsigned>(wv[r][1]), pairs) *
+                            to_f32(sraw[r]);
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                acc[r][i] = dot16_q4_f32(static_cast<unsigned>(wv[r][0]), static_cast<unsigned>(wv[r][1]), xc[i]) *
+                            to_f32(sraw[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r][i] = act ? acc[r][i] : 0.0f;
+    }
+    constexpr int G = 64 / (R * M);
+    const float v = wave_reduce_rows<R, M, (R * M >= 16)>(acc, lane);
+    if (lane % G == 0) {
+        const int j = lane / G, r = j / M, i = j % M, row = row0 + r;
+        if (row < n && i < m) y[static_cast<size_t>(i) * n + row] = from_f32<YT>(v + (bias ? bias[row] : 0.0f));
+    }
+}
+
 // ---- W8A8 (int8 x int8 -> int32) ------------------------------------------------------
 // ACC_OUT: write the raw int32 accumulators instead of the scaled output.
 template <int R, int M, typename YT, bool ACC_OUT>
@@ -1460,6 +1534,28 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
     constexpr int R = 2;
     const int chunks = k >> 5;
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
+    // Short rows: half a chunk per lane in one wave, 2 weight rows per workgroup,
+    // 4 on tall weights (us, old -> new, m = 1 / 2 / 4 / 8, fp16 x: n = 4864, k =
+    // 896 3.66 -> 3.30 / 4.52 -> 3.79 / 5.87 -> 4.75 / 8.78 -> 7.50; n = 9728
+    // 4.39 -> 3.79 (4 rows) / 5.69 -> 4.67 / 8.03 -> 6.18 / 13.9 -> 10.1; fp32
+    // x: n = 4864 4.63 -> 3.56 / 5.53 -> 3.97 / 6.99 -> 4.87 / 9.87 -> 7.68; n =
+    // 9728 5.94 -> 4.22 / 7.12 -> 4.83 / 10.6 -> 6.42 / 17.1 -> 12.2). The
+    // one-chunk kernel left half of each wave idle there (28 of 64 lanes at k =
+    // 896) and re-read 32 activation elements per 16 bytes of codes.
+    if (k <= 1024) {
+        constexpr bool f32x = sizeof(XT) == 4;
+        const bool four = M == 8 ? false
+                          : M == 1 ? n >= 8192
+                          : M == 2 ? n >= (f32x ? 4096 : 8192)
+                                   : f32x && n >= 4096;
+        if (four) {
+            if constexpr (M <= 2 || (M == 4 && f32x))
+                gemv_q4g_short_kernel<4, M, XT, YT, ST><<<(n + 3) / 4, kWave, 0, s>>>(x, w, sc, b, y, m, n, k, g);
+        } else {
+            gemv_q4g_short_kernel<2, M, XT, YT, ST><<<(n + 1) / 2, kWave, 0, s>>>(x, w, sc, b, y, m, n, k, g);
+        }
+        return;
+    }
     // One fp16 activation row on long K: half a chunk per lane, twice the waves
     // (k = 8960, n = 1536: 4.67-4.69 -> 4.52-4.55 us with 2 rows; one row 5.85,
     // 2 or 3 whole chunks per lane 5.6-5.8), 3 rows per workgroup with the
@@ -1544,7 +1640,7 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
     if constexpr (M == 4 && sizeof(XT) == 2) {
         return;  // the pairs above took every m = 3..4 launch
     } else {
-        if constexpr (M >= 2 && M != 4 && sizeof(XT) == 4) {  // (M = 4 pairs on this condition above)
+        if constexpr (M == 2 && sizeof(XT) == 4) {  // (M = 4 and 8 pair on this condition above)
             if (threads <= 320 && n >= 1024) {  // 256+ workgroups (n = 256, m = 5: 5.66 -> 6.76 us with 4 rows)
                 gemv_q4g_kernel<4, M, XT, YT, ST, 320><<<(n + 3) / 4, threads, 0, s>>>(x, w, sc, b, y, m, n, k, g);
                 return;

@@ -215,6 +215,11 @@ Q4_CASES = [
     (6, 1001, 4096, 64, True, F32, F32, F16),   # fp32 x, 4 rows, ragged n
     (4, 4864, 896, 128, False, F32, F32, F32),  # fp32 x, m = 3..4: 4 rows
     (7, 300, 12288, 32, True, F32, F16, F32),   # fp32 x, k > 10240: 2 rows, 576 threads
+    # short rows (k <= 1024): half chunks in one wave; k % group != 0, ragged n, 4 rows on tall weights
+    (1, 301, 992, 64, True, F16, F16, F16),
+    (2, 9000, 1024, 256, False, F32, F32, F32),
+    (4, 517, 96, 32, True, F32, F16, F16),
+    (8, 4864, 896, 128, False, F16, F16, F32),
     (2, 8960, 1536, 32, False, F32, F16, F16),  # fp32 x, m = 2: 4 rows
     (1, 1536, 8960, 32, True, F32, F32, F32),   # fp32 x, m = 1, k >= 4096: 4 rows, unsigned group math
     (1, 1000, 2048, 64, False, F32, F16, F16),  # fp32 x, m = 1, small: 2 rows

@@ -140,6 +140,8 @@ WQ_SHAPES = [  # (m, n, k): GEMV buckets, row-group rules, GEMM tile plans, spli
     (2, 1100, 12288), (4, 1100, 12288),
     # one fp16 row, int8, 9216 < k <= 12288: one chunk per lane over up to 16 waves, 4 rows
     (1, 1030, 11008),
+    # int4 short rows (k <= 1024): half chunks in one wave, 2 or 4 weight rows
+    (1, 8300, 640), (2, 1100, 1024), (2, 8200, 512), (3, 2000, 768), (8, 9000, 640),
     (1, 1536, 1536), (1, 4864, 896), (1, 1536, 8960), (1, 8960, 5120), (1, 40000, 1536), (1, 1024, 4096),
     (2, 1536, 8960), (2, 4864, 896), (2, 40000, 1536), (2, 256, 1536), (2, 8960, 1536),
     (3, 1536, 2048), (4, 4864, 896), (4, 1536, 8960), (4, 256, 1536),
@@ -157,7 +159,7 @@ WQ_SHAPES = [  # (m, n, k): GEMV buckets, row-group rules, GEMM tile plans, spli
     (16, 1536, 4128), (24, 1536, 4128), (24, 6000, 4128), (40, 1536, 4128), (56, 1536, 4128), (100, 1536, 4128), (16, 6000, 4128),
     (24, 1536, 1536), (40, 6000, 1024),
     # one activation row on tall weights: 4 and 8 weight rows per workgroup
-    (1, 24600, 512), (1, 65600, 256),
+    (1, 24600, 1536), (1, 65600, 1056),
     # m = 5..8 on large weights (int8 with fp16 x; fp32 x from n, k >= 4096 or on long K): the MFMA GEMM
     (6, 4160, 4096), (8, 17920, 1024), (7, 64, 9728), (5, 3100, 18464),
     # split wide tiles from k = 2048 (k % 128 == 0)
