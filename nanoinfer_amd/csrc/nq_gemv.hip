@@ -557,59 +557,78 @@ __device__ __forceinline__ float dot16_q4_f32(unsigned w0, unsigned w1, const XC
     }
     return p;
 }
-// Short rows (k <= 1024), one wave per workgroup: half a chunk per lane (8
+// Short rows (k <= 1024, or 2048 with T = 2), one wave per workgroup: half a chunk per lane (8
 // bytes of codes, 16 codes) as the one-row kernel above, so a row of k = 896
 // occupies 56 lanes instead of 28 and each lane's activation vectors (16
 // elements per activation row) serve R rows of 16 codes, the int8 GEMV's ratio
 // at half its code bytes. The lanes holding the row totals after the exchange
-// store them (no LDS, no barrier).
-template <int R, int M, typename XT, typename YT, typename ST>
+// store them (no LDS, no barrier). T = 2: two half chunks per lane (lane l and
+// l + 64), k <= 2048.
+template <int R, int M, typename XT, typename YT, typename ST, int T = 1>
 __global__ __launch_bounds__(kWave) void gemv_q4g_short_kernel(
     const XT* __restrict__ x, const uint8_t* __restrict__ w, const ST* __restrict__ scale,
     const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int group) {
     const int lane = threadIdx.x;
     const int halves = k >> 4, rb = k >> 1;
     const int row0 = xcd_row_group() * R;
-    const bool act = lane < halves;
-    const int hc = act ? lane : 0;  // K columns 16 hc .. 16 hc + 15
-    XChunk<XT> xc[M];
+    bool act[T];
+    int hc[T];  // half chunk of pass t: K columns 16 hc .. 16 hc + 15
 #pragma unroll
-    for (int i = 0; i < M; ++i) xc[i].load(x + static_cast<size_t>(min(i, m - 1)) * k + hc * 16);
+    for (int t = 0; t < T; ++t) {
+        act[t] = lane + kWave * t < halves;
+        hc[t] = act[t] ? lane + kWave * t : 0;
+    }
+    XChunk<XT> xc[T][M];
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int i = 0; i < M; ++i) xc[t][i].load(x + static_cast<size_t>(min(i, m - 1)) * k + hc[t] * 16);
     __builtin_amdgcn_sched_barrier(0);  // the activation requests go out first
     typedef int v2i_t __attribute__((ext_vector_type(2)));
     const unsigned ug = static_cast<unsigned>(group);
     const unsigned blocks = (static_cast<unsigned>(k) + ug - 1) / ug;
-    const unsigned blk = static_cast<unsigned>(hc * 16) / ug;
-    v2i_t wv[R];
-    ST sraw[R];
+    v2i_t wv[R][T];
+    ST sraw[R][T];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const size_t row = static_cast<size_t>(min(row0 + r, n - 1));
-        sraw[r] = scale[row * blocks + blk];
-        wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v2i_t*>(w + row * rb + hc * 8));
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            sraw[r][t] = scale[row * blocks + static_cast<unsigned>(hc[t] * 16) / ug];
+            wv[r][t] = __builtin_nontemporal_load(reinterpret_cast<const v2i_t*>(w + row * rb + hc[t] * 8));
+        }
         __builtin_amdgcn_sched_barrier(0);  // rows in order: row r's dot waits only for rows <= r
     }
     float acc[R][M];
 #pragma unroll
-    for (int i = 0; i < M; ++i) {
-        if constexpr (sizeof(XT) == 2) {
-            h2 pairs[8];
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int d = 0; d < 2; ++d)
+        for (int i = 0; i < M; ++i) acc[r][i] = 0.0f;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) pairs[4 * d + j] = h2{xc[i].v[d][j], xc[i].v[d][j + 4]};
+    for (int t = 0; t < T; ++t) {
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-                acc[r][i] = dot16_q4_f16(static_cast<unsigned>(wv[r][0]), static_cast<unsigned>(wv[r][1]), pairs) *
-                            to_f32(sraw[r]);
-        } else {
+        for (int i = 0; i < M; ++i) {
+            float p[R];
+            if constexpr (sizeof(XT) == 2) {
+                h2 pairs[8];
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-                acc[r][i] = dot16_q4_f32(static_cast<unsigned>(wv[r][0]), static_cast<unsigned>(wv[r][1]), xc[i]) *
-                            to_f32(sraw[r]);
+                for (int d = 0; d < 2; ++d)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) pairs[4 * d + j] = h2{xc[t][i].v[d][j], xc[t][i].v[d][j + 4]};
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    p[r] = dot16_q4_f16(static_cast<unsigned>(wv[r][t][0]), static_cast<unsigned>(wv[r][t][1]), pairs) *
+                           to_f32(sraw[r][t]);
+            } else {
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    p[r] = dot16_q4_f32(static_cast<unsigned>(wv[r][t][0]), static_cast<unsigned>(wv[r][t][1]),
+                                        xc[t][i]) *
+                           to_f32(sraw[r][t]);
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r][i] += act[t] ? p[r] : 0.0f;
         }
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[r][i] = act ? acc[r][i] : 0.0f;
     }
     constexpr int G = 64 / (R * M);
     const float v = wave_reduce_rows<R, M, (R * M >= 16)>(acc, lane);
@@ -1555,6 +1574,30 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
             gemv_q4g_short_kernel<2, M, XT, YT, ST><<<(n + 1) / 2, kWave, 0, s>>>(x, w, sc, b, y, m, n, k, g);
         }
         return;
+    }
+    // k <= 2048: two half chunks per lane (us, old -> new: fp16 x, m = 4, n =
+    // 17920, k = 1536 12.4 -> 11.5; m = 8 22.9 -> 17.9; n = 6144, k = 2048 11.2
+    // -> 8.4; m = 2 5.02 -> 4.71; fp32 x, m = 1, n = 6144 5.78 -> 4.77, with 4
+    // rows n = 17920 8.54 -> 7.92; m = 2, n = k = 1536 4.39 -> 3.71; m = 4 4.86 ->
+    // 4.40). Left out where it lost: one fp16 row on tall weights (n = 8960
+    // 4.58 -> 4.81), fp16 m = 2 and fp32 m = 4 from 8192 rows (8.34 -> 8.46, 11.8
+    // -> 12.1) and fp32 m = 5..8, whose 16 activation chunks per lane spill (19.7
+    // -> 26.7).
+    if (k <= 2048) {
+        constexpr bool f32x = sizeof(XT) == 4;
+        if constexpr (M == 1 && f32x) {
+            if (n >= 8192)
+                gemv_q4g_short_kernel<4, 1, XT, YT, ST, 2><<<(n + 3) / 4, kWave, 0, s>>>(x, w, sc, b, y, m, n, k, g);
+            else
+                gemv_q4g_short_kernel<2, 1, XT, YT, ST, 2><<<(n + 1) / 2, kWave, 0, s>>>(x, w, sc, b, y, m, n, k, g);
+            return;
+        } else if constexpr ((M == 2 || M == 4) || (M == 8 && !f32x)) {
+            const bool two = M == 8 || (M == 2 ? (f32x || n < 8192) : (!f32x || n < 8192));
+            if (two) {
+                gemv_q4g_short_kernel<2, M, XT, YT, ST, 2><<<(n + 1) / 2, kWave, 0, s>>>(x, w, sc, b, y, m, n, k, g);
+                return;
+            }
+        }
     }
     // One fp16 activation row on long K: half a chunk per lane, twice the waves
     // (k = 8960, n = 1536: 4.67-4.69 -> 4.52-4.55 us with 2 rows; one row 5.85,

@@ -135,13 +135,15 @@ WQ_SHAPES = [  # (m, n, k): GEMV buckets, row-group rules, GEMM tile plans, spli
     # one fp16 row, 9216 < k <= 16384: half chunks over up to 16 waves, 3 / 4 / 6 rows per workgroup
     (1, 1000, 11008), (1, 4100, 12288), (1, 8200, 10240),
     # m = 3..4 fp16 on wide weights: 4 weight rows per workgroup (int8 n >= 6144, int4 n >= 3584, k <= 4096)
-    (3, 6200, 2048), (4, 3600, 1536),
+    (3, 6200, 2560), (4, 3600, 3072),
     # fp32 x at m = 2..4 past k = 10240: pairs of 4-row workgroups on the 576-thread bound
     (2, 1100, 12288), (4, 1100, 12288),
     # one fp16 row, int8, 9216 < k <= 12288: one chunk per lane over up to 16 waves, 4 rows
     (1, 1030, 11008),
-    # int4 short rows (k <= 1024): half chunks in one wave, 2 or 4 weight rows
-    (1, 8300, 640), (2, 1100, 1024), (2, 8200, 512), (3, 2000, 768), (8, 9000, 640),
+    # int4 short rows (k <= 1024, or 2048 with two half chunks per lane): one wave, 2 or 4 weight rows
+    (1, 8300, 640), (2, 1100, 1024), (2, 8200, 512), (3, 2000, 768), (8, 9000, 640), (1, 9000, 1088), (3, 9000, 1984),
+    # the one-chunk int4 GEMV forms that now start past k = 2048
+    (1, 2000, 3072), (2, 1536, 3072), (3, 700, 3072), (8, 1536, 3072),
     (1, 1536, 1536), (1, 4864, 896), (1, 1536, 8960), (1, 8960, 5120), (1, 40000, 1536), (1, 1024, 4096),
     (2, 1536, 8960), (2, 4864, 896), (2, 40000, 1536), (2, 256, 1536), (2, 8960, 1536),
     (3, 1536, 2048), (4, 4864, 896), (4, 1536, 8960), (4, 256, 1536),
@@ -159,7 +161,7 @@ WQ_SHAPES = [  # (m, n, k): GEMV buckets, row-group rules, GEMM tile plans, spli
     (16, 1536, 4128), (24, 1536, 4128), (24, 6000, 4128), (40, 1536, 4128), (56, 1536, 4128), (100, 1536, 4128), (16, 6000, 4128),
     (24, 1536, 1536), (40, 6000, 1024),
     # one activation row on tall weights: 4 and 8 weight rows per workgroup
-    (1, 24600, 1536), (1, 65600, 1056),
+    (1, 24600, 2560), (1, 65600, 2080),
     # m = 5..8 on large weights (int8 with fp16 x; fp32 x from n, k >= 4096 or on long K): the MFMA GEMM
     (6, 4160, 4096), (8, 17920, 1024), (7, 64, 9728), (5, 3100, 18464),
     # split wide tiles from k = 2048 (k % 128 == 0)
