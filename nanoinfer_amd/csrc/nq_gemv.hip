@@ -1560,18 +1560,22 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
     // x: n = 4864 4.63 -> 3.56 / 5.53 -> 3.97 / 6.99 -> 4.87 / 9.87 -> 7.68; n =
     // 9728 5.94 -> 4.22 / 7.12 -> 4.83 / 10.6 -> 6.42 / 17.1 -> 12.2). The
     // one-chunk kernel left half of each wave idle there (28 of 64 lanes at k =
-    // 896) and re-read 32 activation elements per 16 bytes of codes.
+    // 896) and re-read 32 activation elements per 16 bytes of codes. m = 5..8
+    // takes 4 rows with fp32 x or from 8192 rows (fp32 x, n = 4864, k = 896 8.2
+    // -> 6.8; n = 9728 12.4 -> 10.4; fp16 x n = 9728 7.7 -> 7.3; fp16 x on fewer
+    // rows even).
     if (k <= 1024) {
         constexpr bool f32x = sizeof(XT) == 4;
-        const bool four = M == 8 ? false
+        const bool four = M == 8 ? f32x || n >= 8192
                           : M == 1 ? n >= 8192
                           : M == 2 ? n >= (f32x ? 4096 : 8192)
                                    : f32x && n >= 4096;
         if (four) {
-            if constexpr (M <= 2 || (M == 4 && f32x))
+            if constexpr (M != 4 || f32x)
                 gemv_q4g_short_kernel<4, M, XT, YT, ST><<<(n + 3) / 4, kWave, 0, s>>>(x, w, sc, b, y, m, n, k, g);
         } else {
-            gemv_q4g_short_kernel<2, M, XT, YT, ST><<<(n + 1) / 2, kWave, 0, s>>>(x, w, sc, b, y, m, n, k, g);
+            if constexpr (M != 8 || !f32x)  // (always four rows there)
+                gemv_q4g_short_kernel<2, M, XT, YT, ST><<<(n + 1) / 2, kWave, 0, s>>>(x, w, sc, b, y, m, n, k, g);
         }
         return;
     }
