@@ -279,6 +279,73 @@ __global__ __launch_bounds__(MAXT) void gemv_q8_kernel(
     }
 }
 
+// Rows of 1024 < k <= 2048 in one wave: two 16-byte chunks per lane (lane l and
+// l + 64), no cross-wave reduction; the lanes holding the row totals after the
+// exchange store them.
+template <int R, int M, typename XT, typename YT>
+__global__ __launch_bounds__(kWave) void gemv_q8_short_kernel(
+    const XT* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ ws,
+    const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k) {
+    constexpr int T = 2;
+    const int lane = threadIdx.x;
+    const int chunks = k >> 4;
+    const int row0 = xcd_row_group() * R;
+    bool act[T];
+    int c[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        act[t] = lane + kWave * t < chunks;
+        c[t] = act[t] ? lane + kWave * t : 0;
+    }
+    XChunk<XT> xc[T][M];
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int i = 0; i < M; ++i) xc[t][i].load(x + static_cast<size_t>(min(i, m - 1)) * k + c[t] * 16);
+    __builtin_amdgcn_sched_barrier(0);
+    v4i wv[R][T];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = min(row0 + r, n - 1);
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+            wv[r][t] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + static_cast<size_t>(row) * k + c[t] * 16));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    constexpr int G = 64 / (R * M);
+    const float ws_early = ws[min(row0 + min(lane / G / M, R - 1), n - 1)];
+    float acc[R][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < M; ++i) acc[r][i] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int i = 0; i < M; ++i)
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float p = 0.0f;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const int wd = wv[r][t][d];
+                    p = __builtin_fmaf(xc[t][i].at(4 * d + 0), sbyte_f32<0>(wd), p);
+                    p = __builtin_fmaf(xc[t][i].at(4 * d + 1), sbyte_f32<1>(wd), p);
+                    p = __builtin_fmaf(xc[t][i].at(4 * d + 2), sbyte_f32<2>(wd), p);
+                    p = __builtin_fmaf(xc[t][i].at(4 * d + 3), sbyte_f32<3>(wd), p);
+                }
+                acc[r][i] += act[t] ? p : 0.0f;
+            }
+    const float v = wave_reduce_rows<R, M, (R * M >= 16)>(acc, lane);
+    if (lane % G == 0) {
+        const int j = lane / G, r = j / M, i = j % M, row = row0 + r;
+        if (row < n && i < m) {
+            const float b = bias ? bias[row] : 0.0f;
+            y[static_cast<size_t>(i) * n + row] = from_f32<YT>(__builtin_fmaf(v, ws_early, b));
+        }
+    }
+}
+
 // ---- group-wise int4 ------------------------------------------------------------------
 // Exact int4 x fp16 dot over one 16-byte chunk (32 codes) with packed fp16 math.
 // Nibble e of dword d is column 8d+e. Masking a dword with 0x000F000F keeps
@@ -1455,6 +1522,18 @@ void launch_q8(const XT* x, const int8_t* w, const float* ws, const float* b, YT
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
     constexpr int R = rows_for<M>();
     const int rows = q8_rows<M, XT>(n, k);
+    // 1024 < k <= 2048 in one wave, two chunks per lane, 2 weight rows: one
+    // activation row on up to 6144 weight rows with fp16 x (us: n = k = 1536 3.23
+    // -> 3.02; n = 6144, k = 2048 4.64 -> 4.42) or 2048 with fp32 x (3.26 -> 3.09;
+    // n = 6144 lost 4.66 -> 4.99), and fp16 m = 3..4 from 6144 rows (n = 6144, k =
+    // 2048 6.94 -> 6.31; n = 17920, k = 1536 11.8 -> 11.5; narrower even or worse).
+    if constexpr (!AM && (M == 1 || (M == 4 && sizeof(XT) == 2))) {
+        const bool take = M == 4 ? n >= 6144 : n <= (sizeof(XT) == 2 ? 6144 : 2048);
+        if (k > 1024 && k <= 2048 && take) {
+            gemv_q8_short_kernel<2, M, XT, YT><<<(n + 1) / 2, kWave, 0, s>>>(x, w, ws, b, y, m, n, k);
+            return;
+        }
+    }
     // m = 2: a workgroup per activation row, the pair on one XCD (n = 1536, k =
     // 8960 fp16 x 7.47 -> 5.88 us, fp32 x 7.71 -> 6.71; n = 4864, k = 896 fp16
     // 3.96 -> 3.58; n = k = 1536 3.87 -> 3.41), except tall short-K weights (n =

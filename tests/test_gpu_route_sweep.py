@@ -144,6 +144,8 @@ WQ_SHAPES = [  # (m, n, k): GEMV buckets, row-group rules, GEMM tile plans, spli
     (1, 8300, 640), (2, 1100, 1024), (2, 8200, 512), (3, 2000, 768), (8, 9000, 640), (1, 9000, 1088), (3, 9000, 1984),
     # the one-chunk int4 GEMV forms that now start past k = 2048
     (1, 2000, 3072), (2, 1536, 3072), (3, 700, 3072), (8, 1536, 3072),
+    # int8 1024 < k <= 2048 in one wave: m = 1 up to 6144 rows, fp16 m = 3..4 from 6144
+    (1, 1100, 2048), (4, 6200, 1088),
     (1, 1536, 1536), (1, 4864, 896), (1, 1536, 8960), (1, 8960, 5120), (1, 40000, 1536), (1, 1024, 4096),
     (2, 1536, 8960), (2, 4864, 896), (2, 40000, 1536), (2, 256, 1536), (2, 8960, 1536),
     (3, 1536, 2048), (4, 4864, 896), (4, 1536, 8960), (4, 256, 1536),
