@@ -2068,17 +2068,27 @@ bool gemv_w8a8_fused_launch(const void* x, nq_dtype xdt, const int8_t* w, const 
         return false;
     const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
     const int threads = ((ki / 16 + kWave - 1) / kWave) * kWave;
+    // 8 weight rows per workgroup from 2048 rows or k = 4096 (every workgroup
+    // quantizes the whole activation row, so more rows share that work; us, 4 ->
+    // 8 rows: n = 1536, k = 8960 7.86 -> 6.43; n = 17920, k = 1536 8.04 -> 7.29;
+    // n = 4096, k = 4096 6.65 -> 5.96; n = 4864, k = 896 3.61 -> 3.12; the LM
+    // head, n = 151936, 50.6 -> 38.0; n = 256 lost 3.04 -> 4.01 and n = k = 1536
+    // was even; 16 rows no better than 8), else 4.
+    const bool big = n >= 2048 || k >= 4096;
     auto go = [&](auto mtag, auto* xp, auto* yp) {
         constexpr int M = decltype(mtag)::value;
-        constexpr int R = rows_for<M>();
         using XT = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
         using YT = std::remove_pointer_t<decltype(yp)>;
-        if (threads == kWave)
-            gemv_w8a8_fused_kernel<R, M, XT, YT, true><<<static_cast<unsigned>((n + R - 1) / R), threads, 0, s>>>(
-                xp, w, ws, bias, yp, mi, ni, ki);
-        else
-            gemv_w8a8_fused_kernel<R, M, XT, YT><<<static_cast<unsigned>((n + R - 1) / R), threads, 0, s>>>(
-                xp, w, ws, bias, yp, mi, ni, ki);
+        auto run = [&](auto rtag) {
+            constexpr int R = decltype(rtag)::value;
+            const unsigned grid = static_cast<unsigned>((n + R - 1) / R);
+            if (threads == kWave)
+                gemv_w8a8_fused_kernel<R, M, XT, YT, true><<<grid, threads, 0, s>>>(xp, w, ws, bias, yp, mi, ni, ki);
+            else
+                gemv_w8a8_fused_kernel<R, M, XT, YT><<<grid, threads, 0, s>>>(xp, w, ws, bias, yp, mi, ni, ki);
+        };
+        if (big) run(std::integral_constant<int, 8>{});
+        else run(std::integral_constant<int, rows_for<M>()>{});
     };
     auto with_y = [&](auto* xp) {
         if (ydt == NQ_F32) go(std::integral_constant<int, 1>{}, xp, static_cast<float*>(y));

@@ -200,7 +200,7 @@ def test_sweep_weight_only(dev, nq, mode, g, sdt, xdt, ydt):
 
 # ---- W8A8 ---------------------------------------------------------------------------------
 W8A8_SHAPES = [
-    (1, 1536, 1536), (1, 4864, 896), (1, 1536, 8960), (1, 64, 4096),
+    (1, 1536, 1536), (1, 4864, 896), (1, 1536, 8960), (1, 64, 4096), (1, 700, 512),
     (2, 1536, 1536), (2, 4864, 896), (2, 8960, 1536), (2, 1536, 8960), (3, 8960, 1536), (3, 1536, 4096),
     (4, 256, 1536), (4, 8960, 1536), (4, 1536, 8960), (5, 1536, 8960), (6, 2048, 4096), (8, 256, 1536),
     (8, 1536, 1536), (8, 4864, 896), (8, 8960, 1536), (8, 1536, 8960), (8, 17920, 1536), (8, 1536, 3072),
