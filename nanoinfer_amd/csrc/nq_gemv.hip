@@ -1689,7 +1689,10 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
     // chunks with 2 / 4 / 6 rows 8.0 / 7.6 / 8.3 us, half chunks with 6 rows 7.3).
     if constexpr (M == 1 && sizeof(XT) == 2) {
         const int th = ((2 * chunks + kWave - 1) / kWave) * kWave;
-        if (chunks >= 160 && th <= kMaxGemvThreads) {
+        // From k = 2048 on tall weights (6 rows; us: n = 14336, k = 4096 9.2 -> 8.75;
+        // n = 6144 5.6 -> 5.3; n = 4608, k = 3584 4.8 -> 4.57; n = 4096 and 28672
+        // even), from k = 5120 below 4096 rows (n = 3584, k = 3584 lost 4.33 -> 4.6).
+        if ((chunks >= 160 || (chunks >= 64 && n >= 4096)) && th <= kMaxGemvThreads) {
             if (n >= 4096)
                 gemv_q4g_x1h_half_kernel<6, YT, ST><<<(n + 5) / 6, th, 0, s>>>(x, w, sc, b, y, n, k, g);
             else

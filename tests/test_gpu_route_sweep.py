@@ -144,6 +144,8 @@ WQ_SHAPES = [  # (m, n, k): GEMV buckets, row-group rules, GEMM tile plans, spli
     (1, 8300, 640), (2, 1100, 1024), (2, 8200, 512), (3, 2000, 768), (8, 9000, 640), (1, 9000, 1088), (3, 9000, 1984),
     # the one-chunk int4 GEMV forms that now start past k = 2048
     (1, 2000, 3072), (2, 1536, 3072), (3, 700, 3072), (8, 1536, 3072),
+    # one fp16 row of int4 from k = 2048 on tall weights: the half-chunk GEMV, 6 rows
+    (1, 4100, 2080),
     # int8 1024 < k <= 2048 in one wave: m = 1 up to 6144 rows, fp16 m = 3..4 from 6144
     (1, 1100, 2048), (4, 6200, 1088),
     (1, 1536, 1536), (1, 4864, 896), (1, 1536, 8960), (1, 8960, 5120), (1, 40000, 1536), (1, 1024, 4096),
@@ -163,7 +165,7 @@ WQ_SHAPES = [  # (m, n, k): GEMV buckets, row-group rules, GEMM tile plans, spli
     (16, 1536, 4128), (24, 1536, 4128), (24, 6000, 4128), (40, 1536, 4128), (56, 1536, 4128), (100, 1536, 4128), (16, 6000, 4128),
     (24, 1536, 1536), (40, 6000, 1024),
     # one activation row on tall weights: 4 and 8 weight rows per workgroup
-    (1, 24600, 2560), (1, 65600, 2080),
+    (1, 24600, 2560), (1, 65600, 1056),
     # m = 5..8 on large weights (int8 with fp16 x; fp32 x from n, k >= 4096 or on long K): the MFMA GEMM
     (6, 4160, 4096), (8, 17920, 1024), (7, 64, 9728), (5, 3100, 18464),
     # split wide tiles from k = 2048 (k % 128 == 0)
