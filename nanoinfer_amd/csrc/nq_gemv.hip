@@ -705,6 +705,95 @@ __global__ __launch_bounds__(kWave) void gemv_q4g_short_kernel(
     }
 }
 
+// Batches of 3..8 fp16 activation rows: a workgroup of S waves owns R weight
+// rows and splits K between its waves (wave w takes half chunks w * 64 + lane,
+// then + 64 S, ...). Each lane converts its 16 codes of a weight row to fp16
+// pairs once and reuses them for all M activation rows (exact products via
+// v_dot2_f32_f16, as dot16_q4_f16), so per 8 bytes of codes it does M dot
+// steps instead of re-reading the codes per activation row; the R x M partial
+// sums are exchanged within the wave, then summed over the S waves in LDS.
+template <int R, int M, typename YT, typename ST>
+__global__ __launch_bounds__(512) void gemv_q4g_tile_kernel(
+    const _Float16* __restrict__ x, const uint8_t* __restrict__ w, const ST* __restrict__ scale,
+    const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int group) {
+    constexpr int NV = R * M, G = 64 / NV;
+    __shared__ float red[8][NV];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = block_threads() >> 6;
+    const int halves = k >> 4, rb = k >> 1;
+    const int row0 = xcd_row_group() * R;
+    const unsigned ug = static_cast<unsigned>(group);
+    const unsigned blocks = (static_cast<unsigned>(k) + ug - 1) / ug;
+    const h2 off1 = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
+    const h2 off16 = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
+    typedef int v2i_t __attribute__((ext_vector_type(2)));
+    float acc[R][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < M; ++i) acc[r][i] = 0.0f;
+#pragma unroll 1
+    for (int h0 = wave * kWave; h0 < halves; h0 += kWave * nw) {
+        const int h = h0 + lane;
+        const bool act = h < halves;
+        const int hc = act ? h : 0;
+        XChunk<_Float16> xc[M];
+#pragma unroll
+        for (int i = 0; i < M; ++i) xc[i].load(x + static_cast<size_t>(min(i, m - 1)) * k + hc * 16);
+        v2i_t wv[R];
+        ST sr[R];
+        const unsigned blk = static_cast<unsigned>(hc * 16) / ug;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const size_t row = static_cast<size_t>(min(row0 + r, n - 1));
+            sr[r] = scale[row * blocks + blk];
+            wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v2i_t*>(w + row * rb + hc * 8));
+        }
+        h2 xp[M][8];
+#pragma unroll
+        for (int i = 0; i < M; ++i)
+#pragma unroll
+            for (int d = 0; d < 2; ++d)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) xp[i][4 * d + j] = h2{xc[i].v[d][j], xc[i].v[d][j + 4]};
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            h2 cp[8];
+#pragma unroll
+            for (int d = 0; d < 2; ++d) {
+                const unsigned wd = static_cast<unsigned>(wv[r][d]), u = wd >> 8;
+                cp[4 * d + 0] = q4_pair(wd, 0x000F000Fu) + off1;
+                cp[4 * d + 1] = q4_pair(wd, 0x00F000F0u) + off16;
+                cp[4 * d + 2] = q4_pair(u, 0x000F000Fu) + off1;
+                cp[4 * d + 3] = q4_pair(u, 0x00F000F0u) + off16;
+            }
+            const float s = act ? to_f32(sr[r]) : 0.0f;
+#pragma unroll
+            for (int i = 0; i < M; ++i) {
+                float p1 = 0.0f, p16 = 0.0f;
+#pragma unroll
+                for (int d = 0; d < 2; ++d) {
+                    p1 = __builtin_amdgcn_fdot2(cp[4 * d + 0], xp[i][4 * d + 0], p1, false);
+                    p16 = __builtin_amdgcn_fdot2(cp[4 * d + 1], xp[i][4 * d + 1], p16, false);
+                    p1 = __builtin_amdgcn_fdot2(cp[4 * d + 2], xp[i][4 * d + 2], p1, false);
+                    p16 = __builtin_amdgcn_fdot2(cp[4 * d + 3], xp[i][4 * d + 3], p16, false);
+                }
+                acc[r][i] = __builtin_fmaf(__builtin_fmaf(p16, 0.0625f, p1), s, acc[r][i]);
+            }
+        }
+    }
+    const float v = wave_reduce_rows<R, M, true>(acc, lane);
+    if (lane % G == 0) red[wave][lane / G] = v;
+    __syncthreads();
+    if (tid < NV) {
+        const int r = tid / M, i = tid % M, row = row0 + r;
+        if (row < n && i < m) {
+            float t = 0.0f;
+            for (int q = 0; q < nw; ++q) t += red[q][tid];
+            y[static_cast<size_t>(i) * n + row] = from_f32<YT>(t + (bias ? bias[row] : 0.0f));
+        }
+    }
+}
+
 // ---- W8A8 (int8 x int8 -> int32) ------------------------------------------------------
 // ACC_OUT: write the raw int32 accumulators instead of the scaled output.
 template <int R, int M, typename YT, bool ACC_OUT>
@@ -1632,6 +1721,30 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
     constexpr int R = 2;
     const int chunks = k >> 5;
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
+    // fp16 activation rows 3..8 on long K (k >= 4096, or 3072 at m = 5..8): the
+    // K-split tile kernel, 4 weight rows per workgroup (8 at m = 5..8 on fewer
+    // than 4096 rows). us, old -> new: m = 4, n = 8960, k = 5120 21.6 -> 17.2; n =
+    // 1536, k = 8960 9.7 -> 8.9; m = 8, n = 1536, k = 8960 12.8 -> 11.7 (4 rows
+    // 14.1); n = 4096, k = 4096 13.2 -> 9.9; n = 6144 20.3 -> 13.3; m = 4, n = 4096,
+    // k = 14336 25.9 -> 19.6. It lost at m = 4, k = 3584 (8.7 -> 9.2), on short K
+    // (k = 1536: 3.8 -> 5.1) and on narrow weights (n = 896, k = 4864: m = 4 4.9
+    // -> 5.3, m = 8 7.9 -> 9.4).
+    if constexpr (sizeof(XT) == 2 && (M == 4 || M == 8)) {
+        if (k >= (M == 8 ? 3072 : 4096) && k <= 18432 && n >= 1024) {
+            const bool r8 = M == 8 && n < 4096;
+            const int RT = r8 ? 8 : 4, groups = (n + RT - 1) / RT;
+            int S = (2048 + groups - 1) / groups;
+            S = S < 1 ? 1 : S > 8 ? 8 : S;
+            if constexpr (M == 8) {
+                if (r8) {
+                    gemv_q4g_tile_kernel<8, 8, YT, ST><<<groups, 64 * S, 0, s>>>(x, w, sc, b, y, m, n, k, g);
+                    return;
+                }
+            }
+            gemv_q4g_tile_kernel<4, M, YT, ST><<<groups, 64 * S, 0, s>>>(x, w, sc, b, y, m, n, k, g);
+            return;
+        }
+    }
     // Short rows: half a chunk per lane in one wave, 2 weight rows per workgroup,
     // 4 on tall weights (us, old -> new, m = 1 / 2 / 4 / 8, fp16 x: n = 4864, k =
     // 896 3.66 -> 3.30 / 4.52 -> 3.79 / 5.87 -> 4.75 / 8.78 -> 7.50; n = 9728

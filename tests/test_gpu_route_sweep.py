@@ -143,7 +143,7 @@ WQ_SHAPES = [  # (m, n, k): GEMV buckets, row-group rules, GEMM tile plans, spli
     # int4 short rows (k <= 1024, or 2048 with two half chunks per lane): one wave, 2 or 4 weight rows
     (1, 8300, 640), (2, 1100, 1024), (2, 8200, 512), (3, 2000, 768), (8, 9000, 640), (1, 9000, 1088), (3, 9000, 1984),
     # the one-chunk int4 GEMV forms that now start past k = 2048
-    (1, 2000, 3072), (2, 1536, 3072), (3, 700, 3072), (8, 1536, 3072),
+    (1, 2000, 3072), (2, 1536, 3072), (3, 700, 3072), (8, 1536, 2560),
     # one fp16 row of int4 from k = 2048 on tall weights: the half-chunk GEMV, 6 rows
     (1, 4100, 2080),
     # int8 1024 < k <= 2048 in one wave: m = 1 up to 6144 rows, fp16 m = 3..4 from 6144
