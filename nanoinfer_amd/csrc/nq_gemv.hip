@@ -346,6 +346,75 @@ __global__ __launch_bounds__(kWave) void gemv_q8_short_kernel(
     }
 }
 
+// int8 codes to fp16 pairs: byte b becomes the half 0x6400 | (b ^ 0x80), i.e.
+// 1024 + (b + 128), and subtracting 1152 leaves b exactly. Pair j of a dword
+// holds codes 2j and 2j + 1 (the activation's natural pair order).
+__device__ __forceinline__ void q8_pairs(unsigned wd, h2& p0, h2& p1) {
+    const h2 off = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
+    const unsigned wx = wd ^ 0x80808080u;
+    p0 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, wx, 0x04010400u)) + off;
+    p1 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, wx, 0x04030402u)) + off;
+}
+// Batches of 3..8 fp16 activation rows of int8 weights: the int4 tile kernel's
+// layout with 16-byte chunks (wave w takes chunks w * 64 + lane, + 64 S, ...);
+// each lane turns its 16 codes of a row into fp16 pairs once and runs one
+// v_dot2 step per pair and activation row (exact products), the row scale after
+// the sums.
+template <int R, int M, typename YT>
+__global__ __launch_bounds__(512) void gemv_q8_tile_kernel(
+    const _Float16* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ ws,
+    const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k) {
+    constexpr int NV = R * M, G = 64 / NV;
+    __shared__ float red[8][NV];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = block_threads() >> 6;
+    const int chunks = k >> 4;
+    const int row0 = xcd_row_group() * R;
+    float acc[R][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < M; ++i) acc[r][i] = 0.0f;
+#pragma unroll 1
+    for (int c0 = wave * kWave; c0 < chunks; c0 += kWave * nw) {
+        const int c = c0 + lane;
+        const bool act = c < chunks;
+        const int cc = act ? c : 0;
+        XChunk<_Float16> xc[M];
+#pragma unroll
+        for (int i = 0; i < M; ++i) xc[i].load(x + static_cast<size_t>(min(i, m - 1)) * k + cc * 16);
+        v4i wv[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            wv[r] = __builtin_nontemporal_load(
+                reinterpret_cast<const v4i*>(w + static_cast<size_t>(min(row0 + r, n - 1)) * k + cc * 16));
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            h2 cp[8];
+#pragma unroll
+            for (int d = 0; d < 4; ++d) q8_pairs(static_cast<unsigned>(wv[r][d]), cp[2 * d], cp[2 * d + 1]);
+#pragma unroll
+            for (int i = 0; i < M; ++i) {
+                const h2* xp = reinterpret_cast<const h2*>(&xc[i].v[0]);
+                float p = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) p = __builtin_amdgcn_fdot2(cp[j], xp[j], p, false);
+                acc[r][i] += act ? p : 0.0f;
+            }
+        }
+    }
+    const float v = wave_reduce_rows<R, M, true>(acc, lane);
+    if (lane % G == 0) red[wave][lane / G] = v;
+    __syncthreads();
+    if (tid < NV) {
+        const int r = tid / M, i = tid % M, row = row0 + r;
+        if (row < n && i < m) {
+            float t = 0.0f;
+            for (int q = 0; q < nw; ++q) t += red[q][tid];
+            y[static_cast<size_t>(i) * n + row] = from_f32<YT>(__builtin_fmaf(t, ws[row], bias ? bias[row] : 0.0f));
+        }
+    }
+}
+
 // ---- group-wise int4 ------------------------------------------------------------------
 // Exact int4 x fp16 dot over one 16-byte chunk (32 codes) with packed fp16 math.
 // Nibble e of dword d is column 8d+e. Masking a dword with 0x000F000F keeps
@@ -1611,6 +1680,27 @@ void launch_q8(const XT* x, const int8_t* w, const float* ws, const float* b, YT
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
     constexpr int R = rows_for<M>();
     const int rows = q8_rows<M, XT>(n, k);
+    // fp16 activation rows 3..8 on 3072 <= k <= 9216 and at least 12 Mi codes: the
+    // K-split tile kernel, 8 weight rows per workgroup from k = 8192 (and at m =
+    // 3..4 from 12288 rows), else 4. us, old -> new: m = 4, n = 8960, k = 5120
+    // 19.0 -> 14.1; n = 4096, k = 4096 8.8 -> 7.1; n = 28672 34.9 -> 28.1; n =
+    // 1536, k = 8960 8.9 -> 7.7; m = 8 (from the MFMA GEMM where it took these):
+    // n = 8960, k = 5120 29.0 -> 20.7; n = 14336, k = 4096 25.3 -> 22.9; n =
+    // 1536, k = 8960 12.4 -> 10.1. Smaller weights (n = 1536, k = 4096 5.0 ->
+    // 5.3) and short K (k = 2048 4.0 -> 4.7) lost, k = 14336 even (m = 3..4).
+    if constexpr (!AM && sizeof(XT) == 2 && (M == 4 || M == 8)) {
+        if (k >= 3072 && k <= 9216 && static_cast<int64_t>(n) * k >= (int64_t(12) << 20)) {
+            const bool r8 = k >= 8192 || (M == 4 && n >= 12288);
+            const int RT = r8 ? 8 : 4, groups = (n + RT - 1) / RT;
+            int S = (2048 + groups - 1) / groups;
+            S = S < 1 ? 1 : S > 8 ? 8 : S;
+            if (r8)
+                gemv_q8_tile_kernel<8, M, YT><<<groups, 64 * S, 0, s>>>(x, w, ws, b, y, m, n, k);
+            else
+                gemv_q8_tile_kernel<4, M, YT><<<groups, 64 * S, 0, s>>>(x, w, ws, b, y, m, n, k);
+            return;
+        }
+    }
     // 1024 < k <= 2048 in one wave, two chunks per lane, 2 weight rows: one
     // activation row on up to 6144 weight rows with fp16 x (us: n = k = 1536 3.23
     // -> 3.02; n = 6144, k = 2048 4.64 -> 4.42) or 2048 with fp32 x (3.26 -> 3.09;

@@ -1078,8 +1078,12 @@ bool wq_q4_batch5_shape(int64_t m, int64_t n, int64_t k) {
 // 18944 39.0 -> 28.6; n = 2048, k = 16384 23.0 -> 15.6; n = 2048, k = 8192 13.5
 // -> 10.8; n = 4096, k = 14336 25.0 -> 24.2; n = 1536, k = 8960 kept, 11.7
 // against 12.2; shorter K kept, n = 3584, k = 3584 9.8 against 11.0).
+// Since the K-split int8 tile GEMV (3072 <= k <= 9216, 12 Mi codes) these tiles
+// and the unsplit GEMM above keep only k > 9216 there (m = 8, us: n = 2048, k =
+// 8192 10.8 -> 9.7; n = 8960, k = 5120 29.0 -> 20.7; n = 4096, k = 14336 stays,
+// 24 against 38).
 bool wq_q8_batch5_shape(int64_t m, int64_t n, int64_t k) {
-    return m >= 5 && m <= 8 && k >= 8192 && k % 128 == 0 && n >= 2048;
+    return m >= 5 && m <= 8 && k > 9216 && k % 128 == 0 && n >= 2048;
 }
 bool wq_gemm_shape_ok(int64_t m, int64_t n, int64_t k, size_t x_elem, bool ws) {
     return m > 8 && (m >= 16 || n >= 1536 || k <= 1024 ||
@@ -1113,7 +1117,7 @@ bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m,
     // k = 8960 keeps the GEMV: 14.6 against 22.9; int4 n = 1536, k = 9728 22.8
     // against 30.7).
     const bool batch5 = m >= 5 && m <= 8 &&
-                        ((!q4 && x_elem == 2 && n >= 4096 && n * k >= (int64_t(16) << 20)) ||
+                        ((!q4 && x_elem == 2 && n >= 4096 && n * k >= (int64_t(16) << 20) && (k < 3072 || k > 9216)) ||
                          (q4 && x_elem == 2 && ws && group <= 64 && wq_q4_batch5_shape(m, n, k)) ||
                          (!q4 && x_elem == 2 && ws && wq_q8_batch5_shape(m, n, k)) ||
                          (x_elem == 4 && ((n >= 4096 && k >= 4096) || (!q4 && k > 9216) ||
