@@ -1688,6 +1688,23 @@ void launch_q8(const XT* x, const int8_t* w, const float* ws, const float* b, YT
     // n = 8960, k = 5120 29.0 -> 20.7; n = 14336, k = 4096 25.3 -> 22.9; n =
     // 1536, k = 8960 12.4 -> 10.1. Smaller weights (n = 1536, k = 4096 5.0 ->
     // 5.3) and short K (k = 2048 4.0 -> 4.7) lost, k = 14336 even (m = 3..4).
+    // m = 2 on the same shapes: 4 weight rows from 4096 rows, 8 on fewer rows
+    // from k = 8192 (us, old -> new: n = 8960, k = 5120 13.6 -> 11.0; n = 28672, k
+    // = 4096 28.4 -> 22.3; n = 2048, k = 8192 6.8 -> 6.2; n = 1536, k = 8960 6.5 ->
+    // 6.4; 4 rows there lost, 7.0).
+    if constexpr (!AM && sizeof(XT) == 2 && M == 2) {
+        if (k >= 3072 && k <= 9216 && static_cast<int64_t>(n) * k >= (int64_t(12) << 20) && (n >= 4096 || k >= 8192)) {
+            const bool r8 = n < 4096;
+            const int RT = r8 ? 8 : 4, groups = (n + RT - 1) / RT;
+            int S = (2048 + groups - 1) / groups;
+            S = S < 1 ? 1 : S > 8 ? 8 : S;
+            if (r8)
+                gemv_q8_tile_kernel<8, 2, YT><<<groups, 64 * S, 0, s>>>(x, w, ws, b, y, m, n, k);
+            else
+                gemv_q8_tile_kernel<4, 2, YT><<<groups, 64 * S, 0, s>>>(x, w, ws, b, y, m, n, k);
+            return;
+        }
+    }
     if constexpr (!AM && sizeof(XT) == 2 && (M == 4 || M == 8)) {
         if (k >= 3072 && k <= 9216 && static_cast<int64_t>(n) * k >= (int64_t(12) << 20)) {
             const bool r8 = k >= 8192 || (M == 4 && n >= 12288);
@@ -1819,6 +1836,18 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
     // k = 14336 25.9 -> 19.6. It lost at m = 4, k = 3584 (8.7 -> 9.2), on short K
     // (k = 1536: 3.8 -> 5.1) and on narrow weights (n = 896, k = 4864: m = 4 4.9
     // -> 5.3, m = 8 7.9 -> 9.4).
+    // m = 2 the same way from k = 4096 on 2048 rows or more (us, old -> new: n =
+    // 4096, k = 14336 16.4 -> 12.9; n = 28672, k = 4096 21.7 -> 19.1; n = 2048, k
+    // = 8192 6.45 -> 5.81; n = 1536, k = 8960 lost 6.1 -> 6.5).
+    if constexpr (sizeof(XT) == 2 && M == 2) {
+        if (k >= 4096 && k <= 18432 && n >= 2048) {
+            const int groups = (n + 3) / 4;
+            int S = (2048 + groups - 1) / groups;
+            S = S < 1 ? 1 : S > 8 ? 8 : S;
+            gemv_q4g_tile_kernel<4, 2, YT, ST><<<groups, 64 * S, 0, s>>>(x, w, sc, b, y, m, n, k, g);
+            return;
+        }
+    }
     if constexpr (sizeof(XT) == 2 && (M == 4 || M == 8)) {
         if (k >= (M == 8 ? 3072 : 4096) && k <= 18432 && n >= 1024) {
             const bool r8 = M == 8 && n < 4096;
