@@ -863,6 +863,97 @@ __global__ __launch_bounds__(512) void gemv_q4g_tile_kernel(
     }
 }
 
+// fp32 activation rows: the tile kernels' layout with fp32 FMAs (the codes of a
+// row converted to float once per lane and reused over the M activation rows).
+// Q4: 16-code half chunks (group scale per half chunk, as the fp16 form); else
+// int8 16-byte chunks, the row scale after the sums.
+template <bool Q4, int R, int M, typename YT, typename ST>
+__global__ __launch_bounds__(512) void gemv_tile_f32_kernel(
+    const float* __restrict__ x, const uint8_t* __restrict__ w, const ST* __restrict__ scale,
+    const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k, int group) {
+    constexpr int NV = R * M, G = 64 / NV;
+    __shared__ float red[8][NV];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = block_threads() >> 6;
+    const int units = k >> 4;  // 16 codes per lane and step
+    const int rb = Q4 ? (k >> 1) : k;
+    const int row0 = xcd_row_group() * R;
+    const unsigned ug = static_cast<unsigned>(group);
+    const unsigned blocks = Q4 ? (static_cast<unsigned>(k) + ug - 1) / ug : 1;
+    typedef int v2i_t __attribute__((ext_vector_type(2)));
+    float acc[R][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < M; ++i) acc[r][i] = 0.0f;
+#pragma unroll 1
+    for (int u0 = wave * kWave; u0 < units; u0 += kWave * nw) {
+        const int u = u0 + lane;
+        const bool act = u < units;
+        const int uc = act ? u : 0;
+        XChunk<float> xc[M];
+#pragma unroll
+        for (int i = 0; i < M; ++i) xc[i].load(x + static_cast<size_t>(min(i, m - 1)) * k + uc * 16);
+        unsigned wd[R][Q4 ? 2 : 4];
+        float sr[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const size_t row = static_cast<size_t>(min(row0 + r, n - 1));
+            if constexpr (Q4) {
+                sr[r] = to_f32(scale[row * blocks + static_cast<unsigned>(uc * 16) / ug]);
+                const v2i_t v = __builtin_nontemporal_load(reinterpret_cast<const v2i_t*>(w + row * rb + uc * 8));
+                wd[r][0] = static_cast<unsigned>(v[0]);
+                wd[r][1] = static_cast<unsigned>(v[1]);
+            } else {
+                const v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(w + row * rb + uc * 16));
+#pragma unroll
+                for (int d = 0; d < 4; ++d) wd[r][d] = static_cast<unsigned>(v[d]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float cf[16];
+            if constexpr (Q4) {
+#pragma unroll
+                for (int d = 0; d < 2; ++d)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        cf[8 * d + e] = static_cast<float>(static_cast<int>((wd[r][d] >> (4 * e)) & 15u) - 8);
+            } else {
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const int v = static_cast<int>(wd[r][d]);
+                    cf[4 * d + 0] = sbyte_f32<0>(v);
+                    cf[4 * d + 1] = sbyte_f32<1>(v);
+                    cf[4 * d + 2] = sbyte_f32<2>(v);
+                    cf[4 * d + 3] = sbyte_f32<3>(v);
+                }
+            }
+            const float s = Q4 ? (act ? sr[r] : 0.0f) : 1.0f;
+#pragma unroll
+            for (int i = 0; i < M; ++i) {
+                float p = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) p = __builtin_fmaf(xc[i].at(e), cf[e], p);
+                if constexpr (Q4) acc[r][i] = __builtin_fmaf(p, s, acc[r][i]);
+                else acc[r][i] += act ? p : 0.0f;
+            }
+        }
+    }
+    const float v = wave_reduce_rows<R, M, true>(acc, lane);
+    if (lane % G == 0) red[wave][lane / G] = v;
+    __syncthreads();
+    if (tid < NV) {
+        const int r = tid / M, i = tid % M, row = row0 + r;
+        if (row < n && i < m) {
+            float t = 0.0f;
+            for (int q = 0; q < nw; ++q) t += red[q][tid];
+            const float b = bias ? bias[row] : 0.0f;
+            if constexpr (Q4) y[static_cast<size_t>(i) * n + row] = from_f32<YT>(t + b);
+            else y[static_cast<size_t>(i) * n + row] = from_f32<YT>(__builtin_fmaf(t, to_f32(scale[row]), b));
+        }
+    }
+}
+
 // ---- W8A8 (int8 x int8 -> int32) ------------------------------------------------------
 // ACC_OUT: write the raw int32 accumulators instead of the scaled output.
 template <int R, int M, typename YT, bool ACC_OUT>
@@ -1688,6 +1779,19 @@ void launch_q8(const XT* x, const int8_t* w, const float* ws, const float* b, YT
     // n = 8960, k = 5120 29.0 -> 20.7; n = 14336, k = 4096 25.3 -> 22.9; n =
     // 1536, k = 8960 12.4 -> 10.1. Smaller weights (n = 1536, k = 4096 5.0 ->
     // 5.3) and short K (k = 2048 4.0 -> 4.7) lost, k = 14336 even (m = 3..4).
+    // fp32 activations, m = 3..4, int8 codes on weights of 8192 rows or more: the
+    // fp32 tile kernel (us: n = 8960, k = 5120 25.5 -> 20.3; n = 14336, k = 4096
+    // 27.9 -> 24.9; narrower weights lost, n = 1536, k = 8960 11.0 -> 12.6).
+    if constexpr (!AM && sizeof(XT) == 4 && M == 4) {
+        if (k >= 3072 && k <= 9216 && n >= 8192) {
+            const int groups = (n + 3) / 4;
+            int S = (2048 + groups - 1) / groups;
+            S = S < 1 ? 1 : S > 8 ? 8 : S;
+            gemv_tile_f32_kernel<false, 4, 4, YT, float><<<groups, 64 * S, 0, s>>>(
+                x, reinterpret_cast<const uint8_t*>(w), ws, b, y, m, n, k, 0);
+            return;
+        }
+    }
     // m = 2 on the same shapes: 4 weight rows from 4096 rows, 8 on fewer rows
     // from k = 8192 (us, old -> new: n = 8960, k = 5120 13.6 -> 11.0; n = 28672, k
     // = 4096 28.4 -> 22.3; n = 2048, k = 8192 6.8 -> 6.2; n = 1536, k = 8960 6.5 ->
@@ -1836,6 +1940,21 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
     // k = 14336 25.9 -> 19.6. It lost at m = 4, k = 3584 (8.7 -> 9.2), on short K
     // (k = 1536: 3.8 -> 5.1) and on narrow weights (n = 896, k = 4864: m = 4 4.9
     // -> 5.3, m = 8 7.9 -> 9.4).
+    // fp32 activations, m = 2..8, int4 codes on long K: the fp32 tile kernel, 4
+    // weight rows (us, old -> new: m = 4, n = 14336, k = 4096 34.6 -> 22.7; n =
+    // 4096, k = 4096 13.0 -> 9.8; n = 1536, k = 8960 15.5 -> 12.6; m = 8, n =
+    // 8960, k = 5120 52.9 -> 45.6 (from the MFMA GEMM); n = 2048, k = 8192 21.3 ->
+    // 16.5; m = 2, n = 14336, k = 4096 21.7 -> 16.4; m = 2 lost on fewer than 2048
+    // rows, n = 1536, k = 8960 8.5 -> 9.2).
+    if constexpr (sizeof(XT) == 4 && (M == 2 || M == 4 || M == 8)) {
+        if (k >= 3072 && k <= 18432 && n >= (M == 2 ? 2048 : 1024)) {
+            const int groups = (n + 3) / 4;
+            int S = (2048 + groups - 1) / groups;
+            S = S < 1 ? 1 : S > 8 ? 8 : S;
+            gemv_tile_f32_kernel<true, 4, M, YT, ST><<<groups, 64 * S, 0, s>>>(x, w, sc, b, y, m, n, k, g);
+            return;
+        }
+    }
     // m = 2 the same way from k = 4096 on 2048 rows or more (us, old -> new: n =
     // 4096, k = 14336 16.4 -> 12.9; n = 28672, k = 4096 21.7 -> 19.1; n = 2048, k
     // = 8192 6.45 -> 5.81; n = 1536, k = 8960 lost 6.1 -> 6.5).
@@ -1973,7 +2092,7 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
                 // activation rows per workgroup (143 VGPRs, no spills; us, 2 -> 4 rows:
                 // m = 2, n = 4096, k = 14336 36.4 -> 26.1; m = 4 64.2 -> 44.6; n = 8192,
                 // k = 11008 103.7 -> 75.4; n = 1536, k = 12288 23.3 -> 16.9).
-                if constexpr (MH <= 2) {
+                if constexpr (MH == 1) {  // (m = 3..4 there: the fp32 tile kernel above)
                     if (threads > 320 && n >= 1024) {
                         gemv_q4g_kernel<4, MH, XT, YT, ST, kMaxGemvThreads, 2><<<(n + 3) / 4 * 2, threads, 0, s>>>(
                             x, w, sc, b, y, m, n, k, g);

@@ -1115,12 +1115,14 @@ bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m,
     // 44.7; n = 3584, k = 18944 128.8 -> 44.9 / 126.3 -> 56.9; n = 6144, k = 4096
     // 19.5 -> 17.4 / 29.4 -> 24.2; int8 n = 2048, k = 10240 37.0 -> 26.8; n = 1536,
     // k = 8960 keeps the GEMV: 14.6 against 22.9; int4 n = 1536, k = 9728 22.8
-    // against 30.7).
+    // against 30.7). int4 codes with fp32 x on k <= 18432 now take the fp32 tile
+    // GEMV instead (n = 8960, k = 5120 52.9 -> 45.6; n = 14336, k = 4096 46.2 ->
+    // 45.0; n = 4096, k = 4096 16.8 -> 15.8).
     const bool batch5 = m >= 5 && m <= 8 &&
                         ((!q4 && x_elem == 2 && n >= 4096 && n * k >= (int64_t(16) << 20) && (k < 3072 || k > 9216)) ||
                          (q4 && x_elem == 2 && ws && group <= 64 && wq_q4_batch5_shape(m, n, k)) ||
                          (!q4 && x_elem == 2 && ws && wq_q8_batch5_shape(m, n, k)) ||
-                         (x_elem == 4 && ((n >= 4096 && k >= 4096) || (!q4 && k > 9216) ||
+                         (x_elem == 4 && ((!q4 && n >= 4096 && k >= 4096) || (!q4 && k > 9216) ||
                                           (q4 && k > 18432 && n >= 3072))));
     if (!forced && !batch5 && !wq_gemm_shape_ok(m, n, k, x_elem, ws)) return false;
     return m > 0 && k > 0 && k % 32 == 0 && (!q4 || (group % 32 == 0 && ((group / 32) & (group / 32 - 1)) == 0)) && aligned(x, 16) && aligned(w, 16) &&

@@ -167,7 +167,7 @@ WQ_SHAPES = [  # (m, n, k): GEMV buckets, row-group rules, GEMM tile plans, spli
     # one activation row on tall weights: 4 and 8 weight rows per workgroup
     (1, 24600, 2560), (1, 65600, 1056),
     # m = 5..8 on large weights (int8 with fp16 x; fp32 x from n, k >= 4096 or on long K): the MFMA GEMM
-    (6, 4160, 4096), (8, 17920, 1024), (7, 64, 9728), (5, 3100, 18464), (6, 2100, 9344), (3, 3100, 4224), (8, 1000, 4160), (2, 4100, 4096), (2, 2048, 8192),
+    (6, 4160, 4096), (8, 17920, 1024), (7, 64, 9728), (5, 3100, 18464), (6, 2100, 9344), (3, 3100, 4224), (8, 1000, 4160), (2, 4100, 4096), (2, 2048, 8192), (4, 8200, 3072), (4, 1536, 2560), (8, 1100, 2560),
     # split wide tiles from k = 2048 (k % 128 == 0)
     (40, 4608, 3584), (16, 1536, 2048),
     # long K (several chunks per lane): int8 past k = 9216, int4 past k = 18432, each m bucket
