@@ -1771,8 +1771,9 @@ void launch_q8(const XT* x, const int8_t* w, const float* ws, const float* b, YT
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
     constexpr int R = rows_for<M>();
     const int rows = q8_rows<M, XT>(n, k);
-    // fp16 activation rows 3..8 on 3072 <= k <= 9216 and at least 12 Mi codes: the
-    // K-split tile kernel, 8 weight rows per workgroup from k = 8192 (and at m =
+    // fp16 activation rows 3..8 on 3072 <= k <= 9216 (4096 at m = 5..8, where the
+    // MFMA GEMM keeps k = 3584: n = 37888 46.4 against 49.3) and at least 12 Mi
+    // codes: the K-split tile kernel, 8 weight rows per workgroup from k = 8192 (and at m =
     // 3..4 from 12288 rows), else 4. us, old -> new: m = 4, n = 8960, k = 5120
     // 19.0 -> 14.1; n = 4096, k = 4096 8.8 -> 7.1; n = 28672 34.9 -> 28.1; n =
     // 1536, k = 8960 8.9 -> 7.7; m = 8 (from the MFMA GEMM where it took these):
@@ -1810,7 +1811,7 @@ void launch_q8(const XT* x, const int8_t* w, const float* ws, const float* b, YT
         }
     }
     if constexpr (!AM && sizeof(XT) == 2 && (M == 4 || M == 8)) {
-        if (k >= 3072 && k <= 9216 && static_cast<int64_t>(n) * k >= (int64_t(12) << 20)) {
+        if (k >= (M == 8 ? 4096 : 3072) && k <= 9216 && static_cast<int64_t>(n) * k >= (int64_t(12) << 20)) {
             const bool r8 = k >= 8192 || (M == 4 && n >= 12288);
             const int RT = r8 ? 8 : 4, groups = (n + RT - 1) / RT;
             int S = (2048 + groups - 1) / groups;
@@ -1932,7 +1933,8 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
     constexpr int R = 2;
     const int chunks = k >> 5;
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
-    // fp16 activation rows 3..8 on long K (k >= 4096, or 3072 at m = 5..8): the
+    // fp16 activation rows 3..8 on long K (k >= 4096; at k = 3584, m = 8 it lost
+    // on n = 3584, 12.1 -> 14.0, and n = 37888, 50.1 -> 51.9): the
     // K-split tile kernel, 4 weight rows per workgroup (8 at m = 5..8 on fewer
     // than 4096 rows). us, old -> new: m = 4, n = 8960, k = 5120 21.6 -> 17.2; n =
     // 1536, k = 8960 9.7 -> 8.9; m = 8, n = 1536, k = 8960 12.8 -> 11.7 (4 rows
@@ -1968,7 +1970,7 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
         }
     }
     if constexpr (sizeof(XT) == 2 && (M == 4 || M == 8)) {
-        if (k >= (M == 8 ? 3072 : 4096) && k <= 18432 && n >= 1024) {
+        if (k >= 4096 && k <= 18432 && n >= 1024) {
             const bool r8 = M == 8 && n < 4096;
             const int RT = r8 ? 8 : 4, groups = (n + RT - 1) / RT;
             int S = (2048 + groups - 1) / groups;

@@ -1066,12 +1066,13 @@ size_t wq_route_bytes(const WqRoute& r, int64_t m, int64_t n) {
 // (n = 1536, k = 8960 12.6 against 13.5; n = 2048, k = 4096 8.5 against 9.7;
 // n = 3072, k = 4096 even), k < 3072 (n = 6144, k = 2048 10.9 against 12.1) and
 // LM heads (n = 65536 even, n = 128256 280 against 296). Since the K-split tile
-// GEMV (3072 <= k <= 18432) these tiles keep only k > 18432 (the tile GEMV, m =
+// GEMV (4096 <= k <= 18432) these tiles keep k < 4096 and k > 18432 (the tile GEMV, m =
 // 8: n = 28672, k = 4096 49.0 -> 41.6; n = 4096, k = 14336 26.5 -> 24.5; n =
 // 6144, k = 4096 15.7 -> 13.4; n = 37888, k = 3584 50.5 vs 51.9; n = 3584, k =
 // 18944 stays 29.3 against 42.9).
 bool wq_q4_batch5_shape(int64_t m, int64_t n, int64_t k) {
-    return m >= 5 && m <= 8 && k > 18432 && k % 128 == 0 && n >= 2048 && n < 65536 && n * k >= (int64_t(14) << 20);
+    return m >= 5 && m <= 8 && ((k >= 3072 && k < 4096) || k > 18432) && k % 128 == 0 && n >= 2048 && n < 65536 &&
+           n * k >= (int64_t(14) << 20);
 }
 // int8 codes with fp16 x at m = 5..8 on long K (k >= 8192) from 2048 rows: the
 // split wide tiles too (us, m = 8, GEMV or unsplit GEMM -> split: n = 3584, k =
@@ -1079,7 +1080,7 @@ bool wq_q4_batch5_shape(int64_t m, int64_t n, int64_t k) {
 // -> 10.8; n = 4096, k = 14336 25.0 -> 24.2; n = 1536, k = 8960 kept, 11.7
 // against 12.2; shorter K kept, n = 3584, k = 3584 9.8 against 11.0).
 // Since the K-split int8 tile GEMV (3072 <= k <= 9216, 12 Mi codes) these tiles
-// and the unsplit GEMM above keep only k > 9216 there (m = 8, us: n = 2048, k =
+// and the unsplit GEMM above keep only k > 9216 and k < 4096 there (m = 8, us: n = 2048, k =
 // 8192 10.8 -> 9.7; n = 8960, k = 5120 29.0 -> 20.7; n = 4096, k = 14336 stays,
 // 24 against 38).
 bool wq_q8_batch5_shape(int64_t m, int64_t n, int64_t k) {
@@ -1119,7 +1120,7 @@ bool wq_gemm_ok(bool q4, const void* x, size_t x_elem, const void* w, int64_t m,
     // GEMV instead (n = 8960, k = 5120 52.9 -> 45.6; n = 14336, k = 4096 46.2 ->
     // 45.0; n = 4096, k = 4096 16.8 -> 15.8).
     const bool batch5 = m >= 5 && m <= 8 &&
-                        ((!q4 && x_elem == 2 && n >= 4096 && n * k >= (int64_t(16) << 20) && (k < 3072 || k > 9216)) ||
+                        ((!q4 && x_elem == 2 && n >= 4096 && n * k >= (int64_t(16) << 20) && (k < 4096 || k > 9216)) ||
                          (q4 && x_elem == 2 && ws && group <= 64 && wq_q4_batch5_shape(m, n, k)) ||
                          (!q4 && x_elem == 2 && ws && wq_q8_batch5_shape(m, n, k)) ||
                          (x_elem == 4 && ((!q4 && n >= 4096 && k >= 4096) || (!q4 && k > 9216) ||
