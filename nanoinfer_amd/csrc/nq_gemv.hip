@@ -2309,6 +2309,87 @@ nq_status gemv_w8a8_launch(const int8_t* xq, const float* as, const int8_t* w, c
     return launch_status("gemv_w8a8_kernel");
 }
 
+namespace {
+// W8A8 batches (m <= 8) over the activation codes: the tile layout with
+// v_dot4_i32_i8 on 16-byte chunks of weight and activation codes (exact int32
+// sums, so the results equal every other W8A8 path bit for bit); a workgroup of
+// S waves owns R weight rows and splits K between its waves.
+template <int R, int M, typename YT>
+__global__ __launch_bounds__(512) void gemv_w8a8_tile_kernel(
+    const int8_t* __restrict__ xq, const float* __restrict__ as, const int8_t* __restrict__ w,
+    const float* __restrict__ ws, const float* __restrict__ bias, YT* __restrict__ y, int m, int n, int k) {
+    constexpr int NV = R * M, G = 64 / NV;
+    __shared__ int red[8][NV];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = block_threads() >> 6;
+    const int chunks = k >> 4;
+    const int row0 = xcd_row_group() * R;
+    int acc[R][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < M; ++i) acc[r][i] = 0;
+#pragma unroll 1
+    for (int c0 = wave * kWave; c0 < chunks; c0 += kWave * nw) {
+        const int c = c0 + lane;
+        const bool act = c < chunks;
+        const int cc = act ? c : 0;
+        v4i xv[M];
+#pragma unroll
+        for (int i = 0; i < M; ++i) xv[i] = *reinterpret_cast<const v4i*>(xq + static_cast<size_t>(min(i, m - 1)) * k + cc * 16);
+        v4i wv[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            wv[r] = __builtin_nontemporal_load(
+                reinterpret_cast<const v4i*>(w + static_cast<size_t>(min(row0 + r, n - 1)) * k + cc * 16));
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int i = 0; i < M; ++i) {
+                int p = 0;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) p = __builtin_amdgcn_sdot4(xv[i][d], wv[r][d], p, false);
+                acc[r][i] += act ? p : 0;
+            }
+    }
+    const int v = wave_reduce_rows<R, M, true>(acc, lane);
+    if (lane % G == 0) red[wave][lane / G] = v;
+    __syncthreads();
+    if (tid < NV) {
+        const int r = tid / M, i = tid % M, row = row0 + r;
+        if (row < n && i < m) {
+            int t = 0;
+            for (int q = 0; q < nw; ++q) t += red[q][tid];
+            const float b = bias ? bias[row] : 0.0f;
+            y[static_cast<size_t>(i) * n + row] = from_f32<YT>(w8a8_epilogue(t, as[i], ws[row], b));
+        }
+    }
+}
+}  // namespace
+
+// Host launch of the W8A8 tile kernel over pre-quantized codes (m <= 8, k % 16
+// == 0, 16-byte aligned codes); returns false (nothing launched) outside that.
+bool w8a8_tile_launch(const int8_t* xq, const float* as, const int8_t* w, const float* ws, const float* bias,
+                      void* y, nq_dtype ydt, int64_t m, int64_t n, int64_t k, hipStream_t s, nq_status* st) {
+    if (!(m >= 1 && m <= 8 && k > 0 && k % 16 == 0 && aligned(w, 16) && aligned(xq, 16) && n <= kMaxIndex))
+        return false;
+    const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
+    auto go = [&](auto mtag, auto* yp) {
+        constexpr int M = decltype(mtag)::value;
+        constexpr int R = 4;
+        const int groups = (ni + R - 1) / R;
+        int S = (2048 + groups - 1) / groups;
+        S = S < 1 ? 1 : S > 8 ? 8 : S;
+        gemv_w8a8_tile_kernel<R, M><<<groups, 64 * S, 0, s>>>(xq, as, w, ws, bias, yp, mi, ni, ki);
+    };
+    auto with_y = [&](auto mtag) {
+        if (ydt == NQ_F32) go(mtag, static_cast<float*>(y));
+        else go(mtag, static_cast<_Float16*>(y));
+    };
+    with_y(std::integral_constant<int, 8>{});
+    *st = launch_status("gemv_w8a8_tile_kernel");
+    return true;
+}
+
 // The decode kernel for m <= 8 (see w8a8_decode_kernel): with pre_scale ==
 // nullptr it quantizes x itself (one launch), else x is the int8 codes of
 // nq_act_quant_i8 and pre_scale their row scales (then also m <= 32, as one

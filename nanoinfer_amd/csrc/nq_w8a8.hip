@@ -891,6 +891,8 @@ constexpr int64_t kDecodePreLongK = 8192;
 // 64 10.50 -> 8.29; n = 1536, m = 32 8.86 -> 8.35, m = 64 10.76 vs 11.49 stays).
 constexpr int64_t kDecodePre32MaxN = 1536, kDecodePre64MaxN = 512;
 nq_status act_quant(const void* x, nq_dtype xdt, int64_t m, int64_t k, int8_t* xq, float* as, hipStream_t s);
+bool w8a8_tile_launch(const int8_t* xq, const float* as, const int8_t* w, const float* ws, const float* bias,
+                      void* y, nq_dtype ydt, int64_t m, int64_t n, int64_t k, hipStream_t s, nq_status* st);
 bool gemv_w8a8_fused_launch(const void* x, nq_dtype xdt, const int8_t* w, const float* ws,
                             const float* bias, void* y, nq_dtype ydt, int64_t m, int64_t n,
                             int64_t k, hipStream_t s, nq_status* st);
@@ -984,6 +986,16 @@ extern "C" nq_status nq_linear_w8a8(const void* x, nq_dtype x_dtype, const int8_
     char* rest = reinterpret_cast<char*>(as) + round_up(static_cast<size_t>(m) * 4, 256);
     const size_t rest_bytes = workspace_bytes - static_cast<size_t>(rest - base);
     if (nq_status st = act_quant(x, x_dtype, m, k, xq, as, s)) return st;
+    // 5..8 rows on large weights with long rows or many of them: the K-split tile
+    // GEMV over the codes, 4 weight rows per workgroup (us, m = 8: n = 4096, k =
+    // 14336 26.4 -> 21.1; n = 4608, k = 3584 14.1 -> 11.6; n = 28672, k = 4096
+    // 32.6 -> 31.2; the Qwen2.5-1.5B shapes and n = k = 4096 lost, 10.2 -> 10.6,
+    // and so did m = 9..16).
+    if (path == NQ_PATH_AUTO && m >= 5 && m <= 8 && n * k >= (int64_t(16) << 20) && k >= 3072 &&
+        (k >= 8192 || n >= 4608)) {
+        nq_status st = NQ_OK;
+        if (w8a8_tile_launch(xq, as, wq, w_scale, bias, y, y_dtype, m, n, k, s, &st)) return st;
+    }
     if (decode16 && ((n <= kDecodePreMaxN && k <= kDecodePreMaxK) ||
                      (m <= 8 && k <= kDecodePreShortK && n <= kDecodePreShortMaxN) ||
                      (m > 4 && m <= 8 && k >= kDecodePreLongK && n <= kDecodePreMaxN)) ||

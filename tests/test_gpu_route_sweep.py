@@ -208,6 +208,8 @@ W8A8_SHAPES = [
     (8, 1536, 1536), (8, 4864, 896), (8, 8960, 1536), (8, 1536, 8960), (8, 17920, 1536), (8, 1536, 3072),
     # the decode kernel's in-kernel quant at m = 2..8 (k up to 4096 at m <= 4)
     (2, 1536, 4096), (2, 8960, 3072), (4, 8960, 1024), (3, 1536, 2560), (5, 8960, 768), (8, 256, 512),
+    # m = 5..8 on large weights with long rows or many rows: the K-split tile GEMV over the codes
+    (6, 4700, 3584), (8, 2100, 8192),
     # the skinny kernel: k % 64 != 0 (no wide tiles), one to four 16-row blocks, 64-row blocks past 64;
     # m <= 16 on long K
     (12, 8960, 1040), (24, 8960, 1040), (40, 8960, 1040), (64, 8960, 1040), (100, 8960, 1040), (12, 8960, 8192),
