@@ -990,9 +990,10 @@ extern "C" nq_status nq_linear_w8a8(const void* x, nq_dtype x_dtype, const int8_
     // GEMV over the codes, 4 weight rows per workgroup (us, m = 8: n = 4096, k =
     // 14336 26.4 -> 21.1; n = 4608, k = 3584 14.1 -> 11.6; n = 28672, k = 4096
     // 32.6 -> 31.2; the Qwen2.5-1.5B shapes and n = k = 4096 lost, 10.2 -> 10.6,
-    // and so did m = 9..16; LM heads keep the MFMA tiles, 111.8 against 114.3).
+    // and so did m = 9..16 and narrow weights, config 3's down projection n = 1536,
+    // k = 8960 11.1 -> 11.6; LM heads keep the MFMA tiles, 111.8 against 114.3).
     if (path == NQ_PATH_AUTO && m >= 5 && m <= 8 && n * k >= (int64_t(12) << 20) && k >= 3072 &&
-        (k >= 8192 || n >= 4608) && n < 65536) {
+        ((k >= 8192 && n >= 2048) || n >= 4608) && n < 65536) {
         nq_status st = NQ_OK;
         if (w8a8_tile_launch(xq, as, wq, w_scale, bias, y, y_dtype, m, n, k, s, &st)) return st;
     }
