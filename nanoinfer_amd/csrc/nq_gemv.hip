@@ -1932,8 +1932,9 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
     constexpr int R = 2;
     const int chunks = k >> 5;
     const int threads = ((chunks + kWave - 1) / kWave) * kWave;
-    // fp16 activation rows 3..8 on long K (k >= 4096; at k = 3584, m = 8 it lost
-    // on n = 3584, 12.1 -> 14.0, and n = 37888, 50.1 -> 51.9): the
+    // fp16 activation rows 3..8 on long K (k >= 4096, or 3072 from 8192 rows: at k
+    // = 3584 it lost on n = 3584, m = 8 12.8 -> 13.9, and won on n = 37888, m = 4
+    // 44.9 -> 40.3, m = 8 54.4 -> 52.9; n = 8960, k = 3072, m = 8 18.5 -> 14.8): the
     // K-split tile kernel, 4 weight rows per workgroup (8 at m = 5..8 on fewer
     // than 4096 rows). us, old -> new: m = 4, n = 8960, k = 5120 21.6 -> 17.2; n =
     // 1536, k = 8960 9.7 -> 8.9; m = 8, n = 1536, k = 8960 12.8 -> 11.7 (4 rows
@@ -1960,7 +1961,7 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
     // 4096, k = 14336 16.4 -> 12.9; n = 28672, k = 4096 21.7 -> 19.1; n = 2048, k
     // = 8192 6.45 -> 5.81; n = 1536, k = 8960 lost 6.1 -> 6.5).
     if constexpr (sizeof(XT) == 2 && M == 2) {
-        if (k >= 4096 && k <= 18432 && n >= 2048) {
+        if ((k >= 4096 || (k >= 3072 && n >= 8192)) && k <= 18432 && n >= 2048) {
             const int groups = (n + 3) / 4;
             int S = (2048 + groups - 1) / groups;
             S = S < 1 ? 1 : S > 8 ? 8 : S;
@@ -1969,7 +1970,7 @@ void launch_q4g(const XT* x, const uint8_t* w, const ST* sc, const float* b, YT*
         }
     }
     if constexpr (sizeof(XT) == 2 && (M == 4 || M == 8)) {
-        if (k >= 4096 && k <= 18432 && n >= 1024) {
+        if ((k >= 4096 || (k >= 3072 && n >= 8192)) && k <= 18432 && n >= 1024) {
             const bool r8 = M == 8 && n < 4096;
             const int RT = r8 ? 8 : 4, groups = (n + RT - 1) / RT;
             int S = (2048 + groups - 1) / groups;

@@ -1066,12 +1066,13 @@ size_t wq_route_bytes(const WqRoute& r, int64_t m, int64_t n) {
 // (n = 1536, k = 8960 12.6 against 13.5; n = 2048, k = 4096 8.5 against 9.7;
 // n = 3072, k = 4096 even), k < 3072 (n = 6144, k = 2048 10.9 against 12.1) and
 // LM heads (n = 65536 even, n = 128256 280 against 296). Since the K-split tile
-// GEMV (4096 <= k <= 18432) these tiles keep k < 4096 and k > 18432 (the tile GEMV, m =
+// GEMV (4096 <= k <= 18432, or from 3072 on 8192 rows) these tiles keep the rest of
+// k < 4096 and k > 18432 (the tile GEMV, m =
 // 8: n = 28672, k = 4096 49.0 -> 41.6; n = 4096, k = 14336 26.5 -> 24.5; n =
 // 6144, k = 4096 15.7 -> 13.4; n = 37888, k = 3584 50.5 vs 51.9; n = 3584, k =
 // 18944 stays 29.3 against 42.9).
 bool wq_q4_batch5_shape(int64_t m, int64_t n, int64_t k) {
-    return m >= 5 && m <= 8 && ((k >= 3072 && k < 4096) || k > 18432) && k % 128 == 0 && n >= 2048 && n < 65536 &&
+    return m >= 5 && m <= 8 && ((k >= 3072 && k < 4096 && n < 8192) || k > 18432) && k % 128 == 0 && n >= 2048 && n < 65536 &&
            n * k >= (int64_t(14) << 20);
 }
 // int8 codes with fp16 x at m = 5..8 on long K (k >= 8192) from 2048 rows: the
